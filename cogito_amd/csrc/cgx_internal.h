@@ -1,0 +1,62 @@
+/*
+ * cgx_internal.h -- the C-ABI seam between the host C code (the cogito API
+ * implementation, *.c) and the HIP side (*.hip).  Plain C types only: device
+ * pointers, sizes, ints and floats.  Every cgk_* launcher enqueues work on
+ * the library stream and returns 0, or -1 with the last error set.
+ */
+#ifndef CGX_INTERNAL_H
+#define CGX_INTERNAL_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include "cg_mi355x.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ----------------------------------------------------------- runtime */
+void cgx_set_error(const char* fmt, ...);
+int cgx_ensure_init(void);
+/* Grow-only device scratch buffers for staging host arguments.  Slots are
+ * reused by later calls, so their contents live until the next call that
+ * names the same slot. */
+enum { CGX_SLOT_IN0 = 0, CGX_SLOT_IN1, CGX_SLOT_IN2, CGX_SLOT_IN3,
+       CGX_SLOT_OUT0, CGX_SLOT_OUT1, CGX_SLOT_WS0, CGX_SLOT_WS1,
+       CGX_SLOT_WS2, CGX_SLOT_WS3, CGX_NUM_SLOTS };
+void* cgx_scratch(int slot, size_t bytes);
+/* Zero-initialised counters that kernels reset themselves after use. */
+unsigned int* cgx_counters(size_t count);
+/* Device view of a host-or-device argument: returns p itself when it is a
+ * device pointer, else copies `bytes` into scratch `slot`. */
+const void* cgx_dev_in(const void* p, size_t bytes, int slot);
+
+/* ------------------------------------------------ quantized-weight registry */
+enum { CGX_LAYOUT_HOST = 0, CGX_LAYOUT_FLAT = 1, CGX_LAYOUT_TILED = 2 };
+typedef struct {
+    int layout;
+    int K, N, group_size;
+} cgx_qinfo;
+int cgx_quant_lookup(const cg_tensor_quant* q, cgx_qinfo* info);
+void cgx_quant_register(const cg_tensor_quant* q, const cgx_qinfo* info);
+void cgx_quant_unregister(const cg_tensor_quant* q);
+
+/* ------------------------------------------------------- INT4 kernels */
+int cgk_int4_quantize(const float* x, int n, int gs, uint8_t* data,
+                      float* scales);
+int cgk_int4_dequantize_flat(const uint8_t* data, const float* scales, int n,
+                             int gs, float* out);
+int cgk_int4_repack_tiled(const uint8_t* flat, const float* scales, int K,
+                          int N, int gs, uint8_t* tiled, float* scales_t);
+int cgk_int4_dequantize_tiled(const uint8_t* tiled, const float* scales_t,
+                              int K, int N, int gs, float* out);
+int cgk_int4_gemv_tiled(const float* x, int M, int K, int N, int gs,
+                        const uint8_t* tiled, const float* scales_t, float* y);
+int cgk_int4_matmul_generic(const float* x, int M, int K, int N, int gs,
+                            const uint8_t* flat, const float* scales, float* y);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CGX_INTERNAL_H */

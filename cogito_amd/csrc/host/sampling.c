@@ -1,0 +1,179 @@
+/*
+ * sampling.c -- cogito's samplers and the chain-verification composition on
+ * top of the acceptance kernels (accept.hip).
+ *
+ *   cg_sample_temperature  reference src/inference/speculative.c:54-75
+ *   cg_sample_corrected    reference src/inference/speculative.c:148-172
+ *   cgx_verify_chain       composition of those with cg_acceptance_prob
+ *                          (:49-52); the reference only declares
+ *                          cg_target_verify (include/cg_speculative.h:99-103)
+ *
+ * The drop-in samplers take host or device rows and draw their uniform from
+ * the same global LCG as the reference, so a program switching libraries
+ * gets the same tokens.  The cgx_*_u / cgx_verify_* forms take pre-drawn
+ * uniforms.
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include "cg_mi355x.h"
+#include "cg_speculative.h"
+#include "cgx_internal.h"
+
+float cgx_lcg_draw(void);
+
+int cgk_exact_expf(const float* x, float* y, int n);
+int cgk_ordered_sum(const float* x, int n, float* out);
+int cgk_sample_temperature(const float* logits, int V, float T, float u, int* out);
+int cgk_sample_corrected(const float* q, const float* p, int V, float u, int* out);
+int cgk_temperature_probs(const float* logits, int V, float T, float* probs);
+int cgk_verify_chain(const float* target, const float* draft, const int* tokens,
+                     const float* u, int batch, int gamma, int V, float T,
+                     float* accept_prob, int* correction, int* bonus,
+                     int* out_tokens, int* n_accepted);
+
+static int uses_filters(int V, int top_k, float top_p) {
+    return (top_k > 0 && top_k < V) || top_p < 1.0f;
+}
+
+static int read_token(const int* dev) {
+    int tok = -1;
+    if (cgx_memcpy_d2h(&tok, dev, sizeof(int))) return -1;
+    return tok;
+}
+
+/* ------------------------------------------------ explicit-uniform forms */
+
+int cgx_sample_temperature_u(const float* logits, int V, float T, float u) {
+    if (!logits || V <= 0) {
+        cgx_set_error("cgx_sample_temperature_u: invalid argument");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    const float* d = (const float*)cgx_dev_in(logits, (size_t)V * 4, CGX_SLOT_IN0);
+    int* out = (int*)cgx_scratch(CGX_SLOT_OUT1, sizeof(int));
+    if (!d || !out || cgk_sample_temperature(d, V, T, u, out)) return -1;
+    return read_token(out);
+}
+
+int cgx_sample_corrected_u(const float* draft_probs, const float* target_probs,
+                           int V, float u) {
+    if (!draft_probs || !target_probs || V <= 0) {
+        cgx_set_error("cgx_sample_corrected_u: invalid argument");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    const float* q = (const float*)cgx_dev_in(draft_probs, (size_t)V * 4, CGX_SLOT_IN0);
+    const float* p = (const float*)cgx_dev_in(target_probs, (size_t)V * 4, CGX_SLOT_IN1);
+    int* out = (int*)cgx_scratch(CGX_SLOT_OUT1, sizeof(int));
+    if (!q || !p || !out || cgk_sample_corrected(q, p, V, u, out)) return -1;
+    return read_token(out);
+}
+
+int cgx_filtered_dist(const float* logits, int V, float T, int top_k, float top_p,
+                      float* dist_out) {
+    if (!logits || !dist_out || V <= 0) {
+        cgx_set_error("cgx_filtered_dist: invalid argument");
+        return -1;
+    }
+    if (uses_filters(V, top_k, top_p)) {
+        cgx_set_error("cgx_filtered_dist: top-k / top-p kernels not implemented yet");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    const float* d = (const float*)cgx_dev_in(logits, (size_t)V * 4, CGX_SLOT_IN0);
+    int out_dev = cgx_is_device_ptr(dist_out);
+    float* o = out_dev ? dist_out : (float*)cgx_scratch(CGX_SLOT_OUT0, (size_t)V * 4);
+    if (!d || !o || cgk_temperature_probs(d, V, T, o)) return -1;
+    if (!out_dev) return cgx_memcpy_d2h(dist_out, o, (size_t)V * 4);
+    return cgx_synchronize();
+}
+
+int cgx_exact_expf_dev(const float* x, float* y, int n) {
+    if (!x || !y || n < 0) {
+        cgx_set_error("cgx_exact_expf_dev: invalid argument");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    return n ? cgk_exact_expf(x, y, n) : 0;
+}
+
+int cgx_ordered_sum_dev(const float* x, int n, float* out_dev) {
+    if (!x || !out_dev || n <= 0) {
+        cgx_set_error("cgx_ordered_sum_dev: invalid argument");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    return cgk_ordered_sum(x, n, out_dev);
+}
+
+/* ------------------------------------------------------ drop-in samplers */
+
+int cg_sample_temperature(float* logits, int vocab_size, float temperature) {
+    float u = cgx_lcg_draw();
+    return cgx_sample_temperature_u(logits, vocab_size, temperature, u);
+}
+
+int cg_sample_corrected(float* draft_probs, float* target_probs, int vocab_size) {
+    float u = cgx_lcg_draw();
+    return cgx_sample_corrected_u(draft_probs, target_probs, vocab_size, u);
+}
+
+/* ------------------------------------------------------------- verify */
+
+int cgx_verify_chain_batch_dev(const float* target_logits, const float* draft_logits,
+                               const int* draft_tokens, const float* u, int batch,
+                               int gamma, int V, float temperature, int top_k,
+                               float top_p, int* out_tokens, int* n_accepted,
+                               float* accept_prob) {
+    if (!target_logits || !draft_logits || !draft_tokens || !u || !out_tokens ||
+        !n_accepted || batch <= 0 || gamma <= 0 || V <= 0) {
+        cgx_set_error("cgx_verify_chain_batch_dev: invalid argument");
+        return -1;
+    }
+    if (uses_filters(V, top_k, top_p)) {
+        cgx_set_error("cgx_verify_chain: top-k / top-p kernels not implemented yet");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    size_t na = (size_t)batch * gamma;
+    char* ws = (char*)cgx_scratch(CGX_SLOT_WS1, na * 4 * 2 + (size_t)batch * 4 + 256);
+    if (!ws) return -1;
+    float* ap = accept_prob ? accept_prob : (float*)ws;
+    int* corr = (int*)(ws + na * 4);
+    int* bonus = (int*)(ws + na * 8);
+    return cgk_verify_chain(target_logits, draft_logits, draft_tokens, u, batch, gamma, V,
+                            temperature, ap, corr, bonus, out_tokens, n_accepted);
+}
+
+int cgx_verify_chain(const float* target_logits, const float* draft_logits,
+                     const int* draft_tokens, const float* u, int gamma, int V,
+                     float temperature, int top_k, float top_p, int* out_tokens,
+                     float* accept_prob) {
+    if (!target_logits || !draft_logits || !draft_tokens || !u || !out_tokens ||
+        gamma <= 0 || V <= 0) {
+        cgx_set_error("cgx_verify_chain: invalid argument");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    const float* t = (const float*)cgx_dev_in(target_logits, (size_t)(gamma + 1) * V * 4,
+                                              CGX_SLOT_IN0);
+    const float* d = (const float*)cgx_dev_in(draft_logits, (size_t)gamma * V * 4,
+                                              CGX_SLOT_IN1);
+    const int* x = (const int*)cgx_dev_in(draft_tokens, (size_t)gamma * 4, CGX_SLOT_IN2);
+    const float* uu = (const float*)cgx_dev_in(u, (size_t)(gamma + 1) * 4, CGX_SLOT_IN3);
+    char* o = (char*)cgx_scratch(CGX_SLOT_OUT1, (size_t)(gamma + 1) * 4 + (size_t)gamma * 4 + 64);
+    if (!t || !d || !x || !uu || !o) return -1;
+    int* dtok = (int*)o;
+    float* dap = (float*)(o + (size_t)(gamma + 1) * 4);
+    int* dn = (int*)(o + (size_t)(gamma + 1) * 4 + (size_t)gamma * 4);
+    if (cgx_verify_chain_batch_dev(t, d, x, uu, 1, gamma, V, temperature, top_k, top_p,
+                                   dtok, dn, dap))
+        return -1;
+    int n = -1;
+    if (cgx_memcpy_d2h(out_tokens, dtok, (size_t)(gamma + 1) * 4) ||
+        cgx_memcpy_d2h(&n, dn, 4))
+        return -1;
+    if (accept_prob && cgx_memcpy_d2h(accept_prob, dap, (size_t)gamma * 4)) return -1;
+    return n;
+}
