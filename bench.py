@@ -36,6 +36,10 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256 * 1024 * 1024
+# HBM bytes per GEMV launch measured with rocprofv3 FETCH_SIZE + WRITE_SIZE,
+# scaled by a copy kernel of known size (profiles/int4_gemv_4096x4096.md).
+# Measured for k_gemv_strip<M, 2, 8>; re-measure when the kernel changes.
+GEMV_TRAFFIC_BYTES = {1: 9136128, 2: 9306112, 3: 9474048, 4: 9641984, 5: 9809920}
 
 
 def log(msg: str) -> None:
@@ -156,6 +160,9 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=5,
                     help="activation rows M of the headline line (gamma+1 = 5)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 256 MiB device-to-device copy (a plain copy kernel "
+                         "of known size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -169,6 +176,17 @@ def main() -> int:
     if lib.cgx_init(0):
         raise RuntimeError(f"cgx_init: {last_error(lib)}")
     log(f"[bench] device: {lib.cgx_device_name().decode()}")
+    if args.calibrate_copy:
+        n = 256 << 20
+        a, b = lib.cgx_malloc(n), lib.cgx_malloc(n)
+        lib.cgx_memset(a, 1, n)
+        for _ in range(5):
+            lib.cgx_memcpy_d2d(b, a, n)
+        lib.cgx_synchronize()
+        log(f"[bench] copied {n} bytes device-to-device 5 times")
+        lib.cgx_free(a)
+        lib.cgx_free(b)
+        return 0
 
     K = N = 4096
     gs = 128
@@ -202,7 +220,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": None},
+                     "traffic": GEMV_TRAFFIC_BYTES.get(args.rows)},
         "cpu_baseline": cpu,
         "per_rows": {str(m): {"us": round(r["us_per_launch"], 3),
                               "GB/s": round(r["gbs"], 1),

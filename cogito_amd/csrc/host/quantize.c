@@ -113,8 +113,10 @@ static cg_tensor_quant* quant_to_device_layout(cg_tensor_quant* q, int want_tile
     int gs = q->group_size;
     int ng = (q->size + gs - 1) / gs;
     size_t nb = ((size_t)q->size + 1) / 2;
-    int tiled = want_tiled && q->ndim == 2 && K % 64 == 0 && N % 64 == 0 &&
-                gs % 64 == 0 && N % gs == 0;
+    /* tiled GEMV layout: 16-column strips of 256-row tiles, one scale group
+     * per strip row */
+    int tiled = want_tiled && q->ndim == 2 && K % 256 == 0 && N % 16 == 0 &&
+                gs % 16 == 0 && N % gs == 0;
 
     cg_tensor_quant* d = (cg_tensor_quant*)calloc(1, sizeof(cg_tensor_quant));
     if (!d) return NULL;

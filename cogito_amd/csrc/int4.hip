@@ -10,14 +10,15 @@
 //   matmul     src/quantize/int4.c:90-114  (y = x @ W, W[K,N], group of
 //                                           element (k,j) = (k*N+j)/gs)
 //
-// Tiled layout (layout 2).  W[K,N] is cut into 64x64 tiles; tiles are stored
-// column-strip major (strip = 64 output columns, all K/64 tiles of a strip
-// contiguous, 2 KiB each).  Inside a tile, lane L of a wave (rb = L/8,
-// cb = L%8) owns rows 8rb..8rb+7 and columns 8cb..8cb+7: 8 little-endian
+// Tiled layout (layout 2).  W[K,N] is cut into column strips of 16 output
+// columns; a strip is stored contiguously as K/256 tiles of 256 rows x 16
+// columns (2 KiB each).  Inside a tile, lane L of a wave (cb = L/32,
+// rb = L%32) owns rows 8rb..8rb+7 and columns 8cb..8cb+7 of the strip: 8
+// little-endian
 // u32 words, one per row, nibble j = column 8cb+j, stored offset-binary
-// (n = v + 8).  One wave-wide pair of 16-byte loads therefore reads a whole
-// 2 KiB tile, fully coalesced.  Scales are transposed to [N/gs][K] so a lane
-// reads the 8 scales of its rows with two 16-byte loads.
+// (n = v + 8).  One wave-wide pair of 16-byte loads reads a whole 2 KiB
+// tile, fully coalesced.  Scales are transposed to [N/gs][K] so a lane reads
+// the 8 scales of its rows with two 16-byte loads.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -28,8 +29,37 @@ namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kTile = 64;                  // rows == cols per tile
-constexpr int kTileBytes = kTile * kTile / 2;
+constexpr int kStripCols = 16;             // output columns per strip
+constexpr int kTileRows = 256;             // rows per tile
+constexpr int kTileBytes = kTileRows * kStripCols / 2;   // 2 KiB
+constexpr int kTileWords = kTileBytes / 4;
+
+// Word index (u32) of row k, columns c..c+7 (c % 8 == 0) in the tiled layout.
+__device__ __forceinline__ size_t tiled_word(int k, int c, int K) {
+    int strip = c / kStripCols, tr = k / kTileRows;
+    int r = k % kTileRows;
+    int lane = ((c % kStripCols) / 8) * 32 + r / 8;
+    size_t tile = (size_t)strip * (K / kTileRows) + tr;
+    return tile * kTileWords + (size_t)lane * 8 + (r % 8);
+}
+
+// v + (v of the lane selected by the DPP control); lanes whose source falls
+// outside the row read 0.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float add_dpp(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL,
+                                                          ROW_MASK, 0xF, true));
+}
+
+// Sum over each 32-lane half of the wave; the totals land in lanes 31 and 63.
+__device__ __forceinline__ float half_wave_sum(float v) {
+    v = add_dpp<0x111>(v);         // row_shr:1
+    v = add_dpp<0x112>(v);         // row_shr:2
+    v = add_dpp<0x114>(v);         // row_shr:4
+    v = add_dpp<0x118>(v);         // row_shr:8  -> lane 15 of each row: row sum
+    v = add_dpp<0x142, 0xA>(v);    // row_bcast:15 into rows 1 and 3
+    return v;
+}
 
 inline hipStream_t stream() { return (hipStream_t)cgx_stream(); }
 
@@ -100,10 +130,7 @@ __global__ void k_repack_tiled(const uint32_t* __restrict__ flat, int K, int N,
     int k = (int)(w / words_per_row);
     int c = (int)(w % words_per_row) * 8;
     uint32_t v = flat[w] ^ 0x88888888u;      // two's complement -> offset binary
-    int strip = c / kTile, tr = k / kTile;
-    int lane = ((k % kTile) / 8) * 8 + (c % kTile) / 8;
-    size_t tile = (size_t)strip * (K / kTile) + tr;
-    tiled[tile * (kTileBytes / 4) + lane * 8 + (k % 8)] = v;
+    tiled[tiled_word(k, c, K)] = v;
 }
 
 __global__ void k_transpose_scales(const float* __restrict__ scales, int K,
@@ -122,10 +149,7 @@ __global__ void k_dequant_tiled(const uint32_t* __restrict__ tiled,
     if (w >= (size_t)K * words_per_row) return;
     int k = (int)(w / words_per_row);
     int c = (int)(w % words_per_row) * 8;
-    int strip = c / kTile, tr = k / kTile;
-    int lane = ((k % kTile) / 8) * 8 + (c % kTile) / 8;
-    size_t tile = (size_t)strip * (K / kTile) + tr;
-    uint32_t v = tiled[tile * (kTileBytes / 4) + lane * 8 + (k % 8)];
+    uint32_t v = tiled[tiled_word(k, c, K)];
     float s = scales_t[(size_t)(c / gs) * K + k];
     for (int j = 0; j < 8; j++)
         out[(size_t)k * N + c + j] = (float)((int)((v >> (4 * j)) & 0xF) - 8) * s;
@@ -133,42 +157,46 @@ __global__ void k_dequant_tiled(const uint32_t* __restrict__ tiled,
 
 // ------------------------------------------------------------------ GEMV
 
-// y[M,N] = x[M,K] @ W for M <= 8.  Grid: (N/64 strips) x ksplit blocks of
-// 256 threads; block (strip, ks) covers tiles [ks*tpb, ks*tpb + tpb) of the
-// strip and wave w takes tiles w, w+4, ... of that range (TPW of them, all
-// loads issued before any arithmetic).  Per lane: 8 columns x M partial
-// sums over its 8 rows of each tile; the offset-binary bias is removed once
-// at the end (sum x*s*(n-8) = sum x*s*n - 8 sum x*s).  Reduction: across the
-// 8 row-blocks of a wave by xor-shuffles, across the 4 waves in LDS, and
-// across the ksplit blocks of a strip through a partial-sum workspace that
-// the last-arriving block sums in fixed order (deterministic, one launch).
-template <int M, int TPW>
-__global__ __launch_bounds__(256) void k_gemv_tiled(
+// y[M,N] = x[M,K] @ W for M <= 8.  One block per 16-column strip, W waves;
+// wave w takes tiles w, w+W, ... of the strip (TPW of them; all weight loads
+// are issued before any arithmetic, activations/scales one tile ahead).
+//
+// Nibble -> float conversion is folded into the FMA: the two nibbles of a
+// 16-bit half, masked to 4 bits, are the binary16 subnormals n * 2^-24, and
+// v_fma_mix_f32 multiplies a binary32 by either half of a packed pair.  The
+// activation carries the 2^24 (x * s * 2^24, exact), so each product is
+// exactly x * s * n, rounded once in the FMA.  Per lane: 8 columns x M
+// partial sums over its 8 rows of each tile; the offset-binary bias is
+// removed at the end (sum x*s*(n-8) = sum x*s*n - 8 sum x*s).  Reduction:
+// lane partials through LDS, 4 threads per output, a quad DPP sum, fixed
+// order (one launch, no inter-block traffic, deterministic).
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+template <int M, int TPW, int W>
+__global__ __launch_bounds__(64 * W) void k_gemv_strip(
     const float* __restrict__ x, int K, int N, int gs,
     const u32x4* __restrict__ tiled, const float* __restrict__ scales_t,
-    float* __restrict__ y, float* __restrict__ partial,
-    unsigned* __restrict__ counters, int ksplit, int tiles_per_block) {
-    const int strip = blockIdx.x / ksplit;
-    const int ks = blockIdx.x % ksplit;
+    float* __restrict__ y) {
+    // Workgroups are dispatched round-robin over the 8 XCDs (block b runs on
+    // XCD b % 8).  Give each XCD a contiguous run of strips so the strips
+    // that share a scale group (and its scale row) hit the same L2.
+    const int per_xcd = gridDim.x / 8;
+    const int strip = (int)blockIdx.x < per_xcd * 8
+                          ? (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8)
+                          : (int)blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int rb = lane >> 3, cb = lane & 7;
-    const int ktiles = K / kTile;
-    const int t_begin = ks * tiles_per_block;
-    const int t_end = min(t_begin + tiles_per_block, ktiles);
-    const float* srow = scales_t + (size_t)((strip * kTile) / gs) * K;
+    const int rb = lane & 31;
+    const int ktiles = K / kTileRows;
+    const float* srow = scales_t + (size_t)((strip * kStripCols) / gs) * K;
     const u32x4* wbase = tiled + (size_t)strip * ktiles * (kTileBytes / 16) + lane * 2;
 
     u32x4 wv[TPW][2];
 #pragma unroll
     for (int j = 0; j < TPW; j++) {
-        int t = t_begin + wave + 4 * j;
-        if (t < t_end) {
-            wv[j][0] = __builtin_nontemporal_load(wbase + (size_t)t * (kTileBytes / 16));
-            wv[j][1] = __builtin_nontemporal_load(wbase + (size_t)t * (kTileBytes / 16) + 1);
-        } else {
-            wv[j][0] = (u32x4)(0x88888888u);
-            wv[j][1] = wv[j][0];
-        }
+        int t = wave + W * j;
+        int tc = t < ktiles ? t : 0;          // clamped: an invalid tile adds 0
+        wv[j][0] = __builtin_nontemporal_load(wbase + (size_t)tc * (kTileBytes / 16));
+        wv[j][1] = __builtin_nontemporal_load(wbase + (size_t)tc * (kTileBytes / 16) + 1);
     }
 
     float acc[M][8];
@@ -180,97 +208,82 @@ __global__ __launch_bounds__(256) void k_gemv_tiled(
         for (int c = 0; c < 8; c++) acc[m][c] = 0.0f;
     }
 
-#pragma unroll
-    for (int j = 0; j < TPW; j++) {
-        int t = t_begin + wave + 4 * j;
-        if (t >= t_end) break;
-        int k0 = t * kTile + rb * 8;
+    float sc[2][8];
+    float xv[2][M][8];
+    auto load_tile = [&](int j, int b) {
+        int t = wave + W * j;
+        bool valid = t < ktiles;
+        int k0 = (valid ? t : 0) * kTileRows + rb * 8;
         float4 sa = *(const float4*)(srow + k0);
         float4 sb = *(const float4*)(srow + k0 + 4);
-        float sc[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
-        float xv[M][8];
+        float z = valid ? 0x1p24f : 0.0f;
+        sc[b][0] = sa.x * z; sc[b][1] = sa.y * z; sc[b][2] = sa.z * z; sc[b][3] = sa.w * z;
+        sc[b][4] = sb.x * z; sc[b][5] = sb.y * z; sc[b][6] = sb.z * z; sc[b][7] = sb.w * z;
 #pragma unroll
         for (int m = 0; m < M; m++) {
             float4 xa = *(const float4*)(x + (size_t)m * K + k0);
             float4 xb = *(const float4*)(x + (size_t)m * K + k0 + 4);
-            xv[m][0] = xa.x; xv[m][1] = xa.y; xv[m][2] = xa.z; xv[m][3] = xa.w;
-            xv[m][4] = xb.x; xv[m][5] = xb.y; xv[m][6] = xb.z; xv[m][7] = xb.w;
+            xv[b][m][0] = xa.x; xv[b][m][1] = xa.y; xv[b][m][2] = xa.z; xv[b][m][3] = xa.w;
+            xv[b][m][4] = xb.x; xv[b][m][5] = xb.y; xv[b][m][6] = xb.z; xv[b][m][7] = xb.w;
         }
+    };
+    load_tile(0, 0);
+#pragma unroll
+    for (int j = 0; j < TPW; j++) {
+        const int b = j & 1;
+        if (j + 1 < TPW) load_tile(j + 1, b ^ 1);
         uint32_t wr[8] = {wv[j][0].x, wv[j][0].y, wv[j][0].z, wv[j][0].w,
                           wv[j][1].x, wv[j][1].y, wv[j][1].z, wv[j][1].w};
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            uint32_t lo = wr[i] & 0x0F0F0F0Fu;
-            uint32_t hi = (wr[i] >> 4) & 0x0F0F0F0Fu;
-            float f[8];
-            f[0] = (float)(lo & 0xFF);         f[1] = (float)(hi & 0xFF);
-            f[2] = (float)((lo >> 8) & 0xFF);  f[3] = (float)((hi >> 8) & 0xFF);
-            f[4] = (float)((lo >> 16) & 0xFF); f[5] = (float)((hi >> 16) & 0xFF);
-            f[6] = (float)(lo >> 24);          f[7] = (float)(hi >> 24);
+            uint32_t w = wr[i];
+            f16x2 h[4] = {__builtin_bit_cast(f16x2, w & 0x000F000Fu),
+                          __builtin_bit_cast(f16x2, (w >> 4) & 0x000F000Fu),
+                          __builtin_bit_cast(f16x2, (w >> 8) & 0x000F000Fu),
+                          __builtin_bit_cast(f16x2, (w >> 12) & 0x000F000Fu)};
 #pragma unroll
             for (int m = 0; m < M; m++) {
-                float xs = xv[m][i] * sc[i];
+                float xs = xv[b][m][i] * sc[b][i];
                 xsum[m] += xs;
 #pragma unroll
-                for (int c = 0; c < 8; c++) acc[m][c] = fmaf(xs, f[c], acc[m][c]);
+                for (int c = 0; c < 4; c++) {
+                    acc[m][c] = fmaf(xs, (float)h[c].x, acc[m][c]);
+                    acc[m][c + 4] = fmaf(xs, (float)h[c].y, acc[m][c + 4]);
+                }
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
     }
 
+    // lane partials -> LDS, row of 8*M (+4 pad) floats per lane
+    constexpr int kStride = 8 * M + 4;
+    __shared__ float red[64 * W * kStride];
 #pragma unroll
-    for (int m = 0; m < M; m++)
+    for (int m = 0; m < M; m++) {
+        float corr = -8.0f * 0x1p-24f * xsum[m];
 #pragma unroll
-        for (int c = 0; c < 8; c++) acc[m][c] = fmaf(-8.0f, xsum[m], acc[m][c]);
-
-    // Sum the 8 row-blocks of the wave (lanes differing in bits 3..5).
-#pragma unroll
-    for (int off = 8; off < 64; off <<= 1)
-#pragma unroll
-        for (int m = 0; m < M; m++)
-#pragma unroll
-            for (int c = 0; c < 8; c++) acc[m][c] += __shfl_xor(acc[m][c], off);
-
-    __shared__ float red[4][M][kTile];
-    __shared__ int s_last;
-    if (lane < 8) {
-#pragma unroll
-        for (int m = 0; m < M; m++)
-#pragma unroll
-            for (int c = 0; c < 8; c++) red[wave][m][cb * 8 + c] = acc[m][c];
+        for (int c = 0; c < 8; c++) red[threadIdx.x * kStride + m * 8 + c] = acc[m][c] + corr;
     }
     __syncthreads();
-
-    const int col0 = strip * kTile;
-    if (ksplit == 1) {
-        for (int i = threadIdx.x; i < M * kTile; i += 256) {
-            int m = i / kTile, col = i % kTile;
-            y[(size_t)m * N + col0 + col] =
-                (red[0][m][col] + red[1][m][col]) + (red[2][m][col] + red[3][m][col]);
-        }
-        return;
+    // 4 threads per output (m, col): part p sums row blocks p, p+4, ... of
+    // every wave; a quad DPP sum combines the parts.
+    const int o = threadIdx.x >> 2, part = threadIdx.x & 3;
+    float v = 0.0f;
+    if (o < kStripCols * M) {
+        int m = o / kStripCols, col = o % kStripCols;
+        int cbo = col / 8, c = col % 8;
+#pragma unroll
+        for (int w = 0; w < W; w++)
+#pragma unroll
+            for (int r = part; r < 32; r += 4)
+                v += red[(w * 64 + cbo * 32 + r) * kStride + m * 8 + c];
     }
-    for (int i = threadIdx.x; i < M * kTile; i += 256) {
-        int m = i / kTile, col = i % kTile;
-        partial[((size_t)ks * M + m) * N + col0 + col] =
-            (red[0][m][col] + red[1][m][col]) + (red[2][m][col] + red[3][m][col]);
+    v = add_dpp<0xB1>(v);            // quad_perm [1,0,3,2]
+    v = add_dpp<0x4E>(v);            // quad_perm [2,3,0,1]
+    if (o < kStripCols * M && part == 0) {
+        int m = o / kStripCols, col = o % kStripCols;
+        y[(size_t)m * N + strip * kStripCols + col] = v;
     }
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned prev = atomicAdd(&counters[strip], 1u);
-        s_last = (prev == (unsigned)(ksplit - 1));
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    for (int i = threadIdx.x; i < M * kTile; i += 256) {
-        int m = i / kTile, col = i % kTile;
-        float v = 0.0f;
-        for (int s = 0; s < ksplit; s++)
-            v += __builtin_nontemporal_load(&partial[((size_t)s * M + m) * N + col0 + col]);
-        y[(size_t)m * N + col0 + col] = v;
-    }
-    if (threadIdx.x == 0) counters[strip] = 0u;
 }
 
 // Reference-order matmul for any K, N, group size: one thread per output,
@@ -297,39 +310,26 @@ __global__ void k_matmul_generic(const float* __restrict__ x, int M, int K,
 template <int M>
 int launch_gemv_m(const float* x, int K, int N, int gs, const uint8_t* tiled,
                   const float* scales_t, float* y) {
-    const int strips = N / kTile, ktiles = K / kTile;
-    // Aim for ~2 blocks (8 waves) per CU on 256 CUs, at least 4 tiles
-    // (8 KiB) per block so the per-block reduction stays amortised.
-    int ksplit = (512 + strips - 1) / strips;
-    int max_split = ktiles / 4 > 0 ? ktiles / 4 : 1;
-    if (ksplit > max_split) ksplit = max_split;
-    if (ksplit < 1) ksplit = 1;
-    int tpb = (ktiles + ksplit - 1) / ksplit;
-    ksplit = (ktiles + tpb - 1) / tpb;
-    int tpw = (tpb + 3) / 4;
-    float* partial = nullptr;
-    unsigned* counters = nullptr;
-    if (ksplit > 1) {
-        partial = (float*)cgx_scratch(CGX_SLOT_WS0, (size_t)ksplit * M * N * sizeof(float));
-        counters = cgx_counters((size_t)strips);
-        if (!partial || !counters) return -1;
-    }
-    dim3 grid(strips * ksplit), block(256);
+    const int strips = N / kStripCols, ktiles = K / kTileRows;
+    constexpr int W = 8;
+    int tpw = (ktiles + W - 1) / W;
+    dim3 grid(strips), block(64 * W);
     const u32x4* t = (const u32x4*)tiled;
-#define CGX_GEMV_CASE(TPW)                                                         \
-    hipLaunchKernelGGL((k_gemv_tiled<M, TPW>), grid, block, 0, stream(), x, K, N, \
-                       gs, t, scales_t, y, partial, counters, ksplit, tpb)
+#define CGX_GEMV_CASE(TPW)                                                          \
+    hipLaunchKernelGGL((k_gemv_strip<M, TPW, W>), grid, block, 0, stream(), x, K, N, \
+                       gs, t, scales_t, y)
     if (tpw <= 1) CGX_GEMV_CASE(1);
     else if (tpw <= 2) CGX_GEMV_CASE(2);
+    else if (tpw <= 3) CGX_GEMV_CASE(3);
     else if (tpw <= 4) CGX_GEMV_CASE(4);
+    else if (tpw <= 6) CGX_GEMV_CASE(6);
     else if (tpw <= 8) CGX_GEMV_CASE(8);
-    else if (tpw <= 16) CGX_GEMV_CASE(16);
     else {
-        cgx_set_error("gemv: K=%d too deep for one launch (tpw %d)", K, tpw);
+        cgx_set_error("gemv: K=%d too deep for one launch (%d tiles per wave)", K, tpw);
         return -1;
     }
 #undef CGX_GEMV_CASE
-    return launch_check("k_gemv_tiled");
+    return launch_check("k_gemv_strip");
 }
 
 }  // namespace
@@ -382,7 +382,7 @@ extern "C" int cgk_int4_dequantize_tiled(const uint8_t* tiled,
 extern "C" int cgk_int4_gemv_tiled(const float* x, int M, int K, int N, int gs,
                                    const uint8_t* tiled, const float* scales_t,
                                    float* y) {
-    if (M < 1 || K % kTile || N % kTile || gs % kTile || N % gs) {
+    if (M < 1 || K % kTileRows || N % kStripCols || gs % kStripCols || N % gs) {
         cgx_set_error("gemv_tiled: unsupported shape M=%d K=%d N=%d gs=%d", M, K,
                       N, gs);
         return -1;

@@ -54,7 +54,7 @@ cg_tensor* cgx_tensor_to_device(cg_tensor* host);
 int cgx_tensor_to_host(cg_tensor* t, float* host_out);
 
 /* Uploads a quantized 2-D weight W[K,N] (reference layout, host or device)
- * into HBM.  When K % 64 == 0, N % 64 == 0, group_size % 64 == 0 and
+ * into HBM.  When K % 256 == 0, N % 16 == 0, group_size % 16 == 0 and
  * N % group_size == 0 the data is re-tiled for the GEMV kernel (layout 2);
  * otherwise it is kept in the reference layout (layout 1).  Free with
  * cg_tensor_quant_free. */

@@ -40,7 +40,7 @@ def test_quantize_bitexact(gpu, oracle, rng, shape, gs):
 
 def test_unpack_all_bytes_on_gpu(gpu, oracle):
     # all 256 bytes, flat and tiled layouts: dequantised values bit-exact
-    K, N, gs = 64, 512, 64
+    K, N, gs = 256, 512, 64
     data = np.tile(np.arange(256, dtype=np.uint8), K * N // 2 // 256)
     rng = np.random.default_rng(7)
     scales = rng.uniform(0.005, 0.02, K * N // gs).astype(np.float32)
@@ -76,7 +76,8 @@ def _make_weight(oracle, rng, K, N, gs, config2=False):
 
 
 @pytest.mark.parametrize("K,N,gs", [(4096, 4096, 128), (256, 512, 64), (1024, 2048, 128),
-                                    (4096, 1024, 128), (11008, 4096, 128), (64, 64, 64)])
+                                    (4096, 1024, 128), (11008, 4096, 128), (256, 16, 16),
+                                    (768, 2304, 128), (3072, 768, 128)])
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
 def test_gemv_tiled_vs_oracle(gpu, oracle, rng, K, N, gs, M):
     if K * N > 4096 * 4096 and M not in (1, 5):
