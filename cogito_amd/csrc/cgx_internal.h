@@ -55,6 +55,33 @@ int cgk_int4_gemv_tiled(const float* x, int M, int K, int N, int gs,
 int cgk_int4_matmul_generic(const float* x, int M, int K, int N, int gs,
                             const uint8_t* flat, const float* scales, float* y);
 
+/* ---------------------------------------- KV cache, attention, RoPE */
+/* attention mask kinds of cgk_attention */
+enum {
+    CGK_MASK_NONE = 0,
+    CGK_MASK_CAUSAL_ALIGNED = 1, /* query q sees keys <= Nk - Nq + q */
+    CGK_MASK_WINDOW = 2,         /* |key - q| <= window */
+    CGK_MASK_CUSTOM = 3,         /* additive fp32 [Nq][Nk] */
+    CGK_MASK_TREE = 4,           /* keys < Nk - Nq, plus ancestor bits */
+    CGK_MASK_CAUSAL = 5          /* query q sees keys <= q */
+};
+int cgk_kv_append(const float* k, const float* v, int T, int H, int D, int gs, int pos,
+                  uint8_t* kc, uint8_t* vc, float* ks, float* vs);
+int cgk_kv_get(const uint8_t* kc, const uint8_t* vc, const float* ks, const float* vs,
+               int len, int H, int D, int gs, float* ko, float* vo);
+/* Q [B][Nq][H][D]; INT4 cache slice (int4 != 0, B must be 1) or fp32
+ * K/V [B][Nk][Hk][D]; O [B][Nq][H][D]; lse optional [B][H][Nq].  anc: HOST
+ * array of Nq <= 64 ancestor bitmasks (tree mask only), passed by value. */
+int cgk_attention(const float* Q, int int4, const uint8_t* kc, const uint8_t* vc,
+                  const float* ks, const float* vs, int gs, const float* K, const float* V,
+                  int B, int Nq, int Nk, int H, int Hk, int D, float scale, int mask_kind,
+                  int window, const float* mask, const unsigned long long* anc, float* O,
+                  float* lse);
+int cgk_rope(float* x, int S, int H, int D, int pos0, float theta);
+int cgk_rope_freqs(float* cs, float* sn, int S, int D, float theta);
+int cgk_alibi_slopes(float* slopes, int H);
+int cgk_alibi_bias(float* bias, int Sq, int Sk, int H, const float* slopes);
+
 #ifdef __cplusplus
 }
 #endif

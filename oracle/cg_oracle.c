@@ -551,6 +551,20 @@ void orc_apply_rope(float* x, int S, int H, int D, int pos0, float theta) {
     }
 }
 
+void orc_alibi_slopes(float* slopes, int H) {
+    /* flash_attn.c:368-374: base = 2^(-8/H), slope_h = base^(h+1) */
+    float base = powf(2.0f, -8.0f / H);
+    for (int h = 0; h < H; h++) slopes[h] = powf(base, (float)(h + 1));
+}
+
+void orc_alibi_bias(float* bias, int Sq, int Sk, int H, const float* slopes) {
+    /* flash_attn.c:376-388: bias[h][q][k] = slope_h * (k - q) */
+    for (int h = 0; h < H; h++)
+        for (int q = 0; q < Sq; q++)
+            for (int k = 0; k < Sk; k++)
+                bias[((size_t)h * Sq + q) * Sk + k] = slopes[h] * (k - q);
+}
+
 void orc_rmsnorm(const float* x, const float* w, float* y, int rows, int d,
                  float eps) {
     /* tensor_kernels.c:894-907 */

@@ -111,6 +111,9 @@ void orc_flash_fwd(const float* Q, const float* K, const float* V, float* O,
 void orc_apply_rope(float* x, int S, int H, int D, int pos0, float theta);
 /* src/attention/flash_attn.c:318-328. */
 void orc_rope_freqs(float* cos_c, float* sin_c, int max_s, int D, float theta);
+/* ALiBi slopes and bias (src/attention/flash_attn.c:368-388). */
+void orc_alibi_slopes(float* slopes, int H);
+void orc_alibi_bias(float* bias, int Sq, int Sk, int H, const float* slopes);
 
 /* A19: src/cuda/tensor_kernels.c:888-909. */
 void orc_rmsnorm(const float* x, const float* w, float* y, int rows, int d,

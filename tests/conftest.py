@@ -55,6 +55,15 @@ def gpu(lib):
     return lib
 
 
+@pytest.fixture(autouse=True)
+def _fresh_error(request):
+    """Each GPU test starts with an empty last-error message (the library
+    keeps the last failure until it is cleared)."""
+    if "gpu" in request.fixturenames:
+        request.getfixturevalue("gpu").cgx_clear_error()
+    yield
+
+
 @pytest.fixture()
 def rng():
     return np.random.default_rng(1234)

@@ -43,6 +43,8 @@ _ORACLE_SIGS = {
     "orc_flash_fwd": (None, [VP, VP, VP, VP, VP, I, I, I, I, I, I, F, I, I, VP]),
     "orc_apply_rope": (None, [VP, I, I, I, I, F]),
     "orc_rope_freqs": (None, [VP, VP, I, I, F]),
+    "orc_alibi_slopes": (None, [VP, I]),
+    "orc_alibi_bias": (None, [VP, I, I, I, VP]),
     "orc_rmsnorm": (None, [VP, VP, VP, I, I, F]),
     "orc_swiglu": (None, [VP, VP, VP, I]),
     "orc_softmax_rows": (None, [VP, VP, I, I]),
@@ -123,6 +125,9 @@ _REF_SIGS = {
     "cg_flash_attention_forward_cpu": (None, [VP]),
     "cg_apply_rope": (None, [VP, VP, I, I, I, I, F]),
     "cg_rope_precompute_freqs": (None, [VP, VP, I, I, F]),
+    "cg_alibi_slopes": (None, [VP, I]),
+    "cg_alibi_bias": (None, [VP, I, I, I, VP]),
+    "cg_kv_cache_int4_reset": (None, [C.POINTER(RefKv)]),
     "cg_cuda_rmsnorm_forward": (None, [C.POINTER(RefTensor), C.POINTER(RefTensor),
                                        C.POINTER(RefTensor), F]),
     "cg_cuda_softmax_forward": (None, [C.POINTER(RefTensor), C.POINTER(RefTensor), I]),
