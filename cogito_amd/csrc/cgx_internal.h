@@ -55,6 +55,30 @@ int cgk_int4_gemv_tiled(const float* x, int M, int K, int N, int gs,
 int cgk_int4_matmul_generic(const float* x, int M, int K, int N, int gs,
                             const uint8_t* flat, const float* scales, float* y);
 
+/* ------------------------------------------- acceptance and filters */
+int cgk_exact_expf(const float* x, float* y, int n);
+int cgk_ordered_sum(const float* x, int n, float* out);
+int cgk_sample_temperature(const float* logits, int V, float T, float u, int* out);
+int cgk_sample_corrected(const float* q, const float* p, int V, float u, int* out);
+int cgk_temperature_probs(const float* logits, int V, float T, float* probs);
+int cgk_verify_chain(const float* target, const float* draft, const int* tokens,
+                     const float* u, int batch, int gamma, int V, float T,
+                     float* accept_prob, int* correction, int* bonus,
+                     int* out_tokens, int* n_accepted);
+/* Verify over dense (filtered) distributions: p [batch][gamma + 1][V]
+ * target (row gamma unused), q [batch][gamma][V] draft; bonus[batch] drawn
+ * beforehand. */
+int cgk_verify_chain_dist(const float* p, const float* q, const int* tokens, const float* u,
+                          int batch, int gamma, int V, const int* bonus, float* accept_prob,
+                          int* correction, int* out_tokens, int* n_accepted);
+/* z = x / T elementwise. */
+int cgk_scale(const float* x, float* z, size_t n, float T);
+/* Top-k (0 < top_k < V) or top-p over rows of z [rows][V]: a token per row
+ * drawn with u[row] (tokens != NULL), or dense filtered distributions
+ * (dist != NULL).  Uses scratch slot WS0. */
+int cgk_filter_rows(const float* z, int rows, int V, int top_k, float top_p, const float* u,
+                    int* tokens, float* dist);
+
 /* ---------------------------------------- KV cache, attention, RoPE */
 /* attention mask kinds of cgk_attention */
 enum {

@@ -1,0 +1,512 @@
+// filter.hip -- top-k and top-p (nucleus) filtering on gfx950, bit-identical
+// to cogito's CPU samplers (src/inference/speculative.c).
+//
+//   cg_sample_top_k  :122-146  insertion top-k with strict '>' against a
+//                              -1e30 floor (ties: the lower index is kept
+//                              and ordered first), then cg_sample_temperature
+//                              over the k values at T = 1
+//   cg_sample_top_p  :77-120   softmax (T = 1); O(V^2) selection sort that
+//                              swaps on every strictly larger element; first
+//                              i with cumsum >= p; r = u * cumsum; scan
+//
+// Top-k: one workgroup per row.  A 4-pass radix select over order-preserving
+// 32-bit keys finds the k-th largest key; elements above it plus the
+// lowest-index ties at it are the reference's list, which a bitonic sort in
+// LDS orders by (value desc, index asc).
+//
+// Top-p: probabilities (exact expf and ordered sum), a bitonic sort of the
+// values in LDS, the exact sequential cumsum over the sorted values for the
+// cutoff and the draw, and the reference's tie order for the one tie group
+// that matters.  The selection sort's order of equal values is not stable
+// but follows a rule that depends only on counts: let the members of the
+// group of value v be i_1 < ... < i_n and g_t the number of elements > v
+// after i_t and before i_(t+1) (g_n: after i_n).  Start with R = [], then
+// for t = 1..n append i_t and rotate R left by g_t (mod t).  R is the order
+// in which the sort emits the group.  (Each pass of the sort moves the chain
+// of strict running maxima one record slot to the right; for the smallest
+// value v present, only its leading run moves, and each pass that consumes an
+// element > v behind that run rotates it by one.)
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cstdint>
+
+#include "cgx_internal.h"
+
+#include "eos.hpp"
+
+namespace {
+
+inline hipStream_t stream() { return (hipStream_t)cgx_stream(); }
+
+int launch_check(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        cgx_set_error("%s launch failed: %s", what, hipGetErrorString(e));
+        return -1;
+    }
+    return 0;
+}
+
+constexpr int kSortMax = 32768;        // top-p: values sorted in LDS
+constexpr int kTopKMax = 4096;         // top-k: list held in LDS
+constexpr float kTopKFloor = -1e30f;   // speculative.c:128
+
+// Order-preserving key of a float; -0 and +0 map to the same key.
+__device__ __forceinline__ uint32_t order_key(float x) {
+    uint32_t b = __float_as_uint(x);
+    if ((b & 0x7fffffffu) == 0) b = 0;
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// Largest float below x: `s >= x` is `x_below < s` for finite fp32 s.
+__device__ __forceinline__ float float_below(float x) {
+    if (x != x || x == -__builtin_inff()) return x;
+    if (x == 0.0f) return -0x1p-149f;
+    uint32_t b = __float_as_uint(x);
+    return __uint_as_float(x > 0.0f ? b - 1 : b + 1);
+}
+
+// Exclusive block scan of one int per thread (1024 threads); *total gets the
+// sum.  `lds` holds kWaves ints.
+__device__ __forceinline__ int block_excl_scan(int v, int* total, int* lds) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        int y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    __syncthreads();
+    if (lane == 63) lds[w] = x;
+    __syncthreads();
+    int off = 0, tot = 0;
+    for (int i = 0; i < kWaves; i++) {
+        int s = lds[i];
+        if (i < w) off += s;
+        tot += s;
+    }
+    __syncthreads();
+    *total = tot;
+    return off + x - v;
+}
+
+__device__ __forceinline__ int block_sum_int(int v, int* lds) {
+    int tot;
+    block_excl_scan(v, &tot, lds);
+    return tot;
+}
+
+// Number of leading entries of a descending array that are > v.
+__device__ __forceinline__ int count_above_sorted(const float* s, int n, float v) {
+    int lo = 0, hi = n;
+    while (lo < hi) {
+        int mid = (lo + hi) >> 1;
+        if (s[mid] > v) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// Number of leading entries of a descending array that are >= v.
+__device__ __forceinline__ int count_atleast_sorted(const float* s, int n, float v) {
+    int lo = 0, hi = n;
+    while (lo < hi) {
+        int mid = (lo + hi) >> 1;
+        if (s[mid] >= v) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// ---------------------------------------------------------------- top-p
+
+// z / T, elementwise (the filtered distribution's first step).
+__global__ void k_scale(const float* __restrict__ x, float* __restrict__ z, size_t n, float T) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) z[i] = __fdiv_rn(x[i], T);
+}
+
+// Softmax at T = 1 of each row (speculative.c:81-90): max, expf(z - max),
+// running fp32 sum, division.
+__global__ __launch_bounds__(kThreads) void k_probs_rows(const float* __restrict__ z, int V,
+                                                         float* __restrict__ probs) {
+    __shared__ EosShared sh;
+    RowSrc src{z + (size_t)blockIdx.x * V};
+    float m = gen_max(src, V, sh);
+    ExpGen<RowSrc> e{src, m, 1.0f};
+    float S = eos_sum(e, V, sh);
+    float* pr = probs + (size_t)blockIdx.x * V;
+    for (int j = threadIdx.x; j < V; j += kThreads) pr[j] = __fdiv_rn(e(j), S);
+}
+
+// Descending bitonic sort of one row of n <= kSortMax non-negative values.
+__global__ __launch_bounds__(kThreads) void k_sort_desc(const float* __restrict__ in, int n,
+                                                        int npow2, float* __restrict__ out) {
+    __shared__ float buf[kSortMax];
+    const float* src = in + (size_t)blockIdx.x * n;
+    for (int i = threadIdx.x; i < npow2; i += kThreads) buf[i] = i < n ? src[i] : -1.0f;
+    __syncthreads();
+    for (int k = 2; k <= npow2; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int p = threadIdx.x; p < npow2 / 2; p += kThreads) {
+                int i = 2 * j * (p / j) + (p % j);
+                int l = i + j;
+                float a = buf[i], b = buf[l];
+                bool desc = (i & k) == 0;
+                if (desc ? (a < b) : (a > b)) {
+                    buf[i] = b;
+                    buf[l] = a;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    float* dst = out + (size_t)blockIdx.x * n;
+    for (int i = threadIdx.x; i < n; i += kThreads) dst[i] = buf[i];
+}
+
+// The tie group {j : p[j] == v} in index order: member indices -> wi[0..m),
+// number of elements > v before each member -> wc[0..m).  Returns m; the
+// count of elements > v in the whole row goes to *gt_total.
+__device__ int tie_members(const float* p, int V, float v, int* wi, int* wc, int* gt_total,
+                           int* lds) {
+    const int per = (V + kThreads - 1) / kThreads;
+    const int lo = threadIdx.x * per, hi = min(V, lo + per);
+    int eq = 0, gt = 0;
+    for (int j = lo; j < hi; j++) {
+        float x = p[j];
+        eq += x == v;
+        gt += x > v;
+    }
+    int m, gtt;
+    int e = block_excl_scan(eq, &m, lds);
+    int g = block_excl_scan(gt, &gtt, lds);
+    for (int j = lo; j < hi; j++) {
+        float x = p[j];
+        if (x == v) {
+            wi[e] = j;
+            wc[e] = g;
+            e++;
+        } else if (x > v) {
+            g++;
+        }
+    }
+    __syncthreads();
+    *gt_total = gtt;
+    return m;
+}
+
+// g_t of the tie rule for 1-based t.
+__device__ __forceinline__ int tie_gap(const int* wc, int m, int gtt, int t) {
+    return (t < m ? wc[t] : gtt) - wc[t - 1];
+}
+
+// Cutoff, draw and (optionally) the filtered distribution of top-p over
+// one row: `probs` (index order) and `sorted` (descending).  ws holds 2V
+// ints per row.
+__global__ __launch_bounds__(kThreads) void k_top_p_finish(
+    const float* __restrict__ probs, const float* __restrict__ sorted, int V, float top_p,
+    const float* __restrict__ u, int* __restrict__ tokens, float* __restrict__ dist,
+    int* __restrict__ ws) {
+    __shared__ EosShared sh;
+    __shared__ int lds[kWaves];
+    __shared__ int s_tok;
+    const int row = blockIdx.x;
+    const float* pr = probs + (size_t)row * V;
+    const float* sr = sorted + (size_t)row * V;
+    int* wi = ws + (size_t)row * 2 * V;
+    int* wc = wi + V;
+    RowSrc s{sr};
+    const float total = eos_sum(s, V, sh);
+    float C;
+    const int ci = gen_find_val(s, V, float_below(top_p), -1, total, &C, sh);
+    const int cutoff = ci < 0 ? V : ci + 1;
+
+    if (tokens) {
+        // speculative.c:109-115: r = u * cumsum; first i < cutoff with r < cumsum
+        float r = __fmul_rn(u[row], C);
+        int pos = gen_find(s, V, r, 0, sh);
+        if (pos >= cutoff) pos = 0;
+        float v = sr[pos];
+        int rank = pos - count_above_sorted(sr, V, v);
+        int gtt;
+        int m = tie_members(pr, V, v, wi, wc, &gtt, lds);
+        if (threadIdx.x == 0) {
+            // walk the rotations backwards from the final slot `rank`
+            int p = rank, tok = wi[0];
+            for (int t = m; t >= 1; t--) {
+                p = (int)(((long long)p + tie_gap(wc, m, gtt, t)) % t);
+                if (p == t - 1) {
+                    tok = wi[t - 1];
+                    break;
+                }
+            }
+            s_tok = tok;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) tokens[row] = s_tok;
+        return;
+    }
+
+    // filtered distribution: kept elements are the first `cutoff` of the
+    // sorted order, divided by the kept mass C
+    float* dr = dist + (size_t)row * V;
+    const float vc = sr[cutoff - 1];
+    const int above = count_above_sorted(sr, V, vc);
+    const int eq_end = count_atleast_sorted(sr, V, vc);
+    const int kept_in_group = cutoff - above;
+    const bool whole = kept_in_group >= eq_end - above;
+    for (int j = threadIdx.x; j < V; j += kThreads) {
+        float x = pr[j];
+        dr[j] = (x > vc || (whole && x == vc)) ? __fdiv_rn(x, C) : 0.0f;
+    }
+    __syncthreads();
+    if (whole) return;
+    int gtt;
+    int m = tie_members(pr, V, vc, wi, wc, &gtt, lds);
+    const float val = __fdiv_rn(vc, C);
+    for (int tt = threadIdx.x; tt < m; tt += kThreads) {
+        int p = tt;
+        for (int t = tt + 1; t <= m; t++) {
+            int g = tie_gap(wc, m, gtt, t) % t;
+            p = (p - g + t) % t;
+        }
+        if (p < kept_in_group) dr[wi[tt]] = val;
+    }
+}
+
+// ---------------------------------------------------------------- top-k
+
+__device__ __forceinline__ unsigned long long topk_entry(uint32_t key, int j) {
+    return ((unsigned long long)key << 32) | (0xFFFFFFFFu - (uint32_t)j);
+}
+
+// Top-k over one row of z (k < V, k <= kTopKMax), then either a token
+// (cg_sample_top_k; with top_p < 1 the nucleus rule over the list) or the
+// filtered distribution (dense row).
+__global__ __launch_bounds__(kThreads) void k_top_k(const float* __restrict__ z, int V, int k,
+                                                    int kpow2, float top_p,
+                                                    const float* __restrict__ u,
+                                                    int* __restrict__ tokens,
+                                                    float* __restrict__ dist) {
+    __shared__ EosShared sh;
+    __shared__ unsigned long long cand[kTopKMax];
+    __shared__ int hist[256];
+    __shared__ int lds[kWaves];
+    __shared__ int s_digit, s_need, s_ncand;
+    const int row = blockIdx.x, t = threadIdx.x;
+    const float* zr = z + (size_t)row * V;
+    const uint32_t kfloor = order_key(kTopKFloor);
+
+    // eligible: value > -1e30 (never inserted otherwise; NaN never is)
+    int elig = 0;
+    for (int j = t; j < V; j += kThreads) {
+        float x = zr[j];
+        elig += (x > kTopKFloor);
+    }
+    const int E = block_sum_int(elig, lds);
+    const bool all = E <= k;
+
+    // radix select of the k-th largest key among eligible elements
+    uint32_t prefix = 0, pmask = 0;
+    int need = k;
+    if (!all) {
+        for (int pass = 0; pass < 4; pass++) {
+            const int shift = 24 - 8 * pass;
+            for (int i = t; i < 256; i += kThreads) hist[i] = 0;
+            __syncthreads();
+            for (int j = t; j < V; j += kThreads) {
+                float x = zr[j];
+                uint32_t key = order_key(x);
+                if (x > kTopKFloor && (key & pmask) == prefix)
+                    atomicAdd(&hist[(key >> shift) & 255], 1);
+            }
+            __syncthreads();
+            if (t == 0) {
+                int nd = need, d = 255;
+                for (; d > 0; d--) {
+                    if (nd <= hist[d]) break;
+                    nd -= hist[d];
+                }
+                s_digit = d;
+                s_need = nd;
+            }
+            __syncthreads();
+            prefix |= (uint32_t)s_digit << shift;
+            pmask |= 0xFFu << shift;
+            need = s_need;
+            __syncthreads();
+        }
+    }
+    const uint32_t T = prefix;              // key of the k-th largest
+
+    // collect: every eligible key > T, then the first `need` keys == T by index
+    if (t == 0) s_ncand = 0;
+    __syncthreads();
+    for (int j = t; j < V; j += kThreads) {
+        float x = zr[j];
+        uint32_t key = order_key(x);
+        if (x > kTopKFloor && (all || key > T)) cand[atomicAdd(&s_ncand, 1)] = topk_entry(key, j);
+    }
+    if (!all) {
+        const int per = (V + kThreads - 1) / kThreads;
+        const int lo = t * per, hi = min(V, lo + per);
+        int eq = 0;
+        for (int j = lo; j < hi; j++) eq += (zr[j] > kTopKFloor && order_key(zr[j]) == T);
+        int tot;
+        int r = block_excl_scan(eq, &tot, lds);
+        for (int j = lo; j < hi && r < need; j++) {
+            float x = zr[j];
+            if (x > kTopKFloor && order_key(x) == T) {
+                cand[atomicAdd(&s_ncand, 1)] = topk_entry(order_key(x), j);
+                r++;
+            }
+        }
+    }
+    __syncthreads();
+    const int ncand = s_ncand;
+    // unfilled slots keep the reference's initial (-1e30, 0); sort padding last
+    for (int i = ncand + t; i < kpow2; i += kThreads)
+        cand[i] = i < k ? topk_entry(kfloor, 0) : 0ull;
+    __syncthreads();
+    for (int kk = 2; kk <= kpow2; kk <<= 1) {
+        for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+            for (int p = t; p < kpow2 / 2; p += kThreads) {
+                int i = 2 * jj * (p / jj) + (p % jj);
+                int l = i + jj;
+                unsigned long long a = cand[i], b = cand[l];
+                bool desc = (i & kk) == 0;
+                if (desc ? (a < b) : (a > b)) {
+                    cand[i] = b;
+                    cand[l] = a;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    // decode in place into vals[kTopKMax] | idx[kTopKMax]
+    float rv[kTopKMax / kThreads];
+    int ri[kTopKMax / kThreads];
+#pragma unroll
+    for (int q = 0; q < kTopKMax / kThreads; q++) {
+        int i = t + q * kThreads;
+        rv[q] = 0.0f;
+        ri[q] = 0;
+        if (i < k) {
+            unsigned long long c = cand[i];
+            uint32_t key = (uint32_t)(c >> 32);
+            int j = (int)(0xFFFFFFFFu - (uint32_t)c);
+            if (key == kfloor) {
+                rv[q] = kTopKFloor;
+                ri[q] = 0;
+            } else {
+                rv[q] = zr[j];
+                ri[q] = j;
+            }
+        }
+    }
+    __syncthreads();
+    float* vals = (float*)cand;
+    int* idx = (int*)cand + kTopKMax;
+#pragma unroll
+    for (int q = 0; q < kTopKMax / kThreads; q++) {
+        int i = t + q * kThreads;
+        if (i < k) {
+            vals[i] = rv[q];
+            idx[i] = ri[q];
+        }
+    }
+    __syncthreads();
+
+    const bool use_p = top_p < 1.0f;
+    RowSrc vs{vals};
+    if (tokens && !use_p) {
+        int j = sample_temperature_gen(vs, k, 1.0f, u[row], sh);
+        if (t == 0) tokens[row] = idx[j];
+        return;
+    }
+    // list probabilities: cg_sample_temperature's softmax at T = 1
+    float m = gen_max(vs, k, sh);
+    ExpGen<RowSrc> e{vs, m, 1.0f};
+    float S = eos_sum(e, k, sh);
+    DivGen<ExpGen<RowSrc>> pr{e, S};
+    int keep = k;
+    float mass = 1.0f;
+    if (use_p) {
+        float tot = eos_sum(pr, k, sh);
+        int ci = gen_find_val(pr, k, float_below(top_p), -1, tot, &mass, sh);
+        keep = ci < 0 ? k : ci + 1;
+    }
+    if (tokens) {
+        int j = gen_find(pr, k, __fmul_rn(u[row], mass), 0, sh);
+        if (j >= keep) j = 0;
+        if (t == 0) tokens[row] = idx[j];
+        return;
+    }
+    float* dr = dist + (size_t)row * V;
+    for (int j = t; j < V; j += kThreads) dr[j] = 0.0f;
+    __syncthreads();
+    // list indices are distinct except the (-1e30, 0) fillers, whose
+    // probability is 0 and which are never written
+    for (int j = t; j < keep; j += kThreads) {
+        float v = use_p ? __fdiv_rn(pr(j), mass) : pr(j);
+        if (v != 0.0f) dr[idx[j]] = v;
+    }
+}
+
+}  // namespace
+
+// -------------------------------------------------------------- launchers
+
+extern "C" int cgk_scale(const float* x, float* z, size_t n, float T) {
+    if (!n) return 0;
+    hipLaunchKernelGGL(k_scale, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream(), x,
+                       z, n, T);
+    return launch_check("k_scale");
+}
+
+// Top-k / top-p over `rows` rows of z [rows][V]: tokens[row] drawn with
+// u[row] (tokens != NULL), or dense filtered distributions (dist != NULL).
+extern "C" int cgk_filter_rows(const float* z, int rows, int V, int top_k, float top_p,
+                               const float* u, int* tokens, float* dist) {
+    if (rows <= 0 || V <= 0 || rows > 65535 || (!tokens == !dist)) {
+        cgx_set_error("filter: invalid arguments");
+        return -1;
+    }
+    if (V > kRound * kMaxRounds) {
+        cgx_set_error("filter: vocabulary size %d above %d", V, kRound * kMaxRounds);
+        return -1;
+    }
+    if (top_k > 0 && top_k < V) {
+        if (top_k > kTopKMax) {
+            cgx_set_error("top-k: k = %d above the supported %d", top_k, kTopKMax);
+            return -1;
+        }
+        int kpow2 = 64;
+        while (kpow2 < top_k) kpow2 <<= 1;
+        hipLaunchKernelGGL(k_top_k, dim3(rows), dim3(kThreads), 0, stream(), z, V, top_k,
+                           kpow2, top_p, u, tokens, dist);
+        return launch_check("k_top_k");
+    }
+    if (V > kSortMax) {
+        cgx_set_error("top-p: vocabulary size %d above the supported %d", V, kSortMax);
+        return -1;
+    }
+    size_t n = (size_t)rows * V;
+    char* w = (char*)cgx_scratch(CGX_SLOT_WS0, n * (4 + 4 + 8));
+    if (!w) return -1;
+    float* probs = (float*)w;
+    float* sorted = probs + n;
+    int* ws = (int*)(sorted + n);
+    int npow2 = 64;
+    while (npow2 < V) npow2 <<= 1;
+    hipLaunchKernelGGL(k_probs_rows, dim3(rows), dim3(kThreads), 0, stream(), z, V, probs);
+    if (launch_check("k_probs_rows")) return -1;
+    hipLaunchKernelGGL(k_sort_desc, dim3(rows), dim3(kThreads), 0, stream(), probs, V, npow2,
+                       sorted);
+    if (launch_check("k_sort_desc")) return -1;
+    hipLaunchKernelGGL(k_top_p_finish, dim3(rows), dim3(kThreads), 0, stream(), probs, sorted,
+                       V, top_p, u, tokens, dist, ws);
+    return launch_check("k_top_p_finish");
+}

@@ -12,8 +12,6 @@
 #define PENDING(name) cgx_set_error("%s: not implemented yet", name)
 
 /* cg_speculative.h: sampling and verification */
-int cg_sample_top_p(float* l, int V, float p) { (void)l; (void)V; (void)p; PENDING("cg_sample_top_p"); return -1; }
-int cg_sample_top_k(float* l, int V, int k) { (void)l; (void)V; (void)k; PENDING("cg_sample_top_k"); return -1; }
 int cg_sample_typical(float* l, int V, float p) { (void)l; (void)V; (void)p; PENDING("cg_sample_typical"); return -1; }
 int cg_target_verify(cg_speculative_decoder* d, cg_tensor* ids, cg_token_tree* t) {
     (void)d; (void)ids; (void)t; PENDING("cg_target_verify"); return -1;
@@ -36,5 +34,3 @@ cg_token_tree* cg_eagle_generate_tree(cg_eagle_draft* e, cg_tensor* in, int d) {
 int* cg_eagle_compute_branching(cg_eagle_draft* e, cg_tensor* f) {
     (void)e; (void)f; PENDING("cg_eagle_compute_branching"); return NULL;
 }
-int cgx_sample_top_k_u(const float* l, int V, int k, float u) { (void)l; (void)V; (void)k; (void)u; PENDING("x"); return -1; }
-int cgx_sample_top_p_u(const float* l, int V, float p, float u) { (void)l; (void)V; (void)p; (void)u; PENDING("x"); return -1; }

@@ -4,6 +4,8 @@
  *
  *   cg_sample_temperature  reference src/inference/speculative.c:54-75
  *   cg_sample_corrected    reference src/inference/speculative.c:148-172
+ *   cg_sample_top_p        reference src/inference/speculative.c:77-120
+ *   cg_sample_top_k        reference src/inference/speculative.c:122-146
  *   cgx_verify_chain       composition of those with cg_acceptance_prob
  *                          (:49-52); the reference only declares
  *                          cg_target_verify (include/cg_speculative.h:99-103)
@@ -21,16 +23,6 @@
 #include "cgx_internal.h"
 
 float cgx_lcg_draw(void);
-
-int cgk_exact_expf(const float* x, float* y, int n);
-int cgk_ordered_sum(const float* x, int n, float* out);
-int cgk_sample_temperature(const float* logits, int V, float T, float u, int* out);
-int cgk_sample_corrected(const float* q, const float* p, int V, float u, int* out);
-int cgk_temperature_probs(const float* logits, int V, float T, float* probs);
-int cgk_verify_chain(const float* target, const float* draft, const int* tokens,
-                     const float* u, int batch, int gamma, int V, float T,
-                     float* accept_prob, int* correction, int* bonus,
-                     int* out_tokens, int* n_accepted);
 
 static int uses_filters(int V, int top_k, float top_p) {
     return (top_k > 0 && top_k < V) || top_p < 1.0f;
@@ -76,15 +68,19 @@ int cgx_filtered_dist(const float* logits, int V, float T, int top_k, float top_
         cgx_set_error("cgx_filtered_dist: invalid argument");
         return -1;
     }
-    if (uses_filters(V, top_k, top_p)) {
-        cgx_set_error("cgx_filtered_dist: top-k / top-p kernels not implemented yet");
-        return -1;
-    }
     if (cgx_ensure_init()) return -1;
     const float* d = (const float*)cgx_dev_in(logits, (size_t)V * 4, CGX_SLOT_IN0);
     int out_dev = cgx_is_device_ptr(dist_out);
     float* o = out_dev ? dist_out : (float*)cgx_scratch(CGX_SLOT_OUT0, (size_t)V * 4);
-    if (!d || !o || cgk_temperature_probs(d, V, T, o)) return -1;
+    if (!d || !o) return -1;
+    if (uses_filters(V, top_k, top_p)) {
+        float* z = (float*)cgx_scratch(CGX_SLOT_WS3, (size_t)V * 4);
+        if (!z || cgk_scale(d, z, (size_t)V, T) ||
+            cgk_filter_rows(z, 1, V, top_k, top_p, NULL, NULL, o))
+            return -1;
+    } else if (cgk_temperature_probs(d, V, T, o)) {
+        return -1;
+    }
     if (!out_dev) return cgx_memcpy_d2h(dist_out, o, (size_t)V * 4);
     return cgx_synchronize();
 }
@@ -119,7 +115,81 @@ int cg_sample_corrected(float* draft_probs, float* target_probs, int vocab_size)
     return cgx_sample_corrected_u(draft_probs, target_probs, vocab_size, u);
 }
 
+/* cg_sample_top_k (speculative.c:122-146): k >= V is cg_sample_temperature
+ * at T = 1; k <= 0 is rejected (the reference indexes top_vals[-1]). */
+int cgx_sample_top_k_u(const float* logits, int V, int top_k, float u) {
+    if (!logits || V <= 0 || top_k <= 0) {
+        cgx_set_error("cgx_sample_top_k_u: invalid argument (logits, V > 0, top_k > 0)");
+        return -1;
+    }
+    if (top_k >= V) return cgx_sample_temperature_u(logits, V, 1.0f, u);
+    if (cgx_ensure_init()) return -1;
+    const float* d = (const float*)cgx_dev_in(logits, (size_t)V * 4, CGX_SLOT_IN0);
+    float* du = (float*)cgx_scratch(CGX_SLOT_IN1, sizeof(float));
+    int* out = (int*)cgx_scratch(CGX_SLOT_OUT1, sizeof(int));
+    if (!d || !du || !out || cgx_memcpy_h2d(du, &u, sizeof(float)) ||
+        cgk_filter_rows(d, 1, V, top_k, 1.0f, du, out, NULL))
+        return -1;
+    return read_token(out);
+}
+
+/* cg_sample_top_p (speculative.c:77-120), for any top_p. */
+int cgx_sample_top_p_u(const float* logits, int V, float top_p, float u) {
+    if (!logits || V <= 0) {
+        cgx_set_error("cgx_sample_top_p_u: invalid argument");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    const float* d = (const float*)cgx_dev_in(logits, (size_t)V * 4, CGX_SLOT_IN0);
+    float* du = (float*)cgx_scratch(CGX_SLOT_IN1, sizeof(float));
+    int* out = (int*)cgx_scratch(CGX_SLOT_OUT1, sizeof(int));
+    if (!d || !du || !out || cgx_memcpy_h2d(du, &u, sizeof(float)) ||
+        cgk_filter_rows(d, 1, V, 0, top_p, du, out, NULL))
+        return -1;
+    return read_token(out);
+}
+
+int cg_sample_top_k(float* logits, int vocab_size, int top_k) {
+    float u = cgx_lcg_draw();
+    return cgx_sample_top_k_u(logits, vocab_size, top_k, u);
+}
+
+int cg_sample_top_p(float* logits, int vocab_size, float top_p) {
+    float u = cgx_lcg_draw();
+    return cgx_sample_top_p_u(logits, vocab_size, top_p, u);
+}
+
 /* ------------------------------------------------------------- verify */
+
+/* D5 verify: filtered distributions of every row, then the same accept /
+ * correction composition over them; the bonus token is the filtered
+ * sampler's draw from target row gamma. */
+static int verify_filtered(const float* target, const float* draft, const int* tokens,
+                           const float* u, int batch, int gamma, int V, float T, int top_k,
+                           float top_p, float* ap, int* corr, int* bonus, int* out_tokens,
+                           int* n_accepted) {
+    size_t rt = (size_t)batch * (gamma + 1), rd = (size_t)batch * gamma;
+    float* z = (float*)cgx_scratch(CGX_SLOT_WS3, (rt + rd) * V * 4);
+    float* dist = (float*)cgx_scratch(CGX_SLOT_WS2, (rt + rd) * V * 4);
+    if (!z || !dist) return -1;
+    float* zt = z;
+    float* zd = z + rt * V;
+    float* p = dist;
+    float* q = dist + rt * V;
+    if (cgk_scale(target, zt, rt * V, T) || cgk_scale(draft, zd, rd * V, T) ||
+        cgk_filter_rows(zt, (int)rt, V, top_k, top_p, NULL, NULL, p) ||
+        cgk_filter_rows(zd, (int)rd, V, top_k, top_p, NULL, NULL, q))
+        return -1;
+    for (int c = 0; c < batch; c++) {
+        const float* zb = zt + ((size_t)c * (gamma + 1) + gamma) * V;
+        if (cgk_filter_rows(zb, 1, V, top_k, top_p, u + (size_t)c * (gamma + 1) + gamma,
+                            bonus + c, NULL))
+            return -1;
+    }
+    return cgk_verify_chain_dist(p, q, tokens, u, batch, gamma, V, bonus, ap, corr, out_tokens,
+                                 n_accepted);
+}
+
 
 int cgx_verify_chain_batch_dev(const float* target_logits, const float* draft_logits,
                                const int* draft_tokens, const float* u, int batch,
@@ -131,10 +201,6 @@ int cgx_verify_chain_batch_dev(const float* target_logits, const float* draft_lo
         cgx_set_error("cgx_verify_chain_batch_dev: invalid argument");
         return -1;
     }
-    if (uses_filters(V, top_k, top_p)) {
-        cgx_set_error("cgx_verify_chain: top-k / top-p kernels not implemented yet");
-        return -1;
-    }
     if (cgx_ensure_init()) return -1;
     size_t na = (size_t)batch * gamma;
     char* ws = (char*)cgx_scratch(CGX_SLOT_WS1, na * 4 * 2 + (size_t)batch * 4 + 256);
@@ -142,6 +208,10 @@ int cgx_verify_chain_batch_dev(const float* target_logits, const float* draft_lo
     float* ap = accept_prob ? accept_prob : (float*)ws;
     int* corr = (int*)(ws + na * 4);
     int* bonus = (int*)(ws + na * 8);
+    if (uses_filters(V, top_k, top_p))
+        return verify_filtered(target_logits, draft_logits, draft_tokens, u, batch, gamma, V,
+                               temperature, top_k, top_p, ap, corr, bonus, out_tokens,
+                               n_accepted);
     return cgk_verify_chain(target_logits, draft_logits, draft_tokens, u, batch, gamma, V,
                             temperature, ap, corr, bonus, out_tokens, n_accepted);
 }

@@ -239,3 +239,38 @@ def test_expf_formula_matches_host_libm(tmp_path):
     n, bad = map(int, subprocess.run([str(exe)], capture_output=True, text=True,
                                      check=True).stdout.split())
     assert n > 80_000_000 and bad == 0
+
+
+def _tie_rule_order(p):
+    """Order in which the reference's selection sort (speculative.c:93-100)
+    emits equal values, from counts only: members i_1 < ... < i_n of the
+    group of value v, g_t = number of elements > v between i_t and i_(t+1)
+    (g_n after i_n); for t = 1..n append i_t to R and rotate R left by g_t.
+    The GPU top-p kernel (filter.hip) uses this rule."""
+    out = []
+    for v in sorted(set(p.tolist()), reverse=True):
+        mem = [i for i in range(len(p)) if p[i] == v]
+        gt = np.concatenate([[0], np.cumsum(p > v)])
+        cnt = [int(gt[i]) for i in mem]
+        R = []
+        for t, i in enumerate(mem):
+            R.append(i)
+            g = (cnt[t + 1] if t + 1 < len(mem) else int(gt[-1])) - cnt[t]
+            g %= len(R)
+            R = R[g:] + R[:g]
+        out.extend(R)
+    return out
+
+
+@pytest.mark.parametrize("V,levels", [(12, 3), (40, 4), (200, 6), (1000, 40)])
+def test_top_p_tie_rule_matches_selection_sort(oracle, rng, V, levels):
+    for _ in range(30):
+        x = rng.integers(0, levels, V).astype(np.float32)
+        probs = np.zeros(V, np.float32)
+        idx = np.zeros(V, np.int32)
+        cum = C.c_float()
+        oracle.orc_top_p_sorted(ptr(x), V, 2.0, ptr(probs), ptr(idx), C.byref(cum))
+        # the rule applied to the (index-order) probabilities
+        pi = np.zeros(V, np.float32)
+        pi[idx] = probs
+        assert _tie_rule_order(pi) == idx.tolist()
