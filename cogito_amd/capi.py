@@ -118,6 +118,16 @@ class CgFlashAttnConfig(C.Structure):
     ]
 
 
+class CgxModelConfig(C.Structure):
+    _fields_ = [
+        ("n_layers", C.c_int), ("d_model", C.c_int), ("n_heads", C.c_int),
+        ("n_kv_heads", C.c_int), ("head_dim", C.c_int), ("d_ff", C.c_int),
+        ("vocab", C.c_int), ("group_size", C.c_int), ("kv_group_size", C.c_int),
+        ("max_seq", C.c_int), ("max_tokens", C.c_int), ("rope_theta", C.c_float),
+        ("norm_eps", C.c_float), ("init_std", C.c_float),
+    ]
+
+
 PT = C.POINTER(CgTensor)
 PQ = C.POINTER(CgTensorQuant)
 PKV = C.POINTER(CgKvCacheInt4)
@@ -240,6 +250,25 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_kv_cache_int4_write": (I, [PKV, I, I, VP, VP, I]),
     "cgx_kv_cache_int4_set_len": (I, [PKV, I]),
     "cgx_attention_int4_kv_dev": (I, [VP, I, I, PKV, I, I, VP, VP]),
+    # synthetic decoder and the speculative loop
+    "cgx_model_new": (VP, [C.POINTER(CgxModelConfig), C.c_uint64, VP]),
+    "cgx_model_free": (None, [VP]),
+    "cgx_model_forward": (I, [VP, VP, I, I, VP]),
+    "cgx_model_logits": (VP, [VP]),
+    "cgx_model_get_config": (I, [VP, C.POINTER(CgxModelConfig)]),
+    "cgx_model_len": (I, [VP]),
+    "cgx_model_truncate": (I, [VP, I]),
+    "cgx_model_kv": (PKV, [VP]),
+    "cgx_model_fill_context": (I, [VP, I, C.c_uint64]),
+    "cgx_model_export": (I, [VP, I, I, VP, VP]),
+    "cgx_fill_normal_dev": (I, [VP, SZ, C.c_uint64, C.c_uint32, F]),
+    "cgx_spec_new": (VP, [VP, VP, I, F, I, F]),
+    "cgx_spec_free": (None, [VP]),
+    "cgx_spec_prefill": (I, [VP, VP, I]),
+    "cgx_spec_set_last": (I, [VP, I]),
+    "cgx_spec_step": (I, [VP, VP, VP, VP]),
+    "cgx_spec_stats": (None, [VP, C.POINTER(C.c_longlong), C.POINTER(C.c_longlong),
+                              C.POINTER(C.c_longlong)]),
 }
 
 # The subset implemented so far; the rest are declared in the headers and

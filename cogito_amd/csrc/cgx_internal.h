@@ -52,6 +52,12 @@ int cgk_int4_dequantize_tiled(const uint8_t* tiled, const float* scales_t,
                               int K, int N, int gs, float* out);
 int cgk_int4_gemv_tiled(const float* x, int M, int K, int N, int gs,
                         const uint8_t* tiled, const float* scales_t, float* y);
+/* GEMV with the decoder's fusions: pro 0 none, 1 RMSNorm of the rows
+ * (weights norm_w[K], eps) before the product, 2 SwiGLU of the gate|up rows
+ * (x row = [g | u], ldx >= 2K); accumulate: y += result. */
+int cgk_int4_gemv_fused(const float* x, int ldx, int M, int K, int N, int gs,
+                        const uint8_t* tiled, const float* scales_t, float* y, int pro,
+                        const float* norm_w, float eps, int accumulate);
 int cgk_int4_matmul_generic(const float* x, int M, int K, int N, int gs,
                             const uint8_t* flat, const float* scales, float* y);
 

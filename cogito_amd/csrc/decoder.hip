@@ -1,0 +1,169 @@
+// decoder.hip -- the small kernels of the synthetic decoder stack that sit
+// between the INT4 GEMVs (int4.hip) and attention (attn.hip):
+//
+//   k_embed        embedding rows of the step's tokens (token ids on device)
+//   k_rope_append  RoPE of the step's Q and K (cg_apply_rope arithmetic,
+//                  src/attention/flash_attn.c:335-360) and the INT4 KV-cache
+//                  append of K and V (src/quantize/int4.c:155-231), one
+//                  workgroup per (token, head)
+//   k_fill_normal  seeded weights: a counter-based hash (lowbias32) gives
+//                  four 16-bit uniforms per value; their centred sum scaled
+//                  to unit variance (Irwin-Hall, n = 4) times std.  Integer
+//                  arithmetic up to one int->float conversion and one
+//                  multiply, so a CPU restatement produces the same bits.
+//
+// Block order of a layer (pre-norm, no bias, src/layers/transformer.c:26-149):
+//   x += o_proj(attn(rope(qkv_proj(rmsnorm(x)))))
+//   x += down(silu(gate(rmsnorm(x))) * up(rmsnorm(x)))
+// with the RMSNorms fused into the following GEMV and the residual adds into
+// the GEMV epilogue.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "cgx_internal.h"
+
+namespace {
+
+inline hipStream_t stream() { return (hipStream_t)cgx_stream(); }
+
+int launch_check(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        cgx_set_error("%s launch failed: %s", what, hipGetErrorString(e));
+        return -1;
+    }
+    return 0;
+}
+
+__global__ void k_embed(const float* __restrict__ table, const int* __restrict__ tokens,
+                        int M, int d, int V, float* __restrict__ x) {
+    int m = blockIdx.y;
+    int tok = tokens[m];
+    tok = tok < 0 ? 0 : (tok >= V ? V - 1 : tok);
+    const float* row = table + (size_t)tok * d;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < d; i += gridDim.x * blockDim.x)
+        x[(size_t)m * d + i] = row[i];
+}
+
+// One workgroup of D/2 threads per (token m, head): heads [0, H) are query
+// heads (rotated into q_out), heads [H, H + Hk) are KV heads (K rotated, then
+// K and V quantised into the cache row of position pos0 + m).
+__global__ void k_rope_append(const float* __restrict__ qkv, int ld, int H, int Hk, int D,
+                              int gs, int pos0, float theta, float* __restrict__ q_out,
+                              uint8_t* __restrict__ kc, uint8_t* __restrict__ vc,
+                              float* __restrict__ ks, float* __restrict__ vs) {
+    __shared__ float sk[256], sv[256];
+    const int m = blockIdx.x, head = blockIdx.y, i = threadIdx.x, half = D / 2;
+    const int pos = pos0 + m;
+    const float* row = qkv + (size_t)m * ld;
+    float freq = __fdiv_rn(1.0f, powf(theta, __fdiv_rn((float)(2 * i), (float)D)));
+    float angle = __fmul_rn((float)pos, freq);
+    float c = cosf(angle), s = sinf(angle);
+    if (head < H) {
+        const float* q = row + head * D;
+        float x0 = q[i], x1 = q[i + half];
+        float* o = q_out + ((size_t)m * H + head) * D;
+        o[i] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
+        o[i + half] = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
+        return;
+    }
+    const int hk = head - H;
+    const float* k = row + H * D + hk * D;
+    const float* v = row + (H + Hk) * D + hk * D;
+    float k0 = k[i], k1 = k[i + half];
+    sk[i] = __fsub_rn(__fmul_rn(k0, c), __fmul_rn(k1, s));
+    sk[i + half] = __fadd_rn(__fmul_rn(k0, s), __fmul_rn(k1, c));
+    sv[i] = v[i];
+    sv[i + half] = v[i + half];
+    __syncthreads();
+    // quantise: thread i packs dims 2i, 2i+1 (same group: gs is even)
+    const int ngh = D / gs, g = (2 * i) / gs;
+    float mk = 0.0f, mv = 0.0f;
+    for (int e = g * gs; e < (g + 1) * gs; e++) {
+        float ak = fabsf(sk[e]), av = fabsf(sv[e]);
+        if (ak > mk) mk = ak;
+        if (av > mv) mv = av;
+    }
+    float sck = __fdiv_rn(mk, 7.0f), scv = __fdiv_rn(mv, 7.0f);
+    if (sck < 1e-8f) sck = 1.0f;
+    if (scv < 1e-8f) scv = 1.0f;
+    const size_t th = (size_t)pos * Hk + hk;
+    if ((2 * i) % gs == 0) {
+        ks[th * ngh + g] = sck;
+        vs[th * ngh + g] = scv;
+    }
+    int a0 = (int)roundf(__fdiv_rn(sk[2 * i], sck)), a1 = (int)roundf(__fdiv_rn(sk[2 * i + 1], sck));
+    int b0 = (int)roundf(__fdiv_rn(sv[2 * i], scv)), b1 = (int)roundf(__fdiv_rn(sv[2 * i + 1], scv));
+    a0 = a0 > 7 ? 7 : (a0 < -8 ? -8 : a0);
+    a1 = a1 > 7 ? 7 : (a1 < -8 ? -8 : a1);
+    b0 = b0 > 7 ? 7 : (b0 < -8 ? -8 : b0);
+    b1 = b1 > 7 ? 7 : (b1 < -8 ? -8 : b1);
+    kc[th * half + i] = (uint8_t)((a0 & 0xF) | ((a1 & 0xF) << 4));
+    vc[th * half + i] = (uint8_t)((b0 & 0xF) | ((b1 & 0xF) << 4));
+}
+
+__device__ __forceinline__ uint32_t lowbias32(uint32_t x) {
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+
+__global__ void k_fill_normal(float* __restrict__ out, size_t n, uint32_t key, float scale) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) {
+        uint32_t a = lowbias32(key + 2u * (uint32_t)i);
+        uint32_t b = lowbias32(key + 2u * (uint32_t)i + 1u);
+        int s = (int)(a & 0xFFFF) + (int)(a >> 16) + (int)(b & 0xFFFF) + (int)(b >> 16);
+        out[i] = (float)(s - 131070) * scale;
+    }
+}
+
+}  // namespace
+
+extern "C" int cgk_embed(const float* table, const int* tokens, int M, int d, int V,
+                         float* x) {
+    if (M <= 0) return 0;
+    int bx = (d + 255) / 256;
+    hipLaunchKernelGGL(k_embed, dim3(bx > 16 ? 16 : bx, M), dim3(256), 0, stream(), table,
+                       tokens, M, d, V, x);
+    return launch_check("k_embed");
+}
+
+extern "C" int cgk_rope_append(const float* qkv, int ld, int M, int H, int Hk, int D, int gs,
+                               int pos0, float theta, float* q_out, uint8_t* kc, uint8_t* vc,
+                               float* ks, float* vs) {
+    if (M <= 0) return 0;
+    if (D < 2 || D > 256 || (D & 1) || gs <= 0 || (gs & 1) || D % gs) {
+        cgx_set_error("rope_append: unsupported head_dim %d / group %d", D, gs);
+        return -1;
+    }
+    hipLaunchKernelGGL(k_rope_append, dim3(M, H + Hk), dim3(D / 2), 0, stream(), qkv, ld, H,
+                       Hk, D, gs, pos0, theta, q_out, kc, vc, ks, vs);
+    return launch_check("k_rope_append");
+}
+
+// Per-matrix key: mixes the seed and the matrix id.
+extern "C" uint32_t cgx_fill_key(uint64_t seed, uint32_t stream_id) {
+    uint32_t k = (uint32_t)seed ^ (uint32_t)(seed >> 32) * 0x9E3779B9u;
+    k = k * 0x85EBCA6Bu + stream_id * 0xC2B2AE35u;
+    k ^= k >> 15;
+    k *= 0x2C1B3C6Du;
+    k ^= k >> 12;
+    return k;
+}
+
+extern "C" int cgk_fill_normal(float* out, size_t n, uint64_t seed, uint32_t stream_id,
+                               float stddev) {
+    if (!n) return 0;
+    // unit variance: 4 uniforms on [0, 65535] have variance 4 * (65536^2 - 1) / 12
+    float scale = (float)((double)stddev * sqrt(3.0) / 65536.0);
+    hipLaunchKernelGGL(k_fill_normal, dim3(4096), dim3(256), 0, stream(), out, n,
+                       cgx_fill_key(seed, stream_id), scale);
+    return launch_check("k_fill_normal");
+}

@@ -1,0 +1,351 @@
+/*
+ * model.c -- the synthetic decoder stack of the verify path (INT4 weights
+ * and KV cache in HBM).  Layer order and layouts follow the reference
+ * (src/layers/transformer.c:26-149, src/layers/linear.c:53-98); every
+ * linear layer is one INT4 GEMV launch with the RMSNorm / SwiGLU / residual
+ * work fused around it (int4.hip), attention reads the INT4 cache directly
+ * (attn.hip).  Per layer: 4 GEMVs, RoPE + KV append, attention (+ split
+ * combine).
+ */
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "cg_mi355x.h"
+#include "cgx_internal.h"
+
+int cgk_embed(const float* table, const int* tokens, int M, int d, int V, float* x);
+int cgk_rope_append(const float* qkv, int ld, int M, int H, int Hk, int D, int gs, int pos0,
+                    float theta, float* q_out, uint8_t* kc, uint8_t* vc, float* ks, float* vs);
+int cgk_fill_normal(float* out, size_t n, uint64_t seed, uint32_t stream_id, float stddev);
+
+enum { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SWIGLU = 2 };
+enum { W_QKV = 0, W_O = 1, W_GU = 2, W_DOWN = 3, W_LM = 4 };
+
+typedef struct {
+    uint8_t* tiled;
+    float* scales_t;
+    int K, N;
+    uint32_t sid;
+} lin_t;
+
+typedef struct {
+    lin_t w[4];
+} layer_t;
+
+struct cgx_model {
+    cgx_model_config c;
+    uint64_t seed;
+    float* embed;
+    lin_t lm;
+    int shared;              /* embed / lm_head borrowed from another model */
+    float* ones;             /* RMSNorm weights */
+    layer_t* layers;
+    cg_kv_cache_int4* kv;
+    int* tok;
+    float *x, *qkv, *q, *attn, *gu, *logits;
+};
+
+static int nqkv(const cgx_model_config* c) { return (c->n_heads + 2 * c->n_kv_heads) * c->head_dim; }
+
+static void lin_shape(const cgx_model_config* c, int which, int* K, int* N) {
+    int d = c->d_model, hq = c->n_heads * c->head_dim;
+    switch (which) {
+        case W_QKV: *K = d; *N = nqkv(c); break;
+        case W_O: *K = hq; *N = d; break;
+        case W_GU: *K = d; *N = 2 * c->d_ff; break;
+        case W_DOWN: *K = c->d_ff; *N = d; break;
+        default: *K = d; *N = c->vocab; break;
+    }
+}
+
+static uint32_t lin_sid(int layer, int which) {
+    return which == W_LM ? 2u : (uint32_t)(16 * layer + 3 + which);
+}
+
+/* Seeded fp32 values -> reference-layout INT4 (flat) in tmp buffers. */
+static int gen_flat(const cgx_model* m, uint32_t sid, int K, int N, float* tf, uint8_t* tq,
+                    float* ts) {
+    size_t n = (size_t)K * N;
+    if (cgk_fill_normal(tf, n, m->seed, sid, m->c.init_std)) return -1;
+    return cgk_int4_quantize(tf, (int)n, m->c.group_size, tq, ts);
+}
+
+static int make_lin(cgx_model* m, lin_t* L, int which, int layer, float* tf, uint8_t* tq,
+                    float* ts) {
+    lin_shape(&m->c, which, &L->K, &L->N);
+    L->sid = lin_sid(layer, which);
+    size_t n = (size_t)L->K * L->N;
+    L->tiled = (uint8_t*)cgx_malloc(n / 2);
+    L->scales_t = (float*)cgx_malloc(n / m->c.group_size * 4);
+    if (!L->tiled || !L->scales_t) return -1;
+    if (gen_flat(m, L->sid, L->K, L->N, tf, tq, ts)) return -1;
+    return cgk_int4_repack_tiled(tq, ts, L->K, L->N, m->c.group_size, L->tiled, L->scales_t);
+}
+
+static void free_lin(lin_t* L) {
+    cgx_free(L->tiled);
+    cgx_free(L->scales_t);
+    L->tiled = NULL;
+    L->scales_t = NULL;
+}
+
+static int check_config(const cgx_model_config* c) {
+    int gs = c->group_size;
+    if (c->n_layers < 1 || c->d_model < 1 || c->n_heads < 1 || c->n_kv_heads < 1 ||
+        c->n_heads % c->n_kv_heads || c->head_dim < 2 || c->head_dim > 128 ||
+        (c->head_dim & 1) || c->d_ff < 1 || c->vocab < 2 || gs < 16 || gs % 16 ||
+        c->kv_group_size < 2 || (c->kv_group_size & 1) || c->head_dim % c->kv_group_size ||
+        c->max_seq < 1 || c->max_tokens < 1 || c->max_tokens > c->max_seq) {
+        cgx_set_error("cgx_model_new: invalid configuration");
+        return -1;
+    }
+    for (int w = 0; w <= W_LM; w++) {
+        int K, N;
+        lin_shape(c, w, &K, &N);
+        if (K % 256 || N % 16 || N % gs) {
+            cgx_set_error("cgx_model_new: linear %d is %d x %d; the GEMV layout needs K %% 256 "
+                          "== 0 and N a multiple of 16 and of group_size %d", w, K, N, gs);
+            return -1;
+        }
+    }
+    return 0;
+}
+
+void cgx_model_free(cgx_model* m) {
+    if (!m) return;
+    if (m->layers) {
+        for (int l = 0; l < m->c.n_layers; l++)
+            for (int w = 0; w < 4; w++) free_lin(&m->layers[l].w[w]);
+        free(m->layers);
+    }
+    if (!m->shared) {
+        cgx_free(m->embed);
+        free_lin(&m->lm);
+    }
+    cgx_free(m->ones);
+    cg_kv_cache_int4_free(m->kv);
+    cgx_free(m->tok);
+    cgx_free(m->x);
+    cgx_free(m->qkv);
+    cgx_free(m->q);
+    cgx_free(m->attn);
+    cgx_free(m->gu);
+    cgx_free(m->logits);
+    free(m);
+}
+
+cgx_model* cgx_model_new(const cgx_model_config* cfg, uint64_t seed, cgx_model* share_from) {
+    if (!cfg || check_config(cfg)) return NULL;
+    if (share_from && (share_from->c.d_model != cfg->d_model ||
+                       share_from->c.vocab != cfg->vocab ||
+                       share_from->c.group_size != cfg->group_size)) {
+        cgx_set_error("cgx_model_new: share_from has another d_model / vocab / group size");
+        return NULL;
+    }
+    if (cgx_ensure_init()) return NULL;
+    cgx_model* m = (cgx_model*)calloc(1, sizeof(*m));
+    if (!m) return NULL;
+    m->c = *cfg;
+    m->seed = seed;
+    const cgx_model_config* c = &m->c;
+    int d = c->d_model, V = c->vocab, Mx = c->max_tokens;
+    size_t maxn = 0;
+    for (int w = 0; w <= W_LM; w++) {
+        int K, N;
+        lin_shape(c, w, &K, &N);
+        if ((size_t)K * N > maxn) maxn = (size_t)K * N;
+    }
+    if ((size_t)V * d > maxn) maxn = (size_t)V * d;
+    float* tf = (float*)cgx_malloc(maxn * 4);
+    uint8_t* tq = (uint8_t*)cgx_malloc(maxn / 2 + 16);
+    float* ts = (float*)cgx_malloc(maxn / c->group_size * 4 + 16);
+    m->layers = (layer_t*)calloc((size_t)c->n_layers, sizeof(layer_t));
+    int ok = tf && tq && ts && m->layers;
+    if (ok && share_from) {
+        m->shared = 1;
+        m->embed = share_from->embed;
+        m->lm = share_from->lm;
+    } else if (ok) {
+        m->embed = (float*)cgx_malloc((size_t)V * d * 4);
+        ok = m->embed && !cgk_fill_normal(m->embed, (size_t)V * d, seed, 1u, c->init_std) &&
+             !make_lin(m, &m->lm, W_LM, 0, tf, tq, ts);
+    }
+    for (int l = 0; ok && l < c->n_layers; l++)
+        for (int w = 0; ok && w < 4; w++) ok = !make_lin(m, &m->layers[l].w[w], w, l, tf, tq, ts);
+    if (ok) {
+        int maxd = d > c->d_ff ? d : c->d_ff;
+        m->ones = (float*)cgx_malloc((size_t)maxd * 4);
+        float* h = (float*)malloc((size_t)maxd * 4);
+        ok = m->ones && h;
+        if (ok) {
+            for (int i = 0; i < maxd; i++) h[i] = 1.0f;
+            ok = !cgx_memcpy_h2d(m->ones, h, (size_t)maxd * 4);
+        }
+        free(h);
+    }
+    if (ok) {
+        m->kv = cg_kv_cache_int4_new(c->n_layers, c->max_seq, c->n_kv_heads, c->head_dim,
+                                     c->kv_group_size);
+        m->tok = (int*)cgx_malloc((size_t)Mx * 4);
+        m->x = (float*)cgx_malloc((size_t)Mx * d * 4);
+        m->qkv = (float*)cgx_malloc((size_t)Mx * nqkv(c) * 4);
+        m->q = (float*)cgx_malloc((size_t)Mx * c->n_heads * c->head_dim * 4);
+        m->attn = (float*)cgx_malloc((size_t)Mx * c->n_heads * c->head_dim * 4);
+        m->gu = (float*)cgx_malloc((size_t)Mx * 2 * c->d_ff * 4);
+        m->logits = (float*)cgx_malloc((size_t)Mx * V * 4);
+        ok = m->kv && m->tok && m->x && m->qkv && m->q && m->attn && m->gu && m->logits;
+    }
+    if (ok) ok = !cgx_synchronize();
+    cgx_free(tf);
+    cgx_free(tq);
+    cgx_free(ts);
+    if (!ok) {
+        cgx_model_free(m);
+        return NULL;
+    }
+    return m;
+}
+
+float* cgx_model_logits(cgx_model* m) { return m ? m->logits : NULL; }
+
+int cgx_model_get_config(const cgx_model* m, cgx_model_config* out) {
+    if (!m || !out) {
+        cgx_set_error("cgx_model_get_config: NULL argument");
+        return -1;
+    }
+    *out = m->c;
+    return 0;
+}
+int cgx_model_len(const cgx_model* m) { return m ? m->kv->current_len : -1; }
+cg_kv_cache_int4* cgx_model_kv(cgx_model* m) { return m ? m->kv : NULL; }
+
+int cgx_model_truncate(cgx_model* m, int len) {
+    if (!m) {
+        cgx_set_error("cgx_model_truncate: NULL model");
+        return -1;
+    }
+    return cgx_kv_cache_int4_truncate(m->kv, len);
+}
+
+static size_t kv_layer_bytes(const cg_kv_cache_int4* c) {
+    return (size_t)c->max_seq_len * c->n_heads * (c->head_dim / 2);
+}
+
+static size_t kv_layer_groups(const cg_kv_cache_int4* c) {
+    return (size_t)c->max_seq_len * c->n_heads * (c->head_dim / c->group_size);
+}
+
+int cgx_model_forward(cgx_model* m, const int* tokens, int M, int n_logits, float* logits) {
+    if (!m || !tokens || M < 1 || M > m->c.max_tokens || n_logits < 0 || n_logits > M) {
+        cgx_set_error("cgx_model_forward: invalid argument (M=%d, n_logits=%d)", M, n_logits);
+        return -1;
+    }
+    const cgx_model_config* c = &m->c;
+    cg_kv_cache_int4* kv = m->kv;
+    const int pos0 = kv->current_len;
+    if (pos0 + M > c->max_seq) {
+        cgx_set_error("cgx_model_forward: KV cache full (%d + %d > %d)", pos0, M, c->max_seq);
+        return -1;
+    }
+    const int* dtok = tokens;
+    if (!cgx_is_device_ptr(tokens)) {
+        if (cgx_memcpy_h2d(m->tok, tokens, (size_t)M * 4)) return -1;
+        dtok = m->tok;
+    }
+    const int d = c->d_model, H = c->n_heads, Hk = c->n_kv_heads, hd = c->head_dim;
+    const int hq = H * hd, gs = c->group_size, ff = c->d_ff, nq = nqkv(c);
+    const float eps = c->norm_eps, scale = 1.0f / sqrtf((float)hd);
+    if (cgk_embed(m->embed, dtok, M, d, c->vocab, m->x)) return -1;
+    const size_t lb = kv_layer_bytes(kv), lg = kv_layer_groups(kv);
+    for (int l = 0; l < c->n_layers; l++) {
+        const lin_t* w = m->layers[l].w;
+        uint8_t* kc = kv->k_cache + lb * l;
+        uint8_t* vc = kv->v_cache + lb * l;
+        float* ks = kv->k_scales + lg * l;
+        float* vs = kv->v_scales + lg * l;
+        if (cgk_int4_gemv_fused(m->x, d, M, d, nq, gs, w[W_QKV].tiled, w[W_QKV].scales_t,
+                                m->qkv, PRO_RMSNORM, m->ones, eps, 0) ||
+            cgk_rope_append(m->qkv, nq, M, H, Hk, hd, kv->group_size, pos0, c->rope_theta,
+                            m->q, kc, vc, ks, vs) ||
+            cgk_attention(m->q, 1, kc, vc, ks, vs, kv->group_size, NULL, NULL, 1, M, pos0 + M,
+                          H, Hk, hd, scale, CGK_MASK_CAUSAL_ALIGNED, 0, NULL, NULL, m->attn,
+                          NULL) ||
+            cgk_int4_gemv_fused(m->attn, hq, M, hq, d, gs, w[W_O].tiled, w[W_O].scales_t, m->x,
+                                PRO_NONE, NULL, 0.0f, 1) ||
+            cgk_int4_gemv_fused(m->x, d, M, d, 2 * ff, gs, w[W_GU].tiled, w[W_GU].scales_t,
+                                m->gu, PRO_RMSNORM, m->ones, eps, 0) ||
+            cgk_int4_gemv_fused(m->gu, 2 * ff, M, ff, d, gs, w[W_DOWN].tiled,
+                                w[W_DOWN].scales_t, m->x, PRO_SWIGLU, NULL, 0.0f, 1))
+            return -1;
+    }
+    if (n_logits > 0 &&
+        cgk_int4_gemv_fused(m->x + (size_t)(M - n_logits) * d, d, n_logits, d, c->vocab, gs,
+                            m->lm.tiled, m->lm.scales_t, logits ? logits : m->logits,
+                            PRO_RMSNORM, m->ones, eps, 0))
+        return -1;
+    kv->current_len = pos0 + M;
+    return 0;
+}
+
+int cgx_model_fill_context(cgx_model* m, int len, uint64_t seed) {
+    if (!m || len < 0 || len > m->c.max_seq) {
+        cgx_set_error("cgx_model_fill_context: invalid length");
+        return -1;
+    }
+    cg_kv_cache_int4* kv = m->kv;
+    if (!len) return cgx_kv_cache_int4_set_len(kv, 0);
+    size_t n = (size_t)len * kv->n_heads * kv->head_dim;
+    float* k = (float*)cgx_malloc(n * 4);
+    float* v = (float*)cgx_malloc(n * 4);
+    int rc = (k && v) ? 0 : -1;
+    for (int l = 0; !rc && l < kv->num_layers; l++) {
+        rc = cgk_fill_normal(k, n, seed, 0x40000000u + 2u * (uint32_t)l, 1.0f) ||
+             cgk_fill_normal(v, n, seed, 0x40000001u + 2u * (uint32_t)l, 1.0f) ||
+             cgx_kv_cache_int4_write(kv, l, 0, k, v, len);
+    }
+    if (!rc) rc = cgx_synchronize();
+    cgx_free(k);
+    cgx_free(v);
+    if (!rc) rc = cgx_kv_cache_int4_set_len(kv, len);
+    return rc ? -1 : 0;
+}
+
+int cgx_model_export(cgx_model* m, int layer, int which, uint8_t* data, float* scales) {
+    if (!m || !data || !scales || which < 0 || which > W_LM ||
+        (which != W_LM && (layer < 0 || layer >= m->c.n_layers))) {
+        cgx_set_error("cgx_model_export: invalid argument");
+        return -1;
+    }
+    int K, N;
+    lin_shape(&m->c, which, &K, &N);
+    size_t n = (size_t)K * N;
+    float* tf = (float*)cgx_malloc(n * 4);
+    uint8_t* tq = (uint8_t*)cgx_malloc(n / 2 + 16);
+    float* ts = (float*)cgx_malloc(n / m->c.group_size * 4 + 16);
+    int rc = (tf && tq && ts) ? 0 : -1;
+    uint32_t sid = which == W_LM ? m->lm.sid : m->layers[layer].w[which].sid;
+    /* a shared lm_head was generated with the owner's seed */
+    if (which == W_LM && m->shared) {
+        cgx_set_error("cgx_model_export: lm_head of a sharing model: export it from the owner");
+        rc = -1;
+    }
+    if (!rc) rc = gen_flat(m, sid, K, N, tf, tq, ts);
+    if (!rc) rc = cgx_memcpy_d2h(data, tq, n / 2);
+    if (!rc) rc = cgx_memcpy_d2h(scales, ts, n / m->c.group_size * 4);
+    cgx_free(tf);
+    cgx_free(tq);
+    cgx_free(ts);
+    return rc ? -1 : 0;
+}
+
+int cgx_fill_normal_dev(float* out, size_t n, uint64_t seed, uint32_t stream_id,
+                        float stddev) {
+    if (!out) {
+        cgx_set_error("cgx_fill_normal_dev: NULL output");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    if (cgk_fill_normal(out, n, seed, stream_id, stddev)) return -1;
+    return cgx_synchronize();
+}

@@ -1,0 +1,228 @@
+/*
+ * spec.c -- chain speculative decoding over two device-resident models:
+ * gamma draft forwards (one token each; every drafted token is sampled on
+ * the GPU straight into the target's input row), one target forward over
+ * [last, d_1 .. d_gamma], the verify kernels (sampling.c: D4-D6), then KV
+ * rollback of both models to the accepted prefix.  One host round trip per
+ * step (the emitted tokens and the accepted count).
+ *
+ * The reference declares the driver (cg_speculative_step / _generate,
+ * include/cg_speculative.h:71-94) without defining it.
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include "cg_mi355x.h"
+#include "cg_speculative.h"
+#include "cgx_internal.h"
+
+struct cgx_spec {
+    cgx_model* draft;
+    cgx_model* target;
+    int gamma, V;
+    float T;
+    int top_k;
+    float top_p;
+    int filtered;
+    int* d_tokens;        /* [gamma + 1]: last, d_1 .. d_gamma */
+    int* d_pending;       /* [2]: draft inputs not yet in the draft cache */
+    float* d_draft_logits;
+    float* d_target_logits;
+    float* d_u;           /* [2 gamma + 1]: draft draws, then verify draws */
+    float* d_z;           /* [V] scaled draft row for the filtered samplers */
+    int* d_out;           /* [gamma + 1] emitted tokens, then n accepted */
+    float* d_ap;
+    int last;
+    int have_last;
+    int pend_extra;       /* the draft cache lacks d_gamma of the last step */
+    int pend_tok;
+    long long steps, drafted, accepted;
+};
+
+void cgx_spec_free(cgx_spec* s) {
+    if (!s) return;
+    cgx_free(s->d_tokens);
+    cgx_free(s->d_pending);
+    cgx_free(s->d_draft_logits);
+    cgx_free(s->d_target_logits);
+    cgx_free(s->d_u);
+    cgx_free(s->d_z);
+    cgx_free(s->d_out);
+    cgx_free(s->d_ap);
+    free(s);
+}
+
+cgx_spec* cgx_spec_new(cgx_model* draft, cgx_model* target, int gamma, float temperature,
+                       int top_k, float top_p) {
+    cgx_model_config cd, ct;
+    if (!draft || !target || draft == target || gamma < 1 ||
+        cgx_model_get_config(draft, &cd) || cgx_model_get_config(target, &ct)) {
+        cgx_set_error("cgx_spec_new: two distinct models and gamma >= 1 are required");
+        return NULL;
+    }
+    if (cd.vocab != ct.vocab || ct.max_tokens < gamma + 1 || cd.max_tokens < 2) {
+        cgx_set_error("cgx_spec_new: vocabularies differ or max_tokens too small "
+                      "(target needs gamma + 1, draft 2)");
+        return NULL;
+    }
+    cgx_spec* s = (cgx_spec*)calloc(1, sizeof(*s));
+    if (!s) return NULL;
+    s->draft = draft;
+    s->target = target;
+    s->gamma = gamma;
+    s->V = ct.vocab;
+    s->T = temperature;
+    s->top_k = top_k;
+    s->top_p = top_p;
+    s->filtered = (top_k > 0 && top_k < s->V) || top_p < 1.0f;
+    size_t V = (size_t)s->V;
+    s->d_tokens = (int*)cgx_malloc((size_t)(gamma + 1) * 4);
+    s->d_pending = (int*)cgx_malloc(2 * 4);
+    s->d_draft_logits = (float*)cgx_malloc((size_t)gamma * V * 4);
+    s->d_target_logits = (float*)cgx_malloc((size_t)(gamma + 1) * V * 4);
+    s->d_u = (float*)cgx_malloc((size_t)(2 * gamma + 1) * 4);
+    s->d_z = (float*)cgx_malloc(V * 4);
+    s->d_out = (int*)cgx_malloc((size_t)(gamma + 2) * 4);
+    s->d_ap = (float*)cgx_malloc((size_t)gamma * 4);
+    if (!s->d_tokens || !s->d_pending || !s->d_draft_logits || !s->d_target_logits ||
+        !s->d_u || !s->d_z || !s->d_out || !s->d_ap) {
+        cgx_spec_free(s);
+        return NULL;
+    }
+    return s;
+}
+
+void cgx_spec_stats(const cgx_spec* s, long long* steps, long long* drafted,
+                    long long* accepted) {
+    if (steps) *steps = s ? s->steps : 0;
+    if (drafted) *drafted = s ? s->drafted : 0;
+    if (accepted) *accepted = s ? s->accepted : 0;
+}
+
+int cgx_spec_set_last(cgx_spec* s, int last_token) {
+    if (!s || last_token < 0 || last_token >= s->V) {
+        cgx_set_error("cgx_spec_set_last: invalid argument");
+        return -1;
+    }
+    if (cgx_model_len(s->draft) != cgx_model_len(s->target)) {
+        cgx_set_error("cgx_spec_set_last: draft and target caches hold %d and %d positions",
+                      cgx_model_len(s->draft), cgx_model_len(s->target));
+        return -1;
+    }
+    s->last = last_token;
+    s->have_last = 1;
+    s->pend_extra = 0;
+    return 0;
+}
+
+int cgx_spec_prefill(cgx_spec* s, const int* prompt, int n) {
+    if (!s || !prompt || n < 1) {
+        cgx_set_error("cgx_spec_prefill: invalid argument");
+        return -1;
+    }
+    for (int i = 0; i < n; i++) {
+        if (prompt[i] < 0 || prompt[i] >= s->V) {
+            cgx_set_error("cgx_spec_prefill: token %d out of range", prompt[i]);
+            return -1;
+        }
+    }
+    cgx_model* ms[2] = {s->draft, s->target};
+    for (int k = 0; k < 2; k++) {
+        cgx_model_config c;
+        cgx_model_get_config(ms[k], &c);
+        for (int i = 0; i < n - 1; i += c.max_tokens) {
+            int M = n - 1 - i < c.max_tokens ? n - 1 - i : c.max_tokens;
+            if (cgx_model_forward(ms[k], prompt + i, M, 0, NULL)) return -1;
+        }
+    }
+    if (cgx_synchronize()) return -1;
+    return cgx_spec_set_last(s, prompt[n - 1]);
+}
+
+/* Draft token i + 1 from the draft logits row i, written to d_tokens[i + 1]. */
+static int draft_sample(cgx_spec* s, int i, float u_host) {
+    const float* row = s->d_draft_logits + (size_t)i * s->V;
+    int* out = s->d_tokens + i + 1;
+    if (!s->filtered) return cgk_sample_temperature(row, s->V, s->T, u_host, out);
+    if (cgk_scale(row, s->d_z, (size_t)s->V, s->T)) return -1;
+    return cgk_filter_rows(s->d_z, 1, s->V, s->top_k, s->top_p, s->d_u + i, out, NULL);
+}
+
+int cgx_spec_step(cgx_spec* s, const float* u_draft, const float* u_verify, int* out_tokens) {
+    if (!s || !u_draft || !u_verify || !out_tokens) {
+        cgx_set_error("cgx_spec_step: invalid argument");
+        return -1;
+    }
+    if (!s->have_last) {
+        cgx_set_error("cgx_spec_step: no context (call cgx_spec_prefill or cgx_spec_set_last)");
+        return -1;
+    }
+    const int g = s->gamma;
+    const int L = cgx_model_len(s->target);
+    cgx_model_config ct, cd;
+    cgx_model_get_config(s->target, &ct);
+    cgx_model_get_config(s->draft, &cd);
+    if (L + g + 1 > ct.max_seq || L + g + 1 > cd.max_seq) {
+        cgx_set_error("cgx_spec_step: KV cache full (%d + %d)", L, g + 1);
+        return -1;
+    }
+    /* inputs of the step: draws, the last token, the draft's pending tokens */
+    float hu[2 * 64 + 1];
+    float* hbuf = (2 * g + 1) <= (int)(sizeof(hu) / sizeof(hu[0]))
+                      ? hu
+                      : (float*)malloc((size_t)(2 * g + 1) * sizeof(float));
+    if (!hbuf) return -1;
+    memcpy(hbuf, u_draft, (size_t)g * sizeof(float));
+    memcpy(hbuf + g, u_verify, (size_t)(g + 1) * sizeof(float));
+    int pend[2] = {s->pend_tok, s->last};
+    int np = s->pend_extra ? 2 : 1;
+    int rc = cgx_memcpy_h2d(s->d_u, hbuf, (size_t)(2 * g + 1) * sizeof(float)) ||
+             cgx_memcpy_h2d(s->d_tokens, &s->last, sizeof(int)) ||
+             cgx_memcpy_h2d(s->d_pending, pend + (2 - np), (size_t)np * sizeof(int));
+    if (hbuf != hu) free(hbuf);
+    if (rc) return -1;
+
+    /* draft: gamma tokens */
+    if (cgx_model_forward(s->draft, s->d_pending, np, 1, s->d_draft_logits) ||
+        draft_sample(s, 0, u_draft[0]))
+        return -1;
+    for (int i = 1; i < g; i++) {
+        if (cgx_model_forward(s->draft, s->d_tokens + i, 1, 1,
+                              s->d_draft_logits + (size_t)i * s->V) ||
+            draft_sample(s, i, u_draft[i]))
+            return -1;
+    }
+    /* target: gamma + 1 rows in one forward, then the verify kernels */
+    if (cgx_model_forward(s->target, s->d_tokens, g + 1, g + 1, s->d_target_logits) ||
+        cgx_verify_chain_batch_dev(s->d_target_logits, s->d_draft_logits, s->d_tokens + 1,
+                                   s->d_u + g, 1, g, s->V, s->T, s->top_k, s->top_p, s->d_out,
+                                   s->d_out + g + 1, s->d_ap))
+        return -1;
+    int hout[64 + 2];
+    int* ho = (g + 2) <= 66 ? hout : (int*)malloc((size_t)(g + 2) * sizeof(int));
+    if (!ho) return -1;
+    if (cgx_memcpy_d2h(ho, s->d_out, (size_t)(g + 2) * sizeof(int))) {
+        if (ho != hout) free(ho);
+        return -1;
+    }
+    const int n = ho[g + 1];
+    memcpy(out_tokens, ho, (size_t)(n + 1) * sizeof(int));
+    for (int i = n + 1; i <= g; i++) out_tokens[i] = -1;
+    /* rollback: the target keeps last, d_1 .. d_n; the draft the same
+     * positions it has (it never saw d_gamma) */
+    const int keep = L + n + 1;
+    const int dlen = cgx_model_len(s->draft);
+    if (cgx_model_truncate(s->target, keep) ||
+        cgx_model_truncate(s->draft, dlen < keep ? dlen : keep)) {
+        if (ho != hout) free(ho);
+        return -1;
+    }
+    s->pend_extra = n == g;
+    s->pend_tok = n == g ? ho[g - 1] : 0;
+    s->last = ho[n];
+    if (ho != hout) free(ho);
+    s->steps++;
+    s->drafted += g;
+    s->accepted += n;
+    return n;
+}

@@ -172,11 +172,28 @@ __global__ void k_dequant_tiled(const uint32_t* __restrict__ tiled,
 // order (one launch, no inter-block traffic, deterministic).
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-template <int M, int TPW, int W>
+// Fusions around the GEMV (the decoder's linear layers):
+//   PRO = kProNone:    activations x[m][k] as given (row stride ldx);
+//   PRO = kProRmsNorm: RMSNorm of the rows first: x * nw[k], and the output
+//                      is scaled by 1/sqrt(mean(x^2) + eps) of its row (the
+//                      block computes the row sums of squares itself);
+//   PRO = kProSwiGlu:  activations silu(g) * u with g = x[m][k] and
+//                      u = x[m][K + k] (the fused gate|up output).
+//   accumulate:        y += result (residual connection) instead of y =.
+enum { kProNone = 0, kProRmsNorm = 1, kProSwiGlu = 2 };
+
+struct GemvEpi {
+    int ldx;                     // row stride of x in floats
+    const float* nw;             // RMSNorm weights [K]
+    float eps;
+    int accumulate;
+};
+
+template <int M, int TPW, int W, int PRO>
 __global__ __launch_bounds__(64 * W) void k_gemv_strip(
     const float* __restrict__ x, int K, int N, int gs,
     const u32x4* __restrict__ tiled, const float* __restrict__ scales_t,
-    float* __restrict__ y) {
+    float* __restrict__ y, GemvEpi ep) {
     // Workgroups are dispatched round-robin over the 8 XCDs (block b runs on
     // XCD b % 8).  Give each XCD a contiguous run of strips so the strips
     // that share a scale group (and its scale row) hit the same L2.
@@ -201,9 +218,11 @@ __global__ __launch_bounds__(64 * W) void k_gemv_strip(
 
     float acc[M][8];
     float xsum[M];
+    float ssq[M];
 #pragma unroll
     for (int m = 0; m < M; m++) {
         xsum[m] = 0.0f;
+        ssq[m] = 0.0f;
 #pragma unroll
         for (int c = 0; c < 8; c++) acc[m][c] = 0.0f;
     }
@@ -219,12 +238,36 @@ __global__ __launch_bounds__(64 * W) void k_gemv_strip(
         float z = valid ? 0x1p24f : 0.0f;
         sc[b][0] = sa.x * z; sc[b][1] = sa.y * z; sc[b][2] = sa.z * z; sc[b][3] = sa.w * z;
         sc[b][4] = sb.x * z; sc[b][5] = sb.y * z; sc[b][6] = sb.z * z; sc[b][7] = sb.w * z;
+        float nw[8];
+        if (PRO == kProRmsNorm) {
+            float4 na = *(const float4*)(ep.nw + k0);
+            float4 nb = *(const float4*)(ep.nw + k0 + 4);
+            nw[0] = na.x; nw[1] = na.y; nw[2] = na.z; nw[3] = na.w;
+            nw[4] = nb.x; nw[5] = nb.y; nw[6] = nb.z; nw[7] = nb.w;
+        }
 #pragma unroll
         for (int m = 0; m < M; m++) {
-            float4 xa = *(const float4*)(x + (size_t)m * K + k0);
-            float4 xb = *(const float4*)(x + (size_t)m * K + k0 + 4);
-            xv[b][m][0] = xa.x; xv[b][m][1] = xa.y; xv[b][m][2] = xa.z; xv[b][m][3] = xa.w;
-            xv[b][m][4] = xb.x; xv[b][m][5] = xb.y; xv[b][m][6] = xb.z; xv[b][m][7] = xb.w;
+            const float* xr = x + (size_t)m * ep.ldx + k0;
+            float4 xa = *(const float4*)(xr);
+            float4 xb = *(const float4*)(xr + 4);
+            float v[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+            if (PRO == kProSwiGlu) {
+                float4 ua = *(const float4*)(xr + K);
+                float4 ub = *(const float4*)(xr + K + 4);
+                float u[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] = v[i] / (1.0f + __expf(-v[i])) * u[i];
+            }
+            if (PRO == kProRmsNorm) {
+                if (valid && lane < 32) {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) ssq[m] = fmaf(v[i], v[i], ssq[m]);
+                }
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] *= nw[i];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) xv[b][m][i] = v[i];
         }
     };
     load_tile(0, 0);
@@ -258,11 +301,21 @@ __global__ __launch_bounds__(64 * W) void k_gemv_strip(
     // lane partials -> LDS, row of 8*M (+4 pad) floats per lane
     constexpr int kStride = 8 * M + 4;
     __shared__ float red[64 * W * kStride];
+    __shared__ float s_ssq[PRO == kProRmsNorm ? W * M : 1];
 #pragma unroll
     for (int m = 0; m < M; m++) {
         float corr = -8.0f * 0x1p-24f * xsum[m];
 #pragma unroll
         for (int c = 0; c < 8; c++) red[threadIdx.x * kStride + m * 8 + c] = acc[m][c] + corr;
+    }
+    if (PRO == kProRmsNorm) {
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            float v = ssq[m];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+            if (lane == 0) s_ssq[wave * M + m] = v;
+        }
     }
     __syncthreads();
     // 4 threads per output (m, col): part p sums row blocks p, p+4, ... of
@@ -282,7 +335,13 @@ __global__ __launch_bounds__(64 * W) void k_gemv_strip(
     v = add_dpp<0x4E>(v);            // quad_perm [2,3,0,1]
     if (o < kStripCols * M && part == 0) {
         int m = o / kStripCols, col = o % kStripCols;
-        y[(size_t)m * N + strip * kStripCols + col] = v;
+        if (PRO == kProRmsNorm) {
+            float ss = 0.0f;
+            for (int w = 0; w < W; w++) ss += s_ssq[w * M + m];
+            v *= 1.0f / sqrtf(ss / (float)K + ep.eps);
+        }
+        float* yp = y + (size_t)m * N + strip * kStripCols + col;
+        *yp = ep.accumulate ? *yp + v : v;
     }
 }
 
@@ -307,17 +366,17 @@ __global__ void k_matmul_generic(const float* __restrict__ x, int M, int K,
     y[o] = sum;
 }
 
-template <int M>
+template <int M, int PRO>
 int launch_gemv_m(const float* x, int K, int N, int gs, const uint8_t* tiled,
-                  const float* scales_t, float* y) {
+                  const float* scales_t, float* y, const GemvEpi& ep) {
     const int strips = N / kStripCols, ktiles = K / kTileRows;
     constexpr int W = 8;
     int tpw = (ktiles + W - 1) / W;
     dim3 grid(strips), block(64 * W);
     const u32x4* t = (const u32x4*)tiled;
-#define CGX_GEMV_CASE(TPW)                                                          \
-    hipLaunchKernelGGL((k_gemv_strip<M, TPW, W>), grid, block, 0, stream(), x, K, N, \
-                       gs, t, scales_t, y)
+#define CGX_GEMV_CASE(TPW)                                                               \
+    hipLaunchKernelGGL((k_gemv_strip<M, TPW, W, PRO>), grid, block, 0, stream(), x, K, N, \
+                       gs, t, scales_t, y, ep)
     if (tpw <= 1) CGX_GEMV_CASE(1);
     else if (tpw <= 2) CGX_GEMV_CASE(2);
     else if (tpw <= 3) CGX_GEMV_CASE(3);
@@ -330,6 +389,21 @@ int launch_gemv_m(const float* x, int K, int N, int gs, const uint8_t* tiled,
     }
 #undef CGX_GEMV_CASE
     return launch_check("k_gemv_strip");
+}
+
+template <int PRO>
+int launch_gemv_pro(int mc, const float* x, int K, int N, int gs, const uint8_t* tiled,
+                    const float* scales_t, float* y, const GemvEpi& ep) {
+    switch (mc) {
+        case 1: return launch_gemv_m<1, PRO>(x, K, N, gs, tiled, scales_t, y, ep);
+        case 2: return launch_gemv_m<2, PRO>(x, K, N, gs, tiled, scales_t, y, ep);
+        case 3: return launch_gemv_m<3, PRO>(x, K, N, gs, tiled, scales_t, y, ep);
+        case 4: return launch_gemv_m<4, PRO>(x, K, N, gs, tiled, scales_t, y, ep);
+        case 5: return launch_gemv_m<5, PRO>(x, K, N, gs, tiled, scales_t, y, ep);
+        case 6: return launch_gemv_m<6, PRO>(x, K, N, gs, tiled, scales_t, y, ep);
+        case 7: return launch_gemv_m<7, PRO>(x, K, N, gs, tiled, scales_t, y, ep);
+        default: return launch_gemv_m<8, PRO>(x, K, N, gs, tiled, scales_t, y, ep);
+    }
 }
 
 }  // namespace
@@ -379,33 +453,39 @@ extern "C" int cgk_int4_dequantize_tiled(const uint8_t* tiled,
     return launch_check("k_dequant_tiled");
 }
 
-extern "C" int cgk_int4_gemv_tiled(const float* x, int M, int K, int N, int gs,
-                                   const uint8_t* tiled, const float* scales_t,
-                                   float* y) {
-    if (M < 1 || K % kTileRows || N % kStripCols || gs % kStripCols || N % gs) {
-        cgx_set_error("gemv_tiled: unsupported shape M=%d K=%d N=%d gs=%d", M, K,
-                      N, gs);
+extern "C" int cgk_int4_gemv_fused(const float* x, int ldx, int M, int K, int N, int gs,
+                                   const uint8_t* tiled, const float* scales_t, float* y,
+                                   int pro, const float* norm_w, float eps, int accumulate) {
+    if (M < 1 || K % kTileRows || N % kStripCols || gs % kStripCols || N % gs ||
+        ldx < (pro == kProSwiGlu ? 2 * K : K) || (pro == kProRmsNorm && !norm_w) ||
+        pro < kProNone || pro > kProSwiGlu) {
+        cgx_set_error("gemv_tiled: unsupported shape M=%d K=%d N=%d gs=%d ldx=%d", M, K, N, gs,
+                      ldx);
         return -1;
     }
+    GemvEpi ep{ldx, norm_w, eps, accumulate};
     // M > 8: process rows in chunks of 8 (each chunk streams W once).
     for (int m0 = 0; m0 < M; m0 += 8) {
         int mc = M - m0 < 8 ? M - m0 : 8;
-        const float* xc = x + (size_t)m0 * K;
+        const float* xc = x + (size_t)m0 * ldx;
         float* yc = y + (size_t)m0 * N;
         int rc;
-        switch (mc) {
-            case 1: rc = launch_gemv_m<1>(xc, K, N, gs, tiled, scales_t, yc); break;
-            case 2: rc = launch_gemv_m<2>(xc, K, N, gs, tiled, scales_t, yc); break;
-            case 3: rc = launch_gemv_m<3>(xc, K, N, gs, tiled, scales_t, yc); break;
-            case 4: rc = launch_gemv_m<4>(xc, K, N, gs, tiled, scales_t, yc); break;
-            case 5: rc = launch_gemv_m<5>(xc, K, N, gs, tiled, scales_t, yc); break;
-            case 6: rc = launch_gemv_m<6>(xc, K, N, gs, tiled, scales_t, yc); break;
-            case 7: rc = launch_gemv_m<7>(xc, K, N, gs, tiled, scales_t, yc); break;
-            default: rc = launch_gemv_m<8>(xc, K, N, gs, tiled, scales_t, yc); break;
-        }
+        if (pro == kProRmsNorm)
+            rc = launch_gemv_pro<kProRmsNorm>(mc, xc, K, N, gs, tiled, scales_t, yc, ep);
+        else if (pro == kProSwiGlu)
+            rc = launch_gemv_pro<kProSwiGlu>(mc, xc, K, N, gs, tiled, scales_t, yc, ep);
+        else
+            rc = launch_gemv_pro<kProNone>(mc, xc, K, N, gs, tiled, scales_t, yc, ep);
         if (rc) return rc;
     }
     return 0;
+}
+
+extern "C" int cgk_int4_gemv_tiled(const float* x, int M, int K, int N, int gs,
+                                   const uint8_t* tiled, const float* scales_t,
+                                   float* y) {
+    return cgk_int4_gemv_fused(x, K, M, K, N, gs, tiled, scales_t, y, kProNone, nullptr, 0.0f,
+                               0);
 }
 
 extern "C" int cgk_int4_matmul_generic(const float* x, int M, int K, int N,

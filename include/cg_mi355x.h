@@ -133,6 +133,97 @@ int cgx_attention_int4_kv_dev(const float* Q, int Nq, int H,
                               cg_kv_cache_int4* cache, int layer_idx,
                               int mask_kind, const int* parents, float* O);
 
+/* ------------------------------------------------- synthetic decoder */
+/* Decoder-only transformer with INT4 weights resident in HBM, the model the
+ * verify stack runs (reference src/layers/transformer.c:26-149 block order,
+ * src/layers/linear.c:53-98 layout y = x @ W with W [in, out]):
+ *   x = embed[token]
+ *   per layer: x += attn(rope(rmsnorm(x) @ Wqkv)) @ Wo
+ *              x += (silu(h @ Wg) * (h @ Wu)) @ Wd,  h = rmsnorm(x)
+ *   logits = rmsnorm(x) @ Wlm
+ * RMSNorm weights are 1, eps = norm_eps; RoPE rotate-half with rope_theta;
+ * INT4 KV cache with kv_group_size; attention scale 1/sqrt(head_dim).
+ *
+ * Seeded weights: every matrix is filled by cgx_fill_normal semantics
+ * (Irwin-Hall of four 16-bit uniforms from a lowbias32 counter hash, unit
+ * variance, times init_std), row-major, then quantized with
+ * cg_quantize_int4's rule (groups of group_size along the flat index).
+ * Stream ids: embedding [V][d] 1; lm_head [d][V] 2; layer l:
+ * Wqkv [d][(H + 2 Hk) hd] 16 l + 3 (columns q | k | v), Wo [H hd][d]
+ * 16 l + 4, Wgate|up [d][2 ff] 16 l + 5 (columns gate | up), Wd [ff][d]
+ * 16 l + 6.  A model built with `share_from` uses that model's embedding
+ * and lm_head (a draft head over the target's vocabulary projection). */
+typedef struct {
+    int n_layers;
+    int d_model;
+    int n_heads;
+    int n_kv_heads;
+    int head_dim;
+    int d_ff;
+    int vocab;
+    int group_size;       /* INT4 weight group along the flat index */
+    int kv_group_size;    /* INT4 KV-cache group along head_dim */
+    int max_seq;          /* KV-cache capacity (positions) */
+    int max_tokens;       /* largest number of tokens per forward */
+    float rope_theta;
+    float norm_eps;
+    float init_std;
+} cgx_model_config;
+
+typedef struct cgx_model cgx_model;
+
+cgx_model* cgx_model_new(const cgx_model_config* cfg, uint64_t seed,
+                         cgx_model* share_from);
+void cgx_model_free(cgx_model* m);
+/* Forward of M tokens (host or device ids) at positions len..len+M-1: KV
+ * rows appended, len advanced by M.  Logits of the last `n_logits` tokens
+ * go to logits [n_logits][V] (device pointer, or NULL for the model's own
+ * buffer, see cgx_model_logits).  Asynchronous on the library stream when
+ * `tokens` is a device pointer. */
+int cgx_model_forward(cgx_model* m, const int* tokens, int M, int n_logits,
+                      float* logits);
+float* cgx_model_logits(cgx_model* m);
+int cgx_model_get_config(const cgx_model* m, cgx_model_config* out);
+int cgx_model_len(const cgx_model* m);
+int cgx_model_truncate(cgx_model* m, int len);
+cg_kv_cache_int4* cgx_model_kv(cgx_model* m);
+/* Synthetic context: K/V rows of positions [0, len) of every layer filled
+ * with seeded values (std 1) and len set, as if a prompt had been run. */
+int cgx_model_fill_context(cgx_model* m, int len, uint64_t seed);
+/* Weight export for checkers: the reference layout (flat nibbles, scales)
+ * of one matrix: which = 0 Wqkv, 1 Wo, 2 Wgate|up, 3 Wd (of `layer`),
+ * 4 lm_head.  data: K*N/2 bytes, scales: K*N/group_size floats (host). */
+int cgx_model_export(cgx_model* m, int layer, int which, uint8_t* data,
+                     float* scales);
+/* The fill rule of the seeded weights, into device memory. */
+int cgx_fill_normal_dev(float* out, size_t n, uint64_t seed, uint32_t stream_id,
+                        float stddev);
+
+/* ------------------------------------------ chain speculative decoding */
+/* Draft / target pair stepping gamma-token chains entirely on the GPU: the
+ * draft proposes gamma tokens (one forward and one filtered draw each), the
+ * target scores [last, d_1..d_gamma] in one forward, the verify kernels
+ * accept a prefix, and both KV caches roll back to the accepted tokens. */
+typedef struct cgx_spec cgx_spec;
+
+cgx_spec* cgx_spec_new(cgx_model* draft, cgx_model* target, int gamma,
+                       float temperature, int top_k, float top_p);
+void cgx_spec_free(cgx_spec* s);
+/* Runs both models over the prompt (host ids) and makes its last token the
+ * next input.  The target and draft must be empty or at the same length. */
+int cgx_spec_prefill(cgx_spec* s, const int* prompt, int n);
+/* Continues from a filled context (cgx_model_fill_context at the same
+ * length on both models) with `last_token` as the next input. */
+int cgx_spec_set_last(cgx_spec* s, int last_token);
+/* One step.  u_draft[gamma]: draws of the draft samplers; u_verify[gamma+1]
+ * (D6 order) for the verify.  Host arrays.  Writes the n+1 emitted tokens
+ * to out_tokens (host, gamma+1 entries) and returns n (0..gamma). */
+int cgx_spec_step(cgx_spec* s, const float* u_draft, const float* u_verify,
+                  int* out_tokens);
+/* totals since cgx_spec_new: steps, drafted tokens, accepted tokens */
+void cgx_spec_stats(const cgx_spec* s, long long* steps, long long* drafted,
+                    long long* accepted);
+
 #ifdef __cplusplus
 }
 #endif

@@ -551,6 +551,35 @@ void orc_apply_rope(float* x, int S, int H, int D, int pos0, float theta) {
     }
 }
 
+static uint32_t lowbias32(uint32_t x) {
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+
+uint32_t orc_fill_key(uint64_t seed, uint32_t stream_id) {
+    uint32_t k = (uint32_t)seed ^ (uint32_t)(seed >> 32) * 0x9E3779B9u;
+    k = k * 0x85EBCA6Bu + stream_id * 0xC2B2AE35u;
+    k ^= k >> 15;
+    k *= 0x2C1B3C6Du;
+    k ^= k >> 12;
+    return k;
+}
+
+void orc_fill_normal(float* out, size_t n, uint64_t seed, uint32_t stream_id, float stddev) {
+    uint32_t key = orc_fill_key(seed, stream_id);
+    float scale = (float)((double)stddev * sqrt(3.0) / 65536.0);
+    for (size_t i = 0; i < n; i++) {
+        uint32_t a = lowbias32(key + 2u * (uint32_t)i);
+        uint32_t b = lowbias32(key + 2u * (uint32_t)i + 1u);
+        int s = (int)(a & 0xFFFF) + (int)(a >> 16) + (int)(b & 0xFFFF) + (int)(b >> 16);
+        out[i] = (float)(s - 131070) * scale;
+    }
+}
+
 void orc_alibi_slopes(float* slopes, int H) {
     /* flash_attn.c:368-374: base = 2^(-8/H), slope_h = base^(h+1) */
     float base = powf(2.0f, -8.0f / H);

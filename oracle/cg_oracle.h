@@ -19,6 +19,7 @@
 #ifndef CG_ORACLE_H
 #define CG_ORACLE_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -111,6 +112,13 @@ void orc_flash_fwd(const float* Q, const float* K, const float* V, float* O,
 void orc_apply_rope(float* x, int S, int H, int D, int pos0, float theta);
 /* src/attention/flash_attn.c:318-328. */
 void orc_rope_freqs(float* cos_c, float* sin_c, int max_s, int D, float theta);
+/* Seeded weights of the synthetic stack (no reference counterpart; the
+ * rule the library documents for cgx_fill_normal_dev): lowbias32 counter
+ * hash, four 16-bit uniforms per value, centred sum times
+ * std * sqrt(3) / 65536. */
+uint32_t orc_fill_key(uint64_t seed, uint32_t stream_id);
+void orc_fill_normal(float* out, size_t n, uint64_t seed, uint32_t stream_id, float stddev);
+
 /* ALiBi slopes and bias (src/attention/flash_attn.c:368-388). */
 void orc_alibi_slopes(float* slopes, int H);
 void orc_alibi_bias(float* bias, int Sq, int Sk, int H, const float* slopes);

@@ -44,6 +44,8 @@ _ORACLE_SIGS = {
     "orc_apply_rope": (None, [VP, I, I, I, I, F]),
     "orc_rope_freqs": (None, [VP, VP, I, I, F]),
     "orc_alibi_slopes": (None, [VP, I]),
+    "orc_fill_key": (C.c_uint32, [C.c_uint64, C.c_uint32]),
+    "orc_fill_normal": (None, [VP, C.c_size_t, C.c_uint64, C.c_uint32, F]),
     "orc_alibi_bias": (None, [VP, I, I, I, VP]),
     "orc_rmsnorm": (None, [VP, VP, VP, I, I, F]),
     "orc_swiglu": (None, [VP, VP, VP, I]),

@@ -298,3 +298,26 @@ def test_alibi_vs_reference_and_closed_form(ref, oracle, H):
     np.testing.assert_array_equal(_bits(b), _bits(rb))
     exp = s[:, None, None] * (np.arange(Sk)[None, None, :] - np.arange(Sq)[None, :, None])
     np.testing.assert_array_equal(b.reshape(H, Sq, Sk), exp.astype(np.float32))
+
+
+# ------------------------------------------------------------ seeded fill
+
+def test_fill_normal_moments_and_determinism(oracle):
+    # the synthetic weights' rule: unit variance (Irwin-Hall n = 4 scaled by
+    # sqrt(3)), mean 0, bounded by 2*sqrt(3); same seed/stream -> same bits,
+    # another stream -> independent values
+    from oracle_model import fill
+    n = 400000
+    a = fill(oracle, n, 123, 7, 1.0).astype(np.float64)
+    assert abs(a.mean()) < 0.01
+    assert abs(a.std() - 1.0) < 0.01
+    assert np.abs(a).max() <= 2 * np.sqrt(3) + 1e-6
+    # excess kurtosis of Irwin-Hall(4) is -0.3
+    kurt = ((a - a.mean()) ** 4).mean() / a.var() ** 2 - 3
+    assert abs(kurt + 0.3) < 0.05
+    b = fill(oracle, n, 123, 7, 1.0)
+    np.testing.assert_array_equal(a.astype(np.float32), b)
+    c = fill(oracle, n, 123, 8, 1.0).astype(np.float64)
+    assert abs(np.corrcoef(a, c)[0, 1]) < 0.01
+    s = fill(oracle, 1000, 123, 7, 0.02)
+    np.testing.assert_allclose(s, (a[:1000] * 0.02).astype(np.float32), rtol=1e-6)

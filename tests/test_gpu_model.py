@@ -1,0 +1,183 @@
+"""GPU parity of the synthetic decoder stack and the speculative loop.
+
+* seeded weights: the GPU fill and the oracle's restatement agree bit for
+  bit, and so do the exported INT4 weights;
+* forward: logits within 1e-3 of max|logits| per row of the oracle stack
+  (tests/oracle_model.py) across prefill, decode, verify-sized steps and a
+  KV rollback;
+* speculative loop: a draft identical to the target (same seed, separate
+  caches) must accept every drafted token (p == q exactly); with a
+  different draft, the loop keeps both caches at the accepted prefix.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from cogito_amd.capi import DeviceArray, last_error
+from gpu_util import rel_err_rows
+from oracle_lib import ptr
+from oracle_model import W_GU, W_LM, W_QKV, Cfg, OracleModel, fill
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+TINY = Cfg(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, d_ff=512,
+           vocab=1024, group_size=128, kv_group_size=64, max_seq=64, max_tokens=8,
+           init_std=0.05)
+
+
+def new_model(gpu, cfg, seed, share=None):
+    cc = cfg.ctype()
+    m = gpu.cgx_model_new(C.byref(cc), seed, share)
+    assert m, last_error(gpu)
+    return m
+
+
+def logits_np(gpu, m, rows, V):
+    out = np.empty((rows, V), np.float32)
+    assert gpu.cgx_memcpy_d2h(out.ctypes.data, gpu.cgx_model_logits(m), out.nbytes) == 0
+    return out
+
+
+@pytest.mark.parametrize("seed,sid,n", [(1, 1, 100000), (2**40 + 7, 35, 4097), (0, 2, 33)])
+def test_fill_normal_bitexact(gpu, oracle, seed, sid, n):
+    d = DeviceArray(gpu, n * 4)
+    assert gpu.cgx_fill_normal_dev(d.ptr, n, seed, sid, 0.02) == 0, last_error(gpu)
+    got = d.numpy(np.float32, (n,))
+    exp = fill(oracle, n, seed, sid, 0.02)
+    np.testing.assert_array_equal(got.view(np.uint32), exp.view(np.uint32))
+    d.free()
+
+
+def test_model_export_matches_oracle(gpu, oracle):
+    m = new_model(gpu, TINY, 11)
+    om = OracleModel(oracle, TINY, 11)
+    for layer, which, lin in ((0, W_QKV, om.layers[0][0]), (1, W_GU, om.layers[1][2]),
+                              (0, W_LM, om.lm)):
+        data, scales, K, N = lin
+        gd = np.zeros_like(data)
+        gs = np.zeros_like(scales)
+        assert gpu.cgx_model_export(m, layer, which, gd.ctypes.data, gs.ctypes.data) == 0, \
+            last_error(gpu)
+        np.testing.assert_array_equal(gd, data)
+        np.testing.assert_array_equal(gs.view(np.uint32), scales.view(np.uint32))
+    gpu.cgx_model_free(m)
+
+
+def test_model_forward_vs_oracle(gpu, oracle, rng):
+    m = new_model(gpu, TINY, 5)
+    om = OracleModel(oracle, TINY, 5)
+    V = TINY.vocab
+    steps = [5, 1, 3, 8, 2]
+    for M in steps:
+        toks = rng.integers(0, V, M).astype(np.int32)
+        assert gpu.cgx_model_forward(m, toks.ctypes.data, M, M, None) == 0, last_error(gpu)
+        got = logits_np(gpu, m, M, V)
+        exp = om.forward(toks)
+        err = rel_err_rows(got, exp)
+        assert err <= TOL, (M, err)
+        assert gpu.cgx_model_len(m) == om.len
+    # rollback: drop the last 4 positions and continue
+    assert gpu.cgx_model_truncate(m, om.len - 4) == 0
+    om.truncate(om.len - 4)
+    toks = rng.integers(0, V, 3).astype(np.int32)
+    assert gpu.cgx_model_forward(m, toks.ctypes.data, 3, 1, None) == 0
+    got = logits_np(gpu, m, 1, V)
+    assert rel_err_rows(got, om.forward(toks, n_logits=1)) <= TOL
+    gpu.cgx_model_free(m)
+
+
+def test_model_forward_head_dim_128_gqa(gpu, oracle, rng):
+    cfg = Cfg(n_layers=1, d_model=512, n_heads=8, n_kv_heads=2, head_dim=128, d_ff=768,
+              vocab=2048, group_size=128, kv_group_size=128, max_seq=300, max_tokens=5,
+              init_std=0.05)
+    m = new_model(gpu, cfg, 9)
+    om = OracleModel(oracle, cfg, 9)
+    # a longer context through several forwards, then verify-sized steps
+    for M in [5] * 40 + [1, 5, 5]:
+        toks = rng.integers(0, cfg.vocab, M).astype(np.int32)
+        assert gpu.cgx_model_forward(m, toks.ctypes.data, M, M, None) == 0, last_error(gpu)
+        exp = om.forward(toks)
+    got = logits_np(gpu, m, 5, cfg.vocab)
+    assert rel_err_rows(got, exp) <= TOL
+    gpu.cgx_model_free(m)
+
+
+def test_model_rejects_bad_config(gpu):
+    bad = Cfg(n_layers=1, d_model=200, n_heads=4, n_kv_heads=2, head_dim=50, d_ff=512,
+              vocab=1000)
+    cc = bad.ctype()
+    gpu.cgx_clear_error()
+    assert not gpu.cgx_model_new(C.byref(cc), 1, None)
+    assert last_error(gpu)
+
+
+def run_spec(gpu, draft, target, gamma, T, k, p, prompt, steps, rng):
+    s = gpu.cgx_spec_new(draft, target, gamma, T, k, p)
+    assert s, last_error(gpu)
+    pr = np.asarray(prompt, np.int32)
+    assert gpu.cgx_spec_prefill(s, pr.ctypes.data, len(pr)) == 0, last_error(gpu)
+    ns, emitted = [], []
+    for _ in range(steps):
+        ud = rng.uniform(0, 1, gamma).astype(np.float32)
+        uv = rng.uniform(0, 1, gamma + 1).astype(np.float32)
+        out = np.zeros(gamma + 1, np.int32)
+        L = gpu.cgx_model_len(target)
+        n = gpu.cgx_spec_step(s, ud.ctypes.data, uv.ctypes.data, out.ctypes.data)
+        assert 0 <= n <= gamma, last_error(gpu)
+        assert gpu.cgx_model_len(target) == L + n + 1
+        assert gpu.cgx_model_len(draft) == L + min(n, gamma - 1) + 1
+        assert np.all((out[:n + 1] >= 0) & (out[:n + 1] < 1024 * 64))
+        ns.append(n)
+        emitted.extend(out[:n + 1].tolist())
+    st = [C.c_longlong() for _ in range(3)]
+    gpu.cgx_spec_stats(s, *[C.byref(x) for x in st])
+    assert st[0].value == steps and st[1].value == steps * gamma and st[2].value == sum(ns)
+    gpu.cgx_spec_free(s)
+    return ns, emitted
+
+
+@pytest.mark.parametrize("T,k,p", [(1.0, 0, 1.0), (0.8, 0, 0.9), (0.7, 50, 1.0)])
+def test_spec_identical_draft_accepts_everything(gpu, rng, T, k, p):
+    cfg = Cfg(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, d_ff=512,
+              vocab=1024, max_seq=128, max_tokens=8, init_std=0.05)
+    target = new_model(gpu, cfg, 21)
+    draft = new_model(gpu, cfg, 21)
+    ns, emitted = run_spec(gpu, draft, target, 4, T, k, p, [1, 2, 3, 4, 5], 10, rng)
+    assert ns == [4] * 10
+    assert len(emitted) == 50
+    gpu.cgx_model_free(draft)
+    gpu.cgx_model_free(target)
+
+
+def test_spec_with_draft_head_rolls_back(gpu, rng):
+    cfg = Cfg(n_layers=3, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, d_ff=512,
+              vocab=1024, max_seq=200, max_tokens=8, init_std=0.05)
+    dcfg = Cfg(**{**cfg.__dict__, "n_layers": 1})
+    target = new_model(gpu, cfg, 31)
+    draft = new_model(gpu, dcfg, 32, target)        # shares embedding and lm_head
+    ns, _ = run_spec(gpu, draft, target, 4, 1.0, 0, 1.0, list(range(1, 12)), 25, rng)
+    assert 0 < sum(ns) < 4 * 25          # some accepted, some rejected
+    gpu.cgx_model_free(draft)
+    gpu.cgx_model_free(target)
+
+
+def test_spec_from_filled_context(gpu, rng):
+    cfg = Cfg(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, d_ff=512,
+              vocab=1024, max_seq=600, max_tokens=8, init_std=0.05)
+    target = new_model(gpu, cfg, 41)
+    draft = new_model(gpu, cfg, 41)
+    for mdl in (target, draft):
+        assert gpu.cgx_model_fill_context(mdl, 512, 7) == 0, last_error(gpu)
+        assert gpu.cgx_model_len(mdl) == 512
+    s = gpu.cgx_spec_new(draft, target, 4, 1.0, 0, 1.0)
+    assert gpu.cgx_spec_set_last(s, 3) == 0
+    out = np.zeros(5, np.int32)
+    u = rng.uniform(0, 1, 5).astype(np.float32)
+    assert gpu.cgx_spec_step(s, u.ctypes.data, u.ctypes.data, out.ctypes.data) == 4
+    gpu.cgx_spec_free(s)
+    gpu.cgx_model_free(draft)
+    gpu.cgx_model_free(target)
