@@ -58,7 +58,7 @@ def make_config2_weight(rng, K: int, N: int, gs: int):
     return data, scales
 
 
-def bench_gemv(lib, M_list, K, N, gs, steps, warmup, seed=2024):
+def bench_gemv(lib, M_list, K, N, gs, steps, warmup, seed=2024, layout=3):
     from cogito_amd.capi import DeviceArray, host_quant_from_arrays, last_error
 
     rng = np.random.default_rng(seed)
@@ -70,8 +70,8 @@ def bench_gemv(lib, M_list, K, N, gs, steps, warmup, seed=2024):
         f"({copies * per_copy / 1e6:.0f} MB) to defeat the MALL")
     dws = []
     for _ in range(copies):
-        dq = lib.cgx_quant_to_device(C.byref(hq))
-        if not dq or lib.cgx_quant_layout(dq) != 2:
+        dq = lib.cgx_quant_to_device_layout(C.byref(hq), layout)
+        if not dq or lib.cgx_quant_layout(dq) != layout:
             raise RuntimeError(f"weight upload failed: {last_error(lib)}")
         dws.append(dq)
     results = {}
@@ -100,6 +100,246 @@ def bench_gemv(lib, M_list, K, N, gs, steps, warmup, seed=2024):
     for dq in dws:
         lib.cg_tensor_quant_free(dq)
     return results
+
+
+def _rotations(per_copy: int, floor: int = 2) -> int:
+    """Copies needed so one pass over them streams >= 2x the MALL."""
+    return max(floor, -(-2 * MALL_BYTES // per_copy) + 1)
+
+
+def bench_gemv_shapes(lib, shapes, M, steps, warmup, gs=128, seed=77):
+    """GEMV launches at the linear-layer shapes of the 7B-shape stack (one
+    launch streams W[K,N] once), weights rotated past the MALL."""
+    from cogito_amd.capi import DeviceArray, host_quant_from_arrays, last_error
+
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, K, N in shapes:
+        data = rng.integers(0, 256, size=K * N // 2, dtype=np.uint8)
+        scales = rng.uniform(0.005, 0.02, K * N // gs).astype(np.float16).astype(np.float32)
+        hq, keep = host_quant_from_arrays(data, scales, K, N, gs)
+        per_copy = K * N // 2 + (K * N // gs) * 4
+        copies = _rotations(per_copy)
+        dws = []
+        for _ in range(copies):
+            dq = lib.cgx_quant_to_device_layout(C.byref(hq), 3)
+            if not dq or lib.cgx_quant_layout(dq) != 3:
+                raise RuntimeError(f"weight upload failed: {last_error(lib)}")
+            dws.append(dq)
+        del keep, data, scales
+        dx = DeviceArray.from_numpy(lib, rng.normal(0, 1, (M, K)).astype(np.float32))
+        dy = DeviceArray(lib, M * N * 4)
+        for i in range(warmup):
+            lib.cgx_matmul_int4_dev(dx.ptr, M, dws[i % copies], dy.ptr)
+        if lib.cgx_synchronize():
+            raise RuntimeError(last_error(lib))
+        lib.cgx_event_record(0)
+        for i in range(steps):
+            lib.cgx_matmul_int4_dev(dx.ptr, M, dws[i % copies], dy.ptr)
+        lib.cgx_event_record(1)
+        if lib.cgx_synchronize():
+            raise RuntimeError(last_error(lib))
+        us = lib.cgx_event_elapsed_ms(0, 1) / steps * 1e3
+        nbytes = gemv_bytes(M, K, N, gs)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"K": K, "N": N, "M": M, "us": round(us, 3), "bytes": nbytes,
+                     "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"[bench] gemv {name} {K}x{N} M={M}: {us:.2f} us, {gbs:.0f} GB/s "
+            f"({gbs / HBM_PEAK_GBS:.1%})")
+        dx.free()
+        dy.free()
+        for dq in dws:
+            lib.cg_tensor_quant_free(dq)
+    return out
+
+
+def _draft_tokens_from(logits: np.ndarray, u: np.ndarray) -> np.ndarray:
+    """Draft ids drawn from softmax(draft row) by inverse CDF (fp64)."""
+    z = logits.astype(np.float64)
+    z -= z.max(axis=-1, keepdims=True)
+    p = np.exp(z)
+    cdf = np.cumsum(p, axis=-1)
+    cdf /= cdf[..., -1:]
+    flat = cdf.reshape(-1, cdf.shape[-1])
+    toks = [min(int(np.searchsorted(row, uu, side="right")), row.size - 1)
+            for row, uu in zip(flat, u.reshape(-1))]
+    return np.asarray(toks, np.int32).reshape(u.shape)
+
+
+def bench_accept(lib, V, B, gamma, T, steps, warmup, sets=1, seed=5, top_k=0, top_p=1.0):
+    """cgx_verify_chain_batch_dev on B independent chains: target logits
+    [B][gamma+1][V], draft [B][gamma][V] ~ N(0, 2^2), draft ids drawn from
+    the draft softmax, pre-drawn uniforms.  `sets` rotating input sets."""
+    from cogito_amd.capi import DeviceArray, last_error
+
+    rng = np.random.default_rng(seed)
+    bufs = []
+    for s in range(sets):
+        nt, nd = B * (gamma + 1) * V, B * gamma * V
+        dt, dd = DeviceArray(lib, nt * 4), DeviceArray(lib, nd * 4)
+        if (lib.cgx_fill_normal_dev(dt.ptr, nt, seed, 100 + 2 * s, 2.0) or
+                lib.cgx_fill_normal_dev(dd.ptr, nd, seed, 101 + 2 * s, 2.0)):
+            raise RuntimeError(last_error(lib))
+        ud = rng.random((B, gamma), dtype=np.float32)
+        toks = _draft_tokens_from(dd.numpy(np.float32, (B, gamma, V)) / T, ud)
+        uv = rng.random((B, gamma + 1), dtype=np.float32)
+        bufs.append((dt, dd, DeviceArray.from_numpy(lib, toks),
+                     DeviceArray.from_numpy(lib, uv)))
+    dout = DeviceArray(lib, B * (gamma + 1) * 4)
+    dn = DeviceArray(lib, B * 4)
+    dap = DeviceArray(lib, B * gamma * 4)
+
+    def call(i):
+        dt, dd, dtok, du = bufs[i % sets]
+        return lib.cgx_verify_chain_batch_dev(dt.ptr, dd.ptr, dtok.ptr, du.ptr, B, gamma, V,
+                                              T, top_k, top_p, dout.ptr, dn.ptr, dap.ptr)
+    for i in range(warmup):
+        if call(i):
+            raise RuntimeError(last_error(lib))
+    if lib.cgx_synchronize():
+        raise RuntimeError(last_error(lib))
+    lib.cgx_event_record(0)
+    for i in range(steps):
+        call(i)
+    lib.cgx_event_record(1)
+    if lib.cgx_synchronize():
+        raise RuntimeError(last_error(lib))
+    us = lib.cgx_event_elapsed_ms(0, 1) / steps * 1e3
+    nacc = dn.numpy(np.int32, (B,))
+    nbytes = (2 * gamma + 1) * V * 4 * B
+    gbs = nbytes / (us * 1e-6) / 1e9
+    for b in bufs:
+        for d in b:
+            d.free()
+    for d in (dout, dn, dap):
+        d.free()
+    log(f"[bench] accept V={V} B={B} gamma={gamma} T={T} top_k={top_k} top_p={top_p}: "
+        f"{us:.2f} us/call, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}), "
+        f"mean accepted {nacc.mean():.2f}")
+    return {"V": V, "batch": B, "gamma": gamma, "temperature": T, "top_k": top_k,
+            "top_p": top_p, "us_per_call": round(us, 3), "bytes": nbytes,
+            "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "rotating_sets": sets, "mean_accepted_last_call": float(nacc.mean())}
+
+
+def bench_attention(lib, ctx, Nq, H, Hk, D, kv_gs, steps, warmup, seed=9):
+    """INT4-KV verify attention (chain mask) of one layer per launch at the
+    7B shape; launches rotate over enough layers to stream past the MALL."""
+    from cogito_amd.capi import DeviceArray, last_error
+
+    Nk = ctx + Nq
+    per_layer = Nk * Hk * D // 2 * 2 + Nk * Hk * (D // kv_gs) * 4 * 2
+    layers = _rotations(per_layer)
+    cache = lib.cg_kv_cache_int4_new(layers, Nk, Hk, D, kv_gs)
+    if not cache:
+        raise RuntimeError(last_error(lib))
+    n = Nk * Hk * D
+    dk, dv = DeviceArray(lib, n * 4), DeviceArray(lib, n * 4)
+    if (lib.cgx_fill_normal_dev(dk.ptr, n, seed, 1, 1.0) or
+            lib.cgx_fill_normal_dev(dv.ptr, n, seed, 2, 1.0)):
+        raise RuntimeError(last_error(lib))
+    for l in range(layers):
+        if lib.cgx_kv_cache_int4_write(cache, l, 0, dk.ptr, dv.ptr, Nk):
+            raise RuntimeError(last_error(lib))
+    lib.cgx_kv_cache_int4_set_len(cache, Nk)
+    dk.free()
+    dv.free()
+    dq = DeviceArray(lib, Nq * H * D * 4)
+    lib.cgx_fill_normal_dev(dq.ptr, Nq * H * D, seed, 3, 1.0)
+    do = DeviceArray(lib, Nq * H * D * 4)
+    for i in range(warmup):
+        if lib.cgx_attention_int4_kv_dev(dq.ptr, Nq, H, cache, i % layers, 0, None, do.ptr):
+            raise RuntimeError(last_error(lib))
+    if lib.cgx_synchronize():
+        raise RuntimeError(last_error(lib))
+    lib.cgx_event_record(0)
+    for i in range(steps):
+        lib.cgx_attention_int4_kv_dev(dq.ptr, Nq, H, cache, i % layers, 0, None, do.ptr)
+    lib.cgx_event_record(1)
+    if lib.cgx_synchronize():
+        raise RuntimeError(last_error(lib))
+    us = lib.cgx_event_elapsed_ms(0, 1) / steps * 1e3
+    nbytes = per_layer + 2 * Nq * H * D * 4
+    gbs = nbytes / (us * 1e-6) / 1e9
+    lib.cg_kv_cache_int4_free(cache)
+    dq.free()
+    do.free()
+    log(f"[bench] attention ctx={ctx} Nq={Nq} H={H} Hk={Hk} D={D}: {us:.2f} us/layer, "
+        f"{gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%})")
+    return {"ctx": ctx, "Nq": Nq, "H": H, "Hk": Hk, "D": D, "kv_group": kv_gs,
+            "us_per_layer": round(us, 3), "bytes": nbytes, "GB/s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "layers_rotated": layers}
+
+
+def _model_cfg(n_layers, d, H, Hk, hd, ff, V, max_seq, max_tokens, kv_gs):
+    from cogito_amd.capi import CgxModelConfig
+    return CgxModelConfig(n_layers=n_layers, d_model=d, n_heads=H, n_kv_heads=Hk,
+                          head_dim=hd, d_ff=ff, vocab=V, group_size=128,
+                          kv_group_size=kv_gs, max_seq=max_seq, max_tokens=max_tokens,
+                          rope_theta=10000.0, norm_eps=1e-5, init_std=0.02)
+
+
+def bench_e2e(lib, name, tgt, drf, share_head, ctx, gamma, T, top_k, top_p, steps, warmup,
+              seed=2025):
+    """Chain speculative decoding on the GPU (cgx_spec_step): the draft
+    proposes gamma tokens, the target verifies gamma+1 rows in one forward,
+    the verify kernels accept a prefix, both KV caches roll back.  Verified
+    tok/s = sum(accepted + 1) / wall time over the timed steps (host round
+    trip per step included)."""
+    from cogito_amd.capi import last_error
+
+    max_seq = ctx + (gamma + 1) * (steps + warmup + 2) + 8
+    ct = _model_cfg(*tgt, max_seq=max_seq, max_tokens=gamma + 1, kv_gs=tgt[4])
+    cd = _model_cfg(*drf, max_seq=max_seq, max_tokens=2, kv_gs=drf[4])
+    t0 = time.perf_counter()
+    mt = lib.cgx_model_new(C.byref(ct), seed, None)
+    if not mt:
+        raise RuntimeError(last_error(lib))
+    md = lib.cgx_model_new(C.byref(cd), seed + 1, mt if share_head else None)
+    if not md:
+        raise RuntimeError(last_error(lib))
+    if (lib.cgx_model_fill_context(mt, ctx, seed) or
+            lib.cgx_model_fill_context(md, ctx, seed + 7)):
+        raise RuntimeError(last_error(lib))
+    log(f"[bench] {name}: models built and context {ctx} filled in "
+        f"{time.perf_counter() - t0:.1f} s")
+    sp = lib.cgx_spec_new(md, mt, gamma, T, top_k, top_p)
+    if not sp or lib.cgx_spec_set_last(sp, 1):
+        raise RuntimeError(last_error(lib))
+    rng = np.random.default_rng(seed)
+    out = np.zeros(gamma + 1, np.int32)
+
+    def step():
+        ud = rng.random(gamma, dtype=np.float32)
+        uv = rng.random(gamma + 1, dtype=np.float32)
+        n = lib.cgx_spec_step(sp, ud.ctypes.data, uv.ctypes.data, out.ctypes.data)
+        if n < 0:
+            raise RuntimeError(last_error(lib))
+        return n
+    for _ in range(warmup):
+        step()
+    lib.cgx_synchronize()
+    emitted = 0
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        emitted += step() + 1
+    lib.cgx_synchronize()
+    wall = time.perf_counter() - t0
+    lib.cgx_spec_free(sp)
+    lib.cgx_model_free(md)
+    lib.cgx_model_free(mt)
+    tps = emitted / wall
+    acc = (emitted - steps) / (steps * gamma)
+    log(f"[bench] {name}: {tps:.0f} verified tok/s, {wall / steps * 1e3:.3f} ms/step, "
+        f"acceptance {acc:.3f}")
+    return {"verified_tok_s": round(tps, 1), "ms_per_step": round(wall / steps * 1e3, 4),
+            "acceptance_rate": round(acc, 4), "tokens_per_step": round(emitted / steps, 3),
+            "steps": steps, "gamma": gamma, "temperature": T, "top_k": top_k, "top_p": top_p,
+            "ctx": ctx, "target": dict(zip(("layers", "d", "H", "Hk", "hd", "ff", "V"), tgt)),
+            "draft": dict(zip(("layers", "d", "H", "Hk", "hd", "ff", "V"), drf)),
+            "draft_shares_embed_lm_head": bool(share_head), "batch": 1}
+
+
 
 
 def cpu_baseline_gemv(M, K, N, gs, budget_s=12.0, seed=2024):
@@ -160,6 +400,12 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=5,
                     help="activation rows M of the headline line (gamma+1 = 5)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--legs", default="valu,shapes,accept,attn,e2e",
+                    help="comma list of legs beside the headline GEMV: valu (the VALU "
+                         "GEMV on the headline workload), shapes (7B-stack "
+                         "GEMV shapes), accept (acceptance sampling C1 + V=128256 x 64 "
+                         "chains), attn (INT4-KV verify attention, 7B shape), e2e "
+                         "(verified tok/s, tiny and 7B-shape stacks)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy (a plain copy kernel "
                          "of known size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -190,9 +436,36 @@ def main() -> int:
 
     K = N = 4096
     gs = 128
+    legs = set(x for x in args.legs.split(",") if x)
     M_list = sorted(set([1, 2, 3, 4, 5, args.rows]))
-    res = bench_gemv(lib, M_list, K, N, gs, args.steps, args.warmup)
+    res = bench_gemv(lib, M_list, K, N, gs, args.steps, args.warmup, layout=3)
     head = res[args.rows]
+    extra = {}
+    if "valu" in legs:
+        # the VALU GEMV (weight layout 2) on the same workload, for comparison
+        rv = bench_gemv(lib, M_list, K, N, gs, args.steps, args.warmup, layout=2)
+        extra["gemv_valu_per_rows"] = {str(m): {"us": round(r["us_per_launch"], 3),
+                                                "GB/s": round(r["gbs"], 1)}
+                                       for m, r in rv.items()}
+    if "shapes" in legs:
+        d, ff, hd = 4096, 11008, 128
+        extra["gemv_7b_shapes"] = bench_gemv_shapes(
+            lib, [("qkv", d, (32 + 2 * 8) * hd), ("o", d, d), ("gate_up", d, 2 * ff),
+                  ("down", ff, d), ("lm_head", d, 32000), ("lm_head_128k", d, 128256)],
+            args.rows, max(50, args.steps // 4), 10)
+    if "accept" in legs:
+        extra["accept_c1"] = bench_accept(lib, 32000, 1, 4, 1.0, args.steps, args.warmup)
+        extra["accept_roofline"] = bench_accept(lib, 128256, 64, 4, 1.0, 50, 5, sets=2)
+    if "attn" in legs:
+        extra["attention_7b"] = bench_attention(lib, 4096, 5, 32, 8, 128, 128, args.steps,
+                                                args.warmup)
+    if "e2e" in legs:
+        extra["e2e_tiny_c3"] = bench_e2e(
+            lib, "C3 tiny", (12, 768, 12, 12, 64, 3072, 32000),
+            (2, 768, 12, 12, 64, 3072, 32000), False, 1024, 4, 0.8, 0, 0.9, 100, 10)
+        extra["e2e_7b_c4"] = bench_e2e(
+            lib, "C4 7B-shape", (32, 4096, 32, 8, 128, 11008, 32000),
+            (1, 4096, 32, 8, 128, 11008, 32000), True, 4096, 4, 1.0, 0, 1.0, 40, 5)
 
     cpu = None
     if not args.no_cpu:
@@ -226,6 +499,7 @@ def main() -> int:
                               "GB/s": round(r["gbs"], 1),
                               "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}
                      for m, r in res.items()},
+        "legs": extra,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -232,6 +232,7 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_tensor_to_host": (I, [PT, C.POINTER(F)]),
     "cgx_quant_to_device": (PQ, [PQ]),
     "cgx_quant_to_device_flat": (PQ, [PQ]),
+    "cgx_quant_to_device_layout": (PQ, [PQ, I]),
     "cgx_quant_layout": (I, [PQ]),
     "cgx_matmul_int4_dev": (I, [VP, I, PQ, VP]),
     "cgx_matmul_int4_dev_kernel": (I, [VP, I, PQ, VP, I]),

@@ -500,6 +500,8 @@ extern "C" int cgk_attention(const float* Q, int int4, const uint8_t* kc, const 
         cgx_set_error("attention: tree mask needs ancestor bits for at most 64 new tokens");
         return -1;
     }
+    if (int4 && !lse && cgk_attn_dec_supported(D, gs, B, mask_kind))
+        return cgk_attn_dec(Q, kc, vc, ks, vs, Nq, Nk, H, Hk, D, scale, mask_kind, anc, O);
     AttnArgs a;
     a.Q = Q; a.int4 = int4; a.kc = kc; a.vc = vc; a.ks = ks; a.vs = vs; a.gs = gs;
     a.K = K; a.V = V; a.B = B; a.Nq = Nq; a.Nk = Nk; a.H = H; a.Hk = Hk; a.D = D;

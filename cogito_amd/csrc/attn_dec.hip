@@ -1,0 +1,496 @@
+// attn_dec.hip -- flash decoding / verification over the INT4 KV cache on
+// the gfx950 matrix cores (the speculative verify shape: a few query rows per
+// KV head against a long cached context).
+//
+// Reference semantics (cogito-ml/cogito):
+//   src/cuda/flash_attn_kernels.c:261-396  online softmax; GQA: query head h
+//                                           reads KV head h * Hk / H; masked
+//                                           scores are -FLT_MAX
+//   src/quantize/int4.c:236-289            K/V value = nibble * scale, one
+//                                           scale per (position, head, group)
+// This kernel takes the cache with one scale group per head row (group ==
+// head_dim, the cache the decoder builds); other groupings use k_attn.
+//
+// Arithmetic.  Scores S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_16x16x32_f16:
+// the K and V nibbles are exact fp16 integers; Q (times the softmax scale)
+// and P (times the V scale of its key) are each carried as hi + lo fp16
+// (22 significant bits) after a power-of-two scaling into fp16 range; the
+// products are exact and accumulate in fp32.  The K scale multiplies the
+// fp32 score of its key.
+//
+// Work split.  Block = (key split, KV head, chunk of 16*RT query rows), 4
+// waves; wave w takes the 32-key tiles w, w+4, ... of the split (a split is
+// one round of 128 keys unless the context is very long, so the 7B verify
+// shape runs ~260 blocks); the first tile's loads are issued before the Q
+// operands are built.  In the
+// S^T orientation a lane holds one query row and 8 keys of a tile -- exactly
+// the B operand of the P^T side, so P never moves.  V^T needs each lane to
+// hold 8 keys of one head-dim column: the lane loads one u32 (8 columns) of
+// each of its 8 keys and v_perm_b32 gathers nibble t of two keys at a time.
+// Waves merge through LDS; splits merge in k_attn_dec_combine.
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cmath>
+#include <cstdint>
+
+#include "cgx_internal.h"
+
+namespace {
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWaves = 4;
+constexpr int kTile = 32;                  // keys per wave tile
+constexpr int kSplitKeys = kWaves * kTile; // keys per block round
+
+inline hipStream_t stream() { return (hipStream_t)cgx_stream(); }
+
+int launch_check(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        cgx_set_error("%s launch failed: %s", what, hipGetErrorString(e));
+        return -1;
+    }
+    return 0;
+}
+
+enum { kMaskNone = 0, kMaskCausal = 1, kMaskTree = 4 };
+
+struct DecArgs {
+    const float* Q;              // [Nq][H][D]
+    const uint8_t* kc;           // [pos][Hk][D/2] two's complement nibbles
+    const uint8_t* vc;
+    const float* ks;             // [pos][Hk] (one group per head row)
+    const float* vs;
+    int Nq, Nk, H, Hk;
+    float scale;
+    int mask_kind;
+    int splits, keys_per_split;
+    float* O;                    // [Nq][H][D] when splits == 1
+    float* part_o;               // [splits][Nq*H][D]
+    float* part_ml;              // [splits][Nq*H][2]
+    unsigned long long anc[64];  // tree: ancestor bits over the last Nq keys
+};
+
+__device__ __forceinline__ int head_begin(int hk, int H, int Hk) { return (hk * H + Hk - 1) / Hk; }
+
+// nibble slot of MFMA position p inside a u32 of 8 nibbles (see nib_pairs)
+__device__ __forceinline__ int slot_of(int p) { return (p >> 1) + 4 * (p & 1); }
+
+// Eight offset-binary nibbles of w as exact fp16 (o - 8), in position order
+// p -> slot {0,4,1,5,2,6,3,7}[p].
+__device__ __forceinline__ f16x8 nib_to_f16(uint32_t w) {
+    const uint32_t w8 = w >> 8;
+    const f16x2 m1032 = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const f16x2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const f16x2 m72 = {(_Float16)-72.0f, (_Float16)-72.0f};
+    f16x2 p0 = __builtin_bit_cast(f16x2, (w & 0x000F000Fu) | 0x64006400u) + m1032;
+    f16x2 p1 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (w & 0x00F000F0u) | 0x64006400u),
+                                         s16, m72);
+    f16x2 p2 = __builtin_bit_cast(f16x2, (w8 & 0x000F000Fu) | 0x64006400u) + m1032;
+    f16x2 p3 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (w8 & 0x00F000F0u) | 0x64006400u),
+                                         s16, m72);
+    f16x8 r;
+    r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+    r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+    return r;
+}
+
+// Nibble t (0..7) of two offset-binary words as an exact fp16 pair (o - 8).
+__device__ __forceinline__ f16x2 nib_pair(uint32_t wlo, uint32_t whi, int t) {
+    const uint32_t b = (uint32_t)(t >> 1);
+    const uint32_t sel = 0x0C000C00u | ((4u + b) << 16) | b;
+    const uint32_t v = __builtin_amdgcn_perm(whi, wlo, sel);
+    if (t & 1) {
+        const f16x2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+        const f16x2 m72 = {(_Float16)-72.0f, (_Float16)-72.0f};
+        return __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (v & 0x00F000F0u) | 0x64006400u),
+                                         s16, m72);
+    }
+    const f16x2 m1032 = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    return __builtin_bit_cast(f16x2, (v & 0x000F000Fu) | 0x64006400u) + m1032;
+}
+
+__device__ __forceinline__ void split16(float v, _Float16& hi, _Float16& lo) {
+    hi = (_Float16)v;
+    lo = (_Float16)(v - (float)hi);
+}
+
+// key of MFMA position pos (0..31) of a tile: positions 8g..8g+3 are keys
+// 4g..4g+3, positions 8g+4..8g+7 are keys 16+4g..16+4g+3 (the S^T rows a
+// lane of group g holds)
+__device__ __forceinline__ int key_of_pos(int g, int p) { return p < 4 ? 4 * g + p : 16 + 4 * g + p - 4; }
+
+template <int D, int RT>
+__global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
+    constexpr int NC = D / 32;          // QK MFMAs per 16 keys (32 head-dim values each)
+    constexpr int DPL = D / 4;          // head-dim values per lane group
+    constexpr int ROWS = 16 * RT;
+    __shared__ float s_o[kWaves][ROWS][D + 4];
+    __shared__ float s_m[kWaves][ROWS], s_l[kWaves][ROWS];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = lane & 15, g = lane >> 4;
+    const int split = blockIdx.x, hk = blockIdx.y;
+    const int h0 = head_begin(hk, a.H, a.Hk), h1 = head_begin(hk + 1, a.H, a.Hk);
+    const int R = (h1 - h0) * a.Nq;
+    const int row0 = blockIdx.z * ROWS;
+    const int Hk = a.Hk;
+    const size_t krow = (size_t)Hk * (D / 2);       // bytes between positions
+
+    const int k_begin = split * a.keys_per_split;
+    const int k_end = min(a.Nk, k_begin + a.keys_per_split);
+    const int ntiles = (k_end - k_begin + kTile - 1) / kTile;
+    const int base = a.Nk - a.Nq;                    // first of the new positions
+
+    float m_run[RT], l_part[RT];
+    f32x4 o[RT][8];                                  // O^T tiles t = 0..7
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        m_run[rt] = -__builtin_inff();
+        l_part[rt] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 8; t++) o[rt][t] = (f32x4)(0.0f);
+    }
+    int ev_cur = 0;                                  // O is held times 2^ev_cur
+
+    // -- loads of one tile: K rows (A operand: key n (+16 kh), head-dim part
+    //    g), V words (A of V^T: column block n, keys of positions 8g..8g+7),
+    //    K and V scales of the keys this lane scores
+    struct TileData {
+        uint32_t kw[2][NC];
+        uint32_t vw[8];
+        float sk[8], sv[8];
+    };
+    auto load_tile = [&](int kt, TileData& t) {
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++) {
+            int key = kt + 16 * kh + n;
+            key = key < k_end ? key : k_end - 1;
+            const uint8_t* p = a.kc + (size_t)key * krow + (size_t)hk * (D / 2) + (D / 8) * g;
+            if (NC == 4) {
+                u32x4 v = *(const u32x4*)p;
+                t.kw[kh][0] = v.x; t.kw[kh][1] = v.y; t.kw[kh][2 % NC] = v.z; t.kw[kh][3 % NC] = v.w;
+            } else if (NC == 2) {
+                u32x2 v = *(const u32x2*)p;
+                t.kw[kh][0] = v.x; t.kw[kh][1 % NC] = v.y;
+            } else {
+                t.kw[kh][0] = *(const uint32_t*)p;
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < 8; p++) {
+            int key = kt + key_of_pos(g, p);
+            key = key < k_end ? key : k_end - 1;
+            t.vw[p] = n < D / 8 ? *(const uint32_t*)(a.vc + (size_t)key * krow +
+                                                     (size_t)hk * (D / 2) + 4 * n)
+                                : 0u;   // a zero nibble: rows of O^T past D are not stored
+            t.sk[p] = a.ks[(size_t)key * Hk + hk];
+            t.sv[p] = a.vs[(size_t)key * Hk + hk];
+        }
+    };
+    TileData td;
+    if (wave < ntiles) load_tile(k_begin + wave * kTile, td);
+
+    // ---- Q^T operands of this lane's rows (B operand: row n, 8 positions per MFMA)
+    f16x8 qh[RT][NC], ql[RT][NC];
+    float qinv[RT];
+    int rq[RT];
+    bool rok[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const int r = row0 + 16 * rt + n;
+        rok[rt] = r < R;
+        const int h = h0 + (rok[rt] ? r / a.Nq : 0), q = rok[rt] ? r % a.Nq : 0;
+        rq[rt] = q;
+        const float* qp = a.Q + ((size_t)q * a.H + h) * D + DPL * g;
+        float qv[DPL];
+        float qmax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < DPL; i += 4) {
+            float4 t = rok[rt] ? *(const float4*)(qp + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            qv[i] = t.x * a.scale; qv[i + 1] = t.y * a.scale;
+            qv[i + 2] = t.z * a.scale; qv[i + 3] = t.w * a.scale;
+            qmax = fmaxf(qmax, fmaxf(fmaxf(fabsf(qv[i]), fabsf(qv[i + 1])),
+                                     fmaxf(fabsf(qv[i + 2]), fabsf(qv[i + 3]))));
+        }
+        qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
+        qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
+        int E = 0;
+        if (qmax > 0.0f && qmax < __builtin_inff()) E = 14 - ilogbf(qmax);
+        E = E > 100 ? 100 : (E < -100 ? -100 : E);
+        const float up = ldexpf(1.0f, E);
+        qinv[rt] = ldexpf(1.0f, -E);
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+#pragma unroll
+            for (int p = 0; p < 8; p++) {
+                _Float16 hi, lo;
+                split16(qv[8 * c + slot_of(p)] * up, hi, lo);
+                qh[rt][c][p] = hi;
+                ql[rt][c][p] = lo;
+            }
+    }
+
+
+    for (int tile = wave; tile < ntiles; tile += kWaves) {
+        const int kt = k_begin + tile * kTile;
+        if (tile != wave) load_tile(kt, td);
+        uint32_t (&kw)[2][NC] = td.kw;
+        uint32_t (&vw)[8] = td.vw;
+        float (&sk)[8] = td.sk;
+        float (&sv)[8] = td.sv;
+
+        // -- S^T = K Q^T (lane: row n, keys 4g+i of each 16-key half)
+        f32x4 s[RT][2];
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) s[rt][0] = s[rt][1] = (f32x4)(0.0f);
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                const f16x8 ka = nib_to_f16(kw[kh][c] ^ 0x88888888u);
+#pragma unroll
+                for (int rt = 0; rt < RT; rt++) {
+                    s[rt][kh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[rt][c], s[rt][kh], 0, 0, 0);
+                    s[rt][kh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[rt][c], s[rt][kh], 0, 0, 0);
+                }
+            }
+
+        // -- V^T operands (positions 8g..8g+7 = the lane's keys), exponent of P~
+        float svmax = 0.0f;
+#pragma unroll
+        for (int p = 0; p < 8; p++) svmax = fmaxf(svmax, fabsf(sv[p]));
+        svmax = fmaxf(svmax, __shfl_xor(svmax, 16));
+        svmax = fmaxf(svmax, __shfl_xor(svmax, 32));
+        // P~ = P * s_v * 2^ev stays below 2^15; ev only ever decreases, so
+        // rescaling O by 2^(ev - ev_cur) cannot overflow
+        int ev = 0;
+        if (svmax > 0.0f && svmax < __builtin_inff()) ev = 14 - ilogbf(svmax);
+        ev = ev > 60 ? 60 : (ev < -60 ? -60 : ev);
+        if (tile != wave && ev > ev_cur) ev = ev_cur;
+        const float evup = ldexpf(1.0f, ev);
+        const float evshift = tile == wave ? 1.0f : ldexpf(1.0f, ev - ev_cur);
+        ev_cur = ev;
+#pragma unroll
+        for (int p = 0; p < 8; p++) vw[p] ^= 0x88888888u;
+
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            // scores, mask, online softmax for row (rt, n)
+            float val[8];
+            float tmax = -__builtin_inff();
+#pragma unroll
+            for (int p = 0; p < 8; p++) {
+                const int kk = kt + key_of_pos(g, p);
+                const bool exists = kk < k_end;
+                bool vis = rok[rt];
+                if (a.mask_kind == kMaskCausal) {
+                    vis = vis && kk <= base + rq[rt];
+                } else if (a.mask_kind == kMaskTree) {
+                    vis = vis && (kk < base || ((a.anc[rq[rt]] >> (kk - base)) & 1ull));
+                }
+                const float sc = s[rt][p >> 2][p & 3] * qinv[rt] * sk[p];
+                val[p] = !exists ? -__builtin_inff() : (vis ? sc : -FLT_MAX);
+                tmax = fmaxf(tmax, val[p]);
+            }
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+            const float m_new = fmaxf(m_run[rt], tmax);
+            const float alpha = m_new == -__builtin_inff() ? 1.0f : __expf(m_run[rt] - m_new);
+            m_run[rt] = m_new;
+            f16x8 ph, pl;
+            float psum = 0.0f;
+#pragma unroll
+            for (int p = 0; p < 8; p++) {
+                const float pv = m_new == -__builtin_inff() ? 0.0f : __expf(val[p] - m_new);
+                psum += pv;
+                _Float16 hi, lo;
+                split16(pv * sv[p] * evup, hi, lo);
+                ph[p] = hi;
+                pl[p] = lo;
+            }
+            l_part[rt] = l_part[rt] * alpha + psum;
+            const float oscale = alpha * evshift;
+#pragma unroll
+            for (int t = 0; t < 8; t++) o[rt][t] *= oscale;
+            // -- O^T += V^T P^T (tile t: head-dim columns 8m + t)
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                f16x8 va;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    f16x2 pr = nib_pair(vw[2 * j], vw[2 * j + 1], t);
+                    va[2 * j] = pr[0];
+                    va[2 * j + 1] = pr[1];
+                }
+                o[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, o[rt][t], 0, 0, 0);
+                o[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, o[rt][t], 0, 0, 0);
+            }
+        }
+    }
+
+    // ---- per wave: true-unit O, row max and sum -> LDS
+    const float oun = ldexpf(1.0f, -ev_cur);
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        float l = l_part[rt];
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
+        const int row = 16 * rt + n;
+        if (g == 0) {
+            s_m[wave][row] = m_run[rt];
+            s_l[wave][row] = l;
+        }
+        // lane holds O^T[m = 4g + i][row] for tile t: head-dim 8m + t
+#pragma unroll
+        for (int t = 0; t < 8; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int d = 8 * (4 * g + i) + t;
+                if (d < D) s_o[wave][row][d] = o[rt][t][i] * oun;
+            }
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < ROWS * D; e += 64 * kWaves) {
+        const int row = e / D, d = e % D;
+        const int r = row0 + row;
+        if (r >= R) continue;
+        float M = -__builtin_inff();
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) M = fmaxf(M, s_m[w][row]);
+        float L = 0.0f, acc = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) {
+            const float wgt = s_m[w][row] == -__builtin_inff() ? 0.0f : __expf(s_m[w][row] - M);
+            L += s_l[w][row] * wgt;
+            acc += s_o[w][row][d] * wgt;
+        }
+        const int h = h0 + r / a.Nq, q = r % a.Nq;
+        const size_t orow = (size_t)q * a.H + h;
+        if (a.splits == 1) {
+            a.O[orow * D + d] = L > 0.0f ? acc / L : 0.0f;
+        } else {
+            const size_t nrow = (size_t)a.Nq * a.H;
+            a.part_o[((size_t)split * nrow + orow) * D + d] = acc;
+            if (d == 0) {
+                a.part_ml[((size_t)split * nrow + orow) * 2] = M;
+                a.part_ml[((size_t)split * nrow + orow) * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+// Merge the splits: one block per output row, one thread per head-dim value.
+// The (max, sum) pairs go through LDS; the partial rows are read eight
+// splits at a time with independent loads.
+__global__ void k_attn_dec_combine(const float* __restrict__ part_o,
+                                   const float* __restrict__ part_ml, int splits, int nrow,
+                                   int D, float* __restrict__ O) {
+    const int row = blockIdx.x, d = threadIdx.x;
+    __shared__ float s_m[128], s_w[128];
+    __shared__ float s_M, s_L;
+    for (int s = d; s < splits; s += blockDim.x) s_m[s] = part_ml[((size_t)s * nrow + row) * 2];
+    __syncthreads();
+    if (d == 0) {
+        float M = -__builtin_inff();
+        for (int s = 0; s < splits; s++) M = fmaxf(M, s_m[s]);
+        s_M = M;
+    }
+    __syncthreads();
+    const float M = s_M;
+    for (int s = d; s < splits; s += blockDim.x)
+        s_w[s] = s_m[s] == -__builtin_inff() ? 0.0f : __expf(s_m[s] - M);
+    __syncthreads();
+    if (d == 0) {
+        float L = 0.0f;
+        for (int s = 0; s < splits; s++) L += part_ml[((size_t)s * nrow + row) * 2 + 1] * s_w[s];
+        s_L = L;
+    }
+    float acc = 0.0f;
+    int s = 0;
+    for (; s + 8 <= splits; s += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = part_o[((size_t)(s + j) * nrow + row) * D + d];
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc += v[j] * s_w[s + j];
+    }
+    for (; s < splits; s++) acc += part_o[((size_t)s * nrow + row) * D + d] * s_w[s];
+    __syncthreads();
+    O[(size_t)row * D + d] = s_L > 0.0f ? acc / s_L : 0.0f;
+}
+
+template <int D, int RT>
+int launch(const DecArgs& a, dim3 grid) {
+    hipLaunchKernelGGL((k_attn_dec<D, RT>), grid, dim3(64 * kWaves), 0, stream(), a);
+    return launch_check("k_attn_dec");
+}
+
+}  // namespace
+
+// 1 when the decode kernel takes this attention (INT4 cache, one scale group
+// per head row, head_dim 32/64/128, chain / tree / no mask, batch 1).
+extern "C" int cgk_attn_dec_supported(int D, int gs, int B, int mask_kind) {
+    return (D == 32 || D == 64 || D == 128) && gs == D && B == 1 &&
+           (mask_kind == kMaskNone || mask_kind == kMaskCausal || mask_kind == kMaskTree);
+}
+
+extern "C" int cgk_attn_dec(const float* Q, const uint8_t* kc, const uint8_t* vc, const float* ks,
+                            const float* vs, int Nq, int Nk, int H, int Hk, int D, float scale,
+                            int mask_kind, const unsigned long long* anc, float* O) {
+    if (Nq <= 0 || Nk <= 0 || Hk <= 0 || H % Hk || Nq > Nk ||
+        (mask_kind == kMaskTree && (Nq > 64 || !anc)) || (D != 32 && D != 64 && D != 128)) {
+        cgx_set_error("attn_dec: unsupported shape Nq=%d Nk=%d H=%d Hk=%d D=%d", Nq, Nk, H, Hk, D);
+        return -1;
+    }
+    if (((uintptr_t)Q & 15) || ((uintptr_t)kc & 15)) {
+        cgx_set_error("attn_dec: Q and the K cache must be 16-byte aligned");
+        return -1;
+    }
+    DecArgs a;
+    a.Q = Q; a.kc = kc; a.vc = vc; a.ks = ks; a.vs = vs;
+    a.Nq = Nq; a.Nk = Nk; a.H = H; a.Hk = Hk;
+    a.scale = scale;
+    a.mask_kind = mask_kind;
+    for (int i = 0; i < 64; i++) a.anc[i] = (mask_kind == kMaskTree && i < Nq) ? anc[i] : 0ull;
+    const int R = (H / Hk) * Nq;
+    const int RT = R <= 16 ? 1 : 2;
+    const int chunks = (R + 16 * RT - 1) / (16 * RT);
+    // one block round (256 keys) per split, at most 128 splits
+    int kps = kSplitKeys;
+    while ((Nk + kps - 1) / kps > 128) kps += kSplitKeys;
+    const int splits = (Nk + kps - 1) / kps;
+    a.splits = splits;
+    a.keys_per_split = kps;
+    a.O = O;
+    const int nrow = Nq * H;
+    if (splits > 1) {
+        a.part_o = (float*)cgx_scratch(CGX_SLOT_WS2, (size_t)splits * nrow * D * 4);
+        a.part_ml = (float*)cgx_scratch(CGX_SLOT_WS3, (size_t)splits * nrow * 2 * 4);
+        if (!a.part_o || !a.part_ml) return -1;
+    } else {
+        a.part_o = a.part_ml = nullptr;
+    }
+    dim3 grid(splits, Hk, chunks);
+    int rc;
+    if (D == 128) rc = RT == 1 ? launch<128, 1>(a, grid) : launch<128, 2>(a, grid);
+    else if (D == 64) rc = RT == 1 ? launch<64, 1>(a, grid) : launch<64, 2>(a, grid);
+    else rc = RT == 1 ? launch<32, 1>(a, grid) : launch<32, 2>(a, grid);
+    if (rc) return rc;
+    if (splits > 1) {
+        if (splits > 128) {
+            cgx_set_error("attn_dec: too many splits");
+            return -1;
+        }
+        hipLaunchKernelGGL(k_attn_dec_combine, dim3(nrow), dim3(D), 0, stream(), a.part_o,
+                           a.part_ml, splits, nrow, D, O);
+        if (launch_check("k_attn_dec_combine")) return -1;
+    }
+    return 0;
+}

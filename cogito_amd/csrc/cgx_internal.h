@@ -32,10 +32,11 @@ unsigned int* cgx_counters(size_t count);
 const void* cgx_dev_in(const void* p, size_t bytes, int slot);
 
 /* ------------------------------------------------ quantized-weight registry */
-enum { CGX_LAYOUT_HOST = 0, CGX_LAYOUT_FLAT = 1, CGX_LAYOUT_TILED = 2 };
+enum { CGX_LAYOUT_HOST = 0, CGX_LAYOUT_FLAT = 1, CGX_LAYOUT_TILED = 2, CGX_LAYOUT_MFMA = 3 };
 typedef struct {
     int layout;
     int K, N, group_size;
+    int paired;          /* layout 3: gate|up tiles interleaved (SwiGLU) */
 } cgx_qinfo;
 int cgx_quant_lookup(const cg_tensor_quant* q, cgx_qinfo* info);
 void cgx_quant_register(const cg_tensor_quant* q, const cgx_qinfo* info);
@@ -58,6 +59,19 @@ int cgk_int4_gemv_tiled(const float* x, int M, int K, int N, int gs,
 int cgk_int4_gemv_fused(const float* x, int ldx, int M, int K, int N, int gs,
                         const uint8_t* tiled, const float* scales_t, float* y, int pro,
                         const float* norm_w, float eps, int accumulate);
+int cgk_int4_transpose_scales(const float* scales, int K, int G, float* scales_t);
+/* MFMA GEMV (gemv.hip), weight layout 3: fp16 matrix cores, exact nibble
+ * operands, activations x * scale as two fp16 terms.  pro 0 none / 1
+ * RMSNorm; epi 0 store, 1 accumulate, 2 SwiGLU of a paired gate|up weight
+ * (y [M][N/2]).  M any (launches of 16 rows, 8 for SwiGLU). */
+int cgk_int4_repack_mfma(const uint8_t* flat, const float* scales, int K, int N, int gs,
+                         int paired, uint8_t* w, float* scales_t);
+int cgk_int4_dequantize_mfma(const uint8_t* w, const float* scales_t, int K, int N, int gs,
+                             int paired, float* out);
+int cgk_gemv_mfma(const float* x, int ldx, int M, int K, int N, int gs, const uint8_t* w,
+                  const float* scales_t, float* y, int ldy, int pro, const float* nw, float eps,
+                  int epi);
+int cgk_gemv_mfma_tiles(int N, int gs, int paired);
 int cgk_int4_matmul_generic(const float* x, int M, int K, int N, int gs,
                             const uint8_t* flat, const float* scales, float* y);
 
@@ -107,6 +121,12 @@ int cgk_attention(const float* Q, int int4, const uint8_t* kc, const uint8_t* vc
                   int B, int Nq, int Nk, int H, int Hk, int D, float scale, int mask_kind,
                   int window, const float* mask, const unsigned long long* anc, float* O,
                   float* lse);
+/* MFMA decode/verify attention over an INT4 cache slice with one scale per
+ * head row (attn_dec.hip); cgk_attention routes here when supported. */
+int cgk_attn_dec_supported(int D, int gs, int B, int mask_kind);
+int cgk_attn_dec(const float* Q, const uint8_t* kc, const uint8_t* vc, const float* ks,
+                 const float* vs, int Nq, int Nk, int H, int Hk, int D, float scale,
+                 int mask_kind, const unsigned long long* anc, float* O);
 int cgk_rope(float* x, int S, int H, int D, int pos0, float theta);
 int cgk_rope_freqs(float* cs, float* sn, int S, int D, float theta);
 int cgk_alibi_slopes(float* slopes, int H);

@@ -78,13 +78,23 @@ __global__ void k_rope_append(const float* __restrict__ qkv, int ld, int H, int 
     sv[i] = v[i];
     sv[i + half] = v[i + half];
     __syncthreads();
-    // quantise: thread i packs dims 2i, 2i+1 (same group: gs is even)
+    // quantise: thread i packs dims 2i, 2i+1 (same group: gs is even).  The
+    // group absmax (order-free) is a shuffle reduction over the gs/2 threads
+    // of the group when they are a power of two inside one wave, else a scan.
     const int ngh = D / gs, g = (2 * i) / gs;
-    float mk = 0.0f, mv = 0.0f;
-    for (int e = g * gs; e < (g + 1) * gs; e++) {
-        float ak = fabsf(sk[e]), av = fabsf(sv[e]);
-        if (ak > mk) mk = ak;
-        if (av > mv) mv = av;
+    float mk = fmaxf(fabsf(sk[2 * i]), fabsf(sk[2 * i + 1]));
+    float mv = fmaxf(fabsf(sv[2 * i]), fabsf(sv[2 * i + 1]));
+    const int gt = gs / 2;
+    if ((gt & (gt - 1)) == 0 && gt <= 64) {
+        for (int o = 1; o < gt; o <<= 1) {
+            mk = fmaxf(mk, __shfl_xor(mk, o));
+            mv = fmaxf(mv, __shfl_xor(mv, o));
+        }
+    } else {
+        for (int e = g * gs; e < (g + 1) * gs; e++) {
+            mk = fmaxf(mk, fabsf(sk[e]));
+            mv = fmaxf(mv, fabsf(sv[e]));
+        }
     }
     float sck = __fdiv_rn(mk, 7.0f), scv = __fdiv_rn(mv, 7.0f);
     if (sck < 1e-8f) sck = 1.0f;

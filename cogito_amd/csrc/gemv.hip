@@ -1,0 +1,529 @@
+// gemv.hip -- INT4 dequant GEMV / skinny GEMM on the gfx950 matrix cores.
+//
+// y[M,N] = x[M,K] @ W, W[K,N] INT4 with one scale per (row k, group of gs
+// columns) -- cogito's flat-index groups (src/quantize/int4.c:90-114: element
+// (k, j) uses scales[(k*N + j) / gs]; N % gs == 0 here, so the group of
+// column j in row k is k*(N/gs) + j/gs).  M <= 16 rows per launch.
+//
+// Arithmetic.  The scale varies along the reduction index k, so it is folded
+// into the activation: a[m][k] = x[m][k] * s[k][g].  The nibble side is exact
+// in fp16 (integers -8..7); the activation side is carried as hi + lo, two
+// fp16 numbers with 22 significant bits (relative error <= 2^-22 per
+// element), after scaling by a power of two 2^E chosen per (wave, round) so
+// that |a * 2^E| < 2^15.  v_mfma_f32_16x16x32_f16 forms the exact products and
+// accumulates in fp32; the 2^-E is undone in fp32 at the end of each round.
+//
+// Layout 3 (HBM).  Column tiles of 16 columns; a tile is K/128 chunks of 1
+// KiB; in chunk c, lane l (0..63) owns bytes 16l..16l+15: u32 word j (0..3)
+// holds rows 32(4c+j) + 8(l/16) + p, p = 0..7, of column 16*tile + l%16, the
+// row of position p in nibble slot {0,4,1,5,2,6,3,7}[p], offset-binary
+// (v + 8).  So one dwordx4 per lane reads four MFMA B operands of a tile and
+// a wave reads 1 KiB contiguous.  Optional pairing (SwiGLU): layout tile 2t is
+// column tile t (gate), 2t+1 is column tile ff/16 + t (up).  Scales: fp32
+// [N/gs][K] (transposed), shared with layout 2.
+//
+// Block = 8 waves, T column tiles (T*16 columns), the full K: waves take
+// rounds of 256 rows round-robin, each wave its own accumulators; the waves
+// are summed in a fixed order at the end (deterministic, no atomics).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "cgx_internal.h"
+
+namespace {
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 8;
+constexpr int kRoundK = 256;            // rows per wave round
+constexpr int kChunkK = 128;            // rows per 1 KiB chunk
+constexpr int kChunkBytes = 1024;
+// A-operand rows in LDS: 256 halfs + 16 bytes of padding, so the 16 rows a
+// ds_read_b128 touches start in different bank quads
+constexpr int kRowH = kRoundK + 8;
+
+inline hipStream_t stream() { return (hipStream_t)cgx_stream(); }
+
+int launch_check(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        cgx_set_error("%s launch failed: %s", what, hipGetErrorString(e));
+        return -1;
+    }
+    return 0;
+}
+
+enum { kProNone = 0, kProRmsNorm = 1 };
+enum { kEpiStore = 0, kEpiAccumulate = 1, kEpiSwiGlu = 2 };
+
+struct MfmaArgs {
+    const float* x;          // [M][ldx]
+    int ldx, M, K, N, gs;
+    const uint8_t* w;        // layout 3
+    const float* scales_t;   // [N/gs][K]
+    float* y;                // [M][ldy]
+    int ldy;
+    const float* nw;         // RMSNorm weights [K]
+    float eps;
+    int ff;                  // SwiGLU: columns of the gate half (N / 2)
+};
+
+// Logical column tile of layout tile L.
+__device__ __forceinline__ int logical_tile(int L, int paired, int ff_tiles) {
+    return paired ? ((L & 1) ? ff_tiles + (L >> 1) : (L >> 1)) : L;
+}
+
+// Four MFMA B operands (one per k-block of a chunk) from the lane's 16 bytes.
+__device__ __forceinline__ f16x8 nib_to_f16(uint32_t w) {
+    const uint32_t lo = w & 0x000F000Fu, hi4 = w & 0x00F000F0u;
+    const uint32_t w8 = w >> 8;
+    const uint32_t lo8 = w8 & 0x000F000Fu, hi8 = w8 & 0x00F000F0u;
+    const f16x2 m1032 = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const f16x2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const f16x2 m72 = {(_Float16)-72.0f, (_Float16)-72.0f};
+    f16x2 p0 = __builtin_bit_cast(f16x2, lo | 0x64006400u) + m1032;
+    f16x2 p1 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, hi4 | 0x64006400u), s16, m72);
+    f16x2 p2 = __builtin_bit_cast(f16x2, lo8 | 0x64006400u) + m1032;
+    f16x2 p3 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, hi8 | 0x64006400u), s16, m72);
+    f16x8 r;
+    r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+    r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+    return r;
+}
+
+// Maximum over the wave of non-negative values (DPP within rows of 16, row
+// broadcasts, then lane 63); every lane gets the result.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+#define CGX_DPP_MAX(CTRL, RMASK)                                                           \
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL,    \
+                                                            RMASK, 0xF, true)))
+    CGX_DPP_MAX(0x111, 0xF);      // row_shr:1
+    CGX_DPP_MAX(0x112, 0xF);      // row_shr:2
+    CGX_DPP_MAX(0x114, 0xF);      // row_shr:4
+    CGX_DPP_MAX(0x118, 0xF);      // row_shr:8   -> lane 15 of each row: row max
+    CGX_DPP_MAX(0x142, 0xA);      // row_bcast:15 into rows 1 and 3
+    CGX_DPP_MAX(0x143, 0xC);      // row_bcast:31 into rows 2 and 3
+#undef CGX_DPP_MAX
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// MP: rows padded (4, 8 or 16); T: column tiles per block; NG: scale groups
+// per block (1, or 2 for a gate|up pair).
+template <int MP, int T, int NG, int PRO, int EPI>
+__global__ __launch_bounds__(64 * kWaves) void k_gemv_mfma(MfmaArgs a) {
+    // per wave: A operands of one round, [NG][hi|lo][MP][256] halfs
+    constexpr int kAHalfs = NG * 2 * MP * kRowH;
+    constexpr int kRedFloats = kWaves * T * MP * 16;
+    constexpr int kLdsFloats =
+        (kWaves * kAHalfs / 2) > kRedFloats ? (kWaves * kAHalfs / 2) : kRedFloats;
+    __shared__ float lds[kLdsFloats];
+    __shared__ float s_ssq[kWaves][MP];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int M = a.M;
+    const int paired = EPI == kEpiSwiGlu;
+    const int ff_tiles = a.ff / 16;
+    // XCD-aware order: consecutive blocks share scale rows; give each XCD a
+    // contiguous run (block b runs on XCD b % 8).
+    const int nblk = gridDim.x;
+    const int per_xcd = nblk / 8;
+    const int sb = (int)blockIdx.x < per_xcd * 8
+                       ? (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8)
+                       : (int)blockIdx.x;
+    const int L0 = sb * T;                         // first layout tile
+
+    // scale rows of the block's groups; tile j uses group slot tq[j]
+    int grp[NG];
+    int tq[T];
+#pragma unroll
+    for (int j = 0; j < T; j++) {
+        int lt = logical_tile(L0 + j, paired, ff_tiles);
+        int g = lt * 16 / a.gs;
+        if (NG == 1) {
+            grp[0] = g;
+            tq[j] = 0;
+        } else {
+            // pairs alternate gate / up: slot 0 gate, slot 1 up
+            tq[j] = (L0 + j) & 1;
+            grp[tq[j]] = g;
+        }
+    }
+
+    const int K = a.K;
+    const int rounds = K / kRoundK;
+    const int nchunks = K / kChunkK;
+    const int my_rounds = (rounds - wave + kWaves - 1) / kWaves;   // may be 0
+
+    _Float16* abuf = (_Float16*)lds + (size_t)wave * kAHalfs;
+    const int mrow = (lane & 15) < M ? (lane & 15) : M - 1;    // A row this lane feeds
+    const int g4 = lane >> 4;
+
+    f32x4 tot[T];
+#pragma unroll
+    for (int j = 0; j < T; j++) tot[j] = (f32x4)(0.0f);
+    float ssq[MP];
+#pragma unroll
+    for (int m = 0; m < MP; m++) ssq[m] = 0.0f;
+
+    // weights of one round: T tiles x 2 chunks x 16 bytes per lane
+    u32x4 wcur[T][2], wnxt[T][2];
+    auto load_w = [&](int r, u32x4 (&dst)[T][2]) {
+#pragma unroll
+        for (int j = 0; j < T; j++)
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                size_t off = ((size_t)(L0 + j) * nchunks + 2 * r + c) * kChunkBytes + 16 * lane;
+                dst[j][c] = __builtin_nontemporal_load((const u32x4*)(a.w + off));
+            }
+    };
+    // activations / scales / norm weights of one round (lane -> rows k0..k0+3),
+    // fetched one round ahead like the weights
+    struct ARaw {
+        float4 x[MP];
+        float4 s[NG];
+        float4 nw;
+    };
+    auto load_a = [&](int r, ARaw& d) {
+        const int k0 = r * kRoundK + 4 * lane;
+#pragma unroll
+        for (int q = 0; q < NG; q++) d.s[q] = *(const float4*)(a.scales_t + (size_t)grp[q] * K + k0);
+        d.nw = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+        if (PRO == kProRmsNorm) d.nw = *(const float4*)(a.nw + k0);
+#pragma unroll
+        for (int m = 0; m < MP; m++)
+            d.x[m] = m < M ? *(const float4*)(a.x + (size_t)m * a.ldx + k0)
+                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    };
+    ARaw acur;
+    if (my_rounds > 0) load_w(wave, wcur);
+
+    for (int i = 0; i < my_rounds; i++) {
+        const int r = wave + i * kWaves;
+        if (i + 1 < my_rounds) load_w(r + kWaves, wnxt);
+        load_a(r, acur);
+
+        // ---- A operands of this round
+        float4 xv[MP];
+        float amax = 0.0f;
+#pragma unroll
+        for (int m = 0; m < MP; m++) {
+            float4 t = acur.x[m];
+            if (PRO == kProRmsNorm) {
+                ssq[m] = fmaf(t.x, t.x, ssq[m]);
+                ssq[m] = fmaf(t.y, t.y, ssq[m]);
+                ssq[m] = fmaf(t.z, t.z, ssq[m]);
+                ssq[m] = fmaf(t.w, t.w, ssq[m]);
+                t.x *= acur.nw.x; t.y *= acur.nw.y; t.z *= acur.nw.z; t.w *= acur.nw.w;
+            }
+            xv[m] = t;
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
+        }
+        float smax = 0.0f;
+#pragma unroll
+        for (int q = 0; q < NG; q++)
+            smax = fmaxf(smax, fmaxf(fmaxf(fabsf(acur.s[q].x), fabsf(acur.s[q].y)),
+                                     fmaxf(fabsf(acur.s[q].z), fabsf(acur.s[q].w))));
+        // |x * s| <= amax * smax over the round; scale so that it is < 2^15
+        float bound = wave_max_nonneg(amax) * wave_max_nonneg(smax);
+        int E = 0;
+        if (bound > 0.0f && bound < __builtin_inff()) E = 14 - ilogbf(bound);
+        E = E > 100 ? 100 : (E < -100 ? -100 : E);
+        const float up = ldexpf(1.0f, E);
+        const float down = ldexpf(1.0f, -E);
+#pragma unroll
+        for (int q = 0; q < NG; q++) {
+            const float s0 = acur.s[q].x * up, s1 = acur.s[q].y * up, s2 = acur.s[q].z * up,
+                        s3 = acur.s[q].w * up;
+#pragma unroll
+            for (int m = 0; m < MP; m++) {
+                if (m < M) {
+                    float v0 = xv[m].x * s0, v1 = xv[m].y * s1, v2 = xv[m].z * s2,
+                          v3 = xv[m].w * s3;
+                    _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1, h2 = (_Float16)v2,
+                             h3 = (_Float16)v3;
+                    _Float16 l0 = (_Float16)(v0 - (float)h0), l1 = (_Float16)(v1 - (float)h1),
+                             l2 = (_Float16)(v2 - (float)h2), l3 = (_Float16)(v3 - (float)h3);
+                    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+                    f16x4 hv = {h0, h1, h2, h3}, lv = {l0, l1, l2, l3};
+                    *(f16x4*)(abuf + ((q * 2 + 0) * MP + m) * kRowH + 4 * lane) = hv;
+                    *(f16x4*)(abuf + ((q * 2 + 1) * MP + m) * kRowH + 4 * lane) = lv;
+                }
+            }
+        }
+        // the A buffer is private to this wave: its own LDS writes must land
+        // before its lanes read each other's rows
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_s_waitcnt(0xc07f);    // lgkmcnt(0)
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        f32x4 acc[T];
+#pragma unroll
+        for (int j = 0; j < T; j++) acc[j] = (f32x4)(0.0f);
+#pragma unroll
+        for (int kb = 0; kb < 8; kb++) {
+            f16x8 ah[NG], al[NG];
+#pragma unroll
+            for (int q = 0; q < NG; q++) {
+                ah[q] = *(const f16x8*)(abuf + ((q * 2 + 0) * MP + mrow) * kRowH + 32 * kb + 8 * g4);
+                al[q] = *(const f16x8*)(abuf + ((q * 2 + 1) * MP + mrow) * kRowH + 32 * kb + 8 * g4);
+            }
+#pragma unroll
+            for (int j = 0; j < T; j++) {
+                const u32x4 wv = wcur[j][kb >> 2];
+                const uint32_t word = (kb & 3) == 0 ? wv.x : (kb & 3) == 1 ? wv.y
+                                    : (kb & 3) == 2 ? wv.z : wv.w;
+                f16x8 b = nib_to_f16(word);
+                const int q = NG == 1 ? 0 : tq[j];
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], b, acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], b, acc[j], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < T; j++) {
+            tot[j][0] = fmaf(acc[j][0], down, tot[j][0]);
+            tot[j][1] = fmaf(acc[j][1], down, tot[j][1]);
+            tot[j][2] = fmaf(acc[j][2], down, tot[j][2]);
+            tot[j][3] = fmaf(acc[j][3], down, tot[j][3]);
+        }
+        if (i + 1 < my_rounds) {
+#pragma unroll
+            for (int j = 0; j < T; j++) {
+                wcur[j][0] = wnxt[j][0];
+                wcur[j][1] = wnxt[j][1];
+            }
+        }
+        // the next round overwrites this wave's A buffer
+        __builtin_amdgcn_wave_barrier();
+    }
+
+    if (PRO == kProRmsNorm) {
+#pragma unroll
+        for (int m = 0; m < MP; m++) {
+            float v = wave_sum(ssq[m]);
+            if (lane == 0) s_ssq[wave][m] = v;
+        }
+    }
+    __syncthreads();                 // every wave is done with its A buffer
+    // partials: red[wave][tile][row][col]; lane holds rows 4*g4 .. +3, col lane%16
+    float* red = lds;
+#pragma unroll
+    for (int j = 0; j < T; j++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            int row = 4 * g4 + v;
+            if (row < MP) red[((wave * T + j) * MP + row) * 16 + (lane & 15)] = tot[j][v];
+        }
+    __syncthreads();
+    constexpr int kOuts = T * MP * 16;
+    for (int o = threadIdx.x; o < kOuts; o += 64 * kWaves) {
+        const int j = o / (MP * 16), row = (o / 16) % MP, col = o % 16;
+        if (row >= M) continue;
+        if (EPI == kEpiSwiGlu && (j & 1)) continue;     // the gate thread does the pair
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) v += red[((w * T + j) * MP + row) * 16 + col];
+        float rs = 1.0f;
+        if (PRO == kProRmsNorm) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kWaves; w++) ss += s_ssq[w][row];
+            rs = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+            v *= rs;
+        }
+        const int lt = logical_tile(L0 + j, paired, ff_tiles);
+        if (EPI == kEpiSwiGlu) {
+            float u = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kWaves; w++) u += red[((w * T + j + 1) * MP + row) * 16 + col];
+            u *= rs;
+            float act = v / (1.0f + __expf(-v)) * u;
+            a.y[(size_t)row * a.ldy + lt * 16 + col] = act;
+        } else {
+            float* yp = a.y + (size_t)row * a.ldy + lt * 16 + col;
+            *yp = EPI == kEpiAccumulate ? *yp + v : v;
+        }
+    }
+}
+
+// Repack cogito's row-major nibbles (two's complement, flat) into layout 3.
+// One thread per output u32 word.
+__global__ void k_repack_mfma(const uint8_t* __restrict__ flat, int K, int N, int paired,
+                              uint32_t* __restrict__ out) {
+    size_t wi = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t words = (size_t)K * N / 8;
+    if (wi >= words) return;
+    // word wi: layout tile L, chunk c, lane l, word j
+    const int nchunks = K / kChunkK;
+    size_t t = wi;
+    const int j = (int)(t % 4); t /= 4;
+    const int l = (int)(t % 64); t /= 64;
+    const int c = (int)(t % nchunks); t /= nchunks;
+    const int L = (int)t;
+    const int lt = logical_tile(L, paired, N / 32);
+    const int col = lt * 16 + (l & 15);
+    const int kbase = 32 * (4 * c + j) + 8 * (l >> 4);
+    uint32_t word = 0;
+#pragma unroll
+    for (int p = 0; p < 8; p++) {
+        size_t idx = (size_t)(kbase + p) * N + col;
+        unsigned byte = flat[idx >> 1];
+        unsigned nib = (idx & 1) ? (byte >> 4) : (byte & 0xF);
+        nib ^= 0x8u;                          // two's complement -> offset binary
+        word |= nib << (4 * ((p >> 1) + 4 * (p & 1)));    // slot {0,4,1,5,2,6,3,7}[p]
+    }
+    out[wi] = word;
+}
+
+// Layout 3 -> fp32 W[K,N] (row-major), for cg_dequantize of a device weight.
+__global__ void k_dequant_mfma(const uint32_t* __restrict__ w, const float* __restrict__ scales_t,
+                               int K, int N, int gs, int paired, float* __restrict__ out) {
+    size_t wi = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t words = (size_t)K * N / 8;
+    if (wi >= words) return;
+    const int nchunks = K / kChunkK;
+    size_t t = wi;
+    const int j = (int)(t % 4); t /= 4;
+    const int l = (int)(t % 64); t /= 64;
+    const int c = (int)(t % nchunks); t /= nchunks;
+    const int L = (int)t;
+    const int lt = logical_tile(L, paired, N / 32);
+    const int col = lt * 16 + (l & 15);
+    const int kbase = 32 * (4 * c + j) + 8 * (l >> 4);
+    const uint32_t word = w[wi];
+#pragma unroll
+    for (int p = 0; p < 8; p++) {
+        int k = kbase + p;
+        unsigned nib = (word >> (4 * ((p >> 1) + 4 * (p & 1)))) & 0xFu;
+        float s = scales_t[(size_t)(col / gs) * K + k];
+        out[(size_t)k * N + col] = (float)((int)nib - 8) * s;
+    }
+}
+
+template <int MP, int T, int NG, int PRO, int EPI>
+int launch_t(const MfmaArgs& a, int nblocks) {
+    hipLaunchKernelGGL((k_gemv_mfma<MP, T, NG, PRO, EPI>), dim3(nblocks), dim3(64 * kWaves), 0,
+                       stream(), a);
+    return launch_check("k_gemv_mfma");
+}
+
+template <int MP, int PRO, int EPI>
+int launch_mp(const MfmaArgs& a, int T) {
+    const int tiles = a.N / 16;
+    if constexpr (EPI == kEpiSwiGlu) {
+        if (T == 4) return launch_t<MP, 4, 2, PRO, EPI>(a, tiles / 4);
+        return launch_t<MP, 2, 2, PRO, EPI>(a, tiles / 2);
+    } else {
+        if (T == 4) return launch_t<MP, 4, 1, PRO, EPI>(a, tiles / 4);
+        if (T == 2) return launch_t<MP, 2, 1, PRO, EPI>(a, tiles / 2);
+        return launch_t<MP, 1, 1, PRO, EPI>(a, tiles);
+    }
+}
+
+template <int PRO, int EPI>
+int launch_pe(const MfmaArgs& a, int T) {
+    if (a.M == 1) return launch_mp<1, PRO, EPI>(a, T);
+    if (a.M == 2) return launch_mp<2, PRO, EPI>(a, T);
+    if (a.M <= 4) return launch_mp<4, PRO, EPI>(a, T);
+    if constexpr (EPI == kEpiSwiGlu) {
+        return launch_mp<8, PRO, EPI>(a, T);
+    } else {
+        if (a.M <= 8) return launch_mp<8, PRO, EPI>(a, T);
+        return launch_mp<16, PRO, EPI>(a, T);
+    }
+}
+
+}  // namespace
+
+// Column tiles per block: as many as keep >= 256 blocks (one per CU), within
+// one scale group (or one gate|up pair group each).
+extern "C" int cgk_gemv_mfma_tiles(int N, int gs, int paired) {
+    const int tiles = N / 16;
+    if (paired) {
+        const int ff = N / 2;
+        // gate tiles of a block share a group, and so do the up tiles
+        if (tiles / 4 >= 256 && gs % 32 == 0 && ff % 32 == 0) return 4;
+        return 2;
+    }
+    if (tiles / 4 >= 256 && gs % 64 == 0) return 4;
+    if (tiles / 2 >= 256 && gs % 32 == 0) return 2;
+    return 1;
+}
+
+extern "C" int cgk_int4_repack_mfma(const uint8_t* flat, const float* scales, int K, int N,
+                                    int gs, int paired, uint8_t* w, float* scales_t) {
+    if (K % kRoundK || N % 16 || gs % 16 || N % gs || (paired && (N % 32))) {
+        cgx_set_error("repack_mfma: unsupported shape K=%d N=%d gs=%d", K, N, gs);
+        return -1;
+    }
+    size_t words = (size_t)K * N / 8;
+    hipLaunchKernelGGL(k_repack_mfma, dim3((unsigned)((words + 255) / 256)), dim3(256), 0,
+                       stream(), flat, K, N, paired, (uint32_t*)w);
+    if (launch_check("k_repack_mfma")) return -1;
+    return cgk_int4_transpose_scales(scales, K, N / gs, scales_t);
+}
+
+extern "C" int cgk_int4_dequantize_mfma(const uint8_t* w, const float* scales_t, int K, int N,
+                                        int gs, int paired, float* out) {
+    size_t words = (size_t)K * N / 8;
+    hipLaunchKernelGGL(k_dequant_mfma, dim3((unsigned)((words + 255) / 256)), dim3(256), 0,
+                       stream(), (const uint32_t*)w, scales_t, K, N, gs, paired, out);
+    return launch_check("k_dequant_mfma");
+}
+
+// y = x @ W (layout 3) for M <= 16 rows per launch (larger M in chunks of 16).
+// pro: 0 none, 1 RMSNorm of the rows (weights nw, eps); epi: 0 store,
+// 1 accumulate (y += ...), 2 SwiGLU of a paired gate|up weight (y [M][N/2]).
+extern "C" int cgk_gemv_mfma(const float* x, int ldx, int M, int K, int N, int gs,
+                             const uint8_t* w, const float* scales_t, float* y, int ldy,
+                             int pro, const float* nw, float eps, int epi) {
+    const int paired = epi == kEpiSwiGlu;
+    if (M < 1 || K % kRoundK || N % 16 || gs % 16 || N % gs || ldx < K ||
+        (paired && N % 32) || (pro == kProRmsNorm && !nw) || pro < 0 || pro > 1 || epi < 0 ||
+        epi > 2 || ldy < (paired ? N / 2 : N)) {
+        cgx_set_error("gemv_mfma: unsupported shape M=%d K=%d N=%d gs=%d", M, K, N, gs);
+        return -1;
+    }
+    if (((uintptr_t)x & 15) || (ldx & 3) || (nw && ((uintptr_t)nw & 15))) {
+        cgx_set_error("gemv_mfma: x / norm weights must be 16-byte aligned with ldx %% 4 == 0");
+        return -1;
+    }
+    const int T = cgk_gemv_mfma_tiles(N, gs, paired);
+    // rows per launch: 16 (8 for the SwiGLU pair, whose A buffers are twice
+    // as large); each launch streams W once
+    const int mstep = paired ? 8 : 16;
+    for (int m0 = 0; m0 < M; m0 += mstep) {
+        MfmaArgs a;
+        a.x = x + (size_t)m0 * ldx;
+        a.ldx = ldx;
+        a.M = M - m0 < mstep ? M - m0 : mstep;
+        a.K = K; a.N = N; a.gs = gs;
+        a.w = w; a.scales_t = scales_t;
+        a.y = y + (size_t)m0 * ldy;
+        a.ldy = ldy;
+        a.nw = nw; a.eps = eps;
+        a.ff = N / 2;
+        int rc;
+        if (pro == kProRmsNorm) {
+            rc = epi == kEpiSwiGlu ? launch_pe<kProRmsNorm, kEpiSwiGlu>(a, T)
+               : epi == kEpiAccumulate ? launch_pe<kProRmsNorm, kEpiAccumulate>(a, T)
+               : launch_pe<kProRmsNorm, kEpiStore>(a, T);
+        } else {
+            rc = epi == kEpiSwiGlu ? launch_pe<kProNone, kEpiSwiGlu>(a, T)
+               : epi == kEpiAccumulate ? launch_pe<kProNone, kEpiAccumulate>(a, T)
+               : launch_pe<kProNone, kEpiStore>(a, T);
+        }
+        if (rc) return rc;
+    }
+    return 0;
+}

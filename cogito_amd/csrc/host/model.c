@@ -2,9 +2,11 @@
  * model.c -- the synthetic decoder stack of the verify path (INT4 weights
  * and KV cache in HBM).  Layer order and layouts follow the reference
  * (src/layers/transformer.c:26-149, src/layers/linear.c:53-98); every
- * linear layer is one INT4 GEMV launch with the RMSNorm / SwiGLU / residual
- * work fused around it (int4.hip), attention reads the INT4 cache directly
- * (attn.hip).  Per layer: 4 GEMVs, RoPE + KV append, attention (+ split
+ * linear layer is one MFMA GEMV launch with the RMSNorm / SwiGLU / residual
+ * work fused around it (gemv.hip: RMSNorm folded into the activation side,
+ * SwiGLU computed in the epilogue of the gate|up product, whose gate and up
+ * column tiles are interleaved), attention reads the INT4 cache directly
+ * (attn_dec.hip).  Per layer: 4 GEMVs, RoPE + KV append, attention (+ split
  * combine).
  */
 #include <math.h>
@@ -19,7 +21,8 @@ int cgk_rope_append(const float* qkv, int ld, int M, int H, int Hk, int D, int g
                     float theta, float* q_out, uint8_t* kc, uint8_t* vc, float* ks, float* vs);
 int cgk_fill_normal(float* out, size_t n, uint64_t seed, uint32_t stream_id, float stddev);
 
-enum { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_SWIGLU = 2 };
+enum { PRO_NONE = 0, PRO_RMSNORM = 1 };
+enum { EPI_STORE = 0, EPI_ACCUMULATE = 1, EPI_SWIGLU = 2 };
 enum { W_QKV = 0, W_O = 1, W_GU = 2, W_DOWN = 3, W_LM = 4 };
 
 typedef struct {
@@ -80,7 +83,8 @@ static int make_lin(cgx_model* m, lin_t* L, int which, int layer, float* tf, uin
     L->scales_t = (float*)cgx_malloc(n / m->c.group_size * 4);
     if (!L->tiled || !L->scales_t) return -1;
     if (gen_flat(m, L->sid, L->K, L->N, tf, tq, ts)) return -1;
-    return cgk_int4_repack_tiled(tq, ts, L->K, L->N, m->c.group_size, L->tiled, L->scales_t);
+    return cgk_int4_repack_mfma(tq, ts, L->K, L->N, m->c.group_size, which == W_GU, L->tiled,
+                                L->scales_t);
 }
 
 static void free_lin(lin_t* L) {
@@ -192,7 +196,7 @@ cgx_model* cgx_model_new(const cgx_model_config* cfg, uint64_t seed, cgx_model* 
         m->qkv = (float*)cgx_malloc((size_t)Mx * nqkv(c) * 4);
         m->q = (float*)cgx_malloc((size_t)Mx * c->n_heads * c->head_dim * 4);
         m->attn = (float*)cgx_malloc((size_t)Mx * c->n_heads * c->head_dim * 4);
-        m->gu = (float*)cgx_malloc((size_t)Mx * 2 * c->d_ff * 4);
+        m->gu = (float*)cgx_malloc((size_t)Mx * c->d_ff * 4);      /* SwiGLU output */
         m->logits = (float*)cgx_malloc((size_t)Mx * V * 4);
         ok = m->kv && m->tok && m->x && m->qkv && m->q && m->attn && m->gu && m->logits;
     }
@@ -264,25 +268,25 @@ int cgx_model_forward(cgx_model* m, const int* tokens, int M, int n_logits, floa
         uint8_t* vc = kv->v_cache + lb * l;
         float* ks = kv->k_scales + lg * l;
         float* vs = kv->v_scales + lg * l;
-        if (cgk_int4_gemv_fused(m->x, d, M, d, nq, gs, w[W_QKV].tiled, w[W_QKV].scales_t,
-                                m->qkv, PRO_RMSNORM, m->ones, eps, 0) ||
+        if (cgk_gemv_mfma(m->x, d, M, d, nq, gs, w[W_QKV].tiled, w[W_QKV].scales_t, m->qkv, nq,
+                          PRO_RMSNORM, m->ones, eps, EPI_STORE) ||
             cgk_rope_append(m->qkv, nq, M, H, Hk, hd, kv->group_size, pos0, c->rope_theta,
                             m->q, kc, vc, ks, vs) ||
             cgk_attention(m->q, 1, kc, vc, ks, vs, kv->group_size, NULL, NULL, 1, M, pos0 + M,
                           H, Hk, hd, scale, CGK_MASK_CAUSAL_ALIGNED, 0, NULL, NULL, m->attn,
                           NULL) ||
-            cgk_int4_gemv_fused(m->attn, hq, M, hq, d, gs, w[W_O].tiled, w[W_O].scales_t, m->x,
-                                PRO_NONE, NULL, 0.0f, 1) ||
-            cgk_int4_gemv_fused(m->x, d, M, d, 2 * ff, gs, w[W_GU].tiled, w[W_GU].scales_t,
-                                m->gu, PRO_RMSNORM, m->ones, eps, 0) ||
-            cgk_int4_gemv_fused(m->gu, 2 * ff, M, ff, d, gs, w[W_DOWN].tiled,
-                                w[W_DOWN].scales_t, m->x, PRO_SWIGLU, NULL, 0.0f, 1))
+            cgk_gemv_mfma(m->attn, hq, M, hq, d, gs, w[W_O].tiled, w[W_O].scales_t, m->x, d,
+                          PRO_NONE, NULL, 0.0f, EPI_ACCUMULATE) ||
+            cgk_gemv_mfma(m->x, d, M, d, 2 * ff, gs, w[W_GU].tiled, w[W_GU].scales_t, m->gu, ff,
+                          PRO_RMSNORM, m->ones, eps, EPI_SWIGLU) ||
+            cgk_gemv_mfma(m->gu, ff, M, ff, d, gs, w[W_DOWN].tiled, w[W_DOWN].scales_t, m->x, d,
+                          PRO_NONE, NULL, 0.0f, EPI_ACCUMULATE))
             return -1;
     }
     if (n_logits > 0 &&
-        cgk_int4_gemv_fused(m->x + (size_t)(M - n_logits) * d, d, n_logits, d, c->vocab, gs,
-                            m->lm.tiled, m->lm.scales_t, logits ? logits : m->logits,
-                            PRO_RMSNORM, m->ones, eps, 0))
+        cgk_gemv_mfma(m->x + (size_t)(M - n_logits) * d, d, n_logits, d, c->vocab, gs,
+                      m->lm.tiled, m->lm.scales_t, logits ? logits : m->logits, c->vocab,
+                      PRO_RMSNORM, m->ones, eps, EPI_STORE))
         return -1;
     kv->current_len = pos0 + M;
     return 0;

@@ -95,7 +95,7 @@ static int quant_dims(const cg_tensor_quant* q, int* K, int* N) {
     return (*K) * (*N) == q->size ? 0 : -1;
 }
 
-static cg_tensor_quant* quant_to_device_layout(cg_tensor_quant* q, int want_tiled) {
+static cg_tensor_quant* quant_to_device_layout(cg_tensor_quant* q, int want) {
     if (!q || !q->data || !q->scales || q->size <= 0 || q->group_size <= 0) {
         cgx_set_error("cgx_quant_to_device: invalid quantized tensor");
         return NULL;
@@ -113,10 +113,11 @@ static cg_tensor_quant* quant_to_device_layout(cg_tensor_quant* q, int want_tile
     int gs = q->group_size;
     int ng = (q->size + gs - 1) / gs;
     size_t nb = ((size_t)q->size + 1) / 2;
-    /* tiled GEMV layout: 16-column strips of 256-row tiles, one scale group
-     * per strip row */
-    int tiled = want_tiled && q->ndim == 2 && K % 256 == 0 && N % 16 == 0 &&
-                gs % 16 == 0 && N % gs == 0;
+    /* tiled layouts (2: VALU GEMV strips, 3: MFMA GEMV tiles) need K % 256,
+     * N % 16, group % 16 and N % group; otherwise the reference layout */
+    int fits = q->ndim == 2 && K % 256 == 0 && N % 16 == 0 && gs % 16 == 0 && N % gs == 0;
+    int layout = (want != CGX_LAYOUT_FLAT && fits) ? want : CGX_LAYOUT_FLAT;
+    int tiled = layout != CGX_LAYOUT_FLAT;
 
     cg_tensor_quant* d = (cg_tensor_quant*)calloc(1, sizeof(cg_tensor_quant));
     if (!d) return NULL;
@@ -135,7 +136,10 @@ static cg_tensor_quant* quant_to_device_layout(cg_tensor_quant* q, int want_tile
         const uint8_t* fd = (const uint8_t*)cgx_dev_in(q->data, nb, CGX_SLOT_IN0);
         const float* fs = (const float*)cgx_dev_in(q->scales, (size_t)ng * 4, CGX_SLOT_IN1);
         if (!fd || !fs) goto fail;
-        if (cgk_int4_repack_tiled(fd, fs, K, N, gs, d->data, d->scales)) goto fail;
+        if (layout == CGX_LAYOUT_MFMA
+                ? cgk_int4_repack_mfma(fd, fs, K, N, gs, 0, d->data, d->scales)
+                : cgk_int4_repack_tiled(fd, fs, K, N, gs, d->data, d->scales))
+            goto fail;
         if (cgx_synchronize()) goto fail;
     } else {
         int dev = cgx_is_device_ptr(q->data);
@@ -147,7 +151,7 @@ static cg_tensor_quant* quant_to_device_layout(cg_tensor_quant* q, int want_tile
             goto fail;
     }
     {
-        cgx_qinfo info = {tiled ? CGX_LAYOUT_TILED : CGX_LAYOUT_FLAT, K, N, gs};
+        cgx_qinfo info = {layout, K, N, gs, 0};
         cgx_quant_register(d, &info);
     }
     return d;
@@ -160,11 +164,19 @@ fail:
 }
 
 cg_tensor_quant* cgx_quant_to_device(cg_tensor_quant* q) {
-    return quant_to_device_layout(q, 1);
+    return quant_to_device_layout(q, CGX_LAYOUT_MFMA);
 }
 
 cg_tensor_quant* cgx_quant_to_device_flat(cg_tensor_quant* q) {
-    return quant_to_device_layout(q, 0);
+    return quant_to_device_layout(q, CGX_LAYOUT_FLAT);
+}
+
+cg_tensor_quant* cgx_quant_to_device_layout(cg_tensor_quant* q, int layout) {
+    if (layout < CGX_LAYOUT_FLAT || layout > CGX_LAYOUT_MFMA) {
+        cgx_set_error("cgx_quant_to_device_layout: layout must be 1, 2 or 3");
+        return NULL;
+    }
+    return quant_to_device_layout(q, layout);
 }
 
 int cgx_quant_layout(cg_tensor_quant* q) {
@@ -205,6 +217,9 @@ cg_tensor* cg_dequantize(cg_tensor_quant* q) {
         int rc = info.layout == CGX_LAYOUT_TILED
                      ? cgk_int4_dequantize_tiled(q->data, q->scales, info.K, info.N,
                                                  info.group_size, out->data)
+                 : info.layout == CGX_LAYOUT_MFMA
+                     ? cgk_int4_dequantize_mfma(q->data, q->scales, info.K, info.N,
+                                                info.group_size, info.paired, out->data)
                      : cgk_int4_dequantize_flat(q->data, q->scales, q->size,
                                                 q->group_size, out->data);
         if (rc || cgx_synchronize()) {
@@ -243,7 +258,16 @@ int cgx_matmul_int4_dev_kernel(const float* x, int M, cg_tensor_quant* w,
                       "(use cgx_quant_to_device)");
         return -1;
     }
-    if (kernel == 0) kernel = info.layout == CGX_LAYOUT_TILED ? 1 : 2;
+    if (kernel == 0)
+        kernel = info.layout == CGX_LAYOUT_TILED ? 1 : info.layout == CGX_LAYOUT_MFMA ? 3 : 2;
+    if (kernel == 3) {
+        if (info.layout != CGX_LAYOUT_MFMA) {
+            cgx_set_error("cgx_matmul_int4: MFMA kernel needs a layout-3 weight");
+            return -1;
+        }
+        return cgk_gemv_mfma(x, info.K, M, info.K, info.N, info.group_size, w->data,
+                             w->scales, y, info.N, 0, NULL, 0.0f, 0);
+    }
     if (kernel == 1) {
         if (info.layout != CGX_LAYOUT_TILED) {
             cgx_set_error("cgx_matmul_int4: tiled kernel needs a tiled weight");

@@ -443,6 +443,13 @@ extern "C" int cgk_int4_repack_tiled(const uint8_t* flat, const float* scales,
     return launch_check("k_transpose_scales");
 }
 
+extern "C" int cgk_int4_transpose_scales(const float* scales, int K, int G, float* scales_t) {
+    size_t ns = (size_t)K * G;
+    hipLaunchKernelGGL(k_transpose_scales, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0,
+                       stream(), scales, K, G, scales_t);
+    return launch_check("k_transpose_scales");
+}
+
 extern "C" int cgk_int4_dequantize_tiled(const uint8_t* tiled,
                                          const float* scales_t, int K, int N,
                                          int gs, float* out) {

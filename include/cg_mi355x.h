@@ -55,18 +55,23 @@ int cgx_tensor_to_host(cg_tensor* t, float* host_out);
 
 /* Uploads a quantized 2-D weight W[K,N] (reference layout, host or device)
  * into HBM.  When K % 256 == 0, N % 16 == 0, group_size % 16 == 0 and
- * N % group_size == 0 the data is re-tiled for the GEMV kernel (layout 2);
+ * N % group_size == 0 the data is re-tiled for the MFMA GEMV (layout 3);
  * otherwise it is kept in the reference layout (layout 1).  Free with
  * cg_tensor_quant_free. */
 cg_tensor_quant* cgx_quant_to_device(cg_tensor_quant* q);
 /* Same, always keeping the reference layout (for the generic kernel). */
 cg_tensor_quant* cgx_quant_to_device_flat(cg_tensor_quant* q);
-int cgx_quant_layout(cg_tensor_quant* q);   /* 0 host, 1 device flat, 2 device tiled */
+/* Same with the layout chosen: 1 reference, 2 VALU-GEMV strips, 3 MFMA
+ * tiles (2 and 3 fall back to 1 for shapes outside the rule above). */
+cg_tensor_quant* cgx_quant_to_device_layout(cg_tensor_quant* q, int layout);
+/* 0 host, 1 device flat, 2 device VALU tiles, 3 device MFMA tiles */
+int cgx_quant_layout(cg_tensor_quant* q);
 
 /* ------------------------------------------------------ INT4 GEMV (raw) */
 /* y[M,N] = x[M,K] @ W; x and y are device pointers, w a device handle. */
 int cgx_matmul_int4_dev(const float* x, int M, cg_tensor_quant* w, float* y);
-/* Same with the kernel forced: 0 auto, 1 tiled VALU GEMV, 2 generic. */
+/* Same with the kernel forced: 0 auto (by layout), 1 VALU GEMV (layout 2),
+ * 2 generic reference-order kernel (layout 1), 3 MFMA GEMV (layout 3). */
 int cgx_matmul_int4_dev_kernel(const float* x, int M, cg_tensor_quant* w,
                                float* y, int kernel);
 

@@ -170,6 +170,13 @@ CHAIN_CASES = [
     (12, 4, 96, 32, 300, 4),
     (32, 8, 128, 32, 16000, 5),    # many key splits
     (2, 1, 64, 64, 0, 6),          # no context: pure causal block
+    # one scale per head row (the decoder's cache): the MFMA decode kernel
+    (32, 8, 128, 128, 4096, 5),    # 7B-shape verify step
+    (12, 12, 64, 64, 1024, 5),     # tiny-decoder verify step
+    (32, 8, 128, 128, 16000, 5),   # more than one key round per split
+    (8, 2, 32, 32, 300, 7),
+    (32, 8, 128, 128, 255, 1),     # fewer keys than one block round
+    (4, 1, 64, 64, 70, 16),        # 64 query rows per KV head
 ]
 
 
@@ -216,11 +223,13 @@ def random_tree(rng, n):
     return np.array(parents, np.int32)
 
 
-@pytest.mark.parametrize("H,Hk,D,ctx,Nq", [(32, 8, 128, 700, 16), (8, 8, 64, 40, 64),
-                                           (4, 2, 80, 0, 9), (16, 4, 128, 5000, 31)])
-def test_attention_int4_tree(gpu, oracle, rng, H, Hk, D, ctx, Nq):
-    print(f"tree H={H} Hk={Hk} D={D} ctx={ctx} Nq={Nq}", flush=True)
-    gs = 16 if D == 80 else 32
+@pytest.mark.parametrize("H,Hk,D,ctx,Nq,gs", [(32, 8, 128, 700, 16, 32), (8, 8, 64, 40, 64, 32),
+                                              (4, 2, 80, 0, 9, 16), (16, 4, 128, 5000, 31, 32),
+                                              (32, 8, 128, 2048, 64, 128),
+                                              (8, 8, 64, 40, 64, 64),
+                                              (16, 4, 128, 5000, 31, 128)])
+def test_attention_int4_tree(gpu, oracle, rng, H, Hk, D, ctx, Nq, gs):
+    print(f"tree H={H} Hk={Hk} D={D} ctx={ctx} Nq={Nq} gs={gs}", flush=True)
     n = ctx + Nq
     c, K, V = build_cache(gpu, oracle, rng, H, Hk, D, gs, n)
     parents = random_tree(rng, Nq)

@@ -47,10 +47,10 @@ def test_unpack_all_bytes_on_gpu(gpu, oracle):
     exp = np.zeros(K * N, np.float32)
     oracle.orc_dequantize_int4(ptr(data), ptr(scales), K * N, gs, ptr(exp))
     hq, keep = host_quant_from_arrays(data, scales, K, N, gs)
-    for to_dev in ("cgx_quant_to_device", "cgx_quant_to_device_flat"):
-        dq = getattr(gpu, to_dev)(C.byref(hq))
+    for layout in (1, 2, 3):
+        dq = gpu.cgx_quant_to_device_layout(C.byref(hq), layout)
         assert dq, last_error(gpu)
-        assert gpu.cgx_quant_layout(dq) == (2 if to_dev == "cgx_quant_to_device" else 1)
+        assert gpu.cgx_quant_layout(dq) == layout
         t = gpu.cg_dequantize(dq)
         assert t, last_error(gpu)
         got = tensor_np(gpu, t).ravel()
@@ -75,24 +75,65 @@ def _make_weight(oracle, rng, K, N, gs, config2=False):
     return oracle_quantize(oracle, w, gs)
 
 
-@pytest.mark.parametrize("K,N,gs", [(4096, 4096, 128), (256, 512, 64), (1024, 2048, 128),
-                                    (4096, 1024, 128), (11008, 4096, 128), (256, 16, 16),
-                                    (768, 2304, 128), (3072, 768, 128)])
+SHAPES = [(4096, 4096, 128), (256, 512, 64), (1024, 2048, 128), (4096, 1024, 128),
+          (11008, 4096, 128), (256, 16, 16), (768, 2304, 128), (3072, 768, 128)]
+
+
+@pytest.mark.parametrize("K,N,gs", SHAPES)
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
-def test_gemv_tiled_vs_oracle(gpu, oracle, rng, K, N, gs, M):
+@pytest.mark.parametrize("layout,kernel", [(2, 1), (3, 3)], ids=["valu", "mfma"])
+def test_gemv_tiled_vs_oracle(gpu, oracle, rng, K, N, gs, M, layout, kernel):
     if K * N > 4096 * 4096 and M not in (1, 5):
         pytest.skip("large shape: M=1 and M=5 only")
+    _gemv_case(gpu, oracle, rng, K, N, gs, M, layout, kernel)
+
+
+@pytest.mark.parametrize("K,N,gs,M", [(4096, 4096, 128, 16), (1024, 2048, 128, 12),
+                                      (768, 2304, 128, 20), (4096, 22016, 128, 5),
+                                      (4096, 32000, 128, 5), (4096, 8192, 64, 7),
+                                      (256, 512, 16, 40)])
+def test_gemv_mfma_more_rows_and_wide(gpu, oracle, rng, K, N, gs, M):
+    # M > 8 (row chunks of 16), and N wide enough for 2 / 4 column tiles per block
+    _gemv_case(gpu, oracle, rng, K, N, gs, M, 3, 3)
+
+
+def test_gemv_mfma_wide_dynamic_range(gpu, oracle, rng):
+    # activations spanning many binades, a zero row, huge and tiny scales:
+    # the per-round power-of-two scaling keeps the fp16 terms in range
+    K, N, gs, M = 1024, 512, 128, 4
+    data, scales = _make_weight(oracle, rng, K, N, gs)
+    scales = scales.copy()
+    scales[::7] *= 1e4
+    scales[3::11] *= 1e-6
+    x = (rng.normal(0, 1, (M, K)) * np.exp(rng.uniform(-20, 20, (M, K)))).astype(np.float32)
+    x[2] = 0.0
+    y_ref = oracle_matmul(oracle, x, data, scales, K, N, gs)
+    hq, keep = host_quant_from_arrays(data, scales, K, N, gs)
+    dq = gpu.cgx_quant_to_device_layout(C.byref(hq), 3)
+    dx = DeviceArray.from_numpy(gpu, x)
+    dy = DeviceArray(gpu, M * N * 4)
+    assert gpu.cgx_matmul_int4_dev_kernel(dx.ptr, M, dq, dy.ptr, 3) == 0, last_error(gpu)
+    assert gpu.cgx_synchronize() == 0
+    y = dy.numpy(np.float32, (M, N))
+    assert np.all(y[2] == 0.0)
+    keep_rows = [0, 1, 3]
+    assert rel_err_rows(y[keep_rows], y_ref[keep_rows]) <= TOL
+    gpu.cg_tensor_quant_free(dq)
+
+
+def _gemv_case(gpu, oracle, rng, K, N, gs, M, layout, kernel):
     data, scales = _make_weight(oracle, rng, K, N, gs, config2=(K == 4096 and N == 4096))
     x = rng.normal(0, 1, (M, K)).astype(np.float32)
     y_ref = oracle_matmul(oracle, x, data, scales, K, N, gs)
     hq, keep = host_quant_from_arrays(data, scales, K, N, gs)
-    dq = gpu.cgx_quant_to_device(C.byref(hq))
-    assert dq and gpu.cgx_quant_layout(dq) == 2, last_error(gpu)
+    dq = gpu.cgx_quant_to_device_layout(C.byref(hq), layout)
+    assert dq and gpu.cgx_quant_layout(dq) == layout, last_error(gpu)
     dx = DeviceArray.from_numpy(gpu, x)
     dy = DeviceArray(gpu, M * N * 4)
-    for rep in range(2):         # second call exercises the self-reset counters
+    for rep in range(2):         # a second call on the same buffers
         gpu.cgx_memset(dy.ptr, 0xFF, M * N * 4)
-        assert gpu.cgx_matmul_int4_dev_kernel(dx.ptr, M, dq, dy.ptr, 1) == 0, last_error(gpu)
+        assert gpu.cgx_matmul_int4_dev_kernel(dx.ptr, M, dq, dy.ptr, kernel) == 0, \
+            last_error(gpu)
         assert gpu.cgx_synchronize() == 0, last_error(gpu)
         y = dy.numpy(np.float32, (M, N))
         assert np.all(np.isfinite(y))
