@@ -109,13 +109,40 @@ __global__ __launch_bounds__(kThreads) void k_verify_rows(
     }
     const float* drow = draft + ((size_t)chain * gamma + pos) * V;
     RowSrc ts{trow}, ds{drow};
+    const int x = tokens[(size_t)chain * gamma + pos];
+    if (V <= kRound) {
+        // both rows in registers: one read of each row, one expf per element
+        float tv[kCh], dv[kCh];
+        load_vals(ts, V, -__builtin_inff(), tv);
+        load_vals(ds, V, -__builtin_inff(), dv);
+        const float mt = vals_max(tv, sh), md = vals_max(dv, sh);
+        vals_exp(tv, mt, T, V, tv);
+        vals_exp(dv, md, T, V, dv);
+        ExpGen<RowSrc> et{ts, mt, T}, ed{ds, md, T};
+        const float St = eos_sum_vals(tv, et, V, sh);
+        const float Sd = eos_sum_vals(dv, ed, V, sh);
+#pragma unroll
+        for (int k = 0; k < kCh; k++) {
+            tv[k] = __fdiv_rn(tv[k], St);
+            dv[k] = __fdiv_rn(dv[k], Sd);
+        }
+        DivGen<ExpGen<RowSrc>> pt{et, St}, pd{ed, Sd};
+        float a = 1.0f;
+        if (x >= 0 && x < V) {
+            const float px = vals_at(tv, x, sh), qx = vals_at(dv, x, sh);
+            a = qx < 1e-10f ? 1.0f : fminf(1.0f, __fdiv_rn(px, qx));
+        }
+        if (threadIdx.x == 0) accept_prob[(size_t)chain * gamma + pos] = a;
+        const int tok = sample_corrected_vals(tv, dv, pt, pd, V, uu[pos + 1], sh);
+        if (threadIdx.x == 0) correction[(size_t)chain * gamma + pos] = tok;
+        return;
+    }
     float mt = gen_max(ts, V, sh);
     float md = gen_max(ds, V, sh);
     ExpGen<RowSrc> et{ts, mt, T}, ed{ds, md, T};
     float St = eos_sum(et, V, sh);
     float Sd = eos_sum(ed, V, sh);
     DivGen<ExpGen<RowSrc>> pt{et, St}, pd{ed, Sd};
-    int x = tokens[(size_t)chain * gamma + pos];
     float a = 1.0f;
     if (x >= 0 && x < V) {
         float px = gen_at(pt, x, sh), qx = gen_at(pd, x, sh);

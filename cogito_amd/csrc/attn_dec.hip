@@ -131,8 +131,12 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
     constexpr int NC = D / 32;          // QK MFMAs per 16 keys (32 head-dim values each)
     constexpr int DPL = D / 4;          // head-dim values per lane group
     constexpr int ROWS = 16 * RT;
+    // LDS: the Q^T operands (read back per tile, which keeps them out of
+    // the register file), and the waves' partial O at the end
     __shared__ float s_o[kWaves][ROWS][D + 4];
+    __shared__ f16x8 s_q[RT][NC][2][64];
     __shared__ float s_m[kWaves][ROWS], s_l[kWaves][ROWS];
+    __shared__ float s_w[kWaves][ROWS], s_M[ROWS], s_L[ROWS];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
@@ -187,9 +191,10 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
         for (int p = 0; p < 8; p++) {
             int key = kt + key_of_pos(g, p);
             key = key < k_end ? key : k_end - 1;
-            t.vw[p] = n < D / 8 ? *(const uint32_t*)(a.vc + (size_t)key * krow +
-                                                     (size_t)hk * (D / 2) + 4 * n)
-                                : 0u;   // a zero nibble: rows of O^T past D are not stored
+            // lanes n >= D/8 have no column block: they read block 0 and the
+            // O^T rows they produce are never stored
+            const int nb = n < D / 8 ? n : 0;
+            t.vw[p] = *(const uint32_t*)(a.vc + (size_t)key * krow + (size_t)hk * (D / 2) + 4 * nb);
             t.sk[p] = a.ks[(size_t)key * Hk + hk];
             t.sv[p] = a.vs[(size_t)key * Hk + hk];
         }
@@ -197,55 +202,87 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
     TileData td;
     if (wave < ntiles) load_tile(k_begin + wave * kTile, td);
 
-    // ---- Q^T operands of this lane's rows (B operand: row n, 8 positions per MFMA)
-    f16x8 qh[RT][NC], ql[RT][NC];
+    // ---- Q^T operands of the block's rows (B operand: row n, 8 positions per
+    //      MFMA), built once per block: wave w prepares row tile w % RT's
+    //      head-dim part (w / RT) ... and all waves read them back from LDS
     float qinv[RT];
     int rq[RT];
     bool rok[RT];
+    unsigned long long anc_row[RT];
+    int lim_row[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
         const int r = row0 + 16 * rt + n;
         rok[rt] = r < R;
-        const int h = h0 + (rok[rt] ? r / a.Nq : 0), q = rok[rt] ? r % a.Nq : 0;
-        rq[rt] = q;
-        const float* qp = a.Q + ((size_t)q * a.H + h) * D + DPL * g;
-        float qv[DPL];
-        float qmax = 0.0f;
-#pragma unroll
-        for (int i = 0; i < DPL; i += 4) {
-            float4 t = rok[rt] ? *(const float4*)(qp + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-            qv[i] = t.x * a.scale; qv[i + 1] = t.y * a.scale;
-            qv[i + 2] = t.z * a.scale; qv[i + 3] = t.w * a.scale;
-            qmax = fmaxf(qmax, fmaxf(fmaxf(fabsf(qv[i]), fabsf(qv[i + 1])),
-                                     fmaxf(fabsf(qv[i + 2]), fabsf(qv[i + 3]))));
-        }
-        qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
-        qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
-        int E = 0;
-        if (qmax > 0.0f && qmax < __builtin_inff()) E = 14 - ilogbf(qmax);
-        E = E > 100 ? 100 : (E < -100 ? -100 : E);
-        const float up = ldexpf(1.0f, E);
-        qinv[rt] = ldexpf(1.0f, -E);
-#pragma unroll
-        for (int c = 0; c < NC; c++)
-#pragma unroll
-            for (int p = 0; p < 8; p++) {
-                _Float16 hi, lo;
-                split16(qv[8 * c + slot_of(p)] * up, hi, lo);
-                qh[rt][c][p] = hi;
-                ql[rt][c][p] = lo;
-            }
+        rq[rt] = rok[rt] ? r % a.Nq : 0;
+        anc_row[rt] = a.mask_kind == kMaskTree ? a.anc[rq[rt]] : 0ull;
+        // chain: keys up to the query's own position; tree: the cached prefix
+        // (plus ancestor bits); no mask: every key
+        lim_row[rt] = a.mask_kind == kMaskCausal ? a.Nk - a.Nq + rq[rt]
+                    : a.mask_kind == kMaskTree ? a.Nk - a.Nq - 1 : a.Nk;
     }
+    {
+        // rows are per lane (n); every wave computes the row exponent of its
+        // lanes' rows for all RT (cheap), the fp16 splits are divided: wave w
+        // builds the operands of row tile rt for head-dim chunks c with
+        // (rt * NC + c) % kWaves == w
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            const int r = row0 + 16 * rt + n;
+            // rows past R read row 0 (valid memory) and are zeroed: the loads
+            // stay unconditional so they issue together
+            const int h = h0 + (rok[rt] ? r / a.Nq : 0), q = rq[rt];
+            const float* qp = a.Q + ((size_t)q * a.H + h) * D + DPL * g;
+            const float keep = rok[rt] ? 1.0f : 0.0f;
+            float qv[DPL];
+#pragma unroll
+            for (int i = 0; i < DPL; i += 4) {
+                const float4 t = *(const float4*)(qp + i);
+                qv[i] = t.x * keep; qv[i + 1] = t.y * keep; qv[i + 2] = t.z * keep; qv[i + 3] = t.w * keep;
+            }
+            float qmax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < DPL; i++) qmax = fmaxf(qmax, fabsf(qv[i]));
+            qmax *= a.scale;
+            qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
+            qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
+            int E = 0;
+            if (qmax > 0.0f && qmax < __builtin_inff()) E = 14 - ilogbf(qmax);
+            E = E > 100 ? 100 : (E < -100 ? -100 : E);
+            const float up = ldexpf(1.0f, E) * a.scale;
+            qinv[rt] = ldexpf(1.0f, -E);
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                if ((rt * NC + c) % kWaves != wave) continue;
+                f16x8 hv, lv;
+#pragma unroll
+                for (int p = 0; p < 8; p++) {
+                    const float v = qv[8 * c + slot_of(p)] * up;
+                    _Float16 hi, lo;
+                    split16(v, hi, lo);
+                    hv[p] = hi;
+                    lv[p] = lo;
+                }
+                s_q[rt][c][0][lane] = hv;
+                s_q[rt][c][1][lane] = lv;
+            }
+        }
+    }
+    __syncthreads();
 
-
+    TileData tn;                     // the next tile, loaded while this one computes
     for (int tile = wave; tile < ntiles; tile += kWaves) {
         const int kt = k_begin + tile * kTile;
-        if (tile != wave) load_tile(kt, td);
+        if (tile + kWaves < ntiles) load_tile(kt + kWaves * kTile, tn);
         uint32_t (&kw)[2][NC] = td.kw;
         uint32_t (&vw)[8] = td.vw;
         float (&sk)[8] = td.sk;
         float (&sv)[8] = td.sv;
 
+        // the Q^T operands are re-read from LDS every tile (an opaque lane
+        // index keeps the compiler from hoisting them into 64 VGPRs)
+        int ql = lane;
+        asm volatile("" : "+v"(ql));
         // -- S^T = K Q^T (lane: row n, keys 4g+i of each 16-key half)
         f32x4 s[RT][2];
 #pragma unroll
@@ -257,8 +294,8 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
                 const f16x8 ka = nib_to_f16(kw[kh][c] ^ 0x88888888u);
 #pragma unroll
                 for (int rt = 0; rt < RT; rt++) {
-                    s[rt][kh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[rt][c], s[rt][kh], 0, 0, 0);
-                    s[rt][kh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[rt][c], s[rt][kh], 0, 0, 0);
+                    s[rt][kh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, s_q[rt][c][0][ql], s[rt][kh], 0, 0, 0);
+                    s[rt][kh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, s_q[rt][c][1][ql], s[rt][kh], 0, 0, 0);
                 }
             }
 
@@ -277,9 +314,13 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
         const float evup = ldexpf(1.0f, ev);
         const float evshift = tile == wave ? 1.0f : ldexpf(1.0f, ev - ev_cur);
         ev_cur = ev;
+        float svup[8];
+#pragma unroll
+        for (int p = 0; p < 8; p++) svup[p] = sv[p] * evup;
 #pragma unroll
         for (int p = 0; p < 8; p++) vw[p] ^= 0x88888888u;
 
+        f16x8 ph[RT], pl[RT];
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
             // scores, mask, online softmax for row (rt, n)
@@ -289,12 +330,11 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
             for (int p = 0; p < 8; p++) {
                 const int kk = kt + key_of_pos(g, p);
                 const bool exists = kk < k_end;
-                bool vis = rok[rt];
-                if (a.mask_kind == kMaskCausal) {
-                    vis = vis && kk <= base + rq[rt];
-                } else if (a.mask_kind == kMaskTree) {
-                    vis = vis && (kk < base || ((a.anc[rq[rt]] >> (kk - base)) & 1ull));
-                }
+                // keys <= lim_row are visible; a tree row also sees its
+                // ancestors among the new keys
+                const unsigned rel = (unsigned)(kk - base);
+                const bool anc_bit = rel < 64u && ((anc_row[rt] >> (rel & 63u)) & 1ull);
+                const bool vis = rok[rt] && (kk <= lim_row[rt] || anc_bit);
                 const float sc = s[rt][p >> 2][p & 3] * qinv[rt] * sk[p];
                 val[p] = !exists ? -__builtin_inff() : (vis ? sc : -FLT_MAX);
                 tmax = fmaxf(tmax, val[p]);
@@ -304,35 +344,39 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
             const float m_new = fmaxf(m_run[rt], tmax);
             const float alpha = m_new == -__builtin_inff() ? 1.0f : __expf(m_run[rt] - m_new);
             m_run[rt] = m_new;
-            f16x8 ph, pl;
             float psum = 0.0f;
 #pragma unroll
             for (int p = 0; p < 8; p++) {
                 const float pv = m_new == -__builtin_inff() ? 0.0f : __expf(val[p] - m_new);
                 psum += pv;
                 _Float16 hi, lo;
-                split16(pv * sv[p] * evup, hi, lo);
-                ph[p] = hi;
-                pl[p] = lo;
+                split16(pv * svup[p], hi, lo);
+                ph[rt][p] = hi;
+                pl[rt][p] = lo;
             }
             l_part[rt] = l_part[rt] * alpha + psum;
             const float oscale = alpha * evshift;
 #pragma unroll
             for (int t = 0; t < 8; t++) o[rt][t] *= oscale;
-            // -- O^T += V^T P^T (tile t: head-dim columns 8m + t)
+        }
+        // -- O^T += V^T P^T (tile t: head-dim columns 8m + t); the V^T operand
+        //    of a tile serves every row tile
 #pragma unroll
-            for (int t = 0; t < 8; t++) {
-                f16x8 va;
+        for (int t = 0; t < 8; t++) {
+            f16x8 va;
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    f16x2 pr = nib_pair(vw[2 * j], vw[2 * j + 1], t);
-                    va[2 * j] = pr[0];
-                    va[2 * j + 1] = pr[1];
-                }
-                o[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, o[rt][t], 0, 0, 0);
-                o[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, o[rt][t], 0, 0, 0);
+            for (int j = 0; j < 4; j++) {
+                f16x2 pr = nib_pair(vw[2 * j], vw[2 * j + 1], t);
+                va[2 * j] = pr[0];
+                va[2 * j + 1] = pr[1];
+            }
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                o[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph[rt], o[rt][t], 0, 0, 0);
+                o[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[rt], o[rt][t], 0, 0, 0);
             }
         }
+        td = tn;
     }
 
     // ---- per wave: true-unit O, row max and sum -> LDS
@@ -357,30 +401,39 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
             }
     }
     __syncthreads();
+    if (threadIdx.x < ROWS) {
+        const int row = threadIdx.x;
+        float M = -__builtin_inff();
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) M = fmaxf(M, s_m[w][row]);
+        float L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) {
+            const float wgt = s_m[w][row] == -__builtin_inff() ? 0.0f : __expf(s_m[w][row] - M);
+            s_w[w][row] = wgt;
+            L += s_l[w][row] * wgt;
+        }
+        s_M[row] = M;
+        s_L[row] = L;
+    }
+    __syncthreads();
     for (int e = threadIdx.x; e < ROWS * D; e += 64 * kWaves) {
         const int row = e / D, d = e % D;
         const int r = row0 + row;
         if (r >= R) continue;
-        float M = -__builtin_inff();
+        float acc = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kWaves; w++) M = fmaxf(M, s_m[w][row]);
-        float L = 0.0f, acc = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWaves; w++) {
-            const float wgt = s_m[w][row] == -__builtin_inff() ? 0.0f : __expf(s_m[w][row] - M);
-            L += s_l[w][row] * wgt;
-            acc += s_o[w][row][d] * wgt;
-        }
+        for (int w = 0; w < kWaves; w++) acc += s_o[w][row][d] * s_w[w][row];
         const int h = h0 + r / a.Nq, q = r % a.Nq;
         const size_t orow = (size_t)q * a.H + h;
         if (a.splits == 1) {
-            a.O[orow * D + d] = L > 0.0f ? acc / L : 0.0f;
+            a.O[orow * D + d] = s_L[row] > 0.0f ? acc / s_L[row] : 0.0f;
         } else {
             const size_t nrow = (size_t)a.Nq * a.H;
             a.part_o[((size_t)split * nrow + orow) * D + d] = acc;
             if (d == 0) {
-                a.part_ml[((size_t)split * nrow + orow) * 2] = M;
-                a.part_ml[((size_t)split * nrow + orow) * 2 + 1] = L;
+                a.part_ml[((size_t)split * nrow + orow) * 2] = s_M[row];
+                a.part_ml[((size_t)split * nrow + orow) * 2 + 1] = s_L[row];
             }
         }
     }
@@ -460,10 +513,14 @@ extern "C" int cgk_attn_dec(const float* Q, const uint8_t* kc, const uint8_t* vc
     a.mask_kind = mask_kind;
     for (int i = 0; i < 64; i++) a.anc[i] = (mask_kind == kMaskTree && i < Nq) ? anc[i] : 0ull;
     const int R = (H / Hk) * Nq;
-    const int RT = R <= 16 ? 1 : 2;
+    // one 16-row tile per block keeps a wave's registers low enough for two
+    // waves per SIMD; more rows run as more blocks (they re-read K/V from cache)
+    const int RT = 1;
     const int chunks = (R + 16 * RT - 1) / (16 * RT);
-    // one block round (256 keys) per split, at most 128 splits
-    int kps = kSplitKeys;
+    // keys per split: whole block rounds, about 24 splits at most (measured
+    // at the 7B verify shape: 256-key splits beat 128 and 512)
+    const int rounds = (Nk + kSplitKeys * 24 - 1) / (kSplitKeys * 24);
+    int kps = kSplitKeys * (rounds > 1 ? rounds : 1);
     while ((Nk + kps - 1) / kps > 128) kps += kSplitKeys;
     const int splits = (Nk + kps - 1) / kps;
     a.splits = splits;
@@ -479,9 +536,9 @@ extern "C" int cgk_attn_dec(const float* Q, const uint8_t* kc, const uint8_t* vc
     }
     dim3 grid(splits, Hk, chunks);
     int rc;
-    if (D == 128) rc = RT == 1 ? launch<128, 1>(a, grid) : launch<128, 2>(a, grid);
-    else if (D == 64) rc = RT == 1 ? launch<64, 1>(a, grid) : launch<64, 2>(a, grid);
-    else rc = RT == 1 ? launch<32, 1>(a, grid) : launch<32, 2>(a, grid);
+    if (D == 128) rc = launch<128, 1>(a, grid);
+    else if (D == 64) rc = launch<64, 1>(a, grid);
+    else rc = launch<32, 1>(a, grid);
     if (rc) return rc;
     if (splits > 1) {
         if (splits > 128) {

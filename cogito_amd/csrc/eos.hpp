@@ -22,6 +22,7 @@ constexpr int kCh = 32;                      // elements per thread per round
 constexpr int kRound = kThreads * kCh;       // 32768 elements per round
 constexpr int kMaxRounds = 8;                // rows up to 262144 elements
 constexpr int kDirty = -1000;                // binade marker of a replayed chunk
+constexpr int kDirtySlots = 96;              // dirty chunks staged in LDS per round
 
 // ------------------------------------------------------------ exact expf
 
@@ -175,6 +176,11 @@ struct EosShared {
     int seg_last[kThreads];
     float cstart[kMaxRounds][kThreads];
     float cend[kMaxRounds][kThreads];
+    int item_c[kThreads];        // walk items: first chunk of each segment / dirty chunk
+    int wcount[kWaves];
+    int n_items;
+    int dirty_slot[kThreads];    // staging slot of a dirty chunk (-1: none)
+    float dirty_vals[kDirtySlots][kCh];
     float total;
     int result;
     float fval;
@@ -207,9 +213,275 @@ template <class G>
 __device__ __forceinline__ float replay_chunk_wave(const G& g, int base, int n, float s) {
     int j = base + lane_id();
     float x = (lane_id() < kCh && j < n) ? g(j) : 0.0f;
+    // lane k's value straight into a scalar operand: only the adds are serial
 #pragma unroll
-    for (int k = 0; k < kCh; k++) s = __fadd_rn(s, __shfl(x, k));
+    for (int k = 0; k < kCh; k++)
+        s = __fadd_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k)));
     return s;
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int k) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffll), k);
+    const int hi = __builtin_amdgcn_readlane((int)(b >> 32), k);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+// ----------------------------------------------------- DPP wave scans
+// Inclusive scans over the 64 lanes with DPP: row_shr 1, 2, 4, 8 inside each
+// row of 16 lanes, then row_bcast:15 and row_bcast:31 across rows.  Data only
+// flows from lower to higher lanes, so non-commutative operators are fine.
+template <int CTRL, int RMASK>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, RMASK, 0xF, false);
+}
+template <int CTRL, int RMASK>
+__device__ __forceinline__ double dpp_d(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = dpp_i<CTRL, RMASK>((int)(b & 0xffffffffll));
+    const int hi = dpp_i<CTRL, RMASK>((int)(b >> 32));
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+// lane receives a value at this step of the scan
+__device__ __forceinline__ bool dpp_step_valid(int step) {
+    const int l = lane_id();
+    switch (step) {
+        case 0: return (l & 15) >= 1;
+        case 1: return (l & 15) >= 2;
+        case 2: return (l & 15) >= 4;
+        case 3: return (l & 15) >= 8;
+        case 4: return (l >> 4) & 1;         // rows 1 and 3 from lane 15 / 47
+        default: return l >= 32;             // rows 2 and 3 from lane 31
+    }
+}
+
+__device__ __forceinline__ double wave_incl_sum_d(double x) {
+    double o;
+    o = dpp_d<0x111, 0xF>(x); if (dpp_step_valid(0)) x += o;
+    o = dpp_d<0x112, 0xF>(x); if (dpp_step_valid(1)) x += o;
+    o = dpp_d<0x114, 0xF>(x); if (dpp_step_valid(2)) x += o;
+    o = dpp_d<0x118, 0xF>(x); if (dpp_step_valid(3)) x += o;
+    o = dpp_d<0x142, 0xA>(x); if (dpp_step_valid(4)) x += o;
+    o = dpp_d<0x143, 0xC>(x); if (dpp_step_valid(5)) x += o;
+    return x;
+}
+
+template <int CTRL, int RMASK>
+__device__ __forceinline__ SegMono dpp_seg(const SegMono& v) {
+    SegMono o;
+    o.m.q0 = dpp_d<CTRL, RMASK>(v.m.q0);
+    o.m.q1 = dpp_d<CTRL, RMASK>(v.m.q1);
+    o.m.c0 = dpp_i<CTRL, RMASK>(v.m.c0);
+    o.m.c1 = dpp_i<CTRL, RMASK>(v.m.c1);
+    o.head = dpp_i<CTRL, RMASK>(v.head);
+    o.flag = dpp_i<CTRL, RMASK>(v.flag);
+    return o;
+}
+
+__device__ __forceinline__ SegMono wave_incl_seg(SegMono v) {
+    SegMono o;
+    o = dpp_seg<0x111, 0xF>(v); if (dpp_step_valid(0)) v = seg_then(o, v);
+    o = dpp_seg<0x112, 0xF>(v); if (dpp_step_valid(1)) v = seg_then(o, v);
+    o = dpp_seg<0x114, 0xF>(v); if (dpp_step_valid(2)) v = seg_then(o, v);
+    o = dpp_seg<0x118, 0xF>(v); if (dpp_step_valid(3)) v = seg_then(o, v);
+    o = dpp_seg<0x142, 0xA>(v); if (dpp_step_valid(4)) v = seg_then(o, v);
+    o = dpp_seg<0x143, 0xC>(v); if (dpp_step_valid(5)) v = seg_then(o, v);
+    return v;
+}
+
+// Staged values of a dirty chunk, or the generator when it was not staged.
+template <class G>
+__device__ __forceinline__ float replay_chunk_staged(const G& g, int slot, int base, int n,
+                                                     float s, EosShared& sh) {
+    if (slot < 0) return replay_chunk_wave(g, base, n, s);
+    const float x = lane_id() < kCh ? sh.dirty_vals[slot][lane_id()] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < kCh; k++)
+        s = __fadd_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k)));
+    return s;
+}
+
+// One round of the exact ordered sum: this thread's kCh values x (elements
+// rd*kRound + t*kCh + k, zero past n), starting from the exact running value
+// s_round.  Returns the exact value after the round; leaves the exact running
+// value at every chunk boundary of the round in sh.cstart/sh.cend[rd].  `g`
+// regenerates elements for the rare replays of chunks that were not staged.
+template <class G>
+__device__ __forceinline__ float eos_round(const float (&x)[kCh], const G& g, int rd, int n,
+                                           float s_round, EosShared& sh) {
+    const int t = threadIdx.x;
+
+    // fp64 guide: exclusive / inclusive prefix of chunk sums
+    double gs = 0.0;
+#pragma unroll
+    for (int k = 0; k < kCh; k++) gs += (double)x[k];
+    const double inc = wave_incl_sum_d(gs);
+    if (lane_id() == 63) sh.wsum[wave_id()] = inc;
+    __syncthreads();
+    double wpre = 0.0;
+    for (int w = 0; w < wave_id(); w++) wpre += sh.wsum[w];
+    const double p_end = (double)s_round + wpre + inc;
+    const double p_start = p_end - gs;
+    const double delta = (double)(t * kCh + kCh + 1) * 0x1p-24 * (1.0 + 0x1p-20) + 0x1p-40;
+    const double lo = t == 0 ? (double)s_round : p_start * (1.0 - delta);
+    const double hi = p_end * (1.0 + delta);
+    const int b = binade_of(lo);
+    const bool clean = binade_of(hi) == b;
+
+    // own monoid element under binade b
+    Mono own = mono_id();
+    if (clean) {
+        const double sc = ulp_scale(b);
+        int c0 = 0, c1 = 1;
+        double q0 = 0.0, q1 = 0.0;
+#pragma unroll
+        for (int k = 0; k < kCh; k++) {
+            const double y = (double)x[k] * sc;
+            const double f = floor(y);
+            const double fr = y - f;
+            if (fr == 0.5) {
+                const int fo = (int)((long long)f & 1);
+                q0 += f + (double)((c0 ^ fo) & 1);
+                q1 += f + (double)((c1 ^ fo) & 1);
+                c0 = 0;
+                c1 = 0;
+            } else {
+                const double q = f + (fr > 0.5 ? 1.0 : 0.0);
+                const int qo = (int)((long long)q & 1);
+                q0 += q;
+                q1 += q;
+                c0 ^= qo;
+                c1 ^= qo;
+            }
+        }
+        own = Mono{q0, q1, c0, c1};
+    }
+    sh.binade[t] = clean ? b : kDirty;
+
+    // dirty chunks: stage their values for the walk (slots in chunk order)
+    {
+        const unsigned long long bal = __ballot(!clean);
+        const int below = __popcll(bal & ((1ull << lane_id()) - 1ull));
+        if (lane_id() == 0) sh.wcount[wave_id()] = __popcll(bal);
+        __syncthreads();
+        int off = 0;
+        for (int w = 0; w < wave_id(); w++) off += sh.wcount[w];
+        const int slot = off + below;
+        const bool staged = !clean && slot < kDirtySlots;
+        sh.dirty_slot[t] = staged ? slot : -1;
+        if (staged) {
+#pragma unroll
+            for (int k = 0; k < kCh; k++) sh.dirty_vals[slot][k] = x[k];
+        }
+    }
+    __syncthreads();
+
+    // segmented scan of the monoid elements (segments = runs of one binade)
+    const bool is_head = !clean || t == 0 || sh.binade[t - 1] != b;
+    SegMono v;
+    v.m = clean ? own : mono_id();
+    v.head = t;
+    v.flag = is_head ? 1 : 0;
+    v = wave_incl_seg(v);
+    if (lane_id() == 63) sh.wseg[wave_id()] = v;
+    __syncthreads();
+    if (wave_id() > 0) {
+        SegMono pre = sh.wseg[0];
+        for (int w = 1; w < wave_id(); w++) pre = seg_then(pre, sh.wseg[w]);
+        v = seg_then(pre, v);
+    }
+    sh.incl[t] = v.m;
+    sh.head[t] = v.head;
+    const bool is_last = t == kThreads - 1 || sh.binade[t + 1] != sh.binade[t] ||
+                         sh.binade[t] == kDirty;
+    if (clean && is_last) sh.seg_last[v.head] = t;
+
+    // walk items: every dirty chunk, and the first chunk of every run of
+    // clean chunks in one binade (the segment heads above), in order
+    {
+        const unsigned long long bal = __ballot(is_head);
+        const int below = __popcll(bal & ((1ull << lane_id()) - 1ull));
+        __syncthreads();
+        if (lane_id() == 0) sh.wcount[wave_id()] = __popcll(bal);
+        __syncthreads();
+        int off = 0, tot = 0;
+        for (int w = 0; w < kWaves; w++) {
+            const int cw = sh.wcount[w];
+            off += w < wave_id() ? cw : 0;
+            tot += cw;
+        }
+        if (is_head) sh.item_c[off + below] = t;
+        if (t == 0) sh.n_items = tot;
+    }
+    __syncthreads();
+
+    // walk: one wave; each item's data sits in one lane and is read with
+    // readlane, so the serial chain is only the running value
+    if (wave_id() == 0) {
+        float s = s_round;
+        const int n_items = sh.n_items;
+        for (int ib = 0; ib < n_items; ib += 64) {
+            const int idx = ib + lane_id();
+            const int my_c = idx < n_items ? sh.item_c[idx] : 0;
+            const int my_b = sh.binade[my_c];
+            const int my_e = my_b != kDirty ? sh.seg_last[my_c] : my_c;
+            const int my_slot = sh.dirty_slot[my_c];
+            double my_q0 = 0.0, my_q1 = 0.0;
+            if (my_b != kDirty) {
+                my_q0 = sh.incl[my_e].q0;
+                my_q1 = sh.incl[my_e].q1;
+            }
+            const int cnt = n_items - ib < 64 ? n_items - ib : 64;
+            for (int k = 0; k < cnt; k++) {
+                const int c = __builtin_amdgcn_readlane(my_c, k);
+                const int bc = __builtin_amdgcn_readlane(my_b, k);
+                const int e = __builtin_amdgcn_readlane(my_e, k);
+                if (bc == kDirty) {
+                    if (lane_id() == 0) sh.cstart[rd][c] = s;
+                    s = replay_chunk_staged(g, __builtin_amdgcn_readlane(my_slot, k),
+                                            rd * kRound + c * kCh, n, s, sh);
+                    if (lane_id() == 0) sh.cend[rd][c] = s;
+                } else if (binade_of((double)s) != bc) {
+                    // a clean run whose start is not in the binade its chunks
+                    // assumed (excluded by the error bound, handled exactly
+                    // anyway): replay it chunk by chunk from the generator
+                    for (int i = c; i <= e; i++) {
+                        if (lane_id() == 0) {
+                            sh.binade[i] = kDirty;
+                            sh.cstart[rd][i] = s;
+                        }
+                        s = replay_chunk_wave(g, rd * kRound + i * kCh, n, s);
+                        if (lane_id() == 0) sh.cend[rd][i] = s;
+                    }
+                } else {
+                    if (lane_id() == 0) sh.cstart[rd][c] = s;
+                    const double q0 = readlane_f64(my_q0, k), q1 = readlane_f64(my_q1, k);
+                    const double q = parity_of(s, bc) ? q1 : q0;
+                    s = (float)((double)s + q * ulp_of(bc));
+                }
+            }
+        }
+        if (lane_id() == 0) sh.total = s;
+    }
+    __syncthreads();
+
+    // exact chunk boundaries for every clean chunk
+    const int bt = sh.binade[t];
+    if (bt != kDirty) {
+        const int h = sh.head[t];
+        const float sh0 = sh.cstart[rd][h];
+        const int par = parity_of(sh0, bt);
+        const Mono ex = (t == h) ? mono_id() : sh.incl[t - 1];
+        const double u = ulp_of(bt);
+        const double s0 = (double)sh0 + (par ? ex.q1 : ex.q0) * u;
+        const int par2 = par ? ex.c1 : ex.c0;
+        const double s1 = s0 + (par2 ? own.q1 : own.q0) * u;
+        if (t != h) sh.cstart[rd][t] = (float)s0;
+        sh.cend[rd][t] = (float)s1;
+    }
+    const float total = sh.total;
+    __syncthreads();
+    return total;
 }
 
 // Exact ordered sum of g(0..n-1).  Leaves the exact running value at every
@@ -224,194 +496,74 @@ __device__ __forceinline__ float eos_sum(const G& g, int n, EosShared& sh) {
         float x[kCh];
 #pragma unroll
         for (int k = 0; k < kCh; k++) x[k] = (base + k < n) ? g(base + k) : 0.0f;
-
-        // fp64 guide: exclusive / inclusive prefix of chunk sums
-        double gs = 0.0;
-#pragma unroll
-        for (int k = 0; k < kCh; k++) gs += (double)x[k];
-        double inc = gs;
-        for (int d = 1; d < 64; d <<= 1) {
-            double o = __shfl_up(inc, d);
-            if (lane_id() >= d) inc += o;
-        }
-        if (lane_id() == 63) sh.wsum[wave_id()] = inc;
-        __syncthreads();
-        double wpre = 0.0;
-        for (int w = 0; w < wave_id(); w++) wpre += sh.wsum[w];
-        double p_end = (double)s_round + wpre + inc;
-        double p_start = p_end - gs;
-        double delta = (double)(t * kCh + kCh + 1) * 0x1p-24 * (1.0 + 0x1p-20) + 0x1p-40;
-        double lo = t == 0 ? (double)s_round : p_start * (1.0 - delta);
-        double hi = p_end * (1.0 + delta);
-        int b = binade_of(lo);
-        bool clean = binade_of(hi) == b;
-
-        // own monoid element under binade b
-        Mono own = mono_id();
-        if (clean) {
-            double sc = ulp_scale(b);
-            int c0 = 0, c1 = 1;
-            double q0 = 0.0, q1 = 0.0;
-#pragma unroll
-            for (int k = 0; k < kCh; k++) {
-                double y = (double)x[k] * sc;
-                double f = floor(y);
-                double fr = y - f;
-                if (fr == 0.5) {
-                    int fo = (int)((long long)f & 1);
-                    q0 += f + (double)((c0 ^ fo) & 1);
-                    q1 += f + (double)((c1 ^ fo) & 1);
-                    c0 = 0;
-                    c1 = 0;
-                } else {
-                    double q = f + (fr > 0.5 ? 1.0 : 0.0);
-                    int qo = (int)((long long)q & 1);
-                    q0 += q;
-                    q1 += q;
-                    c0 ^= qo;
-                    c1 ^= qo;
-                }
-            }
-            own = Mono{q0, q1, c0, c1};
-        }
-        sh.binade[t] = clean ? b : kDirty;
-        __syncthreads();
-        bool is_head = !clean || t == 0 || sh.binade[t - 1] != b;
-        SegMono v;
-        v.m = clean ? own : mono_id();
-        v.head = t;
-        v.flag = is_head ? 1 : 0;
-        for (int d = 1; d < 64; d <<= 1) {
-            SegMono o = shfl_up_seg(v, d);
-            if (lane_id() >= d) v = seg_then(o, v);
-        }
-        if (lane_id() == 63) sh.wseg[wave_id()] = v;
-        __syncthreads();
-        if (wave_id() > 0) {
-            SegMono pre = sh.wseg[0];
-            for (int w = 1; w < wave_id(); w++) pre = seg_then(pre, sh.wseg[w]);
-            v = seg_then(pre, v);
-        }
-        sh.incl[t] = v.m;
-        sh.head[t] = v.head;
-        bool is_last = t == kThreads - 1 || sh.binade[t + 1] != sh.binade[t] ||
-                       sh.binade[t] == kDirty;
-        if (clean && is_last) sh.seg_last[v.head] = t;
-        __syncthreads();
-
-        // walk: one wave, segments in O(1), replayed chunks in order
-        if (wave_id() == 0) {
-            float s = s_round;
-            int c = 0;
-            while (c < kThreads) {
-                int bc = sh.binade[c];
-                if (bc != kDirty && binade_of((double)s) != bc) {
-                    // cannot happen under the error bound; stay exact anyway
-                    bc = kDirty;
-                    int e = sh.seg_last[c];
-                    for (int i = c; i <= e; i++) sh.binade[i] = kDirty;
-                }
-                if (bc == kDirty) {
-                    if (lane_id() == 0) sh.cstart[rd][c] = s;
-                    s = replay_chunk_wave(g, rd * kRound + c * kCh, n, s);
-                    if (lane_id() == 0) sh.cend[rd][c] = s;
-                    c++;
-                } else {
-                    int e = sh.seg_last[c];
-                    if (lane_id() == 0) sh.cstart[rd][c] = s;
-                    Mono me = sh.incl[e];
-                    double q = parity_of(s, bc) ? me.q1 : me.q0;
-                    s = (float)((double)s + q * ulp_of(bc));
-                    c = e + 1;
-                }
-            }
-            if (lane_id() == 0) sh.total = s;
-        }
-        __syncthreads();
-
-        // exact chunk boundaries for every clean chunk
-        int bt = sh.binade[t];
-        if (bt != kDirty) {
-            int h = sh.head[t];
-            float sh0 = sh.cstart[rd][h];
-            int par = parity_of(sh0, bt);
-            Mono ex = (t == h) ? mono_id() : sh.incl[t - 1];
-            double u = ulp_of(bt);
-            double s0 = (double)sh0 + (par ? ex.q1 : ex.q0) * u;
-            int par2 = par ? ex.c1 : ex.c0;
-            double s1 = s0 + (par2 ? own.q1 : own.q0) * u;
-            if (t != h) sh.cstart[rd][t] = (float)s0;
-            sh.cend[rd][t] = (float)s1;
-        }
-        s_round = sh.total;
-        __syncthreads();
+        s_round = eos_round(x, g, rd, n, s_round, sh);
     }
     return s_round;
 }
 
-// First i in [0, n) with r < (exact running sum through i); `dflt` if none.
-// Must follow eos_sum over the same generator.
+// Same for n <= kRound with this thread's values already in registers.
 template <class G>
-__device__ __forceinline__ int gen_find(const G& g, int n, float r, int dflt, EosShared& sh) {
-    const int t = threadIdx.x;
-    const int rounds = (n + kRound - 1) / kRound;
-    if (t == 0) sh.result = dflt;
-    __syncthreads();
-    for (int rd = 0; rd < rounds; rd++) {
-        float s0 = sh.cstart[rd][t], s1 = sh.cend[rd][t];
-        // the first chunk also takes r below its start (r < 0)
-        if ((!(r < s0) || (rd == 0 && t == 0)) && (r < s1)) {
-            int base = rd * kRound + t * kCh;
-            float s = s0;
-            for (int k = 0; k < kCh && base + k < n; k++) {
-                s = __fadd_rn(s, g(base + k));
-                if (r < s) {
-                    sh.result = base + k;
-                    break;
-                }
-            }
-        }
-    }
-    __syncthreads();
-    int res = sh.result;
-    __syncthreads();
-    return res;
+__device__ __forceinline__ float eos_sum_vals(const float (&x)[kCh], const G& g, int n,
+                                              EosShared& sh) {
+    return eos_round(x, g, 0, n, 0.0f, sh);
 }
 
-// gen_find that also returns the exact running sum through the found index
-// (`*val`); {dflt, total} when no index qualifies.  Must follow eos_sum over
-// the same generator, whose result is `total`.
+// First i in [0, n) with r < (exact running sum through i); `dflt` if none.
+// Must follow eos_sum over the same generator.  The running sum is
+// non-decreasing, so at most one chunk has start <= r < end; one wave
+// replays it (lanes evaluate, readlane feeds the serial adds).
 template <class G>
 __device__ __forceinline__ int gen_find_val(const G& g, int n, float r, int dflt, float total,
                                             float* val, EosShared& sh) {
     const int t = threadIdx.x;
     const int rounds = (n + kRound - 1) / kRound;
     if (t == 0) {
-        sh.result = dflt;
+        sh.result = -1;
         sh.rval = total;
     }
     __syncthreads();
     for (int rd = 0; rd < rounds; rd++) {
-        float s0 = sh.cstart[rd][t], s1 = sh.cend[rd][t];
+        const float s0 = sh.cstart[rd][t], s1 = sh.cend[rd][t];
+        const int base = rd * kRound + t * kCh;
         // the first chunk also takes r below its start (r < 0)
-        if ((!(r < s0) || (rd == 0 && t == 0)) && (r < s1)) {
-            int base = rd * kRound + t * kCh;
-            float s = s0;
+        if (base < n && (!(r < s0) || (rd == 0 && t == 0)) && (r < s1)) sh.result = rd * kThreads + t;
+    }
+    __syncthreads();
+    const int hit = sh.result;
+    if (wave_id() == 0) {
+        int res = dflt;
+        float rv = total;
+        if (hit >= 0) {
+            const int rd = hit / kThreads, c = hit % kThreads;
+            const int base = rd * kRound + c * kCh;
+            const int j = base + lane_id();
+            const float x = (lane_id() < kCh && j < n) ? g(j) : 0.0f;
+            float s = sh.cstart[rd][c];
             for (int k = 0; k < kCh && base + k < n; k++) {
-                s = __fadd_rn(s, g(base + k));
+                s = __fadd_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k)));
                 if (r < s) {
-                    sh.result = base + k;
-                    sh.rval = s;
+                    res = base + k;
+                    rv = s;
                     break;
                 }
             }
         }
+        if (lane_id() == 0) {
+            sh.result = res;
+            sh.rval = rv;
+        }
     }
     __syncthreads();
-    int res = sh.result;
+    const int res = sh.result;
     *val = sh.rval;
     __syncthreads();
     return res;
+}
+
+template <class G>
+__device__ __forceinline__ int gen_find(const G& g, int n, float r, int dflt, EosShared& sh) {
+    float v;
+    return gen_find_val(g, n, r, dflt, 0.0f, &v, sh);
 }
 
 // Broadcast g(j) for one index to the block.
@@ -424,10 +576,75 @@ __device__ __forceinline__ float gen_at(const G& g, int j, EosShared& sh) {
     return v;
 }
 
+// ------------------------------------------- single-round row helpers
+// For rows of at most kRound elements each thread holds its kCh elements
+// (t*kCh + k) in registers, so every pass after the first read works from
+// registers; the values are bit-identical to the generators' (same
+// operations in the same order).
+
+// Row values of `src` for this thread (pad: elements past n).
+template <class S>
+__device__ __forceinline__ void load_vals(const S& src, int n, float pad, float (&x)[kCh]) {
+    const int base = threadIdx.x * kCh;
+#pragma unroll
+    for (int k = 0; k < kCh; k++) x[k] = base + k < n ? src(base + k) : pad;
+}
+
+__device__ __forceinline__ float vals_max(const float (&x)[kCh], EosShared& sh) {
+    float v = -__builtin_inff();
+#pragma unroll
+    for (int k = 0; k < kCh; k++) v = fmaxf(v, x[k]);
+    return block_max_f(v, sh);
+}
+
+// e = expf((x - m) / T) (ExpGen), zero past n
+__device__ __forceinline__ void vals_exp(const float (&x)[kCh], float m, float T, int n,
+                                         float (&e)[kCh]) {
+    const int base = threadIdx.x * kCh;
+#pragma unroll
+    for (int k = 0; k < kCh; k++)
+        e[k] = base + k < n ? exp_glibc(__fdiv_rn(__fsub_rn(x[k], m), T)) : 0.0f;
+}
+
+// the value of element j (any thread's) broadcast to the block
+__device__ __forceinline__ float vals_at(const float (&x)[kCh], int j, EosShared& sh) {
+    if ((int)threadIdx.x == j / kCh) {
+#pragma unroll
+        for (int k = 0; k < kCh; k++)
+            if (k == j % kCh) sh.fval = x[k];
+    }
+    __syncthreads();
+    const float v = sh.fval;
+    __syncthreads();
+    return v;
+}
+
+// cg_sample_temperature on register values of a row (n <= kRound), `src`
+// regenerating elements for replays.
+template <class S>
+__device__ __forceinline__ int sample_temperature_vals(const float (&x)[kCh], const S& src, int V,
+                                                       float T, float u, EosShared& sh) {
+    const float m = vals_max(x, sh);
+    float e[kCh];
+    vals_exp(x, m, T, V, e);
+    ExpGen<S> eg{src, m, T};
+    const float S_ = eos_sum_vals(e, eg, V, sh);
+    DivGen<ExpGen<S>> pg{eg, S_};
+#pragma unroll
+    for (int k = 0; k < kCh; k++) e[k] = __fdiv_rn(e[k], S_);   // (0 / S = 0 past V)
+    eos_sum_vals(e, pg, V, sh);
+    return gen_find(pg, V, u, V - 1, sh);
+}
+
 // cg_sample_temperature on the values of `src` (speculative.c:54-75).
 template <class S>
 __device__ __forceinline__ int sample_temperature_gen(const S& src, int V, float T, float u,
                                       EosShared& sh) {
+    if (V <= kRound) {
+        float x[kCh];
+        load_vals(src, V, -__builtin_inff(), x);
+        return sample_temperature_vals(x, src, V, T, u, sh);
+    }
     float m = gen_max(src, V, sh);
     ExpGen<S> e{src, m, T};
     float S_ = eos_sum(e, V, sh);
@@ -443,6 +660,20 @@ __device__ __forceinline__ int sample_corrected_gen(const P& p, const Q& q, int 
     ResidualGen<P, Q> r{p, q};
     float R = eos_sum(r, V, sh);
     if (R < 1e-10f) return sample_temperature_gen(p, V, 1.0f, u, sh);
+    return gen_find(r, V, __fmul_rn(u, R), 0, sh);
+}
+
+// The same with both probability rows in registers (n <= kRound).
+template <class P, class Q>
+__device__ __forceinline__ int sample_corrected_vals(const float (&pv)[kCh], const float (&qv)[kCh],
+                                                     const P& p, const Q& q, int V, float u,
+                                                     EosShared& sh) {
+    ResidualGen<P, Q> r{p, q};
+    float rv[kCh];
+#pragma unroll
+    for (int k = 0; k < kCh; k++) rv[k] = fmaxf(0.0f, __fsub_rn(pv[k], qv[k]));
+    const float R = eos_sum_vals(rv, r, V, sh);
+    if (R < 1e-10f) return sample_temperature_vals(pv, p, V, 1.0f, u, sh);
     return gen_find(r, V, __fmul_rn(u, R), 0, sh);
 }
 

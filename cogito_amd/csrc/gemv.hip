@@ -209,8 +209,10 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv_mfma(MfmaArgs a) {
 
     for (int i = 0; i < my_rounds; i++) {
         const int r = wave + i * kWaves;
-        if (i + 1 < my_rounds) load_w(r + kWaves, wnxt);
+        // activations first: the A-prep waits for them, and loads complete in
+        // issue order, so the next round's weights stay in flight meanwhile
         load_a(r, acur);
+        if (i + 1 < my_rounds) load_w(r + kWaves, wnxt);
 
         // ---- A operands of this round
         float4 xv[MP];
@@ -445,17 +447,13 @@ int launch_pe(const MfmaArgs& a, int T) {
 
 }  // namespace
 
-// Column tiles per block: as many as keep >= 256 blocks (one per CU), within
-// one scale group (or one gate|up pair group each).
+// Column tiles per block: two when that still gives >= 256 blocks (one per
+// CU) and the pair shares a scale group (measured on the 7B shapes: two beat
+// one by ~20% and four by ~25%, which drops below two blocks per CU), else
+// one.  A gate|up pair always takes one gate and one up tile.
 extern "C" int cgk_gemv_mfma_tiles(int N, int gs, int paired) {
     const int tiles = N / 16;
-    if (paired) {
-        const int ff = N / 2;
-        // gate tiles of a block share a group, and so do the up tiles
-        if (tiles / 4 >= 256 && gs % 32 == 0 && ff % 32 == 0) return 4;
-        return 2;
-    }
-    if (tiles / 4 >= 256 && gs % 64 == 0) return 4;
+    if (paired) return 2;
     if (tiles / 2 >= 256 && gs % 32 == 0) return 2;
     return 1;
 }
