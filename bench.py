@@ -38,8 +38,8 @@ HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256 * 1024 * 1024
 # HBM bytes per GEMV launch measured with rocprofv3 FETCH_SIZE + WRITE_SIZE,
 # scaled by a copy kernel of known size (profiles/int4_gemv_4096x4096.md).
-# Measured for k_gemv_strip<M, 2, 8>; re-measure when the kernel changes.
-GEMV_TRAFFIC_BYTES = {1: 9136128, 2: 9306112, 3: 9474048, 4: 9641984, 5: 9809920}
+# Measured for k_gemv_mfma (layout 3); re-measure when the kernel changes.
+GEMV_TRAFFIC_BYTES = {1: 9107456, 2: 9274368, 3: 9431040, 4: 9578496, 5: 9741312}
 
 
 def log(msg: str) -> None:
@@ -384,6 +384,10 @@ def cpu_baseline_gemv(M, K, N, gs, budget_s=12.0, seed=2024):
         times.append(time.perf_counter() - t0)
         if len(times) >= 50:
             break
+    if kind == "reference":
+        # the reference reports unfreed tensors on stdout at exit
+        ref.cg_tensor_free(tx)
+        ref.cg_tensor_free(ty)
     med = float(np.median(times))
     nbytes = gemv_bytes(M, K, N, gs)
     return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,

@@ -247,6 +247,7 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_filtered_dist": (I, [VP, I, F, I, F, VP]),
     "cgx_exact_expf_dev": (I, [VP, VP, I]),
     "cgx_ordered_sum_dev": (I, [VP, I, VP]),
+    "cgx_exp_fast_maxerr_dev": (I, [F, F, VP]),
     "cgx_kv_cache_int4_truncate": (I, [PKV, I]),
     "cgx_kv_cache_int4_write": (I, [PKV, I, I, VP, VP, I]),
     "cgx_kv_cache_int4_set_len": (I, [PKV, I]),

@@ -59,6 +59,21 @@ __global__ __launch_bounds__(kThreads) void k_exact_expf(const float* x, float* 
     if (i < n) y[i] = exp_glibc(x[i]);
 }
 
+// Largest relative distance between exp_fast and exp_glibc over every fp32
+// in [lo, hi] (lo < hi <= 0), as an ordered-int max of the error's bits.
+__global__ void k_exp_fast_maxerr(float lo, float hi, unsigned int* out) {
+    // negative floats: the bit pattern grows with |x|; hi = 0 starts at -0.0
+    const unsigned int ulo = __float_as_uint(hi) | 0x80000000u, uhi = __float_as_uint(lo);
+    float worst = 0.0f;
+    for (unsigned long long i = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x;
+         i <= (unsigned long long)(uhi - ulo); i += (unsigned long long)gridDim.x * blockDim.x) {
+        const float x = __uint_as_float(ulo + (unsigned int)i);
+        const float g = exp_glibc(x), f = exp_fast(x);
+        if (g > 0.0f) worst = fmaxf(worst, fabsf(f - g) / g);
+    }
+    atomicMax(out, __float_as_uint(worst));
+}
+
 __global__ __launch_bounds__(kThreads) void k_ordered_sum(const float* x, int n, float* out) {
     __shared__ EosShared sh;
     float s = eos_sum(RowSrc{x}, n, sh);
@@ -204,6 +219,15 @@ __global__ void k_verify_combine(const int* __restrict__ tokens, const float* __
 }  // namespace
 
 // -------------------------------------------------------------- launchers
+
+extern "C" int cgk_exp_fast_maxerr(float lo, float hi, unsigned int* out_dev) {
+    if (!(lo < hi) || hi > 0.0f || lo < -104.0f) {
+        cgx_set_error("exp_fast_maxerr: range must satisfy -104 <= lo < hi <= 0");
+        return -1;
+    }
+    hipLaunchKernelGGL(k_exp_fast_maxerr, dim3(4096), dim3(256), 0, stream(), lo, hi, out_dev);
+    return launch_check("k_exp_fast_maxerr");
+}
 
 extern "C" int cgk_exact_expf(const float* x, float* y, int n) {
     hipLaunchKernelGGL(k_exact_expf, dim3((n + kThreads - 1) / kThreads), dim3(kThreads), 0,

@@ -77,6 +77,7 @@ int cgk_int4_matmul_generic(const float* x, int M, int K, int N, int gs,
 
 /* ------------------------------------------- acceptance and filters */
 int cgk_exact_expf(const float* x, float* y, int n);
+int cgk_exp_fast_maxerr(float lo, float hi, unsigned int* out_dev);
 int cgk_ordered_sum(const float* x, int n, float* out);
 int cgk_sample_temperature(const float* logits, int V, float T, float u, int* out);
 int cgk_sample_corrected(const float* q, const float* p, int V, float u, int* out);

@@ -65,6 +65,28 @@ __device__ __forceinline__ float exp_glibc(float x) {
     return (float)y;
 }
 
+// ------------------------------------------------- fast, certified expf
+// exp(x) for x in [kExpFastMin, 0]: x log2(e) = n + f by a two-part
+// Cody-Waite reduction in fp32, 2^f by v_exp_f32, times 2^n exactly.  Its
+// distance to exp_glibc(x) is at most kExpFastRel * exp_glibc(x) over that
+// whole range (checked on every fp32 input by the GPU test of
+// cgx_exp_fast_maxerr_dev); outside it the samplers use exp_glibc itself.
+constexpr float kExpFastMin = -87.0f;
+constexpr float kExpFastRel = 0x1p-20f;
+
+__device__ __forceinline__ float exp_fast(float x) {
+    const float kL2eHi = 0x1.715476p+0f;        // log2(e) rounded to fp32
+    const float kL2eLo = 0x1.4ae0bep-26f;       // log2(e) - kL2eHi
+    const float n = rintf(x * kL2eHi);
+    const float f = fmaf(x, kL2eLo, fmaf(x, kL2eHi, -n));
+    return ldexpf(__builtin_amdgcn_exp2f(f), (int)n);
+}
+
+// exp of x as cogito computes it (exp_glibc), or its certified approximation
+__device__ __forceinline__ float exp_cert(float x) {
+    return (x >= kExpFastMin && x <= 0.0f) ? exp_fast(x) : exp_glibc(x);
+}
+
 // ------------------------------------------------------ element generators
 
 struct RowSrc {                 // raw fp32 row
@@ -301,81 +323,45 @@ __device__ __forceinline__ float replay_chunk_staged(const G& g, int slot, int b
     return s;
 }
 
-// One round of the exact ordered sum: this thread's kCh values x (elements
-// rd*kRound + t*kCh + k, zero past n), starting from the exact running value
-// s_round.  Returns the exact value after the round; leaves the exact running
-// value at every chunk boundary of the round in sh.cstart/sh.cend[rd].  `g`
-// regenerates elements for the rare replays of chunks that were not staged.
+// Monoid element of one chunk in binade b from exact values (fp32 / int32:
+// y = x * 2^(23-b) is exact and below 2^24, so floor and fraction are exact).
+template <class XF>
+__device__ __forceinline__ Mono fold_chunk(XF xk, int b) {
+    const int e = b == -127 ? 149 : 23 - b;
+    int c0 = 0, c1 = 1;
+    int q0 = 0, q1 = 0;
+#pragma unroll
+    for (int k = 0; k < kCh; k++) {
+        const float y = ldexpf(xk(k), e);
+        const float f = floorf(y);
+        const float fr = y - f;
+        const int fi = (int)f;
+        if (fr == 0.5f) {
+            const int fo = fi & 1;
+            q0 += fi + ((c0 ^ fo) & 1);
+            q1 += fi + ((c1 ^ fo) & 1);
+            c0 = 0;
+            c1 = 0;
+        } else {
+            const int qi = fi + (fr > 0.5f ? 1 : 0);
+            const int qo = qi & 1;
+            q0 += qi;
+            q1 += qi;
+            c0 ^= qo;
+            c1 ^= qo;
+        }
+    }
+    return Mono{(double)q0, (double)q1, c0, c1};
+}
+
+// Segmented scan, walk and exact chunk boundaries of one round, shared by the
+// exact and the certified front ends.  `own`/`clean`/`b` are this chunk's
+// monoid element and binade; sh.binade, sh.dirty_slot and sh.dirty_vals are
+// written and synchronised by the caller.
 template <class G>
-__device__ __forceinline__ float eos_round(const float (&x)[kCh], const G& g, int rd, int n,
-                                           float s_round, EosShared& sh) {
+__device__ __forceinline__ float eos_tail(const Mono& own, bool clean, int b, const G& g, int rd,
+                                          int n, float s_round, EosShared& sh) {
     const int t = threadIdx.x;
-
-    // fp64 guide: exclusive / inclusive prefix of chunk sums
-    double gs = 0.0;
-#pragma unroll
-    for (int k = 0; k < kCh; k++) gs += (double)x[k];
-    const double inc = wave_incl_sum_d(gs);
-    if (lane_id() == 63) sh.wsum[wave_id()] = inc;
-    __syncthreads();
-    double wpre = 0.0;
-    for (int w = 0; w < wave_id(); w++) wpre += sh.wsum[w];
-    const double p_end = (double)s_round + wpre + inc;
-    const double p_start = p_end - gs;
-    const double delta = (double)(t * kCh + kCh + 1) * 0x1p-24 * (1.0 + 0x1p-20) + 0x1p-40;
-    const double lo = t == 0 ? (double)s_round : p_start * (1.0 - delta);
-    const double hi = p_end * (1.0 + delta);
-    const int b = binade_of(lo);
-    const bool clean = binade_of(hi) == b;
-
-    // own monoid element under binade b
-    Mono own = mono_id();
-    if (clean) {
-        const double sc = ulp_scale(b);
-        int c0 = 0, c1 = 1;
-        double q0 = 0.0, q1 = 0.0;
-#pragma unroll
-        for (int k = 0; k < kCh; k++) {
-            const double y = (double)x[k] * sc;
-            const double f = floor(y);
-            const double fr = y - f;
-            if (fr == 0.5) {
-                const int fo = (int)((long long)f & 1);
-                q0 += f + (double)((c0 ^ fo) & 1);
-                q1 += f + (double)((c1 ^ fo) & 1);
-                c0 = 0;
-                c1 = 0;
-            } else {
-                const double q = f + (fr > 0.5 ? 1.0 : 0.0);
-                const int qo = (int)((long long)q & 1);
-                q0 += q;
-                q1 += q;
-                c0 ^= qo;
-                c1 ^= qo;
-            }
-        }
-        own = Mono{q0, q1, c0, c1};
-    }
-    sh.binade[t] = clean ? b : kDirty;
-
-    // dirty chunks: stage their values for the walk (slots in chunk order)
-    {
-        const unsigned long long bal = __ballot(!clean);
-        const int below = __popcll(bal & ((1ull << lane_id()) - 1ull));
-        if (lane_id() == 0) sh.wcount[wave_id()] = __popcll(bal);
-        __syncthreads();
-        int off = 0;
-        for (int w = 0; w < wave_id(); w++) off += sh.wcount[w];
-        const int slot = off + below;
-        const bool staged = !clean && slot < kDirtySlots;
-        sh.dirty_slot[t] = staged ? slot : -1;
-        if (staged) {
-#pragma unroll
-            for (int k = 0; k < kCh; k++) sh.dirty_vals[slot][k] = x[k];
-        }
-    }
-    __syncthreads();
-
     // segmented scan of the monoid elements (segments = runs of one binade)
     const bool is_head = !clean || t == 0 || sh.binade[t - 1] != b;
     SegMono v;
@@ -484,6 +470,66 @@ __device__ __forceinline__ float eos_round(const float (&x)[kCh], const G& g, in
     return total;
 }
 
+// Binade of a chunk from the fp64 guide: [lo, hi] certainly contains the
+// sequential running value throughout the chunk (err_pre/err_end: absolute
+// error bounds of the guide values before / through this chunk).
+__device__ __forceinline__ int guide_binade(double gs, double err_pre, double err_end,
+                                            float s_round, EosShared& sh, bool* clean) {
+    const int t = threadIdx.x;
+    const double inc = wave_incl_sum_d(gs);
+    if (lane_id() == 63) sh.wsum[wave_id()] = inc;
+    __syncthreads();
+    double wpre = 0.0;
+    for (int w = 0; w < wave_id(); w++) wpre += sh.wsum[w];
+    const double p_end = (double)s_round + wpre + inc;
+    const double p_start = p_end - gs;
+    // k sequential fp32 additions of non-negative values stay within
+    // (1 +- 2^-24)^k <= 1 +- k 2^-24 (1 + 2^-7) of the real sum (k <= 2^15 + 33)
+    const double delta = (double)(t * kCh + kCh + 1) * 0x1p-24 * (1.0 + 0x1p-7) + 0x1p-40;
+    const double lo = t == 0 ? (double)s_round : (p_start - err_pre) * (1.0 - delta);
+    const double hi = (p_end + err_end) * (1.0 + delta);
+    const int b = binade_of(lo > 0.0 ? lo : 0.0);
+    *clean = binade_of(hi) == b;
+    return b;
+}
+
+// One round of the exact ordered sum: this thread's kCh values x (elements
+// rd*kRound + t*kCh + k, zero past n), starting from the exact running value
+// s_round.  Returns the exact value after the round; leaves the exact running
+// value at every chunk boundary of the round in sh.cstart/sh.cend[rd].  `g`
+// regenerates elements for the rare replays of chunks that were not staged.
+template <class G>
+__device__ __forceinline__ float eos_round(const float (&x)[kCh], const G& g, int rd, int n,
+                                           float s_round, EosShared& sh) {
+    const int t = threadIdx.x;
+    double gs = 0.0;
+#pragma unroll
+    for (int k = 0; k < kCh; k++) gs += (double)x[k];
+    bool clean;
+    const int b = guide_binade(gs, 0.0, 0.0, s_round, sh, &clean);
+    const Mono own = clean ? fold_chunk([&](int k) { return x[k]; }, b) : mono_id();
+    sh.binade[t] = clean ? b : kDirty;
+
+    // dirty chunks: stage their values for the walk (slots in chunk order)
+    {
+        const unsigned long long bal = __ballot(!clean);
+        const int below = __popcll(bal & ((1ull << lane_id()) - 1ull));
+        if (lane_id() == 0) sh.wcount[wave_id()] = __popcll(bal);
+        __syncthreads();
+        int off = 0;
+        for (int w = 0; w < wave_id(); w++) off += sh.wcount[w];
+        const int slot = off + below;
+        const bool staged = !clean && slot < kDirtySlots;
+        sh.dirty_slot[t] = staged ? slot : -1;
+        if (staged) {
+#pragma unroll
+            for (int k = 0; k < kCh; k++) sh.dirty_vals[slot][k] = x[k];
+        }
+    }
+    __syncthreads();
+    return eos_tail(own, clean, b, g, rd, n, s_round, sh);
+}
+
 // Exact ordered sum of g(0..n-1).  Leaves the exact running value at every
 // chunk boundary in sh.cstart / sh.cend (rounds x threads) for gen_find.
 template <class G>
@@ -588,6 +634,25 @@ __device__ __forceinline__ void load_vals(const S& src, int n, float pad, float 
     const int base = threadIdx.x * kCh;
 #pragma unroll
     for (int k = 0; k < kCh; k++) x[k] = base + k < n ? src(base + k) : pad;
+}
+
+// raw rows: 16-byte loads where the thread's 32 elements are whole and aligned
+__device__ __forceinline__ void load_vals(const RowSrc& src, int n, float pad, float (&x)[kCh]) {
+    const int base = threadIdx.x * kCh;
+    if (base + kCh <= n && ((uintptr_t)src.p & 15u) == 0) {
+        const float4* q = reinterpret_cast<const float4*>(src.p + base);
+#pragma unroll
+        for (int j = 0; j < kCh / 4; j++) {
+            const float4 v = q[j];
+            x[4 * j] = v.x;
+            x[4 * j + 1] = v.y;
+            x[4 * j + 2] = v.z;
+            x[4 * j + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < kCh; k++) x[k] = base + k < n ? src.p[base + k] : pad;
+    }
 }
 
 __device__ __forceinline__ float vals_max(const float (&x)[kCh], EosShared& sh) {

@@ -94,6 +94,15 @@ int cgx_exact_expf_dev(const float* x, float* y, int n) {
     return n ? cgk_exact_expf(x, y, n) : 0;
 }
 
+int cgx_exp_fast_maxerr_dev(float lo, float hi, unsigned int* out_dev) {
+    if (!out_dev) {
+        cgx_set_error("cgx_exp_fast_maxerr_dev: invalid argument");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    return cgk_exp_fast_maxerr(lo, hi, out_dev);
+}
+
 int cgx_ordered_sum_dev(const float* x, int n, float* out_dev) {
     if (!x || !out_dev || n <= 0) {
         cgx_set_error("cgx_ordered_sum_dev: invalid argument");

@@ -120,6 +120,11 @@ int cgx_filtered_dist(const float* logits, int V, float T, int top_k,
  * non-negative values. */
 int cgx_exact_expf_dev(const float* x, float* y, int n);
 int cgx_ordered_sum_dev(const float* x, int n, float* out_dev);
+/* Largest relative distance between the samplers' fast exponential and the
+ * exact one over every fp32 in [lo, hi] (-104 <= lo < hi <= 0), folded with
+ * an unsigned max into *out_dev as the float's bits (caller zeroes it).  The
+ * certified sampler paths assume it stays within 2^-20 on [-87, 0]. */
+int cgx_exp_fast_maxerr_dev(float lo, float hi, unsigned int* out_dev);
 
 /* ----------------------------------------------------------- KV cache */
 /* Drops positions >= new_len (rollback after a rejected draft). */

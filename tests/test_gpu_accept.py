@@ -44,6 +44,18 @@ def test_exact_expf_matches_host_libm(gpu, rng):
     np.testing.assert_array_equal(_bits(y[sample]), _bits(ref))
 
 
+def test_exp_fast_within_certified_bound(gpu):
+    # every fp32 in [-87, 0]: the certified sampler paths fold approximate
+    # exponentials and re-evaluate exactly only where 2^-20 relative error
+    # could change a rounding, so the bound must hold everywhere
+    out = DeviceArray.from_numpy(gpu, np.zeros(1, np.uint32))
+    assert gpu.cgx_exp_fast_maxerr_dev(-87.0, 0.0, out.ptr) == 0, last_error(gpu)
+    worst = out.numpy(np.uint32, (1,)).view(np.float32)[0]
+    assert 0.0 < worst <= 2.0 ** -20, worst
+    # and it is tight enough to be worth having: a few fp32 ulps
+    assert worst < 2.0 ** -21
+
+
 def _seq_sum(x: np.ndarray) -> np.float32:
     # left-to-right binary32 accumulation (np.add.accumulate is sequential)
     return np.add.accumulate(np.ascontiguousarray(x, np.float32), dtype=np.float32)[-1]
@@ -96,11 +108,15 @@ def test_temperature_probs_bitexact(gpu, oracle, rng, V, T):
 
 @pytest.mark.parametrize("V", [1, 3, 1000, 32000, 128256])
 def test_sample_temperature_bitexact(gpu, oracle, rng, V):
-    for trial in range(6):
-        T = [1.0, 0.8, 0.7, 1.3, 1.0, 2.0][trial]
+    for trial in range(8):
+        T = [1.0, 0.8, 0.7, 1.3, 1.0, 2.0, 1.0, 0.5][trial]
         x = rng.normal(0, 2, V).astype(np.float32)
         if trial == 4:
             x[rng.integers(0, V, min(V, 7))] = x.max()
+        if trial >= 6:
+            # few distinct logits on a coarse grid: repeated exponentials make
+            # exact roundings and ties in the running sums common
+            x = (rng.integers(-48, 1, V) / 4.0).astype(np.float32)
         p = _oracle_probs(oracle, x, T)
         cdf = np.add.accumulate(p, dtype=np.float32)
         us = list(rng.uniform(0, 1, 6).astype(np.float32))
@@ -179,6 +195,27 @@ def test_verify_chain_shapes(gpu, oracle, V, gamma, T):
     for rep in range(3):
         target, draft, toks, u = _config1_inputs(oracle, rng, V, gamma, T)
         target[:gamma] = draft + rng.normal(0, 0.3 * rep, draft.shape).astype(np.float32)
+        n_g, out_g, ap_g, n_o, out_o, ap_o = _verify_both(gpu, oracle, target, draft, toks,
+                                                          u, gamma, V, T)
+        np.testing.assert_array_equal(_bits(ap_g), _bits(ap_o))
+        assert n_g == n_o
+        np.testing.assert_array_equal(out_g[:n_g + 1], out_o[:n_o + 1])
+
+
+@pytest.mark.parametrize("V", [1000, 32000])
+def test_verify_chain_grid_logits(gpu, oracle, V):
+    # logits on a coarse grid (repeated exponentials, exact roundings and ties
+    # in the running sums of the certified single-round path)
+    rng = np.random.default_rng(5 * V)
+    gamma, T = 4, 1.0
+    for rep in range(4):
+        target, draft, toks, u = _config1_inputs(oracle, rng, V, gamma, T)
+        draft = (rng.integers(-40, 1, draft.shape) / 4.0).astype(np.float32)
+        target = (draft[[0, 1, 2, 3, 3]] + rng.integers(-2 * rep, 2 * rep + 1, target.shape)
+                  / 4.0).astype(np.float32)
+        for i in range(gamma):
+            row = np.ascontiguousarray(draft[i])
+            toks[i] = oracle.orc_sample_temperature(ptr(row), V, T, float(rng.uniform()))
         n_g, out_g, ap_g, n_o, out_o, ap_o = _verify_both(gpu, oracle, target, draft, toks,
                                                           u, gamma, V, T)
         np.testing.assert_array_equal(_bits(ap_g), _bits(ap_o))
