@@ -19,6 +19,7 @@ import numpy as np
 import pytest
 
 from cogito_amd.capi import CgFlashAttnParams
+import oracle_lib
 from oracle_lib import RefKv, ptr, ref_tensor  # noqa: F401
 
 FLT_MAX = np.finfo(np.float32).max
@@ -321,3 +322,39 @@ def test_fill_normal_moments_and_determinism(oracle):
     assert abs(np.corrcoef(a, c)[0, 1]) < 0.01
     s = fill(oracle, 1000, 123, 7, 0.02)
     np.testing.assert_allclose(s, (a[:1000] * 0.02).astype(np.float32), rtol=1e-6)
+
+
+# ----------------------------------------------------- RMSNorm and SwiGLU
+
+@pytest.mark.parametrize("rows,d,eps", [(1, 768, 1e-5), (5, 4096, 1e-5), (3, 70, 1e-6)])
+def test_rmsnorm_vs_reference_and_fp64(ref, oracle, rng, rows, d, eps):
+    # orc_rmsnorm restates tensor_kernels.c:888-909; the compiled reference
+    # pins it bitwise, fp64 pins the formula (a dropped eps or a sum over the
+    # wrong axis fails the second check)
+    x = rng.normal(0, 2, (rows, d)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    y = np.zeros_like(x)
+    oracle.orc_rmsnorm(ptr(x), ptr(w), ptr(y), rows, d, eps)
+    tx, tw, ty = (oracle_lib.ref_tensor(ref, a) for a in (x, w, np.zeros_like(x)))
+    ref.cg_cuda_rmsnorm_forward(tx, tw, ty, eps)
+    yr = oracle_lib.ref_tensor_np(ty)
+    for t in (tx, tw, ty):
+        ref.cg_tensor_free(t)
+    np.testing.assert_array_equal(y.view(np.uint32), yr.view(np.uint32))
+    xd = x.astype(np.float64)
+    exp = w * xd / np.sqrt((xd * xd).mean(axis=1, keepdims=True) + eps)
+    np.testing.assert_allclose(y, exp, rtol=2e-6, atol=1e-7)
+
+
+def test_swiglu_closed_form(oracle, rng):
+    # transformer.c:116-129: g / (1 + exp(-g)) * u
+    g = np.concatenate([rng.normal(0, 3, 5000), [0.0, -0.0, 30.0, -30.0, -100.0, 88.0]])
+    g = g.astype(np.float32)
+    u = rng.normal(0, 1, g.size).astype(np.float32)
+    out = np.zeros_like(g)
+    oracle.orc_swiglu(ptr(g), ptr(u), ptr(out), g.size)
+    gd = g.astype(np.float64)
+    exp = gd / (1.0 + np.exp(-gd)) * u
+    np.testing.assert_allclose(out, exp, rtol=1e-6, atol=1e-30)
+    # g = 0 gives 0; g = -100 overflows exp(100) to inf and gives (signed) 0
+    assert out[-6] == 0.0 and out[-2] == 0.0
