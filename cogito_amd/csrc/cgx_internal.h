@@ -23,7 +23,7 @@ int cgx_ensure_init(void);
  * names the same slot. */
 enum { CGX_SLOT_IN0 = 0, CGX_SLOT_IN1, CGX_SLOT_IN2, CGX_SLOT_IN3,
        CGX_SLOT_OUT0, CGX_SLOT_OUT1, CGX_SLOT_WS0, CGX_SLOT_WS1,
-       CGX_SLOT_WS2, CGX_SLOT_WS3, CGX_NUM_SLOTS };
+       CGX_SLOT_WS2, CGX_SLOT_WS3, CGX_SLOT_WS4, CGX_NUM_SLOTS };
 void* cgx_scratch(int slot, size_t bytes);
 /* Zero-initialised counters that kernels reset themselves after use. */
 unsigned int* cgx_counters(size_t count);
@@ -77,6 +77,10 @@ int cgk_int4_matmul_generic(const float* x, int M, int K, int N, int gs,
 
 /* ------------------------------------------- acceptance and filters */
 int cgk_exact_expf(const float* x, float* y, int n);
+int cgk_verify_pipe_supported(int batch, int gamma, int V, float T);
+int cgk_verify_pipe(const float* target, const float* draft, const int* tokens, const float* u,
+                    int batch, int gamma, int V, float T, float* accept_prob, int* out_tokens,
+                    int* n_accepted);
 int cgk_exp_fast_maxerr(float lo, float hi, unsigned int* out_dev);
 int cgk_ordered_sum(const float* x, int n, float* out);
 int cgk_sample_temperature(const float* logits, int V, float T, float u, int* out);

@@ -87,6 +87,15 @@ __device__ __forceinline__ float exp_cert(float x) {
     return (x >= kExpFastMin && x <= 0.0f) ? exp_fast(x) : exp_glibc(x);
 }
 
+// Absolute error bounds, relative to the approximation, of
+//   e~ = exp_cert(a)                        against expf(a)
+//   p~ = e~ * fl(1 / S)                     against fl(expf(a) / S)
+//   r~ = max(0, p~ - q~) (fp32 subtraction) against max(0, fl(p - q))
+// (exp_cert within 2^-20; each fp32 rounding adds at most 2^-24)
+constexpr float kExpErr = kExpFastRel * (1.0f + 0x1p-10f);
+constexpr float kProbRel = kExpFastRel * (1.0f + 0x1p-10f) + 0x1p-21f;
+constexpr float kResRel = kProbRel + 0x1p-21f;
+
 // ------------------------------------------------------ element generators
 
 struct RowSrc {                 // raw fp32 row

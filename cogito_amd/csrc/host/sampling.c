@@ -221,6 +221,9 @@ int cgx_verify_chain_batch_dev(const float* target_logits, const float* draft_lo
         return verify_filtered(target_logits, draft_logits, draft_tokens, u, batch, gamma, V,
                                temperature, top_k, top_p, ap, corr, bonus, out_tokens,
                                n_accepted);
+    if (cgk_verify_pipe_supported(batch, gamma, V, temperature))
+        return cgk_verify_pipe(target_logits, draft_logits, draft_tokens, u, batch, gamma, V,
+                               temperature, accept_prob, out_tokens, n_accepted);
     return cgk_verify_chain(target_logits, draft_logits, draft_tokens, u, batch, gamma, V,
                             temperature, ap, corr, bonus, out_tokens, n_accepted);
 }

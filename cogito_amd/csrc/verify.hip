@@ -1,0 +1,1124 @@
+// verify.hip -- the verify composition (accept tests, first reject, correction
+// or bonus draw) as a chunk-parallel pipeline over many workgroups per row,
+// bit-identical to cogito's sequential samplers:
+//
+//   cg_sample_temperature  src/inference/speculative.c:54-75
+//   cg_acceptance_prob     speculative.c:49-52
+//   cg_sample_corrected    speculative.c:148-172
+//
+// Every sum the reference forms is a left-to-right binary32 sum; its exact
+// value is reproduced with the binade argument of eos.hpp (inside one binade
+// every addition advances the running value by rne(x / ulp) ulps, ties aside),
+// but the elements are not evaluated exactly up front.  Each element gets a
+// fast approximation with a rigorous error bound (exp_fast, a rounded
+// reciprocal); the approximation decides the rounding whenever no
+// half-integer lies within the bound of x / ulp, and the element is
+// re-evaluated exactly (glibc-identical expf, IEEE division) only otherwise.
+//
+// Rows are cut into segments of 4096 elements (one 256-thread workgroup, 16
+// elements -- one chunk -- per thread).  Per row and pass:
+//   stats : segment maximum and an approximate segment sum with an error
+//           bound (against the segment's own maximum, rescaled later)
+//   fold  : the row maximum; exact arguments; the binade of every chunk from
+//           the approximate prefix (guide) and its bound; chunk summaries
+//           (ulp increments per input parity); a segmented scan into runs of
+//           one binade; chunks that may cross a binade are staged exactly
+//   walk  : one wave per row composes the runs and replays the staged chunks
+//           with real fp32 additions: the exact running value at every
+//           segment and run start, and the row sum
+// Pass 1 covers every target and draft row; the decisions then pick, per
+// chain, the one row (bonus: target row gamma, probabilities p = e / S) or
+// row pair (first reject j: residual max(0, p - q)) whose CDF is searched,
+// pass 2 sums it the same way, and the find replays the one chunk that holds
+// the draw.  Chains with non-finite rows, or a residual mass below 1e-10
+// (the reference then samples softmax(p)), are finished by the single-block
+// exact kernel at the end.
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cstdint>
+
+#include "cgx_internal.h"
+
+#include "eos.hpp"
+
+namespace {
+
+namespace vp {
+
+constexpr int kT = 256;                  // threads per segment workgroup
+constexpr int kW = kT / 64;
+constexpr int kC = 16;                   // elements per chunk (per thread)
+constexpr int kSeg = kT * kC;            // 4096 elements per segment
+constexpr int kItemCap = 64;             // runs per segment (more: exact replay)
+constexpr int kDirtyCap = kT;            // staged chunks per segment (all of them)
+constexpr int kWalkItems = 512;          // walk: runs held in LDS per batch
+constexpr int kMaxGamma = 64;
+constexpr int kMaxSegs = 64;             // segments per row (V <= 262144)
+
+enum { kKindExp = 0, kKindProb = 1, kKindRes = 2 };
+
+inline hipStream_t stream() { return (hipStream_t)cgx_stream(); }
+
+int launch_check(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        cgx_set_error("%s launch failed: %s", what, hipGetErrorString(e));
+        return -1;
+    }
+    return 0;
+}
+
+// One walk item: a run of clean chunks of one binade (total effect on the
+// running value) or a run of chunks whose exact values are staged (chunks
+// that may cross a binade).  A run ends where the next item starts.
+struct Item {
+    int chunk;      // first chunk (within the segment)
+    int binade;     // kDirty for staged chunks
+    int q0, q1;     // run increments in ulps for input parity 0 / 1
+    int c;          // output parities: bit 0 for input parity 0, bit 1 for 1
+    int slot;       // staging slot of the first staged chunk
+    int pad0, pad1;
+};
+
+// Monoid of a run of additions inside one binade, integer form (a run never
+// advances more than 2^24 ulps: it stays in its binade).
+struct MI {
+    int q0, q1, c;
+};
+
+__device__ __forceinline__ MI mi_id() { return MI{0, 0, 2}; }
+
+__device__ __forceinline__ MI mi_then(const MI& a, const MI& b) {
+    const int a0 = a.c & 1, a1 = (a.c >> 1) & 1;
+    const int b0 = b.c & 1, b1 = (b.c >> 1) & 1;
+    MI r;
+    r.q0 = a.q0 + (a0 ? b.q1 : b.q0);
+    r.q1 = a.q1 + (a1 ? b.q1 : b.q0);
+    r.c = (a0 ? b1 : b0) | ((a1 ? b1 : b0) << 1);
+    return r;
+}
+
+struct SMI {
+    MI m;
+    int flag;       // a run starts inside this range
+};
+
+__device__ __forceinline__ SMI smi_then(const SMI& a, const SMI& b) {
+    if (b.flag) return b;
+    return SMI{mi_then(a.m, b.m), a.flag};
+}
+
+template <int CTRL, int RMASK>
+__device__ __forceinline__ SMI dpp_smi(const SMI& v) {
+    SMI o;
+    o.m.q0 = dpp_i<CTRL, RMASK>(v.m.q0);
+    o.m.q1 = dpp_i<CTRL, RMASK>(v.m.q1);
+    o.m.c = dpp_i<CTRL, RMASK>(v.m.c);
+    o.flag = dpp_i<CTRL, RMASK>(v.flag);
+    return o;
+}
+
+__device__ __forceinline__ SMI wave_incl_smi(SMI v) {
+    SMI o;
+    o = dpp_smi<0x111, 0xF>(v); if (dpp_step_valid(0)) v = smi_then(o, v);
+    o = dpp_smi<0x112, 0xF>(v); if (dpp_step_valid(1)) v = smi_then(o, v);
+    o = dpp_smi<0x114, 0xF>(v); if (dpp_step_valid(2)) v = smi_then(o, v);
+    o = dpp_smi<0x118, 0xF>(v); if (dpp_step_valid(3)) v = smi_then(o, v);
+    o = dpp_smi<0x142, 0xA>(v); if (dpp_step_valid(4)) v = smi_then(o, v);
+    o = dpp_smi<0x143, 0xC>(v); if (dpp_step_valid(5)) v = smi_then(o, v);
+    return v;
+}
+
+// Binade of a non-negative fp32 from its bits (-127: zero and subnormals),
+// and s advanced by a run summary in its binade b.  Inside a binade s / ulp
+// is 2^23 + mantissa (bits for b = -127), so the parity is the low bit and
+// adding q ulps adds q to the bit pattern (reaching 2^(b+1) exactly included).
+__device__ __forceinline__ int binade_bits(float s) {
+    const int ex = (int)(__float_as_uint(s) >> 23);
+    return ex == 0 ? -127 : ex - 127;
+}
+
+__device__ __forceinline__ float mi_apply(float s, const MI& m) {
+    const unsigned int u = __float_as_uint(s);
+    return __uint_as_float(u + (unsigned int)((u & 1u) ? m.q1 : m.q0));
+}
+
+// ------------------------------------------------------------- workspace
+
+struct Rows {            // pass-1 rows: per chain target 0..gamma, draft 0..gamma-1
+    const float* target;
+    const float* draft;
+    int gamma, V;
+    __device__ const float* row(int r) const {
+        const int per = 2 * gamma + 1, c = r / per, i = r % per;
+        return i <= gamma ? target + ((size_t)c * (gamma + 1) + i) * V
+                          : draft + ((size_t)c * gamma + (i - gamma - 1)) * V;
+    }
+};
+
+struct Task {            // pass-2 row of a chain
+    int kind;            // kKindProb (bonus), kKindRes (first reject), -1: finished elsewhere
+    int ra, rb;          // pass-1 rows: target (and draft for kKindRes)
+    int j;               // output position
+    float u;             // the draw
+    int pad[3];
+};
+
+struct Work {
+    int R1, chains, nseg;
+    float* seg_m;        // [R1][nseg] segment maxima
+    double* seg_gh;      // [R1][nseg][2] approximate sums G, H (see k_seg_stats)
+    int* seg_bad;        // [R1][nseg] NaN or +inf present
+    float* row_m;        // [R1]
+    float* row_S;        // [R1 + chains] row sums
+    int* cnt;            // [Rall][nseg][2] items, staged chunks (-1: overflow)
+    Item* items;         // [Rall][nseg][kItemCap]
+    float* dirty;        // [Rall][nseg][kDirtyCap][kC]
+    float* seg_start;    // [Rall][nseg + 1] exact running value (last: row sum)
+    float* item_start;   // [Rall][nseg][kItemCap]
+    float* dirty_start;  // [Rall][nseg][kDirtyCap] exact value at each staged chunk start
+    double* task_ge;     // [chains][nseg][2] residual guide sums, bounds
+    Task* task;          // [chains]
+    int* flags;          // [chains] 1: non-finite row, 2: residual mass < 1e-10
+};
+
+__device__ __forceinline__ size_t segi(const Work& w, int row, int seg) {
+    return (size_t)row * w.nseg + seg;
+}
+
+// Row values of one pass: exact element values, and approximations with
+// absolute error bounds, computed from the exact exponent arguments.
+template <int KIND>
+struct Eval {
+    const float* a;
+    const float* b;
+    float ma, mb, Sa, Sb, ia, ib, T;
+    int V;
+
+    __device__ __forceinline__ float arg(float x, float m) const {
+        return T == 1.0f ? __fsub_rn(x, m) : __fdiv_rn(__fsub_rn(x, m), T);
+    }
+    // exact value from arguments
+    __device__ __forceinline__ float exact(float A, float B) const {
+        if constexpr (KIND == kKindExp) {
+            return exp_glibc(A);
+        } else if constexpr (KIND == kKindProb) {
+            return __fdiv_rn(exp_glibc(A), Sa);
+        } else {
+            return fmaxf(0.0f, __fsub_rn(__fdiv_rn(exp_glibc(A), Sa), __fdiv_rn(exp_glibc(B), Sb)));
+        }
+    }
+    // approximation and its bound
+    __device__ __forceinline__ float2 approx(float A, float B) const {
+        if constexpr (KIND == kKindExp) {
+            const float e = exp_cert(A);
+            return make_float2(e, e * kExpErr);
+        } else if constexpr (KIND == kKindProb) {
+            const float p = exp_cert(A) * ia;
+            return make_float2(p, p * kProbRel);
+        } else {
+            const float p = exp_cert(A) * ia, q = exp_cert(B) * ib;
+            return make_float2(fmaxf(0.0f, p - q), kResRel * (p + q));
+        }
+    }
+    // exact value of element j, from memory
+    __device__ __forceinline__ float at(int j) const {
+        if (j < 0 || j >= V) return 0.0f;
+        const float A = arg(a[j], ma);
+        const float B = KIND == kKindRes ? arg(b[j], mb) : 0.0f;
+        return exact(A, B);
+    }
+    // this thread's chunk: exact arguments
+    __device__ __forceinline__ void args(int base, float (&A)[kC], float (&B)[kC]) const;
+};
+
+// exact args of this thread's chunk (-inf past V: value 0)
+__device__ __forceinline__ void load_args(const float* p, float m, float T, int base, int V,
+                                          float (&A)[kC]) {
+    float x[kC];
+    if (base + kC <= V && ((uintptr_t)(p + base) & 15u) == 0) {
+        const float4* q = reinterpret_cast<const float4*>(p + base);
+#pragma unroll
+        for (int i = 0; i < kC / 4; i++) {
+            const float4 v = q[i];
+            x[4 * i] = v.x;
+            x[4 * i + 1] = v.y;
+            x[4 * i + 2] = v.z;
+            x[4 * i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < kC; k++) x[k] = base + k < V ? p[base + k] : -__builtin_inff();
+    }
+    if (T == 1.0f) {
+#pragma unroll
+        for (int k = 0; k < kC; k++)
+            A[k] = base + k < V ? __fsub_rn(x[k], m) : -__builtin_inff();
+    } else {
+#pragma unroll
+        for (int k = 0; k < kC; k++)
+            A[k] = base + k < V ? __fdiv_rn(__fsub_rn(x[k], m), T) : -__builtin_inff();
+    }
+}
+
+template <int KIND>
+__device__ __forceinline__ void Eval<KIND>::args(int base, float (&A)[kC], float (&B)[kC]) const {
+    load_args(a, ma, T, base, V, A);
+    if constexpr (KIND == kKindRes) load_args(b, mb, T, base, V, B);
+}
+
+// Summary of one chunk in binade b from its approximations (v, bound er) and
+// exact arguments: exact, re-evaluating the elements the bound cannot decide.
+template <int KIND>
+__device__ __forceinline__ MI fold_chunk16(const Eval<KIND>& ev, const float (&A)[kC],
+                                           const float (&B)[kC], float (&v)[kC],
+                                           const float (&er)[kC], int b) {
+    const int e = b == -127 ? 149 : 23 - b;
+    unsigned amb = 0u;
+    int Q = 0;
+#pragma unroll
+    for (int k = 0; k < kC; k++) {
+        const float y = ldexpf(v[k], e);
+        const float rr = rintf(y);
+        // a half-integer within the bound of y (ties included)
+        if (fabsf(y - rr) >= 0.5f - ldexpf(er[k], e)) amb |= 1u << k;
+        Q += (int)rr;
+    }
+    if (amb == 0u) return MI{Q, Q, (Q & 1) | (((Q & 1) ^ 1) << 1)};
+#pragma unroll
+    for (int k = 0; k < kC; k++)
+        if ((amb >> k) & 1u) v[k] = ev.exact(A[k], B[k]);
+    int q0 = 0, q1 = 0, c0 = 0, c1 = 1;
+#pragma unroll
+    for (int k = 0; k < kC; k++) {
+        const float y = ldexpf(v[k], e);
+        const float f = floorf(y);
+        const float fr = y - f;
+        const int fi = (int)f;
+        if (fr == 0.5f) {
+            // a tie rounds to the even neighbour: the running parity decides
+            const int fo = fi & 1;
+            q0 += fi + ((c0 ^ fo) & 1);
+            q1 += fi + ((c1 ^ fo) & 1);
+            c0 = 0;
+            c1 = 0;
+        } else {
+            const int qi = fi + (fr > 0.5f ? 1 : 0);
+            q0 += qi;
+            q1 += qi;
+            c0 ^= qi & 1;
+            c1 ^= qi & 1;
+        }
+    }
+    return MI{q0, q1, c0 | (c1 << 1)};
+}
+
+// ------------------------------------------------------ block reductions
+
+__device__ __forceinline__ float block_max256(float v, float* s_w) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    __syncthreads();
+    if (lane_id() == 0) s_w[wave_id()] = v;
+    __syncthreads();
+    float r = s_w[0];
+    for (int w = 1; w < kW; w++) r = fmaxf(r, s_w[w]);
+    return r;
+}
+
+__device__ __forceinline__ double block_sum256_d(double v, double* s_w) {
+    v = wave_incl_sum_d(v);
+    __syncthreads();
+    if (lane_id() == 63) s_w[wave_id()] = v;
+    __syncthreads();
+    double r = 0.0;
+    for (int w = 0; w < kW; w++) r += s_w[w];
+    return r;
+}
+
+// inclusive fp64 scan over the block, and the block total
+__device__ __forceinline__ double block_incl256_d(double v, double* s_w, double* total) {
+    v = wave_incl_sum_d(v);
+    __syncthreads();
+    if (lane_id() == 63) s_w[wave_id()] = v;
+    __syncthreads();
+    double pre = 0.0, tot = 0.0;
+    for (int w = 0; w < kW; w++) {
+        pre += w < wave_id() ? s_w[w] : 0.0;
+        tot += s_w[w];
+    }
+    *total = tot;
+    return pre + v;
+}
+
+// first thread (lowest index) with pred, or kT
+__device__ __forceinline__ int block_first256(bool pred, int* s_w) {
+    const unsigned long long bal = __ballot(pred);
+    __syncthreads();
+    if (lane_id() == 0) s_w[wave_id()] = bal ? wave_id() * 64 + __builtin_ctzll(bal) : kT;
+    __syncthreads();
+    int r = kT;
+    for (int w = 0; w < kW; w++) r = min(r, s_w[w]);
+    return r;
+}
+
+// ------------------------------------------------------- stats (pass 1)
+
+// Per segment of a pass-1 row: its maximum m_s and, against m_s, the
+// approximate sum G = sum g_i of g_i = exp(a'_i), a'_i = (x_i - m_s) / T as
+// rounded, and H = sum g_i |a'_i|.  With c = exp((m_s - m) / T) for the row
+// maximum m, the row's exact elements e_i = expf((x_i - m) / T) satisfy
+//   |sum e_i - c G| <= c (2^-22 1.01 H + (2^-23 1.01 D + 2^-18) G) + 2^-136,
+// D = (m - m_s) / T: the two rounded arguments differ from (x - m)/T and
+// (x - m_s)/T by at most 2^-23 |a| each, expf and exp_cert add 2^-23 and
+// 2^-20 relative, the fp32 partial sums 2^-20, subnormal results 2^-149 each.
+__global__ __launch_bounds__(kT) void k_seg_stats(Rows rows, float T, Work w) {
+    __shared__ float s_f[kW];
+    __shared__ double s_d[kW];
+    const int seg = blockIdx.x, r = blockIdx.y, t = threadIdx.x;
+    const float* p = rows.row(r);
+    const int base = seg * kSeg + t * kC, V = rows.V;
+    float x[kC];
+    bool bad = false;
+    float mx = -__builtin_inff();
+    if (base + kC <= V && ((uintptr_t)(p + base) & 15u) == 0) {
+        const float4* q = reinterpret_cast<const float4*>(p + base);
+#pragma unroll
+        for (int i = 0; i < kC / 4; i++) {
+            const float4 v = q[i];
+            x[4 * i] = v.x;
+            x[4 * i + 1] = v.y;
+            x[4 * i + 2] = v.z;
+            x[4 * i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < kC; k++) x[k] = base + k < V ? p[base + k] : -__builtin_inff();
+    }
+#pragma unroll
+    for (int k = 0; k < kC; k++) {
+        bad |= !(x[k] <= FLT_MAX) && !(x[k] == -__builtin_inff());   // NaN or +inf
+        mx = fmaxf(mx, x[k]);
+    }
+    const float ms = block_max256(mx, s_f);
+    float g = 0.0f, h = 0.0f;
+    if (ms > -__builtin_inff()) {
+#pragma unroll
+        for (int k = 0; k < kC; k++) {
+            if (x[k] > -__builtin_inff()) {
+                const float a = T == 1.0f ? __fsub_rn(x[k], ms) : __fdiv_rn(__fsub_rn(x[k], ms), T);
+                const float e = exp_cert(a);
+                g += e;
+                h += e * fabsf(a);
+            }
+        }
+    }
+    const double G = block_sum256_d((double)g, s_d);
+    const double H = block_sum256_d((double)h, s_d);
+    const int nbad = __syncthreads_or(bad);
+    if (t == 0) {
+        const size_t i = segi(w, r, seg);
+        w.seg_m[i] = ms;
+        w.seg_gh[2 * i] = G;
+        w.seg_gh[2 * i + 1] = H;
+        w.seg_bad[i] = nbad;
+    }
+}
+
+// row maximum of a pass-1 row from its segment maxima
+__device__ __forceinline__ float row_max(const Work& w, int r, float* s_f) {
+    float m = -__builtin_inff();
+    for (int s = threadIdx.x; s < w.nseg; s += kT) m = fmaxf(m, w.seg_m[segi(w, r, s)]);
+    return block_max256(m, s_f);
+}
+
+// guide of pass-1 row r over segments [0, seg): sum of c G and its bound
+__device__ __forceinline__ void exp_prefix(const Work& w, int r, int seg, float m, float T,
+                                           double* s_d, double* P, double* E) {
+    double cg = 0.0, eb = 0.0;
+    const int s = threadIdx.x;
+    if (s < seg) {
+        const size_t i = segi(w, r, s);
+        const double G = w.seg_gh[2 * i], H = w.seg_gh[2 * i + 1];
+        const float ms = w.seg_m[i];
+        if (G > 0.0) {
+            const double D = ((double)m - (double)ms) / (double)T;
+            const double c = exp(-D) * (1.0 + 0x1p-40);
+            cg = c * G;
+            eb = c * (0x1p-22 * 1.01 * H + (0x1p-23 * 1.01 * D + 0x1p-18) * G) + 0x1p-136;
+        }
+    }
+    *P = block_sum256_d(cg, s_d);
+    *E = block_sum256_d(eb, s_d);
+}
+
+// ------------------------------------------------------------ the fold
+
+struct FoldShared {
+    float f[kW];
+    double d[kW];
+    int i[kW];
+    SMI wagg[kW];
+    int bin[kT];
+    int nitems, ndirty;
+};
+
+// One segment of a row through the certified fold: items and staged chunks
+// for the walk.  P0/E0: guide of the row before this segment and its bound.
+template <int KIND>
+__device__ void fold_segment(const Eval<KIND>& ev, const Work& w, int row, int seg, double P0,
+                             double E0, FoldShared& sh) {
+    const int t = threadIdx.x;
+    const int base = seg * kSeg + t * kC;
+    float A[kC], B[kC];
+    ev.args(base, A, B);
+    float v[kC], er[kC];
+    float gs = 0.0f, ge = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kC; k++) {
+        const float2 q = ev.approx(A[k], B[k]);
+        v[k] = q.x;
+        er[k] = q.y;
+        gs += q.x;
+        ge += q.y;
+    }
+    ge += gs * 0x1p-19f;                      // rounding of the 16-term fp32 sum
+    double tot;
+    const double pe = block_incl256_d((double)gs, sh.d, &tot);
+    const double ee = block_incl256_d((double)ge, sh.d, &tot);
+    const double Pend = P0 + pe, Pst = Pend - (double)gs;
+    const double Eend = (E0 + ee) * (1.0 + 0x1p-30) + Pend * 0x1p-40;
+    const double Est = Eend - (double)ge + Pst * 0x1p-40;
+    // k sequential fp32 additions of non-negative values stay within
+    // [(1 - 2^-24)^k, (1 + 2^-24)^k] of the real sum: >= 1 - ku, <= 1 + ku / (1 - ku)
+    const double ks = (double)base * 0x1p-24, ke = (double)(base + kC) * 0x1p-24;
+    double lo = base == 0 ? 0.0 : (Pst - Est) * (1.0 - ks);
+    if (!(lo > 0.0)) lo = 0.0;
+    const double hi = (Pend + Eend) * (1.0 + ke / (1.0 - ke)) + 0x1p-140;
+    const int b = binade_of(lo);
+    const bool clean = binade_of(hi) == b;
+    const MI own = clean ? fold_chunk16(ev, A, B, v, er, b) : mi_id();
+    sh.bin[t] = clean ? b : kDirty;
+    __syncthreads();
+    const bool head = t == 0 || sh.bin[t - 1] != sh.bin[t];
+    const bool last = clean && (t == kT - 1 || sh.bin[t + 1] != b);
+
+    // item index (heads in order) and staging slot (dirty chunks in order)
+    const unsigned long long hb = __ballot(head), db = __ballot(!clean);
+    const unsigned long long below = (1ull << lane_id()) - 1ull;
+    if (lane_id() == 0) sh.i[wave_id()] = __popcll(hb) | (__popcll(db) << 16);
+    SMI sv{own, head ? 1 : 0};
+    sv = wave_incl_smi(sv);
+    if (lane_id() == 63) sh.wagg[wave_id()] = sv;
+    __syncthreads();
+    int hoff = 0, doff = 0, htot = 0, dtot = 0;
+    SMI pre{mi_id(), 0};
+    for (int ww = 0; ww < kW; ww++) {
+        const int hc = sh.i[ww] & 0xffff, dc = sh.i[ww] >> 16;
+        if (ww < wave_id()) {
+            hoff += hc;
+            doff += dc;
+            pre = smi_then(pre, sh.wagg[ww]);
+        }
+        htot += hc;
+        dtot += dc;
+    }
+    if (wave_id() > 0) sv = smi_then(pre, sv);
+    const int item = hoff + __popcll(hb & below) + (head ? 0 : -1);
+    const int slot = doff + __popcll(db & below);     // consecutive within a dirty run
+    const bool over = htot > kItemCap;
+    const size_t si = segi(w, row, seg);
+    Item* it = w.items + si * kItemCap;
+    if (!over) {
+        if (head) {
+            it[item].chunk = t;
+            it[item].binade = clean ? b : kDirty;
+            it[item].slot = clean ? -1 : slot;
+        }
+        if (last) {
+            it[item].q0 = sv.m.q0;
+            it[item].q1 = sv.m.q1;
+            it[item].c = sv.m.c;
+        }
+        if (!clean) {
+            float* dv = w.dirty + (si * kDirtyCap + slot) * kC;
+#pragma unroll
+            for (int k = 0; k < kC; k++) {
+                dv[k] = base + k < ev.V ? ev.exact(A[k], B[k]) : 0.0f;
+                __builtin_amdgcn_sched_barrier(0);   // one exact element live at a time
+            }
+        }
+    }
+    if (t == 0) {
+        w.cnt[2 * si] = over ? -1 : htot;
+        w.cnt[2 * si + 1] = over ? -1 : dtot;
+    }
+}
+
+__device__ __forceinline__ Eval<kKindExp> pass1_eval(const Rows& rows, int r, float m, float T) {
+    Eval<kKindExp> ev;
+    ev.a = rows.row(r);
+    ev.b = nullptr;
+    ev.ma = m;
+    ev.mb = 0.0f;
+    ev.Sa = ev.Sb = 1.0f;
+    ev.ia = ev.ib = 1.0f;
+    ev.T = T;
+    ev.V = rows.V;
+    return ev;
+}
+
+template <int KIND>
+__device__ __forceinline__ Eval<KIND> task_eval(const Rows& rows, const Work& w, const Task& tk,
+                                                float T) {
+    Eval<KIND> ev;
+    ev.a = rows.row(tk.ra);
+    ev.b = KIND == kKindRes ? rows.row(tk.rb) : nullptr;
+    ev.ma = w.row_m[tk.ra];
+    ev.mb = KIND == kKindRes ? w.row_m[tk.rb] : 0.0f;
+    ev.Sa = w.row_S[tk.ra];
+    ev.Sb = KIND == kKindRes ? w.row_S[tk.rb] : 1.0f;
+    ev.ia = 1.0f / ev.Sa;
+    ev.ib = 1.0f / ev.Sb;
+    ev.T = T;
+    ev.V = rows.V;
+    return ev;
+}
+
+__global__ __launch_bounds__(kT) void k_seg_fold1(Rows rows, float T, Work w) {
+    __shared__ FoldShared sh;
+    const int seg = blockIdx.x, r = blockIdx.y;
+    const float m = row_max(w, r, sh.f);
+    if (seg == 0 && threadIdx.x == 0) w.row_m[r] = m;
+    double P0, E0;
+    exp_prefix(w, r, seg, m, T, sh.d, &P0, &E0);
+    fold_segment(pass1_eval(rows, r, m, T), w, r, seg, P0, E0, sh);
+}
+
+// residual guide sums of the first-reject row pairs (pass-2 stats)
+__global__ __launch_bounds__(kT) void k_res_stats(Rows rows, float T, Work w) {
+    __shared__ double s_d[kW];
+    const int seg = blockIdx.x, c = blockIdx.y;
+    const Task tk = w.task[c];
+    if (tk.kind != kKindRes) return;
+    const Eval<kKindRes> ev = task_eval<kKindRes>(rows, w, tk, T);
+    const int base = seg * kSeg + threadIdx.x * kC;
+    float A[kC], B[kC];
+    ev.args(base, A, B);
+    float gs = 0.0f, ge = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kC; k++) {
+        const float2 q = ev.approx(A[k], B[k]);
+        gs += q.x;
+        ge += q.y;
+    }
+    ge += gs * 0x1p-19f;
+    const double G = block_sum256_d((double)gs, s_d);
+    const double E = block_sum256_d((double)ge, s_d);
+    if (threadIdx.x == 0) {
+        const size_t i = (size_t)c * w.nseg + seg;
+        w.task_ge[2 * i] = G;
+        w.task_ge[2 * i + 1] = E * (1.0 + 0x1p-30) + G * 0x1p-40;
+    }
+}
+
+__global__ __launch_bounds__(kT) void k_seg_fold2(Rows rows, float T, Work w) {
+    __shared__ FoldShared sh;
+    const int seg = blockIdx.x, c = blockIdx.y;
+    const Task tk = w.task[c];
+    if (tk.kind < 0) return;
+    if (tk.kind == kKindProb) {
+        // p_i = e_i / S: the pass-1 guide of row ra, divided by S
+        const Eval<kKindProb> ev = task_eval<kKindProb>(rows, w, tk, T);
+        double P, E;
+        exp_prefix(w, tk.ra, seg, ev.ma, T, sh.d, &P, &E);
+        const double P0 = P / (double)ev.Sa;
+        const double E0 = E / (double)ev.Sa + P0 * 0x1p-22;
+        fold_segment(ev, w, w.R1 + c, seg, P0, E0, sh);
+    } else {
+        const Eval<kKindRes> ev = task_eval<kKindRes>(rows, w, tk, T);
+        double g = 0.0, e = 0.0;
+        if ((int)threadIdx.x < seg) {
+            const size_t i = (size_t)c * w.nseg + threadIdx.x;
+            g = w.task_ge[2 * i];
+            e = w.task_ge[2 * i + 1];
+        }
+        const double P0 = block_sum256_d(g, sh.d);
+        const double E0 = block_sum256_d(e, sh.d);
+        fold_segment(ev, w, w.R1 + c, seg, P0, E0, sh);
+    }
+}
+
+// ------------------------------------------------------------- the walk
+
+// s + x_0 + x_1 + ... + x_63 in order (fp32), x_k held by lane k; padding
+// lanes hold +0.0, which leaves a non-negative s unchanged.  Fully unrolled:
+// the readlanes do not depend on s, only the additions chain.
+__device__ __forceinline__ float add64(float s, float x) {
+#pragma unroll
+    for (int k = 0; k < 64; k++)
+        s = __fadd_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k)));
+    return s;
+}
+
+// Exact running value through elements [j0, j1) of a row (one wave: exact
+// values 64 at a time, the next batch loaded before the current one is added).
+template <int KIND>
+__device__ float replay_exact(const Eval<KIND>& ev, int j0, int j1, float s) {
+    float x = j0 + lane_id() < j1 ? ev.at(j0 + lane_id()) : 0.0f;
+    for (int j = j0; j < j1; j += 64) {
+        const float xn = j + 64 + lane_id() < j1 ? ev.at(j + 64 + lane_id()) : 0.0f;
+        s = add64(s, x);
+        x = xn;
+    }
+    return s;
+}
+
+struct WalkShared {
+    Item items[kWalkItems];
+    int ioff[kMaxSegs + 1];
+    int doff[kMaxSegs];
+    int over[kMaxSegs];
+};
+
+// Replay n staged chunks (exact values at dv, global memory) from s: fp32
+// additions in order, the next 64 values loaded while the current ones are
+// added; the exact value at each chunk start goes to out[chunk].
+__device__ __forceinline__ float replay_staged(const float* __restrict__ dv, int n, float s,
+                                               float* __restrict__ out) {
+    const int tot = n * kC;
+    float x = lane_id() < tot ? dv[lane_id()] : 0.0f;
+    for (int i = 0; i < tot; i += 64) {
+        const float xn = i + 64 + lane_id() < tot ? dv[i + 64 + lane_id()] : 0.0f;
+        // chunk starts of this batch (4 chunks of 16) gathered in lanes 0..3
+        float cs = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 64; k++) {
+            if ((k & (kC - 1)) == 0) cs = lane_id() == k / kC ? s : cs;   // s is wave-uniform
+            s = __fadd_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k)));
+        }
+        if (lane_id() < 4 && i + lane_id() * kC < tot) out[i / kC + lane_id()] = cs;
+        x = xn;
+    }
+    return s;
+}
+
+// One wave per row: exact value at every segment and item start, row sum.
+// The runs of a batch of segments are gathered in LDS first (all loads in
+// flight together); staged values stream from global memory.
+template <int KIND>
+__device__ void walk_row(const Eval<KIND>& ev, const Work& w, int row, WalkShared& sh) {
+    const int l = lane_id();
+    // every segment's counts (nseg <= 64), and their prefix sums
+    int c = 0;
+    if (l < w.nseg) c = w.cnt[2 * segi(w, row, l)];
+    int io = c > 0 ? c : 0;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int a = __shfl_up(io, o);
+        if (l >= o) io += a;
+    }
+    if (l < w.nseg) {
+        sh.ioff[l + 1] = io;
+        sh.over[l] = c < 0;
+    }
+    if (l == 0) sh.ioff[0] = 0;
+    __syncthreads();
+    float s = 0.0f;
+    int g0 = 0;
+    while (g0 < w.nseg) {
+        // batch [g0, g1): as many segments as fit
+        int g1 = g0 + 1;
+        while (g1 < w.nseg && sh.ioff[g1 + 1] - sh.ioff[g0] <= kWalkItems) g1++;
+        const int i0 = sh.ioff[g0], ni = sh.ioff[g1] - i0;
+        for (int i = l; i < ni; i += 64) {     // one round trip for up to 64 runs
+            int sg = g0;
+            while (sg + 1 < g1 && sh.ioff[sg + 1] <= i0 + i) sg++;
+            sh.items[i] = w.items[segi(w, row, sg) * kItemCap + (i0 + i - sh.ioff[sg])];
+        }
+        __syncthreads();
+        for (int seg = g0; seg < g1; seg++) {
+            const size_t si = segi(w, row, seg);
+            if (l == 0) w.seg_start[(size_t)row * (w.nseg + 1) + seg] = s;
+            const int segbase = seg * kSeg;
+            if (sh.over[seg]) {
+                s = replay_exact(ev, segbase, min(segbase + kSeg, ev.V), s);
+                continue;
+            }
+            const int n = sh.ioff[seg + 1] - sh.ioff[seg];
+            const Item* its = sh.items + (sh.ioff[seg] - i0);
+            const float* dv = w.dirty + si * kDirtyCap * kC;
+            Item nx = n > 0 ? its[0] : Item{};
+            for (int i = 0; i < n; i++) {
+                const Item it = nx;
+                if (i + 1 < n) nx = its[i + 1];
+                const int cend = i + 1 < n ? nx.chunk : kT;
+                if (l == 0) w.item_start[si * kItemCap + i] = s;
+                if (it.binade == kDirty) {
+                    s = replay_staged(dv + it.slot * kC, cend - it.chunk, s,
+                                      w.dirty_start + si * kDirtyCap + it.slot);
+                } else if (binade_bits(s) != it.binade) {
+                    // the run's start is not in the binade its chunks assumed
+                    // (excluded by the bounds; replayed exactly anyway)
+                    s = replay_exact(ev, segbase + it.chunk * kC, min(segbase + cend * kC, ev.V), s);
+                } else {
+                    s = mi_apply(s, MI{it.q0, it.q1, it.c});
+                }
+            }
+        }
+        __syncthreads();
+        g0 = g1;
+    }
+    if (l == 0) {
+        w.seg_start[(size_t)row * (w.nseg + 1) + w.nseg] = s;
+        w.row_S[row] = s;
+    }
+}
+
+__global__ __launch_bounds__(64) void k_walk1(Rows rows, float T, Work w) {
+    __shared__ WalkShared sh;
+    const int r = blockIdx.x;
+    walk_row(pass1_eval(rows, r, w.row_m[r], T), w, r, sh);
+}
+
+__global__ __launch_bounds__(64) void k_walk2(Rows rows, float T, Work w) {
+    __shared__ WalkShared sh;
+    const int c = blockIdx.x;
+    const Task tk = w.task[c];
+    if (tk.kind == kKindProb) walk_row(task_eval<kKindProb>(rows, w, tk, T), w, w.R1 + c, sh);
+    else if (tk.kind == kKindRes) walk_row(task_eval<kKindRes>(rows, w, tk, T), w, w.R1 + c, sh);
+}
+
+// ----------------------------------------------------------- decisions
+
+// One wave per chain: acceptance ratios (lane i: position i), first reject,
+// the accepted tokens, and the pass-2 task.
+__global__ __launch_bounds__(64) void k_decide(Rows rows, const int* __restrict__ tokens,
+                                               const float* __restrict__ u, float T, Work w,
+                                               float* __restrict__ accept_prob,
+                                               int* __restrict__ out_tokens,
+                                               int* __restrict__ n_accepted) {
+    const int c = blockIdx.x, l = lane_id(), gamma = rows.gamma, V = rows.V;
+    const int per = 2 * gamma + 1;
+    // non-finite rows (NaN, +inf, all -inf) go to the exact single-block path
+    int bad = 0;
+    for (int r = l; r < per; r += 64) {
+        const int rr = c * per + r;
+        bad |= !(w.row_m[rr] > -__builtin_inff()) || !(w.row_S[rr] <= FLT_MAX);
+        for (int s = 0; s < w.nseg; s++) bad |= w.seg_bad[segi(w, rr, s)];
+    }
+    bad = __any(bad);
+    const float* uu = u + (size_t)c * (gamma + 1);
+    bool reject = false;
+    if (l < gamma) {
+        const int x = tokens[(size_t)c * gamma + l];
+        float a = 1.0f;
+        if (x >= 0 && x < V) {
+            const int rt = c * per + l, rd = c * per + gamma + 1 + l;
+            const float at = __fdiv_rn(__fsub_rn(rows.row(rt)[x], w.row_m[rt]), T);
+            const float ad = __fdiv_rn(__fsub_rn(rows.row(rd)[x], w.row_m[rd]), T);
+            const float px = __fdiv_rn(exp_glibc(at), w.row_S[rt]);
+            const float qx = __fdiv_rn(exp_glibc(ad), w.row_S[rd]);
+            a = qx < 1e-10f ? 1.0f : fminf(1.0f, __fdiv_rn(px, qx));
+        }
+        if (!bad) accept_prob[(size_t)c * gamma + l] = a;
+        reject = !(uu[l] < a);
+    }
+    const unsigned long long rb = __ballot(reject);
+    const int j = rb ? __builtin_ctzll(rb) : gamma;
+    if (bad) {
+        if (l == 0) {
+            w.flags[c] = 1;
+            w.task[c].kind = -1;
+        }
+        return;
+    }
+    int* out = out_tokens + (size_t)c * (gamma + 1);
+    for (int i = l; i <= gamma; i += 64) {
+        if (i < j) out[i] = tokens[(size_t)c * gamma + i];
+        else if (i > j) out[i] = -1;
+    }
+    if (l == 0) {
+        n_accepted[c] = j;
+        w.flags[c] = 0;
+        Task tk;
+        tk.kind = j < gamma ? kKindRes : kKindProb;
+        tk.ra = c * per + j;
+        tk.rb = c * per + gamma + 1 + (j < gamma ? j : 0);
+        tk.j = j;
+        tk.u = uu[j < gamma ? j + 1 : gamma];
+        tk.pad[0] = tk.pad[1] = tk.pad[2] = 0;
+        w.task[c] = tk;
+    }
+}
+
+// --------------------------------------------------------------- the find
+
+struct FindShared {
+    FoldShared fold;
+    int item;
+};
+
+// end value of item i of a segment (start of the next item, or of the next segment)
+__device__ __forceinline__ float iend_of(const float* is, int i, int n, const float* ss, int seg) {
+    return i + 1 < n ? is[i + 1] : ss[seg + 1];
+}
+
+// First element i of the row with thr < (running value after i), from the
+// walk's exact starts; dflt when the row sum does not exceed thr.
+template <int KIND>
+__device__ int find_row(const Eval<KIND>& ev, const Work& w, int row, float thr, int dflt,
+                        FindShared& sh) {
+    const int t = threadIdx.x;
+    const float* ss = w.seg_start + (size_t)row * (w.nseg + 1);
+    const int seg = block_first256(t < w.nseg && thr < ss[t + 1], sh.fold.i);
+    if (seg >= w.nseg) return dflt;
+    const size_t si = segi(w, row, seg);
+    const int n = w.cnt[2 * si];
+    const int segbase = seg * kSeg;
+    int j0 = segbase, j1 = min(segbase + kSeg, ev.V);
+    float s0 = ss[seg];
+    if (n >= 0) {
+        const Item* its = w.items + si * kItemCap;
+        const float* is = w.item_start + si * kItemCap;
+        const float iend = t < n ? (t + 1 < n ? is[t + 1] : ss[seg + 1]) : 0.0f;
+        const int i = block_first256(t < n && thr < iend, sh.fold.i);
+        if (i >= n) return dflt;
+        const Item it = its[i];
+        s0 = is[i];
+        if (it.binade == kDirty) {
+            // staged run: the walk left the exact start of each of its chunks
+            const int nc = (i + 1 < n ? its[i + 1].chunk : kT) - it.chunk;
+            const float* ds = w.dirty_start + si * kDirtyCap + it.slot;
+            const float cend = t < nc ? (t + 1 < nc ? ds[t + 1] : iend_of(is, i, n, ss, seg)) : 0.0f;
+            const int ch = block_first256(t < nc && thr < cend, sh.fold.i);
+            if (ch >= nc) return dflt;
+            s0 = ds[ch];
+            j0 = segbase + (it.chunk + ch) * kC;
+            j1 = min(j0 + kC, ev.V);
+        } else {
+            // clean run [c0, c1): exact chunk ends from the chunk summaries
+            const int c0 = it.chunk, c1 = i + 1 < n ? its[i + 1].chunk : kT;
+            const int b = it.binade;
+            const bool mine = t >= c0 && t < c1;
+            MI own = mi_id();
+            if (mine) {
+                float A[kC], B[kC], v[kC], er[kC];
+                ev.args(segbase + t * kC, A, B);
+#pragma unroll
+                for (int k = 0; k < kC; k++) {
+                    const float2 q = ev.approx(A[k], B[k]);
+                    v[k] = q.x;
+                    er[k] = q.y;
+                }
+                own = fold_chunk16(ev, A, B, v, er, b);
+            }
+            SMI sv{own, 0};
+            sv = wave_incl_smi(sv);
+            __syncthreads();
+            if (lane_id() == 63) sh.fold.wagg[wave_id()] = sv;
+            __syncthreads();
+            MI pre = mi_id();
+            for (int ww = 0; ww < wave_id(); ww++) pre = mi_then(pre, sh.fold.wagg[ww].m);
+            const MI incl = mi_then(pre, sv.m);
+            const float cend = mine ? mi_apply(s0, incl) : 0.0f;
+            const int ch = block_first256(mine && thr < cend, sh.fold.i);
+            if (ch >= c1) return dflt;
+            // start of chunk ch: the run start advanced by chunks [c0, ch)
+            SMI bv{(t >= c0 && t < ch) ? own : mi_id(), 0};
+            bv = wave_incl_smi(bv);
+            __syncthreads();
+            if (lane_id() == 63) sh.fold.wagg[wave_id()] = bv;
+            __syncthreads();
+            MI tot = mi_id();
+            for (int ww = 0; ww < kW; ww++) tot = mi_then(tot, sh.fold.wagg[ww].m);
+            s0 = mi_apply(s0, tot);
+            j0 = segbase + ch * kC;
+            j1 = min(j0 + kC, ev.V);
+        }
+    }
+    // exact replay of [j0, j1) from s0 by wave 0 (padding lanes add +0.0 and
+    // cannot be the first to exceed thr)
+    if (wave_id() == 0) {
+        int hit = -1;
+        float s = s0;
+        for (int j = j0; j < j1 && hit < 0; j += 64) {
+            const float x = j + lane_id() < j1 ? ev.at(j + lane_id()) : 0.0f;
+#pragma unroll
+            for (int k = 0; k < 64; k++) {
+                s = __fadd_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k)));
+                if (hit < 0 && thr < s) hit = j + k;
+            }
+        }
+        if (lane_id() == 0) sh.item = hit;
+    }
+    __syncthreads();
+    return sh.item < 0 ? dflt : sh.item;
+}
+
+__global__ __launch_bounds__(kT) void k_find(Rows rows, float T, Work w,
+                                             int* __restrict__ out_tokens) {
+    __shared__ FindShared sh;
+    const int c = blockIdx.x;
+    const Task tk = w.task[c];
+    if (tk.kind < 0) return;
+    const int row = w.R1 + c;
+    const float R = w.row_S[row];
+    int tok;
+    if (tk.kind == kKindRes) {
+        if (R < 1e-10f) {
+            // speculative.c:157-160: softmax of p instead (exact path)
+            if (threadIdx.x == 0) w.flags[c] = 2;
+            return;
+        }
+        tok = find_row(task_eval<kKindRes>(rows, w, tk, T), w, row, __fmul_rn(tk.u, R), 0, sh);
+    } else {
+        tok = find_row(task_eval<kKindProb>(rows, w, tk, T), w, row, tk.u, rows.V - 1, sh);
+    }
+    if (threadIdx.x == 0) out_tokens[(size_t)c * (rows.gamma + 1) + tk.j] = tok;
+}
+
+// ------------------------------------------------------------ fallback
+
+// Chains the pipeline left (non-finite rows, residual mass < 1e-10): the
+// exact single-block samplers of eos.hpp, positions in order.
+__global__ __launch_bounds__(kThreads) void k_verify_fallback(
+    Rows rows, const int* __restrict__ tokens, const float* __restrict__ u, float T, Work w,
+    float* __restrict__ accept_prob, int* __restrict__ out_tokens,
+    int* __restrict__ n_accepted) {
+    __shared__ EosShared sh;
+    const int c = blockIdx.x, gamma = rows.gamma, V = rows.V, per = 2 * gamma + 1;
+    const int flag = w.flags[c];
+    if (flag == 0) return;
+    const float* uu = u + (size_t)c * (gamma + 1);
+    int* out = out_tokens + (size_t)c * (gamma + 1);
+    if (flag == 2) {
+        // the accept tests stand; only the correction draw changes
+        const Task tk = w.task[c];
+        RowSrc ts{rows.row(tk.ra)}, ds{rows.row(tk.rb)};
+        ExpGen<RowSrc> et{ts, w.row_m[tk.ra], T}, ed{ds, w.row_m[tk.rb], T};
+        DivGen<ExpGen<RowSrc>> pt{et, w.row_S[tk.ra]}, pd{ed, w.row_S[tk.rb]};
+        const int tok = sample_corrected_gen(pt, pd, V, tk.u, sh);
+        if (threadIdx.x == 0) out[tk.j] = tok;
+        return;
+    }
+    int j = gamma;
+    for (int i = 0; i < gamma; i++) {
+        RowSrc ts{rows.row(c * per + i)}, ds{rows.row(c * per + gamma + 1 + i)};
+        const float mt = gen_max(ts, V, sh), md = gen_max(ds, V, sh);
+        ExpGen<RowSrc> et{ts, mt, T}, ed{ds, md, T};
+        const float St = eos_sum(et, V, sh), Sd = eos_sum(ed, V, sh);
+        DivGen<ExpGen<RowSrc>> pt{et, St}, pd{ed, Sd};
+        const int x = tokens[(size_t)c * gamma + i];
+        float a = 1.0f;
+        if (x >= 0 && x < V) {
+            const float px = gen_at(pt, x, sh), qx = gen_at(pd, x, sh);
+            a = qx < 1e-10f ? 1.0f : fminf(1.0f, __fdiv_rn(px, qx));
+        }
+        if (threadIdx.x == 0) accept_prob[(size_t)c * gamma + i] = a;
+        if (j == gamma && !(uu[i] < a)) {
+            j = i;
+            const int tok = sample_corrected_gen(pt, pd, V, uu[i + 1], sh);
+            if (threadIdx.x == 0) out[i] = tok;
+        }
+    }
+    if (j == gamma) {
+        const int tok = sample_temperature_gen(RowSrc{rows.row(c * per + gamma)}, V, T,
+                                               uu[gamma], sh);
+        if (threadIdx.x == 0) out[gamma] = tok;
+    }
+    if (threadIdx.x == 0) {
+        for (int i = 0; i < gamma + 1; i++) {
+            if (i < j) out[i] = tokens[(size_t)c * gamma + i];
+            else if (i > j) out[i] = -1;
+        }
+        n_accepted[c] = j;
+    }
+}
+
+}  // namespace vp
+}  // namespace
+
+// ------------------------------------------------------------- launcher
+
+extern "C" int cgk_verify_pipe_supported(int batch, int gamma, int V, float T) {
+    return batch >= 1 && batch <= 65535 && gamma >= 1 && gamma <= vp::kMaxGamma && V >= 1 &&
+           V <= kRound * kMaxRounds && T > 0.0f && T <= FLT_MAX;
+}
+
+extern "C" int cgk_verify_pipe(const float* target, const float* draft, const int* tokens,
+                               const float* u, int batch, int gamma, int V, float T,
+                               float* accept_prob, int* out_tokens, int* n_accepted) {
+    using namespace vp;
+    if (!cgk_verify_pipe_supported(batch, gamma, V, T)) {
+        cgx_set_error("verify: batch %d, gamma %d, V %d, T %g outside the pipeline's range",
+                      batch, gamma, V, (double)T);
+        return -1;
+    }
+    const int nseg = (V + kSeg - 1) / kSeg;
+    const int R1 = batch * (2 * gamma + 1), Rall = R1 + batch;
+    // workspace carve (256-byte aligned pieces)
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off += (bytes + 255) & ~(size_t)255;
+        return o;
+    };
+    const size_t o_segm = take((size_t)R1 * nseg * 4);
+    const size_t o_seggh = take((size_t)R1 * nseg * 16);
+    const size_t o_segbad = take((size_t)R1 * nseg * 4);
+    const size_t o_rowm = take((size_t)R1 * 4);
+    const size_t o_rowS = take((size_t)Rall * 4);
+    const size_t o_cnt = take((size_t)Rall * nseg * 8);
+    const size_t o_items = take((size_t)Rall * nseg * kItemCap * sizeof(Item));
+    const size_t o_dirty = take((size_t)Rall * nseg * kDirtyCap * kC * 4);
+    const size_t o_sst = take((size_t)Rall * (nseg + 1) * 4);
+    const size_t o_ist = take((size_t)Rall * nseg * kItemCap * 4);
+    const size_t o_dst = take((size_t)Rall * nseg * kDirtyCap * 4);
+    const size_t o_tge = take((size_t)batch * nseg * 16);
+    const size_t o_task = take((size_t)batch * sizeof(Task));
+    const size_t o_flags = take((size_t)batch * 4);
+    const size_t o_ap = take((size_t)batch * gamma * 4);
+    char* ws = (char*)cgx_scratch(CGX_SLOT_WS4, off);
+    if (!ws) return -1;
+    Work w;
+    w.R1 = R1;
+    w.chains = batch;
+    w.nseg = nseg;
+    w.seg_m = (float*)(ws + o_segm);
+    w.seg_gh = (double*)(ws + o_seggh);
+    w.seg_bad = (int*)(ws + o_segbad);
+    w.row_m = (float*)(ws + o_rowm);
+    w.row_S = (float*)(ws + o_rowS);
+    w.cnt = (int*)(ws + o_cnt);
+    w.items = (Item*)(ws + o_items);
+    w.dirty = (float*)(ws + o_dirty);
+    w.seg_start = (float*)(ws + o_sst);
+    w.item_start = (float*)(ws + o_ist);
+    w.dirty_start = (float*)(ws + o_dst);
+    w.task_ge = (double*)(ws + o_tge);
+    w.task = (Task*)(ws + o_task);
+    w.flags = (int*)(ws + o_flags);
+    float* ap = accept_prob ? accept_prob : (float*)(ws + o_ap);
+    Rows rows{target, draft, gamma, V};
+    hipStream_t st = stream();
+    hipLaunchKernelGGL(k_seg_stats, dim3(nseg, R1), dim3(kT), 0, st, rows, T, w);
+    if (launch_check("k_seg_stats")) return -1;
+    hipLaunchKernelGGL(k_seg_fold1, dim3(nseg, R1), dim3(kT), 0, st, rows, T, w);
+    if (launch_check("k_seg_fold1")) return -1;
+    hipLaunchKernelGGL(k_walk1, dim3(R1), dim3(64), 0, st, rows, T, w);
+    if (launch_check("k_walk1")) return -1;
+    hipLaunchKernelGGL(k_decide, dim3(batch), dim3(64), 0, st, rows, tokens, u, T, w, ap,
+                       out_tokens, n_accepted);
+    if (launch_check("k_decide")) return -1;
+    hipLaunchKernelGGL(k_res_stats, dim3(nseg, batch), dim3(kT), 0, st, rows, T, w);
+    if (launch_check("k_res_stats")) return -1;
+    hipLaunchKernelGGL(k_seg_fold2, dim3(nseg, batch), dim3(kT), 0, st, rows, T, w);
+    if (launch_check("k_seg_fold2")) return -1;
+    hipLaunchKernelGGL(k_walk2, dim3(batch), dim3(64), 0, st, rows, T, w);
+    if (launch_check("k_walk2")) return -1;
+    hipLaunchKernelGGL(k_find, dim3(batch), dim3(kT), 0, st, rows, T, w, out_tokens);
+    if (launch_check("k_find")) return -1;
+    hipLaunchKernelGGL(k_verify_fallback, dim3(batch), dim3(kThreads), 0, st, rows, tokens, u,
+                       T, w, ap, out_tokens, n_accepted);
+    return launch_check("k_verify_fallback");
+}
