@@ -142,7 +142,7 @@ __global__ __launch_bounds__(kThreads) void k_verify_rows(
             dv[k] = __fdiv_rn(dv[k], Sd);
         }
         DivGen<ExpGen<RowSrc>> pt{et, St}, pd{ed, Sd};
-        float a = 1.0f;
+        float a = 0.0f;   // a draft token outside [0, V) is rejected
         if (x >= 0 && x < V) {
             const float px = vals_at(tv, x, sh), qx = vals_at(dv, x, sh);
             a = qx < 1e-10f ? 1.0f : fminf(1.0f, __fdiv_rn(px, qx));
@@ -158,7 +158,7 @@ __global__ __launch_bounds__(kThreads) void k_verify_rows(
     float St = eos_sum(et, V, sh);
     float Sd = eos_sum(ed, V, sh);
     DivGen<ExpGen<RowSrc>> pt{et, St}, pd{ed, Sd};
-    float a = 1.0f;
+    float a = 0.0f;   // a draft token outside [0, V) is rejected
     if (x >= 0 && x < V) {
         float px = gen_at(pt, x, sh), qx = gen_at(pd, x, sh);
         a = qx < 1e-10f ? 1.0f : fminf(1.0f, __fdiv_rn(px, qx));
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(kThreads) void k_verify_rows_dist(
     const size_t r = (size_t)chain * gamma + pos;
     RowSrc pt{p + ((size_t)chain * (gamma + 1) + pos) * V}, pd{q + r * V};
     int x = tokens[r];
-    float a = 1.0f;
+    float a = 0.0f;   // a draft token outside [0, V) is rejected
     if (x >= 0 && x < V) {
         float px = pt(x), qx = pd(x);
         a = qx < 1e-10f ? 1.0f : fminf(1.0f, __fdiv_rn(px, qx));

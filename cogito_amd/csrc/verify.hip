@@ -209,17 +209,23 @@ struct Eval {
             return fmaxf(0.0f, __fsub_rn(__fdiv_rn(exp_glibc(A), Sa), __fdiv_rn(exp_glibc(B), Sb)));
         }
     }
-    // approximation and its bound
+    // approximation and its bound: exp_fast on [-87, 0]; below, expf is
+    // under 2^-125 and the approximation 0 (absolute bound); 2^-140 covers
+    // subnormal quotients
     __device__ __forceinline__ float2 approx(float A, float B) const {
+        const bool oa = A >= kExpFastMin;
+        const float ea = oa ? exp_fast(A) : 0.0f;
         if constexpr (KIND == kKindExp) {
-            const float e = exp_cert(A);
-            return make_float2(e, e * kExpErr);
+            return make_float2(ea, oa ? ea * kExpErr : 0x1p-125f);
         } else if constexpr (KIND == kKindProb) {
-            const float p = exp_cert(A) * ia;
-            return make_float2(p, p * kProbRel);
+            const float p = ea * ia;
+            return make_float2(p, (oa ? p * kProbRel : 0x1p-124f * ia) + 0x1p-140f);
         } else {
-            const float p = exp_cert(A) * ia, q = exp_cert(B) * ib;
-            return make_float2(fmaxf(0.0f, p - q), kResRel * (p + q));
+            const bool ob = B >= kExpFastMin;
+            const float eb = ob ? exp_fast(B) : 0.0f;
+            const float p = ea * ia, q = eb * ib;
+            const float abs_err = (oa ? 0.0f : 0x1p-124f * ia) + (ob ? 0.0f : 0x1p-124f * ib);
+            return make_float2(fmaxf(0.0f, p - q), kResRel * (p + q) + abs_err + 0x1p-140f);
         }
     }
     // exact value of element j, from memory
@@ -274,21 +280,28 @@ template <int KIND>
 __device__ __forceinline__ MI fold_chunk16(const Eval<KIND>& ev, const float (&A)[kC],
                                            const float (&B)[kC], float (&v)[kC],
                                            const float (&er)[kC], int b) {
+    // y = v / ulp and its bound by a power-of-two scale (exact; ldexp, as the
+    // scale itself can exceed the fp32 range for tiny binades)
     const int e = b == -127 ? 149 : 23 - b;
-    unsigned amb = 0u;
-    int Q = 0;
+    bool amb = false;
+    float Q = 0.0f;                           // < 2^24: exact
 #pragma unroll
     for (int k = 0; k < kC; k++) {
         const float y = ldexpf(v[k], e);
         const float rr = rintf(y);
         // a half-integer within the bound of y (ties included)
-        if (fabsf(y - rr) >= 0.5f - ldexpf(er[k], e)) amb |= 1u << k;
-        Q += (int)rr;
+        amb |= fabsf(y - rr) + ldexpf(er[k], e) >= 0.5f;
+        Q += rr;
     }
-    if (amb == 0u) return MI{Q, Q, (Q & 1) | (((Q & 1) ^ 1) << 1)};
+    if (!amb) {
+        const int q = (int)Q;
+        return MI{q, q, (q & 1) | (((q & 1) ^ 1) << 1)};
+    }
 #pragma unroll
-    for (int k = 0; k < kC; k++)
-        if ((amb >> k) & 1u) v[k] = ev.exact(A[k], B[k]);
+    for (int k = 0; k < kC; k++) {
+        const float y = ldexpf(v[k], e);
+        if (fabsf(y - rintf(y)) + ldexpf(er[k], e) >= 0.5f) v[k] = ev.exact(A[k], B[k]);
+    }
     int q0 = 0, q1 = 0, c0 = 0, c1 = 1;
 #pragma unroll
     for (int k = 0; k < kC; k++) {
@@ -349,6 +362,45 @@ __device__ __forceinline__ double block_incl256_d(double v, double* s_w, double*
     }
     *total = tot;
     return pre + v;
+}
+
+template <int CTRL, int RMASK>
+__device__ __forceinline__ float dppf(float v) {
+    return __int_as_float(dpp_i<CTRL, RMASK>(__float_as_int(v)));
+}
+
+// inclusive fp32 scan over the wave (DPP; row_shr 1, 2, 4, 8, row_bcast 15, 31)
+__device__ __forceinline__ float wave_incl_sum_f(float x) {
+    float o;
+    o = dppf<0x111, 0xF>(x); if (dpp_step_valid(0)) x += o;
+    o = dppf<0x112, 0xF>(x); if (dpp_step_valid(1)) x += o;
+    o = dppf<0x114, 0xF>(x); if (dpp_step_valid(2)) x += o;
+    o = dppf<0x118, 0xF>(x); if (dpp_step_valid(3)) x += o;
+    o = dppf<0x142, 0xA>(x); if (dpp_step_valid(4)) x += o;
+    o = dppf<0x143, 0xC>(x); if (dpp_step_valid(5)) x += o;
+    return x;
+}
+
+// inclusive fp32 scans of two values over the block; each result is within
+// 2^-19 relative of the exact prefix (at most 10 roundings of partial sums
+// of non-negative values)
+__device__ __forceinline__ void block_incl256_f2(float a, float b, float* s_w, float* ia,
+                                                 float* ib) {
+    a = wave_incl_sum_f(a);
+    b = wave_incl_sum_f(b);
+    __syncthreads();
+    if (lane_id() == 63) {
+        s_w[wave_id()] = a;
+        s_w[kW + wave_id()] = b;
+    }
+    __syncthreads();
+    float pa = 0.0f, pb = 0.0f;
+    for (int w = 0; w < wave_id(); w++) {
+        pa += s_w[w];
+        pb += s_w[kW + w];
+    }
+    *ia = pa + a;
+    *ib = pb + b;
 }
 
 // first thread (lowest index) with pred, or kT
@@ -432,30 +484,48 @@ __device__ __forceinline__ float row_max(const Work& w, int r, float* s_f) {
     return block_max256(m, s_f);
 }
 
-// guide of pass-1 row r over segments [0, seg): sum of c G and its bound
+// guide of pass-1 row r over segments [0, seg): sum of c G and its bound.
+// seg < 64, so wave 0 holds every term; c = exp(-D) with exp_fast on the
+// fp32-rounded D (relative error 2^-20 + 2^-24 D), or 0 below 2^-125.
 __device__ __forceinline__ void exp_prefix(const Work& w, int r, int seg, float m, float T,
                                            double* s_d, double* P, double* E) {
-    double cg = 0.0, eb = 0.0;
-    const int s = threadIdx.x;
-    if (s < seg) {
-        const size_t i = segi(w, r, s);
-        const double G = w.seg_gh[2 * i], H = w.seg_gh[2 * i + 1];
-        const float ms = w.seg_m[i];
-        if (G > 0.0) {
-            const double D = ((double)m - (double)ms) / (double)T;
-            const double c = exp(-D) * (1.0 + 0x1p-40);
-            cg = c * G;
-            eb = c * (0x1p-22 * 1.01 * H + (0x1p-23 * 1.01 * D + 0x1p-18) * G) + 0x1p-136;
+    if (wave_id() == 0) {
+        double cg = 0.0, eb = 0.0;
+        const int s = threadIdx.x;
+        if (s < seg) {
+            const size_t i = segi(w, r, s);
+            const double G = w.seg_gh[2 * i], H = w.seg_gh[2 * i + 1];
+            const float ms = w.seg_m[i];
+            if (G > 0.0) {
+                const double D = ((double)m - (double)ms) / (double)T;
+                const bool ok = D <= 87.0;
+                const double c = ok ? (double)exp_fast(-(float)D) : 0.0;
+                cg = c * G;
+                const double cu = ok ? c * (1.0 + 0x1p-19 + 0x1p-23 * D) : 0x1p-125;
+                eb = cu * (0x1p-22 * 1.01 * H + (0x1p-23 * 1.01 * D + 0x1p-18) * G) +
+                     (cu - c) * G + 0x1p-136;
+            }
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+            cg += __shfl_xor(cg, o);
+            eb += __shfl_xor(eb, o);
+        }
+        if (threadIdx.x == 0) {
+            s_d[0] = cg;
+            s_d[1] = eb * (1.0 + 0x1p-40);
         }
     }
-    *P = block_sum256_d(cg, s_d);
-    *E = block_sum256_d(eb, s_d);
+    __syncthreads();
+    *P = s_d[0];
+    *E = s_d[1];
+    __syncthreads();
 }
 
 // ------------------------------------------------------------ the fold
 
 struct FoldShared {
     float f[kW];
+    float f2[2 * kW];
     double d[kW];
     int i[kW];
     SMI wagg[kW];
@@ -483,12 +553,13 @@ __device__ void fold_segment(const Eval<KIND>& ev, const Work& w, int row, int s
         ge += q.y;
     }
     ge += gs * 0x1p-19f;                      // rounding of the 16-term fp32 sum
-    double tot;
-    const double pe = block_incl256_d((double)gs, sh.d, &tot);
-    const double ee = block_incl256_d((double)ge, sh.d, &tot);
-    const double Pend = P0 + pe, Pst = Pend - (double)gs;
-    const double Eend = (E0 + ee) * (1.0 + 0x1p-30) + Pend * 0x1p-40;
-    const double Est = Eend - (double)ge + Pst * 0x1p-40;
+    float pe, ee;
+    block_incl256_f2(gs, ge, sh.f2, &pe, &ee);
+    // fp32 scan roundings: 2^-19 relative of each prefix
+    const double Pend = P0 + (double)pe, Pst = Pend - (double)gs;
+    const double Eend = (E0 + (double)ee * (1.0 + 0x1p-18)) * (1.0 + 0x1p-30) +
+                        (double)pe * 0x1p-18 + Pend * 0x1p-40;
+    const double Est = Eend + (double)gs * 0x1p-18;
     // k sequential fp32 additions of non-negative values stay within
     // [(1 - 2^-24)^k, (1 + 2^-24)^k] of the real sum: >= 1 - ku, <= 1 + ku / (1 - ku)
     const double ks = (double)base * 0x1p-24, ke = (double)(base + kC) * 0x1p-24;
@@ -811,7 +882,7 @@ __global__ __launch_bounds__(64) void k_decide(Rows rows, const int* __restrict_
     bool reject = false;
     if (l < gamma) {
         const int x = tokens[(size_t)c * gamma + l];
-        float a = 1.0f;
+        float a = 0.0f;   // a draft token outside [0, V) is rejected
         if (x >= 0 && x < V) {
             const int rt = c * per + l, rd = c * per + gamma + 1 + l;
             const float at = __fdiv_rn(__fsub_rn(rows.row(rt)[x], w.row_m[rt]), T);
@@ -1009,7 +1080,7 @@ __global__ __launch_bounds__(kThreads) void k_verify_fallback(
         const float St = eos_sum(et, V, sh), Sd = eos_sum(ed, V, sh);
         DivGen<ExpGen<RowSrc>> pt{et, St}, pd{ed, Sd};
         const int x = tokens[(size_t)c * gamma + i];
-        float a = 1.0f;
+        float a = 0.0f;   // a draft token outside [0, V) is rejected
         if (x >= 0 && x < V) {
             const float px = gen_at(pt, x, sh), qx = gen_at(pd, x, sh);
             a = qx < 1e-10f ? 1.0f : fminf(1.0f, __fdiv_rn(px, qx));

@@ -113,12 +113,30 @@ def test_masked_and_out_of_range_tokens(gpu, oracle, V):
         mask = rng.uniform(0, 1, V) < 0.3
         target[:, mask] = -np.inf
         draft[:, mask[::-1]] = -np.inf
-        toks[0] = -1
-        toks[1] = V
         toks[2] = int(np.flatnonzero(mask)[0]) if mask.any() else 0
         u = rng.uniform(0, 1, gamma + 1).astype(np.float32)
         u[:rep] = 0.0
         _run(gpu, oracle, target, draft, toks, u, gamma, V, T)
+
+
+def test_out_of_range_tokens_are_rejected(gpu, oracle):
+    # the reference reads outside the row for such a token (undefined); here
+    # its acceptance ratio is 0, so it is rejected and never emitted
+    rng = np.random.default_rng(8)
+    V, gamma, T = 5000, 4, 1.0
+    for bad, pos in ((-1, 0), (V, 2), (2**31 - 1, 3)):
+        target, draft, toks = _inputs(rng, V, gamma)
+        draft[:] = target[:gamma]                  # in-range tokens: ratio 1
+        toks[pos] = bad
+        u = np.zeros(gamma + 1, np.float32)
+        out = np.zeros(gamma + 1, np.int32)
+        ap = np.zeros(gamma, np.float32)
+        n = gpu.cgx_verify_chain(target.ctypes.data, draft.ctypes.data, toks.ctypes.data,
+                                 u.ctypes.data, gamma, V, T, 0, 1.0, out.ctypes.data,
+                                 ap.ctypes.data)
+        assert n == pos, (bad, pos, n)
+        assert ap[pos] == 0.0
+        assert (out[:pos] == toks[:pos]).all() and 0 <= out[pos] < V
 
 
 def test_spiky_and_tied_rows(gpu, oracle):
