@@ -81,6 +81,8 @@ int cgk_verify_pipe_supported(int batch, int gamma, int V, float T);
 int cgk_verify_pipe(const float* target, const float* draft, const int* tokens, const float* u,
                     int batch, int gamma, int V, float T, float* accept_prob, int* out_tokens,
                     int* n_accepted);
+int cgk_sample_temperature_pipe(const float* logits, int rows, int V, float T, const float* u,
+                                int* out);
 int cgk_exp_fast_maxerr(float lo, float hi, unsigned int* out_dev);
 int cgk_ordered_sum(const float* x, int n, float* out);
 int cgk_sample_temperature(const float* logits, int V, float T, float u, int* out);

@@ -143,7 +143,11 @@ int cgx_spec_prefill(cgx_spec* s, const int* prompt, int n) {
 static int draft_sample(cgx_spec* s, int i, float u_host) {
     const float* row = s->d_draft_logits + (size_t)i * s->V;
     int* out = s->d_tokens + i + 1;
-    if (!s->filtered) return cgk_sample_temperature(row, s->V, s->T, u_host, out);
+    if (!s->filtered) {
+        if (cgk_verify_pipe_supported(1, 0, s->V, s->T))
+            return cgk_sample_temperature_pipe(row, 1, s->V, s->T, s->d_u + i, out);
+        return cgk_sample_temperature(row, s->V, s->T, u_host, out);
+    }
     if (cgk_scale(row, s->d_z, (size_t)s->V, s->T)) return -1;
     return cgk_filter_rows(s->d_z, 1, s->V, s->top_k, s->top_p, s->d_u + i, out, NULL);
 }

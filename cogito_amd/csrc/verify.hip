@@ -1112,7 +1112,7 @@ __global__ __launch_bounds__(kThreads) void k_verify_fallback(
 // ------------------------------------------------------------- launcher
 
 extern "C" int cgk_verify_pipe_supported(int batch, int gamma, int V, float T) {
-    return batch >= 1 && batch <= 65535 && gamma >= 1 && gamma <= vp::kMaxGamma && V >= 1 &&
+    return batch >= 1 && batch <= 65535 && gamma >= 0 && gamma <= vp::kMaxGamma && V >= 1 &&
            V <= kRound * kMaxRounds && T > 0.0f && T <= FLT_MAX;
 }
 
@@ -1149,6 +1149,7 @@ extern "C" int cgk_verify_pipe(const float* target, const float* draft, const in
     const size_t o_task = take((size_t)batch * sizeof(Task));
     const size_t o_flags = take((size_t)batch * 4);
     const size_t o_ap = take((size_t)batch * gamma * 4);
+    const size_t o_n = take((size_t)batch * 4);
     char* ws = (char*)cgx_scratch(CGX_SLOT_WS4, off);
     if (!ws) return -1;
     Work w;
@@ -1170,6 +1171,7 @@ extern "C" int cgk_verify_pipe(const float* target, const float* draft, const in
     w.task = (Task*)(ws + o_task);
     w.flags = (int*)(ws + o_flags);
     float* ap = accept_prob ? accept_prob : (float*)(ws + o_ap);
+    if (!n_accepted) n_accepted = (int*)(ws + o_n);
     Rows rows{target, draft, gamma, V};
     hipStream_t st = stream();
     hipLaunchKernelGGL(k_seg_stats, dim3(nseg, R1), dim3(kT), 0, st, rows, T, w);
@@ -1192,4 +1194,12 @@ extern "C" int cgk_verify_pipe(const float* target, const float* draft, const in
     hipLaunchKernelGGL(k_verify_fallback, dim3(batch), dim3(kThreads), 0, st, rows, tokens, u,
                        T, w, ap, out_tokens, n_accepted);
     return launch_check("k_verify_fallback");
+}
+
+// cg_sample_temperature on `rows` rows at once through the same pipeline: a
+// verify with no drafted tokens is exactly the bonus draw from target row 0
+// (speculative.c:54-75).  u: one draw per row (device); out: one token per row.
+extern "C" int cgk_sample_temperature_pipe(const float* logits, int rows, int V, float T,
+                                           const float* u, int* out) {
+    return cgk_verify_pipe(logits, logits, nullptr, u, rows, 0, V, T, nullptr, out, nullptr);
 }
