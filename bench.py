@@ -342,6 +342,70 @@ def bench_e2e(lib, name, tgt, drf, share_head, ctx, gamma, T, top_k, top_p, step
 
 
 
+def bench_e2e_batch(lib, name, tgt, drf, ctx, gamma, T, B, steps, warmup, seed=2026):
+    """The batched chain loop (cgx_spec_batch_step): B sequences in lockstep,
+    the target verifying B x (gamma+1) rows per forward.  Verified tok/s =
+    sum over sequences of (accepted + 1) / wall time."""
+    from cogito_amd.capi import CgxModelConfig, last_error
+
+    max_seq = ctx + (gamma + 1) * (steps + warmup + 2) + 8
+    ct = _model_cfg(*tgt, max_seq=max_seq, max_tokens=gamma + 1, kv_gs=tgt[4])
+    cd = _model_cfg(*drf, max_seq=max_seq, max_tokens=2, kv_gs=drf[4])
+    ct.max_batch = B
+    cd.max_batch = B
+    t0 = time.perf_counter()
+    mt = lib.cgx_model_new(C.byref(ct), seed, None)
+    if not mt:
+        raise RuntimeError(last_error(lib))
+    md = lib.cgx_model_new(C.byref(cd), seed + 1, mt)
+    if not md:
+        raise RuntimeError(last_error(lib))
+    if (lib.cgx_model_fill_context(mt, ctx, seed) or
+            lib.cgx_model_fill_context(md, ctx, seed + 7)):
+        raise RuntimeError(last_error(lib))
+    log(f"[bench] {name}: models built and {B} contexts of {ctx} filled in "
+        f"{time.perf_counter() - t0:.1f} s")
+    sp = lib.cgx_spec_batch_new(md, mt, gamma, T)
+    prev = np.ones(B, np.int32)
+    last = np.full(B, 2, np.int32)
+    if not sp or lib.cgx_spec_batch_set_last(sp, prev.ctypes.data, last.ctypes.data):
+        raise RuntimeError(last_error(lib))
+    rng = np.random.default_rng(seed)
+    out = np.zeros((B, gamma + 1), np.int32)
+    n = np.zeros(B, np.int32)
+
+    def step():
+        ud = rng.random((B, gamma), dtype=np.float32)
+        uv = rng.random((B, gamma + 1), dtype=np.float32)
+        tot = lib.cgx_spec_batch_step(sp, ud.ctypes.data, uv.ctypes.data, out.ctypes.data,
+                                      n.ctypes.data)
+        if tot < 0:
+            raise RuntimeError(last_error(lib))
+        return tot
+    for _ in range(warmup):
+        step()
+    lib.cgx_synchronize()
+    emitted = 0
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        emitted += step() + B
+    lib.cgx_synchronize()
+    wall = time.perf_counter() - t0
+    lib.cgx_spec_batch_free(sp)
+    lib.cgx_model_free(md)
+    lib.cgx_model_free(mt)
+    tps = emitted / wall
+    acc = (emitted - steps * B) / (steps * B * gamma)
+    log(f"[bench] {name}: {tps:.0f} verified tok/s, {wall / steps * 1e3:.3f} ms/step, "
+        f"acceptance {acc:.3f}")
+    return {"verified_tok_s": round(tps, 1), "ms_per_step": round(wall / steps * 1e3, 4),
+            "acceptance_rate": round(acc, 4), "tokens_per_step": round(emitted / steps, 3),
+            "steps": steps, "gamma": gamma, "temperature": T, "ctx": ctx, "batch": B,
+            "target": dict(zip(("layers", "d", "H", "Hk", "hd", "ff", "V"), tgt)),
+            "draft": dict(zip(("layers", "d", "H", "Hk", "hd", "ff", "V"), drf)),
+            "draft_shares_embed_lm_head": True}
+
+
 def cpu_baseline_gemv(M, K, N, gs, budget_s=12.0, seed=2024):
     """cogito's cg_matmul_int4 on the host, 1 thread, bounded sample."""
     sys.path.insert(0, str(ROOT / "tests"))
@@ -470,6 +534,9 @@ def main() -> int:
         extra["e2e_7b_c4"] = bench_e2e(
             lib, "C4 7B-shape", (32, 4096, 32, 8, 128, 11008, 32000),
             (1, 4096, 32, 8, 128, 11008, 32000), True, 4096, 4, 1.0, 0, 1.0, 40, 5)
+        extra["e2e_7b_c4_b8"] = bench_e2e_batch(
+            lib, "C4 7B-shape batch 8", (32, 4096, 32, 8, 128, 11008, 32000),
+            (1, 4096, 32, 8, 128, 11008, 32000), 4096, 4, 1.0, 8, 20, 3)
 
     cpu = None
     if not args.no_cpu:

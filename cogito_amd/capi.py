@@ -124,7 +124,7 @@ class CgxModelConfig(C.Structure):
         ("n_kv_heads", C.c_int), ("head_dim", C.c_int), ("d_ff", C.c_int),
         ("vocab", C.c_int), ("group_size", C.c_int), ("kv_group_size", C.c_int),
         ("max_seq", C.c_int), ("max_tokens", C.c_int), ("rope_theta", C.c_float),
-        ("norm_eps", C.c_float), ("init_std", C.c_float),
+        ("norm_eps", C.c_float), ("init_std", C.c_float), ("max_batch", C.c_int),
     ]
 
 
@@ -260,6 +260,10 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_model_get_config": (I, [VP, C.POINTER(CgxModelConfig)]),
     "cgx_model_len": (I, [VP]),
     "cgx_model_truncate": (I, [VP, I]),
+    "cgx_model_forward_batch": (I, [VP, VP, I, I, VP]),
+    "cgx_model_batch": (I, [VP]),
+    "cgx_model_len_seq": (I, [VP, I]),
+    "cgx_model_truncate_seq": (I, [VP, I, I]),
     "cgx_model_kv": (PKV, [VP]),
     "cgx_model_fill_context": (I, [VP, I, C.c_uint64]),
     "cgx_model_export": (I, [VP, I, I, VP, VP]),
@@ -271,6 +275,12 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_spec_step": (I, [VP, VP, VP, VP]),
     "cgx_spec_stats": (None, [VP, C.POINTER(C.c_longlong), C.POINTER(C.c_longlong),
                               C.POINTER(C.c_longlong)]),
+    "cgx_spec_batch_new": (VP, [VP, VP, I, F]),
+    "cgx_spec_batch_free": (None, [VP]),
+    "cgx_spec_batch_set_last": (I, [VP, VP, VP]),
+    "cgx_spec_batch_step": (I, [VP, VP, VP, VP, VP]),
+    "cgx_spec_batch_stats": (None, [VP, C.POINTER(C.c_longlong), C.POINTER(C.c_longlong),
+                                    C.POINTER(C.c_longlong)]),
 }
 
 # The subset implemented so far; the rest are declared in the headers and

@@ -60,6 +60,7 @@ int launch_check(const char* what) {
 }
 
 enum { kMaskNone = 0, kMaskCausal = 1, kMaskTree = 4 };
+constexpr int kMaxBatch = 16;
 
 struct DecArgs {
     const float* Q;              // [Nq][H][D]
@@ -75,6 +76,12 @@ struct DecArgs {
     float* part_o;               // [splits][Nq*H][D]
     float* part_ml;              // [splits][Nq*H][2]
     unsigned long long anc[64];  // tree: ancestor bits over the last Nq keys
+    // batch: B sequences, each with Nq query rows (Q, O: [B][Nq][H][D]) and
+    // its own cache at kc + b * seq_kbytes (scales + b * seq_groups) of
+    // nk[b] keys; blockIdx.z = b * chunks + row chunk
+    int B, chunks;
+    size_t seq_kbytes, seq_groups;
+    int nk[kMaxBatch];
 };
 
 __device__ __forceinline__ int head_begin(int hk, int H, int Hk) { return (hk * H + Hk - 1) / Hk; }
@@ -143,14 +150,23 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
     const int split = blockIdx.x, hk = blockIdx.y;
     const int h0 = head_begin(hk, a.H, a.Hk), h1 = head_begin(hk + 1, a.H, a.Hk);
     const int R = (h1 - h0) * a.Nq;
-    const int row0 = blockIdx.z * ROWS;
+    // the block's sequence and its cache
+    const int sq = (int)blockIdx.z / a.chunks;
+    const int row0 = ((int)blockIdx.z % a.chunks) * ROWS;
+    const int Nk = a.B > 1 ? a.nk[sq] : a.Nk;
+    const uint8_t* __restrict__ kcache = a.kc + (size_t)sq * a.seq_kbytes;
+    const uint8_t* __restrict__ vcache = a.vc + (size_t)sq * a.seq_kbytes;
+    const float* __restrict__ kscale = a.ks + (size_t)sq * a.seq_groups;
+    const float* __restrict__ vscale = a.vs + (size_t)sq * a.seq_groups;
+    const float* __restrict__ Qs = a.Q + (size_t)sq * a.Nq * a.H * D;
+    const size_t orow0 = (size_t)sq * a.Nq * a.H;
     const int Hk = a.Hk;
     const size_t krow = (size_t)Hk * (D / 2);       // bytes between positions
 
     const int k_begin = split * a.keys_per_split;
-    const int k_end = min(a.Nk, k_begin + a.keys_per_split);
+    const int k_end = min(Nk, k_begin + a.keys_per_split);
     const int ntiles = (k_end - k_begin + kTile - 1) / kTile;
-    const int base = a.Nk - a.Nq;                    // first of the new positions
+    const int base = Nk - a.Nq;                      // first of the new positions
 
     float m_run[RT], l_part[RT];
     f32x4 o[RT][8];                                  // O^T tiles t = 0..7
@@ -176,7 +192,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
         for (int kh = 0; kh < 2; kh++) {
             int key = kt + 16 * kh + n;
             key = key < k_end ? key : k_end - 1;
-            const uint8_t* p = a.kc + (size_t)key * krow + (size_t)hk * (D / 2) + (D / 8) * g;
+            const uint8_t* p = kcache + (size_t)key * krow + (size_t)hk * (D / 2) + (D / 8) * g;
             if (NC == 4) {
                 u32x4 v = *(const u32x4*)p;
                 t.kw[kh][0] = v.x; t.kw[kh][1] = v.y; t.kw[kh][2 % NC] = v.z; t.kw[kh][3 % NC] = v.w;
@@ -194,9 +210,9 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
             // lanes n >= D/8 have no column block: they read block 0 and the
             // O^T rows they produce are never stored
             const int nb = n < D / 8 ? n : 0;
-            t.vw[p] = *(const uint32_t*)(a.vc + (size_t)key * krow + (size_t)hk * (D / 2) + 4 * nb);
-            t.sk[p] = a.ks[(size_t)key * Hk + hk];
-            t.sv[p] = a.vs[(size_t)key * Hk + hk];
+            t.vw[p] = *(const uint32_t*)(vcache + (size_t)key * krow + (size_t)hk * (D / 2) + 4 * nb);
+            t.sk[p] = kscale[(size_t)key * Hk + hk];
+            t.sv[p] = vscale[(size_t)key * Hk + hk];
         }
     };
     TileData td;
@@ -218,8 +234,8 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
         anc_row[rt] = a.mask_kind == kMaskTree ? a.anc[rq[rt]] : 0ull;
         // chain: keys up to the query's own position; tree: the cached prefix
         // (plus ancestor bits); no mask: every key
-        lim_row[rt] = a.mask_kind == kMaskCausal ? a.Nk - a.Nq + rq[rt]
-                    : a.mask_kind == kMaskTree ? a.Nk - a.Nq - 1 : a.Nk;
+        lim_row[rt] = a.mask_kind == kMaskCausal ? Nk - a.Nq + rq[rt]
+                    : a.mask_kind == kMaskTree ? Nk - a.Nq - 1 : Nk;
     }
     {
         // rows are per lane (n); every wave computes the row exponent of its
@@ -232,7 +248,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
             // rows past R read row 0 (valid memory) and are zeroed: the loads
             // stay unconditional so they issue together
             const int h = h0 + (rok[rt] ? r / a.Nq : 0), q = rq[rt];
-            const float* qp = a.Q + ((size_t)q * a.H + h) * D + DPL * g;
+            const float* qp = Qs + ((size_t)q * a.H + h) * D + DPL * g;
             const float keep = rok[rt] ? 1.0f : 0.0f;
             float qv[DPL];
 #pragma unroll
@@ -425,11 +441,11 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
 #pragma unroll
         for (int w = 0; w < kWaves; w++) acc += s_o[w][row][d] * s_w[w][row];
         const int h = h0 + r / a.Nq, q = r % a.Nq;
-        const size_t orow = (size_t)q * a.H + h;
+        const size_t orow = orow0 + (size_t)q * a.H + h;
         if (a.splits == 1) {
             a.O[orow * D + d] = s_L[row] > 0.0f ? acc / s_L[row] : 0.0f;
         } else {
-            const size_t nrow = (size_t)a.Nq * a.H;
+            const size_t nrow = (size_t)a.B * a.Nq * a.H;
             a.part_o[((size_t)split * nrow + orow) * D + d] = acc;
             if (d == 0) {
                 a.part_ml[((size_t)split * nrow + orow) * 2] = s_M[row];
@@ -494,39 +510,55 @@ extern "C" int cgk_attn_dec_supported(int D, int gs, int B, int mask_kind) {
            (mask_kind == kMaskNone || mask_kind == kMaskCausal || mask_kind == kMaskTree);
 }
 
-extern "C" int cgk_attn_dec(const float* Q, const uint8_t* kc, const uint8_t* vc, const float* ks,
-                            const float* vs, int Nq, int Nk, int H, int Hk, int D, float scale,
-                            int mask_kind, const unsigned long long* anc, float* O) {
-    if (Nq <= 0 || Nk <= 0 || Hk <= 0 || H % Hk || Nq > Nk ||
+// Batched form: B sequences, each Nq query rows against its own cache
+// (sequence b at kc + b * seq_kbytes, scales + b * seq_groups) of nk[b] keys.
+extern "C" int cgk_attn_dec_batch(const float* Q, const uint8_t* kc, const uint8_t* vc,
+                                  const float* ks, const float* vs, int B, const int* nk,
+                                  size_t seq_kbytes, size_t seq_groups, int Nq, int H, int Hk,
+                                  int D, float scale, int mask_kind,
+                                  const unsigned long long* anc, float* O) {
+    int nkmax = 0, nkmin = 1 << 30;
+    for (int b = 0; b < B; b++) {
+        nkmax = nk[b] > nkmax ? nk[b] : nkmax;
+        nkmin = nk[b] < nkmin ? nk[b] : nkmin;
+    }
+    if (B < 1 || B > kMaxBatch || Nq <= 0 || nkmin < Nq || Hk <= 0 || H % Hk ||
         (mask_kind == kMaskTree && (Nq > 64 || !anc)) || (D != 32 && D != 64 && D != 128)) {
-        cgx_set_error("attn_dec: unsupported shape Nq=%d Nk=%d H=%d Hk=%d D=%d", Nq, Nk, H, Hk, D);
+        cgx_set_error("attn_dec: unsupported shape B=%d Nq=%d Nk=%d..%d H=%d Hk=%d D=%d", B, Nq,
+                      nkmin, nkmax, H, Hk, D);
         return -1;
     }
-    if (((uintptr_t)Q & 15) || ((uintptr_t)kc & 15)) {
+    if (((uintptr_t)Q & 15) || ((uintptr_t)kc & 15) || (seq_kbytes & 15)) {
         cgx_set_error("attn_dec: Q and the K cache must be 16-byte aligned");
         return -1;
     }
     DecArgs a;
     a.Q = Q; a.kc = kc; a.vc = vc; a.ks = ks; a.vs = vs;
-    a.Nq = Nq; a.Nk = Nk; a.H = H; a.Hk = Hk;
+    a.Nq = Nq; a.Nk = nkmax; a.H = H; a.Hk = Hk;
     a.scale = scale;
     a.mask_kind = mask_kind;
     for (int i = 0; i < 64; i++) a.anc[i] = (mask_kind == kMaskTree && i < Nq) ? anc[i] : 0ull;
+    a.B = B;
+    a.seq_kbytes = seq_kbytes;
+    a.seq_groups = seq_groups;
+    for (int b = 0; b < kMaxBatch; b++) a.nk[b] = b < B ? nk[b] : 0;
     const int R = (H / Hk) * Nq;
     // one 16-row tile per block keeps a wave's registers low enough for two
     // waves per SIMD; more rows run as more blocks (they re-read K/V from cache)
     const int RT = 1;
     const int chunks = (R + 16 * RT - 1) / (16 * RT);
+    a.chunks = chunks;
     // keys per split: whole block rounds, about 24 splits at most (measured
-    // at the 7B verify shape: 256-key splits beat 128 and 512)
-    const int rounds = (Nk + kSplitKeys * 24 - 1) / (kSplitKeys * 24);
+    // at the 7B verify shape: 256-key splits beat 128 and 512); the splits
+    // follow the longest sequence, shorter ones leave their last splits empty
+    const int rounds = (nkmax + kSplitKeys * 24 - 1) / (kSplitKeys * 24);
     int kps = kSplitKeys * (rounds > 1 ? rounds : 1);
-    while ((Nk + kps - 1) / kps > 128) kps += kSplitKeys;
-    const int splits = (Nk + kps - 1) / kps;
+    while ((nkmax + kps - 1) / kps > 128) kps += kSplitKeys;
+    const int splits = (nkmax + kps - 1) / kps;
     a.splits = splits;
     a.keys_per_split = kps;
     a.O = O;
-    const int nrow = Nq * H;
+    const int nrow = B * Nq * H;
     if (splits > 1) {
         a.part_o = (float*)cgx_scratch(CGX_SLOT_WS2, (size_t)splits * nrow * D * 4);
         a.part_ml = (float*)cgx_scratch(CGX_SLOT_WS3, (size_t)splits * nrow * 2 * 4);
@@ -534,7 +566,7 @@ extern "C" int cgk_attn_dec(const float* Q, const uint8_t* kc, const uint8_t* vc
     } else {
         a.part_o = a.part_ml = nullptr;
     }
-    dim3 grid(splits, Hk, chunks);
+    dim3 grid(splits, Hk, chunks * B);
     int rc;
     if (D == 128) rc = launch<128, 1>(a, grid);
     else if (D == 64) rc = launch<64, 1>(a, grid);
@@ -550,4 +582,11 @@ extern "C" int cgk_attn_dec(const float* Q, const uint8_t* kc, const uint8_t* vc
         if (launch_check("k_attn_dec_combine")) return -1;
     }
     return 0;
+}
+
+extern "C" int cgk_attn_dec(const float* Q, const uint8_t* kc, const uint8_t* vc, const float* ks,
+                            const float* vs, int Nq, int Nk, int H, int Hk, int D, float scale,
+                            int mask_kind, const unsigned long long* anc, float* O) {
+    return cgk_attn_dec_batch(Q, kc, vc, ks, vs, 1, &Nk, 0, 0, Nq, H, Hk, D, scale, mask_kind,
+                              anc, O);
 }

@@ -82,7 +82,14 @@ int cgk_verify_pipe(const float* target, const float* draft, const int* tokens, 
                     int batch, int gamma, int V, float T, float* accept_prob, int* out_tokens,
                     int* n_accepted);
 int cgk_sample_temperature_pipe(const float* logits, int rows, int V, float T, const float* u,
-                                int* out);
+                                int* out, size_t ld);
+/* The loop's token rows: ttok[b] = last_b, d_1 .. d_gamma and vtok[b] = d_1 .. d_gamma from
+ * feed [B][2] (prev, last) and the drafted tokens dtok [gamma][B]. */
+int cgk_spec_tokens(const int* feed, const int* dtok, int B, int gamma, int* ttok, int* vtok);
+/* Batched model forward with the logits rows of each sequence ld floats apart
+ * (host/model.c; the loop writes draft logits straight into [B][gamma][V]). */
+int cgx_model_forward_batch_ld(struct cgx_model* m, const int* tokens, int M, int n_logits,
+                               float* logits, size_t ld);
 int cgk_exp_fast_maxerr(float lo, float hi, unsigned int* out_dev);
 int cgk_ordered_sum(const float* x, int n, float* out);
 int cgk_sample_temperature(const float* logits, int V, float T, float u, int* out);
@@ -134,6 +141,12 @@ int cgk_attn_dec_supported(int D, int gs, int B, int mask_kind);
 int cgk_attn_dec(const float* Q, const uint8_t* kc, const uint8_t* vc, const float* ks,
                  const float* vs, int Nq, int Nk, int H, int Hk, int D, float scale,
                  int mask_kind, const unsigned long long* anc, float* O);
+/* Batched decode attention: B sequences of Nq query rows, sequence b's cache
+ * at kc + b * seq_kbytes (scales + b * seq_groups) with nk[b] keys. */
+int cgk_attn_dec_batch(const float* Q, const uint8_t* kc, const uint8_t* vc, const float* ks,
+                       const float* vs, int B, const int* nk, size_t seq_kbytes,
+                       size_t seq_groups, int Nq, int H, int Hk, int D, float scale,
+                       int mask_kind, const unsigned long long* anc, float* O);
 int cgk_rope(float* x, int S, int H, int D, int pos0, float theta);
 int cgk_rope_freqs(float* cs, float* sn, int S, int D, float theta);
 int cgk_alibi_slopes(float* slopes, int H);

@@ -47,16 +47,32 @@ __global__ void k_embed(const float* __restrict__ table, const int* __restrict__
         x[(size_t)m * d + i] = row[i];
 }
 
-// One workgroup of D/2 threads per (token m, head): heads [0, H) are query
+constexpr int kMaxBatch = 16;
+
+// Token rows of B sequences, M each (row r = b * M + m): sequence b's rows
+// sit at positions pos0[b] + m of its own cache (kc + b * seq_kbytes, scales
+// + b * seq_groups).
+struct RopeBatch {
+    int M;
+    int pos0[kMaxBatch];
+    size_t seq_kbytes, seq_groups;
+};
+
+// One workgroup of D/2 threads per (token row, head): heads [0, H) are query
 // heads (rotated into q_out), heads [H, H + Hk) are KV heads (K rotated, then
-// K and V quantised into the cache row of position pos0 + m).
+// K and V quantised into the cache row of the token's position).
 __global__ void k_rope_append(const float* __restrict__ qkv, int ld, int H, int Hk, int D,
-                              int gs, int pos0, float theta, float* __restrict__ q_out,
+                              int gs, RopeBatch rb, float theta, float* __restrict__ q_out,
                               uint8_t* __restrict__ kc, uint8_t* __restrict__ vc,
                               float* __restrict__ ks, float* __restrict__ vs) {
     __shared__ float sk[256], sv[256];
     const int m = blockIdx.x, head = blockIdx.y, i = threadIdx.x, half = D / 2;
-    const int pos = pos0 + m;
+    const int sq = m / rb.M;
+    const int pos = rb.pos0[sq] + m % rb.M;
+    kc += (size_t)sq * rb.seq_kbytes;
+    vc += (size_t)sq * rb.seq_kbytes;
+    ks += (size_t)sq * rb.seq_groups;
+    vs += (size_t)sq * rb.seq_groups;
     const float* row = qkv + (size_t)m * ld;
     float freq = __fdiv_rn(1.0f, powf(theta, __fdiv_rn((float)(2 * i), (float)D)));
     float angle = __fmul_rn((float)pos, freq);
@@ -114,6 +130,18 @@ __global__ void k_rope_append(const float* __restrict__ qkv, int ld, int H, int 
     vc[th * half + i] = (uint8_t)((b0 & 0xF) | ((b1 & 0xF) << 4));
 }
 
+// ttok[b] = feed[b][1], d_1 .. d_gamma; vtok[b] = d_1 .. d_gamma (dtok [gamma][B])
+__global__ void k_spec_tokens(const int* __restrict__ feed, const int* __restrict__ dtok, int B,
+                              int gamma, int* __restrict__ ttok, int* __restrict__ vtok) {
+    const int b = blockIdx.x, i = threadIdx.x;
+    if (i == 0) ttok[(size_t)b * (gamma + 1)] = feed[2 * b + 1];
+    for (int k = i; k < gamma; k += blockDim.x) {
+        const int t = dtok[(size_t)k * B + b];
+        ttok[(size_t)b * (gamma + 1) + 1 + k] = t;
+        vtok[(size_t)b * gamma + k] = t;
+    }
+}
+
 __device__ __forceinline__ uint32_t lowbias32(uint32_t x) {
     x ^= x >> 16;
     x *= 0x7feb352du;
@@ -145,17 +173,45 @@ extern "C" int cgk_embed(const float* table, const int* tokens, int M, int d, in
     return launch_check("k_embed");
 }
 
-extern "C" int cgk_rope_append(const float* qkv, int ld, int M, int H, int Hk, int D, int gs,
-                               int pos0, float theta, float* q_out, uint8_t* kc, uint8_t* vc,
-                               float* ks, float* vs) {
+extern "C" int cgk_rope_append_batch(const float* qkv, int ld, int B, int M, int H, int Hk,
+                                     int D, int gs, const int* pos0, float theta, float* q_out,
+                                     uint8_t* kc, uint8_t* vc, float* ks, float* vs,
+                                     size_t seq_kbytes, size_t seq_groups) {
     if (M <= 0) return 0;
     if (D < 2 || D > 256 || (D & 1) || gs <= 0 || (gs & 1) || D % gs) {
         cgx_set_error("rope_append: unsupported head_dim %d / group %d", D, gs);
         return -1;
     }
-    hipLaunchKernelGGL(k_rope_append, dim3(M, H + Hk), dim3(D / 2), 0, stream(), qkv, ld, H,
-                       Hk, D, gs, pos0, theta, q_out, kc, vc, ks, vs);
+    if (B < 1 || B > kMaxBatch) {
+        cgx_set_error("rope_append: batch %d outside [1, %d]", B, kMaxBatch);
+        return -1;
+    }
+    RopeBatch rb;
+    rb.M = M;
+    for (int b = 0; b < kMaxBatch; b++) rb.pos0[b] = b < B ? pos0[b] : 0;
+    rb.seq_kbytes = seq_kbytes;
+    rb.seq_groups = seq_groups;
+    hipLaunchKernelGGL(k_rope_append, dim3(B * M, H + Hk), dim3(D / 2), 0, stream(), qkv, ld, H,
+                       Hk, D, gs, rb, theta, q_out, kc, vc, ks, vs);
     return launch_check("k_rope_append");
+}
+
+extern "C" int cgk_rope_append(const float* qkv, int ld, int M, int H, int Hk, int D, int gs,
+                               int pos0, float theta, float* q_out, uint8_t* kc, uint8_t* vc,
+                               float* ks, float* vs) {
+    return cgk_rope_append_batch(qkv, ld, 1, M, H, Hk, D, gs, &pos0, theta, q_out, kc, vc, ks,
+                                 vs, 0, 0);
+}
+
+extern "C" int cgk_spec_tokens(const int* feed, const int* dtok, int B, int gamma, int* ttok,
+                               int* vtok) {
+    if (B < 1 || gamma < 1) {
+        cgx_set_error("spec_tokens: batch %d, gamma %d", B, gamma);
+        return -1;
+    }
+    hipLaunchKernelGGL(k_spec_tokens, dim3(B), dim3(64), 0, stream(), feed, dtok, B, gamma, ttok,
+                       vtok);
+    return launch_check("k_spec_tokens");
 }
 
 // Per-matrix key: mixes the seed and the matrix id.

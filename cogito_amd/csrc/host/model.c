@@ -17,8 +17,9 @@
 #include "cgx_internal.h"
 
 int cgk_embed(const float* table, const int* tokens, int M, int d, int V, float* x);
-int cgk_rope_append(const float* qkv, int ld, int M, int H, int Hk, int D, int gs, int pos0,
-                    float theta, float* q_out, uint8_t* kc, uint8_t* vc, float* ks, float* vs);
+int cgk_rope_append_batch(const float* qkv, int ld, int B, int M, int H, int Hk, int D, int gs,
+                          const int* pos0, float theta, float* q_out, uint8_t* kc, uint8_t* vc,
+                          float* ks, float* vs, size_t seq_kbytes, size_t seq_groups);
 int cgk_fill_normal(float* out, size_t n, uint64_t seed, uint32_t stream_id, float stddev);
 
 enum { PRO_NONE = 0, PRO_RMSNORM = 1 };
@@ -36,8 +37,12 @@ typedef struct {
     lin_t w[4];
 } layer_t;
 
+#define CGX_MAX_BATCH 16
+
 struct cgx_model {
     cgx_model_config c;
+    int nb;                  /* sequences (max_batch, at least 1) */
+    int len[CGX_MAX_BATCH];  /* KV length of each sequence */
     uint64_t seed;
     float* embed;
     lin_t lm;
@@ -100,7 +105,8 @@ static int check_config(const cgx_model_config* c) {
         c->n_heads % c->n_kv_heads || c->head_dim < 2 || c->head_dim > 128 ||
         (c->head_dim & 1) || c->d_ff < 1 || c->vocab < 2 || gs < 16 || gs % 16 ||
         c->kv_group_size < 2 || (c->kv_group_size & 1) || c->head_dim % c->kv_group_size ||
-        c->max_seq < 1 || c->max_tokens < 1 || c->max_tokens > c->max_seq) {
+        c->max_seq < 1 || c->max_tokens < 1 || c->max_tokens > c->max_seq ||
+        c->max_batch < 0 || c->max_batch > CGX_MAX_BATCH) {
         cgx_set_error("cgx_model_new: invalid configuration");
         return -1;
     }
@@ -151,9 +157,10 @@ cgx_model* cgx_model_new(const cgx_model_config* cfg, uint64_t seed, cgx_model* 
     cgx_model* m = (cgx_model*)calloc(1, sizeof(*m));
     if (!m) return NULL;
     m->c = *cfg;
+    m->nb = cfg->max_batch > 0 ? cfg->max_batch : 1;
     m->seed = seed;
     const cgx_model_config* c = &m->c;
-    int d = c->d_model, V = c->vocab, Mx = c->max_tokens;
+    int d = c->d_model, V = c->vocab, Mx = c->max_tokens * m->nb;   /* rows per forward */
     size_t maxn = 0;
     for (int w = 0; w <= W_LM; w++) {
         int K, N;
@@ -189,8 +196,9 @@ cgx_model* cgx_model_new(const cgx_model_config* cfg, uint64_t seed, cgx_model* 
         free(h);
     }
     if (ok) {
-        m->kv = cg_kv_cache_int4_new(c->n_layers, c->max_seq, c->n_kv_heads, c->head_dim,
-                                     c->kv_group_size);
+        /* layer slot l * nb + b holds layer l of sequence b */
+        m->kv = cg_kv_cache_int4_new(c->n_layers * m->nb, c->max_seq, c->n_kv_heads,
+                                     c->head_dim, c->kv_group_size);
         m->tok = (int*)cgx_malloc((size_t)Mx * 4);
         m->x = (float*)cgx_malloc((size_t)Mx * d * 4);
         m->qkv = (float*)cgx_malloc((size_t)Mx * nqkv(c) * 4);
@@ -221,15 +229,39 @@ int cgx_model_get_config(const cgx_model* m, cgx_model_config* out) {
     *out = m->c;
     return 0;
 }
-int cgx_model_len(const cgx_model* m) { return m ? m->kv->current_len : -1; }
+int cgx_model_len(const cgx_model* m) {
+    if (!m) return -1;
+    return m->nb == 1 ? m->kv->current_len : m->len[0];
+}
+int cgx_model_batch(const cgx_model* m) { return m ? m->nb : -1; }
 cg_kv_cache_int4* cgx_model_kv(cgx_model* m) { return m ? m->kv : NULL; }
+
+int cgx_model_len_seq(const cgx_model* m, int seq) {
+    if (!m || seq < 0 || seq >= m->nb) {
+        cgx_set_error("cgx_model_len_seq: invalid sequence");
+        return -1;
+    }
+    return m->len[seq];
+}
+
+int cgx_model_truncate_seq(cgx_model* m, int seq, int len) {
+    if (!m || seq < 0 || seq >= m->nb || len < 0 || len > m->len[seq]) {
+        cgx_set_error("cgx_model_truncate_seq: invalid sequence or length");
+        return -1;
+    }
+    m->len[seq] = len;
+    if (seq == 0) m->kv->current_len = len;
+    return 0;
+}
 
 int cgx_model_truncate(cgx_model* m, int len) {
     if (!m) {
         cgx_set_error("cgx_model_truncate: NULL model");
         return -1;
     }
-    return cgx_kv_cache_int4_truncate(m->kv, len);
+    if (cgx_kv_cache_int4_truncate(m->kv, len)) return -1;
+    m->len[0] = len;
+    return 0;
 }
 
 static size_t kv_layer_bytes(const cg_kv_cache_int4* c) {
@@ -240,56 +272,121 @@ static size_t kv_layer_groups(const cg_kv_cache_int4* c) {
     return (size_t)c->max_seq_len * c->n_heads * (c->head_dim / c->group_size);
 }
 
-int cgx_model_forward(cgx_model* m, const int* tokens, int M, int n_logits, float* logits) {
-    if (!m || !tokens || M < 1 || M > m->c.max_tokens || n_logits < 0 || n_logits > M) {
+/* Forward of B sequences (0..B-1), M tokens each. */
+static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_logits,
+                        float* logits, size_t ldl) {
+    const cgx_model_config* c = &m->c;
+    if (!tokens || M < 1 || M > c->max_tokens || n_logits < 0 || n_logits > M) {
         cgx_set_error("cgx_model_forward: invalid argument (M=%d, n_logits=%d)", M, n_logits);
         return -1;
     }
-    const cgx_model_config* c = &m->c;
     cg_kv_cache_int4* kv = m->kv;
-    const int pos0 = kv->current_len;
-    if (pos0 + M > c->max_seq) {
-        cgx_set_error("cgx_model_forward: KV cache full (%d + %d > %d)", pos0, M, c->max_seq);
-        return -1;
+    /* a single-sequence cache may have been moved through cgx_model_kv */
+    if (m->nb == 1) m->len[0] = kv->current_len;
+    int pos0[CGX_MAX_BATCH], nk[CGX_MAX_BATCH];
+    for (int b = 0; b < B; b++) {
+        pos0[b] = m->len[b];
+        nk[b] = pos0[b] + M;
+        if (nk[b] > c->max_seq) {
+            cgx_set_error("cgx_model_forward: KV cache full (%d + %d > %d)", pos0[b], M,
+                          c->max_seq);
+            return -1;
+        }
     }
+    const int R = B * M;
     const int* dtok = tokens;
     if (!cgx_is_device_ptr(tokens)) {
-        if (cgx_memcpy_h2d(m->tok, tokens, (size_t)M * 4)) return -1;
+        if (cgx_memcpy_h2d(m->tok, tokens, (size_t)R * 4)) return -1;
         dtok = m->tok;
     }
     const int d = c->d_model, H = c->n_heads, Hk = c->n_kv_heads, hd = c->head_dim;
     const int hq = H * hd, gs = c->group_size, ff = c->d_ff, nq = nqkv(c);
     const float eps = c->norm_eps, scale = 1.0f / sqrtf((float)hd);
-    if (cgk_embed(m->embed, dtok, M, d, c->vocab, m->x)) return -1;
+    if (cgk_embed(m->embed, dtok, R, d, c->vocab, m->x)) return -1;
     const size_t lb = kv_layer_bytes(kv), lg = kv_layer_groups(kv);
+    const int batched = cgk_attn_dec_supported(hd, kv->group_size, 1, CGK_MASK_CAUSAL_ALIGNED);
     for (int l = 0; l < c->n_layers; l++) {
         const lin_t* w = m->layers[l].w;
-        uint8_t* kc = kv->k_cache + lb * l;
-        uint8_t* vc = kv->v_cache + lb * l;
-        float* ks = kv->k_scales + lg * l;
-        float* vs = kv->v_scales + lg * l;
-        if (cgk_gemv_mfma(m->x, d, M, d, nq, gs, w[W_QKV].tiled, w[W_QKV].scales_t, m->qkv, nq,
+        /* layer l of sequence b: slot l * nb + b */
+        const size_t slot = (size_t)l * m->nb;
+        uint8_t* kc = kv->k_cache + lb * slot;
+        uint8_t* vc = kv->v_cache + lb * slot;
+        float* ks = kv->k_scales + lg * slot;
+        float* vs = kv->v_scales + lg * slot;
+        if (cgk_gemv_mfma(m->x, d, R, d, nq, gs, w[W_QKV].tiled, w[W_QKV].scales_t, m->qkv, nq,
                           PRO_RMSNORM, m->ones, eps, EPI_STORE) ||
-            cgk_rope_append(m->qkv, nq, M, H, Hk, hd, kv->group_size, pos0, c->rope_theta,
-                            m->q, kc, vc, ks, vs) ||
-            cgk_attention(m->q, 1, kc, vc, ks, vs, kv->group_size, NULL, NULL, 1, M, pos0 + M,
-                          H, Hk, hd, scale, CGK_MASK_CAUSAL_ALIGNED, 0, NULL, NULL, m->attn,
-                          NULL) ||
-            cgk_gemv_mfma(m->attn, hq, M, hq, d, gs, w[W_O].tiled, w[W_O].scales_t, m->x, d,
+            cgk_rope_append_batch(m->qkv, nq, B, M, H, Hk, hd, kv->group_size, pos0,
+                                  c->rope_theta, m->q, kc, vc, ks, vs, lb, lg))
+            return -1;
+        if (batched) {
+            if (cgk_attn_dec_batch(m->q, kc, vc, ks, vs, B, nk, lb, lg, M, H, Hk, hd, scale,
+                                   CGK_MASK_CAUSAL_ALIGNED, NULL, m->attn))
+                return -1;
+        } else {
+            for (int b = 0; b < B; b++)
+                if (cgk_attention(m->q + (size_t)b * M * hq, 1, kc + lb * b, vc + lb * b,
+                                  ks + lg * b, vs + lg * b, kv->group_size, NULL, NULL, 1, M,
+                                  nk[b], H, Hk, hd, scale, CGK_MASK_CAUSAL_ALIGNED, 0, NULL,
+                                  NULL, m->attn + (size_t)b * M * hq, NULL))
+                    return -1;
+        }
+        if (cgk_gemv_mfma(m->attn, hq, R, hq, d, gs, w[W_O].tiled, w[W_O].scales_t, m->x, d,
                           PRO_NONE, NULL, 0.0f, EPI_ACCUMULATE) ||
-            cgk_gemv_mfma(m->x, d, M, d, 2 * ff, gs, w[W_GU].tiled, w[W_GU].scales_t, m->gu, ff,
+            cgk_gemv_mfma(m->x, d, R, d, 2 * ff, gs, w[W_GU].tiled, w[W_GU].scales_t, m->gu, ff,
                           PRO_RMSNORM, m->ones, eps, EPI_SWIGLU) ||
-            cgk_gemv_mfma(m->gu, ff, M, ff, d, gs, w[W_DOWN].tiled, w[W_DOWN].scales_t, m->x, d,
+            cgk_gemv_mfma(m->gu, ff, R, ff, d, gs, w[W_DOWN].tiled, w[W_DOWN].scales_t, m->x, d,
                           PRO_NONE, NULL, 0.0f, EPI_ACCUMULATE))
             return -1;
     }
-    if (n_logits > 0 &&
-        cgk_gemv_mfma(m->x + (size_t)(M - n_logits) * d, d, n_logits, d, c->vocab, gs,
-                      m->lm.tiled, m->lm.scales_t, logits ? logits : m->logits, c->vocab,
-                      PRO_RMSNORM, m->ones, eps, EPI_STORE))
-        return -1;
-    kv->current_len = pos0 + M;
+    float* out = logits ? logits : m->logits;
+    if (!ldl) ldl = (size_t)n_logits * c->vocab;
+    if (n_logits == M && ldl == (size_t)M * c->vocab) {
+        /* every row, sequences in order */
+        if (cgk_gemv_mfma(m->x, d, R, d, c->vocab, gs, m->lm.tiled, m->lm.scales_t, out,
+                          c->vocab, PRO_RMSNORM, m->ones, eps, EPI_STORE))
+            return -1;
+    } else if (n_logits == 1) {
+        /* the last row of each sequence: rows M-1, 2M-1, ... */
+        if (cgk_gemv_mfma(m->x + (size_t)(M - 1) * d, M * d, B, d, c->vocab, gs, m->lm.tiled,
+                          m->lm.scales_t, out, (int)ldl, PRO_RMSNORM, m->ones, eps, EPI_STORE))
+            return -1;
+    } else if (n_logits > 0) {
+        for (int b = 0; b < B; b++)
+            if (cgk_gemv_mfma(m->x + ((size_t)b * M + M - n_logits) * d, d, n_logits, d,
+                              c->vocab, gs, m->lm.tiled, m->lm.scales_t,
+                              out + (size_t)b * ldl, c->vocab, PRO_RMSNORM,
+                              m->ones, eps, EPI_STORE))
+                return -1;
+    }
+    for (int b = 0; b < B; b++) m->len[b] = pos0[b] + M;
+    kv->current_len = m->len[0];
     return 0;
+}
+
+int cgx_model_forward(cgx_model* m, const int* tokens, int M, int n_logits, float* logits) {
+    if (!m) {
+        cgx_set_error("cgx_model_forward: NULL model");
+        return -1;
+    }
+    return forward_rows(m, 1, tokens, M, n_logits, logits, 0);
+}
+
+int cgx_model_forward_batch(cgx_model* m, const int* tokens, int M, int n_logits,
+                            float* logits) {
+    if (!m) {
+        cgx_set_error("cgx_model_forward_batch: NULL model");
+        return -1;
+    }
+    return forward_rows(m, m->nb, tokens, M, n_logits, logits, 0);
+}
+
+int cgx_model_forward_batch_ld(cgx_model* m, const int* tokens, int M, int n_logits,
+                               float* logits, size_t ld) {
+    if (!m) {
+        cgx_set_error("cgx_model_forward_batch: NULL model");
+        return -1;
+    }
+    return forward_rows(m, m->nb, tokens, M, n_logits, logits, ld);
 }
 
 int cgx_model_fill_context(cgx_model* m, int len, uint64_t seed) {
@@ -298,7 +395,10 @@ int cgx_model_fill_context(cgx_model* m, int len, uint64_t seed) {
         return -1;
     }
     cg_kv_cache_int4* kv = m->kv;
-    if (!len) return cgx_kv_cache_int4_set_len(kv, 0);
+    if (!len) {
+        for (int b = 0; b < m->nb; b++) m->len[b] = 0;
+        return cgx_kv_cache_int4_set_len(kv, 0);
+    }
     size_t n = (size_t)len * kv->n_heads * kv->head_dim;
     float* k = (float*)cgx_malloc(n * 4);
     float* v = (float*)cgx_malloc(n * 4);
@@ -312,6 +412,8 @@ int cgx_model_fill_context(cgx_model* m, int len, uint64_t seed) {
     cgx_free(k);
     cgx_free(v);
     if (!rc) rc = cgx_kv_cache_int4_set_len(kv, len);
+    if (!rc)
+        for (int b = 0; b < m->nb; b++) m->len[b] = len;
     return rc ? -1 : 0;
 }
 

@@ -49,7 +49,7 @@ int cgx_sample_temperature_u(const float* logits, int V, float T, float u) {
         /* the draw goes to the device next to the token */
         float* du = (float*)(out + 1);
         if (cgx_memcpy_h2d(du, &u, sizeof(float)) ||
-            cgk_sample_temperature_pipe(d, 1, V, T, du, out))
+            cgk_sample_temperature_pipe(d, 1, V, T, du, out, (size_t)V))
             return -1;
     } else if (cgk_sample_temperature(d, V, T, u, out)) {
         return -1;

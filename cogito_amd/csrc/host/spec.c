@@ -145,7 +145,8 @@ static int draft_sample(cgx_spec* s, int i, float u_host) {
     int* out = s->d_tokens + i + 1;
     if (!s->filtered) {
         if (cgk_verify_pipe_supported(1, 0, s->V, s->T))
-            return cgk_sample_temperature_pipe(row, 1, s->V, s->T, s->d_u + i, out);
+            return cgk_sample_temperature_pipe(row, 1, s->V, s->T, s->d_u + i, out,
+                                               (size_t)s->V);
         return cgk_sample_temperature(row, s->V, s->T, u_host, out);
     }
     if (cgk_scale(row, s->d_z, (size_t)s->V, s->T)) return -1;
@@ -229,4 +230,212 @@ int cgx_spec_step(cgx_spec* s, const float* u_draft, const float* u_verify, int*
     s->drafted += g;
     s->accepted += n;
     return n;
+}
+
+/* ------------------------------------------------------------ batches */
+/*
+ * B sequences in lockstep over two models built with max_batch = B (each
+ * sequence has its own KV caches).  Every step:
+ *   - each draft cache is cut to (target length - 1) and fed (prev, last):
+ *     prev is the token at the target's last cached position, recomputed
+ *     to the same K/V, so every sequence takes two draft tokens at once;
+ *   - gamma - 1 more single-token draft forwards, each draft row sampled on
+ *     the GPU into dtok [gamma][B];
+ *   - one target forward of gamma + 1 tokens per sequence, the batched
+ *     verify (verify.hip), one host round trip for the tokens and counts;
+ *   - each target cache keeps last, d_1 .. d_n.
+ * Unfiltered sampling only (temperature > 0, no top-k / top-p).
+ */
+struct cgx_spec_batch {
+    cgx_model* draft;
+    cgx_model* target;
+    int B, gamma, V;
+    float T;
+    int* d_feed;            /* [B][2] prev, last */
+    int* d_dtok;            /* [gamma][B] drafted tokens */
+    int* d_ttok;            /* [B][gamma + 1] target input */
+    int* d_vtok;            /* [B][gamma] drafted tokens per chain */
+    float* d_draft_logits;  /* [B][gamma][V] */
+    float* d_target_logits; /* [B][gamma + 1][V] */
+    float* d_u;             /* draft draws [gamma][B], then verify draws [B][gamma + 1] */
+    int* d_out;             /* [B][gamma + 1] tokens, then [B] accepted counts */
+    float* d_ap;            /* [B][gamma] */
+    int prev[16], last[16];
+    int have_last;
+    long long steps, drafted, accepted;
+};
+
+void cgx_spec_batch_free(cgx_spec_batch* s) {
+    if (!s) return;
+    cgx_free(s->d_feed);
+    cgx_free(s->d_dtok);
+    cgx_free(s->d_ttok);
+    cgx_free(s->d_vtok);
+    cgx_free(s->d_draft_logits);
+    cgx_free(s->d_target_logits);
+    cgx_free(s->d_u);
+    cgx_free(s->d_out);
+    cgx_free(s->d_ap);
+    free(s);
+}
+
+cgx_spec_batch* cgx_spec_batch_new(cgx_model* draft, cgx_model* target, int gamma,
+                                   float temperature) {
+    cgx_model_config cd, ct;
+    if (!draft || !target || draft == target || gamma < 1 ||
+        cgx_model_get_config(draft, &cd) || cgx_model_get_config(target, &ct)) {
+        cgx_set_error("cgx_spec_batch_new: two distinct models and gamma >= 1 are required");
+        return NULL;
+    }
+    const int B = cgx_model_batch(target);
+    if (cgx_model_batch(draft) != B || cd.vocab != ct.vocab || ct.max_tokens < gamma + 1 ||
+        cd.max_tokens < 2) {
+        cgx_set_error("cgx_spec_batch_new: the models need the same batch and vocabulary, "
+                      "max_tokens >= gamma + 1 (target) and >= 2 (draft)");
+        return NULL;
+    }
+    if (!cgk_verify_pipe_supported(B, gamma, ct.vocab, temperature)) {
+        cgx_set_error("cgx_spec_batch_new: batch %d, gamma %d, vocab %d, temperature %g "
+                      "outside the batched verify", B, gamma, ct.vocab, (double)temperature);
+        return NULL;
+    }
+    cgx_spec_batch* s = (cgx_spec_batch*)calloc(1, sizeof(*s));
+    if (!s) return NULL;
+    s->draft = draft;
+    s->target = target;
+    s->B = B;
+    s->gamma = gamma;
+    s->V = ct.vocab;
+    s->T = temperature;
+    size_t V = (size_t)s->V, g = (size_t)gamma, b = (size_t)B;
+    s->d_feed = (int*)cgx_malloc(b * 2 * 4);
+    s->d_dtok = (int*)cgx_malloc(g * b * 4);
+    s->d_ttok = (int*)cgx_malloc(b * (g + 1) * 4);
+    s->d_vtok = (int*)cgx_malloc(b * g * 4);
+    s->d_draft_logits = (float*)cgx_malloc(b * g * V * 4);
+    s->d_target_logits = (float*)cgx_malloc(b * (g + 1) * V * 4);
+    s->d_u = (float*)cgx_malloc(b * (2 * g + 1) * 4);
+    s->d_out = (int*)cgx_malloc(b * (g + 2) * 4);
+    s->d_ap = (float*)cgx_malloc(b * g * 4);
+    if (!s->d_feed || !s->d_dtok || !s->d_ttok || !s->d_vtok || !s->d_draft_logits ||
+        !s->d_target_logits || !s->d_u || !s->d_out || !s->d_ap) {
+        cgx_spec_batch_free(s);
+        return NULL;
+    }
+    return s;
+}
+
+int cgx_spec_batch_set_last(cgx_spec_batch* s, const int* prev, const int* last) {
+    if (!s || !prev || !last) {
+        cgx_set_error("cgx_spec_batch_set_last: invalid argument");
+        return -1;
+    }
+    for (int b = 0; b < s->B; b++) {
+        const int lt = cgx_model_len_seq(s->target, b), ld = cgx_model_len_seq(s->draft, b);
+        if (prev[b] < 0 || prev[b] >= s->V || last[b] < 0 || last[b] >= s->V || lt < 1 ||
+            ld < lt - 1) {
+            cgx_set_error("cgx_spec_batch_set_last: sequence %d: tokens out of range or "
+                          "caches hold %d (target) / %d (draft) positions", b, lt, ld);
+            return -1;
+        }
+        s->prev[b] = prev[b];
+        s->last[b] = last[b];
+    }
+    s->have_last = 1;
+    return 0;
+}
+
+int cgx_spec_batch_step(cgx_spec_batch* s, const float* u_draft, const float* u_verify,
+                        int* out_tokens, int* n_accepted) {
+    if (!s || !u_draft || !u_verify || !out_tokens || !n_accepted) {
+        cgx_set_error("cgx_spec_batch_step: invalid argument");
+        return -1;
+    }
+    if (!s->have_last) {
+        cgx_set_error("cgx_spec_batch_step: no context (call cgx_spec_batch_set_last)");
+        return -1;
+    }
+    const int B = s->B, g = s->gamma;
+    cgx_model_config ct;
+    cgx_model_get_config(s->target, &ct);
+    int L[16];
+    for (int b = 0; b < B; b++) {
+        L[b] = cgx_model_len_seq(s->target, b);
+        if (L[b] + g + 1 > ct.max_seq) {
+            cgx_set_error("cgx_spec_batch_step: KV cache of sequence %d full", b);
+            return -1;
+        }
+        /* the draft re-takes (prev, last) at positions L - 1, L */
+        if (cgx_model_truncate_seq(s->draft, b, L[b] - 1)) return -1;
+    }
+    /* draws: draft [gamma][B] (transposed), verify [B][gamma + 1]; feed [B][2] */
+    size_t nu = (size_t)B * (2 * g + 1);
+    float* hu = (float*)malloc(nu * sizeof(float));
+    int feed[32];
+    if (!hu) return -1;
+    for (int i = 0; i < g; i++)
+        for (int b = 0; b < B; b++) hu[(size_t)i * B + b] = u_draft[(size_t)b * g + i];
+    memcpy(hu + (size_t)g * B, u_verify, (size_t)B * (g + 1) * sizeof(float));
+    for (int b = 0; b < B; b++) {
+        feed[2 * b] = s->prev[b];
+        feed[2 * b + 1] = s->last[b];
+    }
+    int rc = cgx_memcpy_h2d(s->d_u, hu, nu * sizeof(float)) ||
+             cgx_memcpy_h2d(s->d_feed, feed, (size_t)B * 2 * sizeof(int));
+    free(hu);
+    if (rc) return -1;
+    const size_t V = (size_t)s->V, ldd = (size_t)g * V;
+    const float* ud = s->d_u;
+    const float* uv = s->d_u + (size_t)g * B;
+    /* draft: d_1 from (prev, last), then d_2 .. d_gamma */
+    if (cgx_model_forward_batch_ld(s->draft, s->d_feed, 2, 1, s->d_draft_logits, ldd) ||
+        cgk_sample_temperature_pipe(s->d_draft_logits, B, s->V, s->T, ud, s->d_dtok, ldd))
+        return -1;
+    for (int i = 1; i < g; i++) {
+        if (cgx_model_forward_batch_ld(s->draft, s->d_dtok + (size_t)(i - 1) * B, 1, 1,
+                                       s->d_draft_logits + (size_t)i * V, ldd) ||
+            cgk_sample_temperature_pipe(s->d_draft_logits + (size_t)i * V, B, s->V, s->T,
+                                        ud + (size_t)i * B, s->d_dtok + (size_t)i * B, ldd))
+            return -1;
+    }
+    /* target over last, d_1 .. d_gamma of every sequence, then the verify */
+    int* dn = s->d_out + (size_t)B * (g + 1);
+    if (cgk_spec_tokens(s->d_feed, s->d_dtok, B, g, s->d_ttok, s->d_vtok) ||
+        cgx_model_forward_batch(s->target, s->d_ttok, g + 1, g + 1, s->d_target_logits) ||
+        cgk_verify_pipe(s->d_target_logits, s->d_draft_logits, s->d_vtok, uv, B, g, s->V, s->T,
+                        s->d_ap, s->d_out, dn))
+        return -1;
+    int* ho = (int*)malloc((size_t)B * (g + 2) * sizeof(int));
+    if (!ho) return -1;
+    if (cgx_memcpy_d2h(ho, s->d_out, (size_t)B * (g + 2) * sizeof(int))) {
+        free(ho);
+        return -1;
+    }
+    int total = 0;
+    for (int b = 0; b < B; b++) {
+        const int n = ho[(size_t)B * (g + 1) + b];
+        const int* o = ho + (size_t)b * (g + 1);
+        n_accepted[b] = n;
+        for (int i = 0; i <= g; i++) out_tokens[(size_t)b * (g + 1) + i] = i <= n ? o[i] : -1;
+        /* the target keeps last, d_1 .. d_n */
+        if (cgx_model_truncate_seq(s->target, b, L[b] + n + 1)) {
+            free(ho);
+            return -1;
+        }
+        s->prev[b] = n > 0 ? o[n - 1] : s->last[b];
+        s->last[b] = o[n];
+        total += n;
+        s->accepted += n;
+    }
+    free(ho);
+    s->steps++;
+    s->drafted += (long long)g * B;
+    return total;
+}
+
+void cgx_spec_batch_stats(const cgx_spec_batch* s, long long* steps, long long* drafted,
+                          long long* accepted) {
+    if (steps) *steps = s ? s->steps : 0;
+    if (drafted) *drafted = s ? s->drafted : 0;
+    if (accepted) *accepted = s ? s->accepted : 0;
 }

@@ -150,9 +150,10 @@ struct Rows {            // pass-1 rows: per chain target 0..gamma, draft 0..gam
     const float* target;
     const float* draft;
     int gamma, V;
+    size_t ldt;          // floats between consecutive target rows (V unless strided)
     __device__ const float* row(int r) const {
         const int per = 2 * gamma + 1, c = r / per, i = r % per;
-        return i <= gamma ? target + ((size_t)c * (gamma + 1) + i) * V
+        return i <= gamma ? target + ((size_t)c * (gamma + 1) + i) * ldt
                           : draft + ((size_t)c * gamma + (i - gamma - 1)) * V;
     }
 };
@@ -1116,9 +1117,9 @@ extern "C" int cgk_verify_pipe_supported(int batch, int gamma, int V, float T) {
            V <= kRound * kMaxRounds && T > 0.0f && T <= FLT_MAX;
 }
 
-extern "C" int cgk_verify_pipe(const float* target, const float* draft, const int* tokens,
-                               const float* u, int batch, int gamma, int V, float T,
-                               float* accept_prob, int* out_tokens, int* n_accepted) {
+static int verify_pipe(const float* target, size_t ldt, const float* draft, const int* tokens,
+                       const float* u, int batch, int gamma, int V, float T, float* accept_prob,
+                       int* out_tokens, int* n_accepted) {
     using namespace vp;
     if (!cgk_verify_pipe_supported(batch, gamma, V, T)) {
         cgx_set_error("verify: batch %d, gamma %d, V %d, T %g outside the pipeline's range",
@@ -1172,7 +1173,7 @@ extern "C" int cgk_verify_pipe(const float* target, const float* draft, const in
     w.flags = (int*)(ws + o_flags);
     float* ap = accept_prob ? accept_prob : (float*)(ws + o_ap);
     if (!n_accepted) n_accepted = (int*)(ws + o_n);
-    Rows rows{target, draft, gamma, V};
+    Rows rows{target, draft, gamma, V, ldt};
     hipStream_t st = stream();
     hipLaunchKernelGGL(k_seg_stats, dim3(nseg, R1), dim3(kT), 0, st, rows, T, w);
     if (launch_check("k_seg_stats")) return -1;
@@ -1196,10 +1197,18 @@ extern "C" int cgk_verify_pipe(const float* target, const float* draft, const in
     return launch_check("k_verify_fallback");
 }
 
+extern "C" int cgk_verify_pipe(const float* target, const float* draft, const int* tokens,
+                               const float* u, int batch, int gamma, int V, float T,
+                               float* accept_prob, int* out_tokens, int* n_accepted) {
+    return verify_pipe(target, (size_t)V, draft, tokens, u, batch, gamma, V, T, accept_prob,
+                       out_tokens, n_accepted);
+}
+
 // cg_sample_temperature on `rows` rows at once through the same pipeline: a
 // verify with no drafted tokens is exactly the bonus draw from target row 0
-// (speculative.c:54-75).  u: one draw per row (device); out: one token per row.
+// (speculative.c:54-75).  Row r at logits + r * ld; u: one draw per row
+// (device); out: one token per row.
 extern "C" int cgk_sample_temperature_pipe(const float* logits, int rows, int V, float T,
-                                           const float* u, int* out) {
-    return cgk_verify_pipe(logits, logits, nullptr, u, rows, 0, V, T, nullptr, out, nullptr);
+                                           const float* u, int* out, size_t ld) {
+    return verify_pipe(logits, ld, logits, nullptr, u, rows, 0, V, T, nullptr, out, nullptr);
 }

@@ -178,6 +178,7 @@ typedef struct {
     float rope_theta;
     float norm_eps;
     float init_std;
+    int max_batch;        /* sequences held, each with its own KV cache (0: 1) */
 } cgx_model_config;
 
 typedef struct cgx_model cgx_model;
@@ -196,6 +197,15 @@ float* cgx_model_logits(cgx_model* m);
 int cgx_model_get_config(const cgx_model* m, cgx_model_config* out);
 int cgx_model_len(const cgx_model* m);
 int cgx_model_truncate(cgx_model* m, int len);
+/* Batch of max_batch sequences: each forward advances every sequence by M
+ * tokens (tokens [B][M], host or device); logits of the last n_logits tokens
+ * of each sequence go to logits [B][n_logits][V].  The single-sequence
+ * functions above act on sequence 0. */
+int cgx_model_forward_batch(cgx_model* m, const int* tokens, int M, int n_logits,
+                            float* logits);
+int cgx_model_batch(const cgx_model* m);
+int cgx_model_len_seq(const cgx_model* m, int seq);
+int cgx_model_truncate_seq(cgx_model* m, int seq, int len);
 cg_kv_cache_int4* cgx_model_kv(cgx_model* m);
 /* Synthetic context: K/V rows of positions [0, len) of every layer filled
  * with seeded values (std 1) and len set, as if a prompt had been run. */
@@ -233,6 +243,22 @@ int cgx_spec_step(cgx_spec* s, const float* u_draft, const float* u_verify,
 /* totals since cgx_spec_new: steps, drafted tokens, accepted tokens */
 void cgx_spec_stats(const cgx_spec* s, long long* steps, long long* drafted,
                     long long* accepted);
+
+/* Batched loop: B = max_batch sequences of both models in lockstep (each
+ * with its own caches), unfiltered sampling.  set_last gives, per sequence,
+ * the token at the target's last cached position (prev) and the next token
+ * (last, not cached yet).  A step takes draws u_draft [B][gamma] and
+ * u_verify [B][gamma + 1], writes out_tokens [B][gamma + 1] (-1 past the
+ * emitted ones) and n_accepted [B], and returns the total accepted. */
+typedef struct cgx_spec_batch cgx_spec_batch;
+cgx_spec_batch* cgx_spec_batch_new(cgx_model* draft, cgx_model* target, int gamma,
+                                   float temperature);
+void cgx_spec_batch_free(cgx_spec_batch* s);
+int cgx_spec_batch_set_last(cgx_spec_batch* s, const int* prev, const int* last);
+int cgx_spec_batch_step(cgx_spec_batch* s, const float* u_draft, const float* u_verify,
+                        int* out_tokens, int* n_accepted);
+void cgx_spec_batch_stats(const cgx_spec_batch* s, long long* steps, long long* drafted,
+                          long long* accepted);
 
 #ifdef __cplusplus
 }

@@ -39,6 +39,7 @@ class Cfg:
     rope_theta: float = 10000.0
     norm_eps: float = 1e-5
     init_std: float = 0.02
+    max_batch: int = 0
 
     def ctype(self):
         from cogito_amd.capi import CgxModelConfig

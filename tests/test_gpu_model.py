@@ -90,6 +90,43 @@ def test_model_forward_vs_oracle(gpu, oracle, rng):
     gpu.cgx_model_free(m)
 
 
+@pytest.mark.parametrize("cfg", [TINY, Cfg(n_layers=1, d_model=512, n_heads=8, n_kv_heads=2,
+                                            head_dim=128, d_ff=768, vocab=2048, group_size=128,
+                                            kv_group_size=128, max_seq=300, max_tokens=5,
+                                            init_std=0.05)])
+def test_model_forward_batch_vs_oracle(gpu, oracle, rng, cfg):
+    # B sequences with their own caches in one forward: each matches its own
+    # oracle stack, also after rollbacks to different lengths per sequence
+    from dataclasses import replace
+    B = 3
+    m = new_model(gpu, replace(cfg, max_batch=B), 5)
+    assert gpu.cgx_model_batch(m) == B
+    oms = [OracleModel(oracle, cfg, 5) for _ in range(B)]
+    V = cfg.vocab
+    for step, M in enumerate([5, 1, 3, 2, 5]):
+        M = min(M, cfg.max_tokens)
+        toks = rng.integers(0, V, (B, M)).astype(np.int32)
+        assert gpu.cgx_model_forward_batch(m, toks.ctypes.data, M, M, None) == 0, \
+            last_error(gpu)
+        got = logits_np(gpu, m, B * M, V).reshape(B, M, V)
+        for b in range(B):
+            err = rel_err_rows(got[b], oms[b].forward(toks[b]))
+            assert err <= TOL, (step, b, err)
+            assert gpu.cgx_model_len_seq(m, b) == oms[b].len
+        if step == 1:
+            for b in range(B):
+                n = oms[b].len - b
+                assert gpu.cgx_model_truncate_seq(m, b, n) == 0
+                oms[b].truncate(n)
+    # the last token's logits of each sequence
+    toks = rng.integers(0, V, (B, 2)).astype(np.int32)
+    assert gpu.cgx_model_forward_batch(m, toks.ctypes.data, 2, 1, None) == 0
+    got = logits_np(gpu, m, B, V)
+    for b in range(B):
+        assert rel_err_rows(got[b:b + 1], oms[b].forward(toks[b], n_logits=1)) <= TOL
+    gpu.cgx_model_free(m)
+
+
 def test_model_forward_head_dim_128_gqa(gpu, oracle, rng):
     cfg = Cfg(n_layers=1, d_model=512, n_heads=8, n_kv_heads=2, head_dim=128, d_ff=768,
               vocab=2048, group_size=128, kv_group_size=128, max_seq=300, max_tokens=5,
@@ -181,3 +218,75 @@ def test_spec_from_filled_context(gpu, rng):
     gpu.cgx_spec_free(s)
     gpu.cgx_model_free(draft)
     gpu.cgx_model_free(target)
+
+
+def run_spec_batch(gpu, draft, target, gamma, T, B, prompt_len, steps, rng):
+    """Prefill B prompts into both models, then batched loop steps; checks the
+    per-sequence bookkeeping and returns the accepted counts."""
+    V = 1024
+    prompts = rng.integers(0, V, (B, prompt_len)).astype(np.int32)
+    for mdl in (target, draft):
+        assert gpu.cgx_model_forward_batch(mdl, prompts.ctypes.data, prompt_len, 0,
+                                           None) == 0, last_error(gpu)
+    s = gpu.cgx_spec_batch_new(draft, target, gamma, T)
+    assert s, last_error(gpu)
+    prev = np.ascontiguousarray(prompts[:, -1])
+    last = rng.integers(0, V, B).astype(np.int32)
+    assert gpu.cgx_spec_batch_set_last(s, prev.ctypes.data, last.ctypes.data) == 0, \
+        last_error(gpu)
+    out = np.zeros((B, gamma + 1), np.int32)
+    n = np.zeros(B, np.int32)
+    lens = np.full(B, prompt_len)
+    all_n = []
+    for _ in range(steps):
+        ud = rng.uniform(0, 1, (B, gamma)).astype(np.float32)
+        uv = rng.uniform(0, 1, (B, gamma + 1)).astype(np.float32)
+        tot = gpu.cgx_spec_batch_step(s, ud.ctypes.data, uv.ctypes.data, out.ctypes.data,
+                                      n.ctypes.data)
+        assert tot == n.sum() >= 0, last_error(gpu)
+        for b in range(B):
+            assert 0 <= n[b] <= gamma
+            assert ((out[b, :n[b] + 1] >= 0) & (out[b, :n[b] + 1] < V)).all()
+            assert (out[b, n[b] + 1:] == -1).all()
+            lens[b] += n[b] + 1
+            assert gpu.cgx_model_len_seq(target, b) == lens[b]
+        all_n.append(n.copy())
+    gpu.cgx_spec_batch_free(s)
+    return np.array(all_n)
+
+
+def test_spec_batch_identical_draft(gpu, rng):
+    # same weights and the same prefill: the draft's distributions equal the
+    # target's up to the rounding of a recomputed position, so (nearly) every
+    # drafted token is accepted
+    cfg = Cfg(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, d_ff=512,
+              vocab=1024, max_seq=128, max_tokens=8, init_std=0.05, max_batch=4)
+    target = new_model(gpu, cfg, 21)
+    draft = new_model(gpu, cfg, 21)
+    ns = run_spec_batch(gpu, draft, target, 4, 1.0, 4, 6, 8, rng)
+    assert ns.mean() >= 0.9 * 4, ns
+    gpu.cgx_model_free(draft)
+    gpu.cgx_model_free(target)
+
+
+def test_spec_batch_with_draft_head(gpu, rng):
+    cfg = Cfg(n_layers=3, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, d_ff=512,
+              vocab=1024, max_seq=200, max_tokens=8, init_std=0.05, max_batch=3)
+    dcfg = Cfg(**{**cfg.__dict__, "n_layers": 1})
+    target = new_model(gpu, cfg, 31)
+    draft = new_model(gpu, dcfg, 32, target)
+    ns = run_spec_batch(gpu, draft, target, 4, 1.0, 3, 5, 20, rng)
+    assert 0 < ns.sum() < 4 * ns.size
+    gpu.cgx_model_free(draft)
+    gpu.cgx_model_free(target)
+
+
+def test_spec_batch_rejects_mismatched_models(gpu):
+    cfg = Cfg(n_layers=1, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, d_ff=512,
+              vocab=1024, max_seq=64, max_tokens=8, init_std=0.05, max_batch=2)
+    a = new_model(gpu, cfg, 1)
+    b = new_model(gpu, Cfg(**{**cfg.__dict__, "max_batch": 3}), 2)
+    assert not gpu.cgx_spec_batch_new(a, b, 4, 1.0)
+    assert "batch" in last_error(gpu)
+    gpu.cgx_model_free(a)
+    gpu.cgx_model_free(b)
