@@ -23,7 +23,7 @@ int cgx_ensure_init(void);
  * names the same slot. */
 enum { CGX_SLOT_IN0 = 0, CGX_SLOT_IN1, CGX_SLOT_IN2, CGX_SLOT_IN3,
        CGX_SLOT_OUT0, CGX_SLOT_OUT1, CGX_SLOT_WS0, CGX_SLOT_WS1,
-       CGX_SLOT_WS2, CGX_SLOT_WS3, CGX_SLOT_WS4, CGX_NUM_SLOTS };
+       CGX_SLOT_WS2, CGX_SLOT_WS3, CGX_SLOT_WS4, CGX_SLOT_WS5, CGX_NUM_SLOTS };
 void* cgx_scratch(int slot, size_t bytes);
 /* Zero-initialised counters that kernels reset themselves after use. */
 unsigned int* cgx_counters(size_t count);
@@ -68,6 +68,13 @@ int cgk_int4_repack_mfma(const uint8_t* flat, const float* scales, int K, int N,
                          int paired, uint8_t* w, float* scales_t);
 int cgk_int4_dequantize_mfma(const uint8_t* w, const float* scales_t, int K, int N, int gs,
                              int paired, float* out);
+/* INT4 GEMM for M >= 32 rows over layout 3 (gemv.hip): same arguments and
+ * epilogues as cgk_gemv_mfma plus smax >= every |scale| of the weight. */
+int cgk_gemm_int4_supported(int M, int K, int N, int gs, int paired);
+int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int gs, const uint8_t* w,
+                  const float* scales_t, float smax, float* y, int ldy, int pro,
+                  const float* nw, float eps, int epi);
+int cgk_absmax(const float* s, size_t n, float* out_host);
 int cgk_gemv_mfma(const float* x, int ldx, int M, int K, int N, int gs, const uint8_t* w,
                   const float* scales_t, float* y, int ldy, int pro, const float* nw, float eps,
                   int epi);

@@ -28,6 +28,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstring>
 
 #include "cgx_internal.h"
 
@@ -445,6 +446,212 @@ int launch_pe(const MfmaArgs& a, int T) {
     }
 }
 
+// ------------------------------------------------------------------ GEMM
+// y = x @ W for M >= 32 rows (batched verify, tree verify): the activation
+// tile is shared by the block's 8 waves, one 16-column layout tile each, so
+// the hi/lo preparation of A is paid once per 128 columns instead of once
+// per wave.  Rows carry one power-of-two scale each (k_gemm_rows: RMSNorm
+// rstd and 2^E with |x * s * 2^E| < 2^15 over the row), so the hi + lo fp16
+// pair keeps 22 significant bits of every product factor and the fp16
+// subnormal floor sits 2^-38 below the row's largest term.  K is split over
+// blockIdx.z; k_gemm_reduce sums the splits in a fixed order and applies the
+// epilogue (store, accumulate, SwiGLU of the gate|up pair).
+
+constexpr int kGemmWaves = 8;
+constexpr int kGemmRowH = kChunkK + 8;   // LDS pitch (halfs) of an A row
+
+struct GemmArgs {
+    const float* x;           // [M][ldx]
+    int ldx, M, K, N, gs;
+    const uint8_t* w;         // layout 3
+    const float* scales_t;    // [N/gs][K]
+    const float* nw;          // RMSNorm weights [K] or nullptr
+    const float* rowscale;    // [M] rstd * 2^E
+    float* part;              // [ksplit][M][N] partial sums (times 2^E), logical columns
+    int ksteps;               // 128-row chunks per split
+    int ff;                   // SwiGLU pair: N / 2
+};
+
+template <int RT, int NG>
+__global__ __launch_bounds__(64 * kGemmWaves) void k_gemm_int4(GemmArgs a) {
+    constexpr int BM = 16 * RT;
+    constexpr int RPT = BM > 64 ? BM / 64 : 1;        // rows prepared per thread
+    __shared__ _Float16 sa[NG][2][BM][kGemmRowH];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int paired = NG == 2;
+    const int ff_tiles = a.ff / 16;
+    const int L0 = blockIdx.x * kGemmWaves;
+    const int L = L0 + wave;                           // this wave's layout tile
+    const int lt = logical_tile(L, paired, ff_tiles);
+    const int q = paired ? (L & 1) : 0;                // its A slot (gate / up)
+    int grp[NG];
+#pragma unroll
+    for (int g = 0; g < NG; g++) grp[g] = logical_tile(L0 + g, paired, ff_tiles) * 16 / a.gs;
+    const int row0 = blockIdx.y * BM;
+    const int nchunks = a.K / kChunkK;
+    const int c0 = blockIdx.z * a.ksteps;
+    const int c1 = min(nchunks, c0 + a.ksteps);
+    // preparation: thread -> rows pr + 64 i, 16 k values at pk
+    const int pr = threadIdx.x >> 3, pk = (threadIdx.x & 7) * 16;
+
+    f32x4 acc[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) acc[rt] = (f32x4)(0.0f);
+    auto load_w = [&](int c) {
+        return __builtin_nontemporal_load(
+            (const u32x4*)(a.w + ((size_t)L * nchunks + c) * kChunkBytes + 16 * lane));
+    };
+    u32x4 wcur = c0 < c1 ? load_w(c0) : u32x4{0u, 0u, 0u, 0u};
+    for (int c = c0; c < c1; c++) {
+        const u32x4 wnxt = c + 1 < c1 ? load_w(c + 1) : wcur;
+        const int k0 = c * kChunkK + pk;
+        float4 sv[NG][4];
+#pragma unroll
+        for (int g = 0; g < NG; g++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                sv[g][i] = *(const float4*)(a.scales_t + (size_t)grp[g] * a.K + k0 + 4 * i);
+        if (a.nw) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 n4 = *(const float4*)(a.nw + k0 + 4 * i);
+#pragma unroll
+                for (int g = 0; g < NG; g++) {
+                    sv[g][i].x *= n4.x; sv[g][i].y *= n4.y; sv[g][i].z *= n4.z; sv[g][i].w *= n4.w;
+                }
+            }
+        }
+#pragma unroll
+        for (int ri = 0; ri < RPT; ri++) {
+            const int r = pr + 64 * ri;
+            if (r >= BM) continue;
+            const int row = row0 + r;
+            const bool live = row < a.M;
+            const float rs = live ? a.rowscale[row] : 0.0f;
+            const float* xr = a.x + (size_t)(live ? row : 0) * a.ldx + k0;
+            float xv[16];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 t = live ? *(const float4*)(xr + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+                xv[4 * i] = t.x * rs; xv[4 * i + 1] = t.y * rs;
+                xv[4 * i + 2] = t.z * rs; xv[4 * i + 3] = t.w * rs;
+            }
+#pragma unroll
+            for (int g = 0; g < NG; g++) {
+                f16x8 h[2], l[2];
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float4 s4 = sv[g][i / 4];
+                    const float sc = (i & 3) == 0 ? s4.x : (i & 3) == 1 ? s4.y : (i & 3) == 2 ? s4.z : s4.w;
+                    const float v = xv[i] * sc;
+                    const _Float16 hv = (_Float16)v;
+                    h[i / 8][i % 8] = hv;
+                    l[i / 8][i % 8] = (_Float16)(v - (float)hv);
+                }
+                *(f16x8*)&sa[g][0][r][pk] = h[0];
+                *(f16x8*)&sa[g][0][r][pk + 8] = h[1];
+                *(f16x8*)&sa[g][1][r][pk] = l[0];
+                *(f16x8*)&sa[g][1][r][pk + 8] = l[1];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++) {
+            const uint32_t word = kb == 0 ? wcur.x : kb == 1 ? wcur.y : kb == 2 ? wcur.z : wcur.w;
+            const f16x8 b = nib_to_f16(word);
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                const int ar = rt * 16 + (lane & 15), ak = 32 * kb + 8 * (lane >> 4);
+                const f16x8 ah = *(const f16x8*)&sa[q][0][ar][ak];
+                const f16x8 al = *(const f16x8*)&sa[q][1][ar][ak];
+                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, acc[rt], 0, 0, 0);
+                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, acc[rt], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+        wcur = wnxt;
+    }
+    // partials: lane holds rows 16 rt + 4 (lane / 16) + v of column lane % 16
+    float* pp = a.part + (size_t)blockIdx.z * a.M * a.N;
+    const int col = lt * 16 + (lane & 15);
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int row = row0 + rt * 16 + 4 * (lane >> 4) + v;
+            if (row < a.M) pp[(size_t)row * a.N + col] = acc[rt][v];
+        }
+}
+
+// Per row: RMSNorm rstd (or 1) and the power of two that keeps every
+// x * rstd * nw * s below 2^15 given smax >= every |s|: rowscale = rstd * 2^E,
+// unscale = 2^-E.  One block of 256 threads per row.
+__global__ void k_gemm_rows(const float* __restrict__ x, int ldx, int K, const float* __restrict__ nw,
+                            int rms, float eps, float smax, float* __restrict__ rowscale,
+                            float* __restrict__ unscale) {
+    __shared__ float s_a[4], s_s[4];
+    const int m = blockIdx.x, t = threadIdx.x;
+    const float* xr = x + (size_t)m * ldx;
+    float amax = 0.0f, ssq = 0.0f;
+    for (int k = t; k < K; k += blockDim.x) {
+        const float v = xr[k];
+        ssq = fmaf(v, v, ssq);
+        amax = fmaxf(amax, fabsf(nw ? v * nw[k] : v));
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, o));
+        ssq += __shfl_xor(ssq, o);
+    }
+    if ((t & 63) == 0) {
+        s_a[t >> 6] = amax;
+        s_s[t >> 6] = ssq;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float A = 0.0f, S = 0.0f;
+        for (int w = 0; w < 4; w++) {
+            A = fmaxf(A, s_a[w]);
+            S += s_s[w];
+        }
+        const float rstd = rms ? 1.0f / sqrtf(S / (float)K + eps) : 1.0f;
+        const float bound = A * rstd * smax;
+        int E = 0;
+        if (bound > 0.0f && bound < __builtin_inff()) E = 14 - ilogbf(bound);
+        E = E > 100 ? 100 : (E < -100 ? -100 : E);
+        rowscale[m] = rstd * ldexpf(1.0f, E);
+        unscale[m] = ldexpf(1.0f, -E);
+    }
+}
+
+// Sum of the K splits in order, times 2^-E, and the epilogue.
+template <int EPI>
+__global__ void k_gemm_reduce(const float* __restrict__ part, int ksplit, int M, int N,
+                              const float* __restrict__ unscale, float* __restrict__ y, int ldy) {
+    const int Nout = EPI == kEpiSwiGlu ? N / 2 : N;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)M * Nout) return;
+    const int row = (int)(i / Nout), col = (int)(i % Nout);
+    const size_t mn = (size_t)M * N;
+    float v = 0.0f;
+    for (int z = 0; z < ksplit; z++) v += part[z * mn + (size_t)row * N + col];
+    v *= unscale[row];
+    float* yp = y + (size_t)row * ldy + col;
+    if (EPI == kEpiSwiGlu) {
+        float u = 0.0f;
+        for (int z = 0; z < ksplit; z++) u += part[z * mn + (size_t)row * N + Nout + col];
+        u *= unscale[row];
+        *yp = v / (1.0f + __expf(-v)) * u;
+    } else {
+        *yp = EPI == kEpiAccumulate ? *yp + v : v;
+    }
+}
+
+template <int RT, int NG>
+int launch_gemm(const GemmArgs& a, dim3 grid) {
+    hipLaunchKernelGGL((k_gemm_int4<RT, NG>), grid, dim3(64 * kGemmWaves), 0, stream(), a);
+    return launch_check("k_gemm_int4");
+}
+
 }  // namespace
 
 // Column tiles per block: two when that still gives >= 256 blocks (one per
@@ -523,5 +730,104 @@ extern "C" int cgk_gemv_mfma(const float* x, int ldx, int M, int K, int N, int g
         }
         if (rc) return rc;
     }
+    return 0;
+}
+
+// 1 when cgk_gemm_int4 takes this product: 8 layout tiles per block within
+// one scale group per A slot.
+extern "C" int cgk_gemm_int4_supported(int M, int K, int N, int gs, int paired) {
+    return M >= 1 && K % kRoundK == 0 && N % 128 == 0 && (paired ? gs % 64 == 0 : gs % 128 == 0);
+}
+
+extern "C" int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int gs,
+                             const uint8_t* w, const float* scales_t, float smax, float* y,
+                             int ldy, int pro, const float* nw, float eps, int epi) {
+    const int paired = epi == kEpiSwiGlu;
+    if (!cgk_gemm_int4_supported(M, K, N, gs, paired) || ldx < K || (ldx & 3) ||
+        ((uintptr_t)x & 15) || (pro == kProRmsNorm && !nw) || ldy < (paired ? N / 2 : N)) {
+        cgx_set_error("gemm_int4: unsupported shape M=%d K=%d N=%d gs=%d", M, K, N, gs);
+        return -1;
+    }
+    const int RT = M >= 64 ? (M >= 128 && !paired ? 8 : 4) : (M + 15) / 16;
+    const int BM = 16 * RT;
+    const int rowblocks = (M + BM - 1) / BM;
+    const int colblocks = N / 128;
+    const int nchunks = K / kChunkK;
+    // enough blocks for the chip, splits of at least two chunks
+    int ksplit = (512 + colblocks * rowblocks - 1) / (colblocks * rowblocks);
+    ksplit = ksplit > nchunks / 2 ? nchunks / 2 : ksplit;
+    ksplit = ksplit < 1 ? 1 : (ksplit > 16 ? 16 : ksplit);
+    const int ksteps = (nchunks + ksplit - 1) / ksplit;
+    ksplit = (nchunks + ksteps - 1) / ksteps;
+    char* ws = (char*)cgx_scratch(CGX_SLOT_WS5, (size_t)M * 8 + 256 + (size_t)ksplit * M * N * 4);
+    if (!ws) return -1;
+    float* rowscale = (float*)ws;
+    float* unscale = rowscale + M;
+    float* part = (float*)(ws + (((size_t)M * 8 + 255) & ~(size_t)255));
+    hipLaunchKernelGGL(k_gemm_rows, dim3(M), dim3(256), 0, stream(), x, ldx, K,
+                       pro == kProRmsNorm ? nw : nullptr, pro == kProRmsNorm, eps, smax,
+                       rowscale, unscale);
+    if (launch_check("k_gemm_rows")) return -1;
+    GemmArgs a;
+    a.x = x; a.ldx = ldx; a.M = M; a.K = K; a.N = N; a.gs = gs;
+    a.w = w; a.scales_t = scales_t;
+    a.nw = pro == kProRmsNorm ? nw : nullptr;
+    a.rowscale = rowscale;
+    a.part = part;
+    a.ksteps = ksteps;
+    a.ff = N / 2;
+    dim3 grid(colblocks, rowblocks, ksplit);
+    int rc;
+    if (paired) {
+        rc = RT == 1 ? launch_gemm<1, 2>(a, grid) : RT == 2 ? launch_gemm<2, 2>(a, grid)
+           : RT == 3 ? launch_gemm<3, 2>(a, grid) : launch_gemm<4, 2>(a, grid);
+    } else {
+        rc = RT == 1 ? launch_gemm<1, 1>(a, grid) : RT == 2 ? launch_gemm<2, 1>(a, grid)
+           : RT == 3 ? launch_gemm<3, 1>(a, grid) : RT == 4 ? launch_gemm<4, 1>(a, grid)
+           : launch_gemm<8, 1>(a, grid);
+    }
+    if (rc) return rc;
+    const size_t outs = (size_t)M * (paired ? N / 2 : N);
+    const int blocks = (int)((outs + 255) / 256);
+    if (epi == kEpiSwiGlu)
+        hipLaunchKernelGGL(k_gemm_reduce<kEpiSwiGlu>, dim3(blocks), dim3(256), 0, stream(), part,
+                           ksplit, M, N, unscale, y, ldy);
+    else if (epi == kEpiAccumulate)
+        hipLaunchKernelGGL(k_gemm_reduce<kEpiAccumulate>, dim3(blocks), dim3(256), 0, stream(),
+                           part, ksplit, M, N, unscale, y, ldy);
+    else
+        hipLaunchKernelGGL(k_gemm_reduce<kEpiStore>, dim3(blocks), dim3(256), 0, stream(), part,
+                           ksplit, M, N, unscale, y, ldy);
+    return launch_check("k_gemm_reduce");
+}
+
+// max |s| over a scales array (host result, synchronising): the bound the
+// GEMM's row scaling needs, computed once per weight
+__global__ void k_absmax(const float* __restrict__ s, size_t n, unsigned int* out) {
+    float m = 0.0f;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        m = fmaxf(m, fabsf(s[i]));
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((threadIdx.x & 63) == 0) atomicMax(out, __float_as_uint(m));
+}
+
+extern "C" int cgk_absmax(const float* s, size_t n, float* out_host) {
+    unsigned int* d = (unsigned int*)cgx_scratch(CGX_SLOT_OUT1, 16);
+    if (!d) return -1;
+    unsigned int zero = 0u, r = 0u;
+    if (hipMemcpyAsync(d, &zero, 4, hipMemcpyHostToDevice, stream()) != hipSuccess) {
+        cgx_set_error("absmax: copy failed");
+        return -1;
+    }
+    hipLaunchKernelGGL(k_absmax, dim3(256), dim3(256), 0, stream(), s, n, d);
+    if (launch_check("k_absmax")) return -1;
+    if (hipMemcpyAsync(&r, d, 4, hipMemcpyDeviceToHost, stream()) != hipSuccess ||
+        hipStreamSynchronize(stream()) != hipSuccess) {
+        cgx_set_error("absmax: copy failed");
+        return -1;
+    }
+    float f;
+    memcpy(&f, &r, sizeof f);
+    *out_host = f;
     return 0;
 }

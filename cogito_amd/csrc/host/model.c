@@ -31,6 +31,7 @@ typedef struct {
     float* scales_t;
     int K, N;
     uint32_t sid;
+    float smax;              /* max |scale|: the GEMM's row-scaling bound */
 } lin_t;
 
 typedef struct {
@@ -88,8 +89,10 @@ static int make_lin(cgx_model* m, lin_t* L, int which, int layer, float* tf, uin
     L->scales_t = (float*)cgx_malloc(n / m->c.group_size * 4);
     if (!L->tiled || !L->scales_t) return -1;
     if (gen_flat(m, L->sid, L->K, L->N, tf, tq, ts)) return -1;
-    return cgk_int4_repack_mfma(tq, ts, L->K, L->N, m->c.group_size, which == W_GU, L->tiled,
-                                L->scales_t);
+    if (cgk_int4_repack_mfma(tq, ts, L->K, L->N, m->c.group_size, which == W_GU, L->tiled,
+                             L->scales_t))
+        return -1;
+    return cgk_absmax(L->scales_t, n / m->c.group_size, &L->smax);
 }
 
 static void free_lin(lin_t* L) {
@@ -272,6 +275,17 @@ static size_t kv_layer_groups(const cg_kv_cache_int4* c) {
     return (size_t)c->max_seq_len * c->n_heads * (c->head_dim / c->group_size);
 }
 
+/* One linear layer over R rows: the GEMM from 32 rows on (one pass over the
+ * weight), the GEMV below (it streams the weight once per 16 rows). */
+static int linear(const lin_t* L, const float* x, int ldx, int R, float* y, int ldy, int pro,
+                  const float* nw, float eps, int epi, int gs) {
+    if (R >= 32 && cgk_gemm_int4_supported(R, L->K, L->N, gs, epi == EPI_SWIGLU))
+        return cgk_gemm_int4(x, ldx, R, L->K, L->N, gs, L->tiled, L->scales_t, L->smax, y, ldy,
+                             pro, nw, eps, epi);
+    return cgk_gemv_mfma(x, ldx, R, L->K, L->N, gs, L->tiled, L->scales_t, y, ldy, pro, nw,
+                         eps, epi);
+}
+
 /* Forward of B sequences (0..B-1), M tokens each. */
 static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_logits,
                         float* logits, size_t ldl) {
@@ -313,8 +327,8 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
         uint8_t* vc = kv->v_cache + lb * slot;
         float* ks = kv->k_scales + lg * slot;
         float* vs = kv->v_scales + lg * slot;
-        if (cgk_gemv_mfma(m->x, d, R, d, nq, gs, w[W_QKV].tiled, w[W_QKV].scales_t, m->qkv, nq,
-                          PRO_RMSNORM, m->ones, eps, EPI_STORE) ||
+        if (linear(&w[W_QKV], m->x, d, R, m->qkv, nq, PRO_RMSNORM, m->ones, eps, EPI_STORE,
+                   gs) ||
             cgk_rope_append_batch(m->qkv, nq, B, M, H, Hk, hd, kv->group_size, pos0,
                                   c->rope_theta, m->q, kc, vc, ks, vs, lb, lg))
             return -1;
@@ -330,20 +344,17 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
                                   NULL, m->attn + (size_t)b * M * hq, NULL))
                     return -1;
         }
-        if (cgk_gemv_mfma(m->attn, hq, R, hq, d, gs, w[W_O].tiled, w[W_O].scales_t, m->x, d,
-                          PRO_NONE, NULL, 0.0f, EPI_ACCUMULATE) ||
-            cgk_gemv_mfma(m->x, d, R, d, 2 * ff, gs, w[W_GU].tiled, w[W_GU].scales_t, m->gu, ff,
-                          PRO_RMSNORM, m->ones, eps, EPI_SWIGLU) ||
-            cgk_gemv_mfma(m->gu, ff, R, ff, d, gs, w[W_DOWN].tiled, w[W_DOWN].scales_t, m->x, d,
-                          PRO_NONE, NULL, 0.0f, EPI_ACCUMULATE))
+        if (linear(&w[W_O], m->attn, hq, R, m->x, d, PRO_NONE, NULL, 0.0f, EPI_ACCUMULATE,
+                   gs) ||
+            linear(&w[W_GU], m->x, d, R, m->gu, ff, PRO_RMSNORM, m->ones, eps, EPI_SWIGLU, gs) ||
+            linear(&w[W_DOWN], m->gu, ff, R, m->x, d, PRO_NONE, NULL, 0.0f, EPI_ACCUMULATE, gs))
             return -1;
     }
     float* out = logits ? logits : m->logits;
     if (!ldl) ldl = (size_t)n_logits * c->vocab;
     if (n_logits == M && ldl == (size_t)M * c->vocab) {
         /* every row, sequences in order */
-        if (cgk_gemv_mfma(m->x, d, R, d, c->vocab, gs, m->lm.tiled, m->lm.scales_t, out,
-                          c->vocab, PRO_RMSNORM, m->ones, eps, EPI_STORE))
+        if (linear(&m->lm, m->x, d, R, out, c->vocab, PRO_RMSNORM, m->ones, eps, EPI_STORE, gs))
             return -1;
     } else if (n_logits == 1) {
         /* the last row of each sequence: rows M-1, 2M-1, ... */

@@ -260,10 +260,18 @@ int cgx_matmul_int4_dev_kernel(const float* x, int M, cg_tensor_quant* w,
     }
     if (kernel == 0)
         kernel = info.layout == CGX_LAYOUT_TILED ? 1 : info.layout == CGX_LAYOUT_MFMA ? 3 : 2;
-    if (kernel == 3) {
+    if (kernel == 3 || kernel == 4) {
         if (info.layout != CGX_LAYOUT_MFMA) {
-            cgx_set_error("cgx_matmul_int4: MFMA kernel needs a layout-3 weight");
+            cgx_set_error("cgx_matmul_int4: MFMA kernels need a layout-3 weight");
             return -1;
+        }
+        if (kernel == 4) {
+            /* the GEMM of the batched / tree verify (M >= 32 in the decoder) */
+            float smax;
+            if (cgk_absmax(w->scales, (size_t)info.K * info.N / info.group_size, &smax))
+                return -1;
+            return cgk_gemm_int4(x, info.K, M, info.K, info.N, info.group_size, w->data,
+                                 w->scales, smax, y, info.N, 0, NULL, 0.0f, 0);
         }
         return cgk_gemv_mfma(x, info.K, M, info.K, info.N, info.group_size, w->data,
                              w->scales, y, info.N, 0, NULL, 0.0f, 0);

@@ -71,7 +71,9 @@ int cgx_quant_layout(cg_tensor_quant* q);
 /* y[M,N] = x[M,K] @ W; x and y are device pointers, w a device handle. */
 int cgx_matmul_int4_dev(const float* x, int M, cg_tensor_quant* w, float* y);
 /* Same with the kernel forced: 0 auto (by layout), 1 VALU GEMV (layout 2),
- * 2 generic reference-order kernel (layout 1), 3 MFMA GEMV (layout 3). */
+ * 2 generic reference-order kernel (layout 1), 3 MFMA GEMV (layout 3),
+ * 4 MFMA GEMM with a shared activation tile (layout 3, N % 128 == 0,
+ * group % 128 == 0; the batched and tree verify shapes, M >= 32). */
 int cgx_matmul_int4_dev_kernel(const float* x, int M, cg_tensor_quant* w,
                                float* y, int kernel);
 

@@ -97,6 +97,15 @@ def test_gemv_mfma_more_rows_and_wide(gpu, oracle, rng, K, N, gs, M):
     _gemv_case(gpu, oracle, rng, K, N, gs, M, 3, 3)
 
 
+@pytest.mark.parametrize("K,N,gs,M", [(4096, 4096, 128, 40), (1024, 2048, 128, 32),
+                                      (256, 512, 128, 100), (768, 1280, 256, 64),
+                                      (1024, 1024, 128, 128), (512, 384, 128, 256),
+                                      (4096, 32000, 128, 40), (256, 128, 128, 1)])
+def test_gemm_mfma_vs_oracle(gpu, oracle, rng, K, N, gs, M):
+    # the shared-A-tile GEMM (row blocks of up to 64 / 128 rows, split K)
+    _gemv_case(gpu, oracle, rng, K, N, gs, M, 3, 4)
+
+
 def test_gemv_mfma_wide_dynamic_range(gpu, oracle, rng):
     # activations spanning many binades, a zero row, huge and tiny scales:
     # the per-round power-of-two scaling keeps the fp16 terms in range

@@ -94,11 +94,12 @@ def test_model_forward_vs_oracle(gpu, oracle, rng):
                                             head_dim=128, d_ff=768, vocab=2048, group_size=128,
                                             kv_group_size=128, max_seq=300, max_tokens=5,
                                             init_std=0.05)])
-def test_model_forward_batch_vs_oracle(gpu, oracle, rng, cfg):
+@pytest.mark.parametrize("B", [3, 8])
+def test_model_forward_batch_vs_oracle(gpu, oracle, rng, cfg, B):
     # B sequences with their own caches in one forward: each matches its own
     # oracle stack, also after rollbacks to different lengths per sequence
+    # (B = 8: 40 rows per forward, the GEMM path of every linear layer)
     from dataclasses import replace
-    B = 3
     m = new_model(gpu, replace(cfg, max_batch=B), 5)
     assert gpu.cgx_model_batch(m) == B
     oms = [OracleModel(oracle, cfg, 5) for _ in range(B)]
@@ -115,7 +116,7 @@ def test_model_forward_batch_vs_oracle(gpu, oracle, rng, cfg):
             assert gpu.cgx_model_len_seq(m, b) == oms[b].len
         if step == 1:
             for b in range(B):
-                n = oms[b].len - b
+                n = oms[b].len - b % 3
                 assert gpu.cgx_model_truncate_seq(m, b, n) == 0
                 oms[b].truncate(n)
     # the last token's logits of each sequence
