@@ -37,6 +37,7 @@ typedef struct {
     int layout;
     int K, N, group_size;
     int paired;          /* layout 3: gate|up tiles interleaved (SwiGLU) */
+    float smax;          /* layout 3: max |scale| (the GEMM's row-scaling bound) */
 } cgx_qinfo;
 int cgx_quant_lookup(const cg_tensor_quant* q, cgx_qinfo* info);
 void cgx_quant_register(const cg_tensor_quant* q, const cgx_qinfo* info);

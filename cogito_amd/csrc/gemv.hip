@@ -447,17 +447,22 @@ int launch_pe(const MfmaArgs& a, int T) {
 }
 
 // ------------------------------------------------------------------ GEMM
-// y = x @ W for M >= 32 rows (batched verify, tree verify): the activation
-// tile is shared by the block's 8 waves, one 16-column layout tile each, so
-// the hi/lo preparation of A is paid once per 128 columns instead of once
-// per wave.  Rows carry one power-of-two scale each (k_gemm_rows: RMSNorm
-// rstd and 2^E with |x * s * 2^E| < 2^15 over the row), so the hi + lo fp16
-// pair keeps 22 significant bits of every product factor and the fp16
-// subnormal floor sits 2^-38 below the row's largest term.  K is split over
-// blockIdx.z; k_gemm_reduce sums the splits in a fixed order and applies the
-// epilogue (store, accumulate, SwiGLU of the gate|up pair).
+// y = x @ W for M >= 32 rows (batched verify, tree verify).  A block of 4
+// waves covers two 128-column slots (two neighbouring scale groups, or the
+// gate and up halves of the same 128 SwiGLU columns), each wave 4 column
+// tiles of one slot, so one A fragment read from LDS feeds 4 tiles.  Per
+// slot the activations are prepared once per 128-row step: x * nw * s (the
+// scale of that slot's group at each k) times a per-row factor rstd * 2^E,
+// split into hi + lo fp16 (22 significant bits); the MFMA sums are scaled by
+// 2^-E at the end.  k_gemm_rows fixes the row factors before the GEMM from
+// the whole row: max|x * nw| * rstd * max|s| * 2^E < 2^15.  The next step's
+// activations and the weights two steps ahead are loaded while a step is
+// multiplied.  K is split over blockIdx.z; k_gemm_reduce sums the splits in
+// a fixed order and applies the epilogue (store, accumulate, SwiGLU of the
+// gate|up pair).
 
-constexpr int kGemmWaves = 8;
+constexpr int kGemmWaves = 4;
+constexpr int kGemmTiles = 4;            // column tiles per wave
 constexpr int kGemmRowH = kChunkK + 8;   // LDS pitch (halfs) of an A row
 
 struct GemmArgs {
@@ -467,136 +472,226 @@ struct GemmArgs {
     const float* scales_t;    // [N/gs][K]
     const float* nw;          // RMSNorm weights [K] or nullptr
     const float* rowscale;    // [M] rstd * 2^E
-    float* part;              // [ksplit][M][N] partial sums (times 2^E), logical columns
+    const float* unscale;     // [M] 2^-E
+    float* part;              // [ksplit][M][N] partial sums, logical columns
     int ksteps;               // 128-row chunks per split
     int ff;                   // SwiGLU pair: N / 2
 };
 
-template <int RT, int NG>
+template <int RT, int NG, int PRO>
 __global__ __launch_bounds__(64 * kGemmWaves) void k_gemm_int4(GemmArgs a) {
     constexpr int BM = 16 * RT;
-    constexpr int RPT = BM > 64 ? BM / 64 : 1;        // rows prepared per thread
-    __shared__ _Float16 sa[NG][2][BM][kGemmRowH];
+    constexpr int RPT = BM / 8;                 // rows prepared per thread
+    __shared__ _Float16 sa[2][2][BM][kGemmRowH];
+    __shared__ float s_unscale[BM];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int paired = NG == 2;
-    const int ff_tiles = a.ff / 16;
-    const int L0 = blockIdx.x * kGemmWaves;
-    const int L = L0 + wave;                           // this wave's layout tile
-    const int lt = logical_tile(L, paired, ff_tiles);
-    const int q = paired ? (L & 1) : 0;                // its A slot (gate / up)
-    int grp[NG];
-#pragma unroll
-    for (int g = 0; g < NG; g++) grp[g] = logical_tile(L0 + g, paired, ff_tiles) * 16 / a.gs;
-    const int row0 = blockIdx.y * BM;
     const int nchunks = a.K / kChunkK;
+    const int bx = blockIdx.x;
+    // slots: logical 128-column groups and their scale-group rows
+    int slot_ok[2], grp[2], lcol[2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        if (paired) {
+            lcol[s] = (s ? a.ff : 0) + 128 * bx;
+            slot_ok[s] = 1;
+        } else {
+            lcol[s] = 128 * (2 * bx + s);
+            slot_ok[s] = lcol[s] < a.N;
+        }
+        grp[s] = slot_ok[s] ? lcol[s] / a.gs : 0;
+    }
+    const int row0 = blockIdx.y * BM;
     const int c0 = blockIdx.z * a.ksteps;
     const int c1 = min(nchunks, c0 + a.ksteps);
-    // preparation: thread -> rows pr + 64 i, 16 k values at pk
-    const int pr = threadIdx.x >> 3, pk = (threadIdx.x & 7) * 16;
+    // preparation: thread -> 4 k values at pk, rows pr + 8 i (a row's 32
+    // threads are one half wave)
+    const int pk = 4 * (threadIdx.x & 31), pr = threadIdx.x >> 5;
+    int xrow[RPT];
+    uint32_t rowmask[RPT];
+    float rsc[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; i++) {
+        xrow[i] = min(row0 + pr + 8 * i, a.M - 1);
+        rowmask[i] = row0 + pr + 8 * i < a.M ? ~0u : 0u;
+        rsc[i] = a.rowscale[xrow[i]];
+    }
+    if (threadIdx.x < BM) s_unscale[threadIdx.x] = a.unscale[min(row0 + (int)threadIdx.x, a.M - 1)];
+    const float* nwp = PRO == kProRmsNorm ? a.nw : a.scales_t;
 
-    f32x4 acc[RT];
+    // ---- this wave's tiles: slot ws, tiles 4 (wave & 1) + j of the slot.  A
+    // wave of a missing slot (odd number of 128-column slots) runs on tile 0
+    // and stores nothing, so that every wave takes the same path.
+    const int ws = wave >> 1;
+    const int wave_ok = slot_ok[ws];
+    const uint8_t* wp[kGemmTiles];
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++) acc[rt] = (f32x4)(0.0f);
-    auto load_w = [&](int c) {
-        return __builtin_nontemporal_load(
-            (const u32x4*)(a.w + ((size_t)L * nchunks + c) * kChunkBytes + 16 * lane));
+    for (int j = 0; j < kGemmTiles; j++) {
+        const int t = 4 * (wave & 1) + j;               // tile within the slot
+        const int L = paired ? 2 * (8 * bx + t) + ws : 8 * (2 * bx + ws) + t;
+        wp[j] = a.w + ((size_t)(wave_ok ? L : 0) * nchunks) * kChunkBytes + 16 * lane;
+    }
+    // steps run in pairs; a step at or past c1 (odd count) prepares zeros and
+    // reads the split's last chunk again
+    const int cend = c0 + ((c1 - c0 + 1) & ~1);
+    auto wload = [&](int c, u32x4 (&d)[kGemmTiles]) {
+        const size_t off = (size_t)min(c, c1 - 1) * kChunkBytes;
+#pragma unroll
+        for (int j = 0; j < kGemmTiles; j++)
+            d[j] = __builtin_nontemporal_load((const u32x4*)(wp[j] + off));
     };
-    u32x4 wcur = c0 < c1 ? load_w(c0) : u32x4{0u, 0u, 0u, 0u};
-    for (int c = c0; c < c1; c++) {
-        const u32x4 wnxt = c + 1 < c1 ? load_w(c + 1) : wcur;
-        const int k0 = c * kChunkK + pk;
-        float4 sv[NG][4];
+    u32x4 wb0[kGemmTiles], wb1[kGemmTiles];
+    __builtin_amdgcn_sched_barrier(0);
+    wload(c0, wb0);
+
+    f32x4 acc[kGemmTiles][RT];
 #pragma unroll
-        for (int g = 0; g < NG; g++)
+    for (int j = 0; j < kGemmTiles; j++)
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                sv[g][i] = *(const float4*)(a.scales_t + (size_t)grp[g] * a.K + k0 + 4 * i);
-        if (a.nw) {
+        for (int rt = 0; rt < RT; rt++) acc[j][rt] = (f32x4)(0.0f);
+
+    // prefetched preparation inputs
+    float4 px[RPT], ps[2], pn = make_float4(1.f, 1.f, 1.f, 1.f);
+    uint32_t plive;
+    auto load_prep = [&](int c) {
+        const int cc = min(c, c1 - 1);
+        const int k = cc * kChunkK + pk;
+        if (PRO == kProRmsNorm) pn = *(const float4*)(nwp + k);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float4 n4 = *(const float4*)(a.nw + k0 + 4 * i);
+        for (int s_ = 0; s_ < 2; s_++) ps[s_] = *(const float4*)(a.scales_t + (size_t)grp[s_] * a.K + k);
 #pragma unroll
-                for (int g = 0; g < NG; g++) {
-                    sv[g][i].x *= n4.x; sv[g][i].y *= n4.y; sv[g][i].z *= n4.z; sv[g][i].w *= n4.w;
-                }
+        for (int i = 0; i < RPT; i++) px[i] = *(const float4*)(a.x + (size_t)xrow[i] * a.ldx + k);
+        plive = c < c1 ? ~0u : 0u;
+    };
+    // the same load order as at the end of a step pair, so that the loop
+    // entry needs no stricter wait than the back edge
+    __builtin_amdgcn_sched_barrier(0);
+    load_prep(c0);
+    __builtin_amdgcn_sched_barrier(0);
+    wload(c0 + 1, wb1);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // sched_barrier(0) keeps the phases in this order, so that the waits
+    // for the loads of the next step fall where they are consumed
+    auto step = [&](int c, u32x4 (&wcur)[kGemmTiles]) {
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();                       // the previous step's A reads are done
+        const float4 n4 = pn;
+        // rows past M and steps past c1 prepare zeros (masked, not
+        // multiplied, so that no inf or NaN of a clamped load leaks in; bit
+        // masks keep the step free of branches)
+        float4 xv[RPT];
+#pragma unroll
+        for (int i = 0; i < RPT; i++) {
+            const uint32_t m = plive & rowmask[i];
+            xv[i].x = __uint_as_float(__float_as_uint(px[i].x) & m);
+            xv[i].y = __uint_as_float(__float_as_uint(px[i].y) & m);
+            xv[i].z = __uint_as_float(__float_as_uint(px[i].z) & m);
+            xv[i].w = __uint_as_float(__float_as_uint(px[i].w) & m);
+        }
+        // a missing slot (odd slot count) prepares from valid memory and is
+        // never stored
+#pragma unroll
+        for (int s_ = 0; s_ < 2; s_++) {
+            const float n0 = n4.x * ps[s_].x, n1 = n4.y * ps[s_].y;
+            const float n2 = n4.z * ps[s_].z, n3 = n4.w * ps[s_].w;
+#pragma unroll
+            for (int i = 0; i < RPT; i++) {
+                const float r = rsc[i];
+                const float v0 = xv[i].x * n0 * r, v1 = xv[i].y * n1 * r;
+                const float v2 = xv[i].z * n2 * r, v3 = xv[i].w * n3 * r;
+                const f16x2 h01 = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(v0, v1));
+                const f16x2 h23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(v2, v3));
+                const f16x2 l01 = __builtin_bit_cast(
+                    f16x2, __builtin_amdgcn_cvt_pkrtz(v0 - (float)h01[0], v1 - (float)h01[1]));
+                const f16x2 l23 = __builtin_bit_cast(
+                    f16x2, __builtin_amdgcn_cvt_pkrtz(v2 - (float)h23[0], v3 - (float)h23[1]));
+                const int r_ = pr + 8 * i;
+                *(uint2*)&sa[s_][0][r_][pk] = make_uint2(__builtin_bit_cast(uint32_t, h01),
+                                                         __builtin_bit_cast(uint32_t, h23));
+                *(uint2*)&sa[s_][1][r_][pk] = make_uint2(__builtin_bit_cast(uint32_t, l01),
+                                                         __builtin_bit_cast(uint32_t, l23));
             }
         }
-#pragma unroll
-        for (int ri = 0; ri < RPT; ri++) {
-            const int r = pr + 64 * ri;
-            if (r >= BM) continue;
-            const int row = row0 + r;
-            const bool live = row < a.M;
-            const float rs = live ? a.rowscale[row] : 0.0f;
-            const float* xr = a.x + (size_t)(live ? row : 0) * a.ldx + k0;
-            float xv[16];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float4 t = live ? *(const float4*)(xr + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
-                xv[4 * i] = t.x * rs; xv[4 * i + 1] = t.y * rs;
-                xv[4 * i + 2] = t.z * rs; xv[4 * i + 3] = t.w * rs;
-            }
-#pragma unroll
-            for (int g = 0; g < NG; g++) {
-                f16x8 h[2], l[2];
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const float4 s4 = sv[g][i / 4];
-                    const float sc = (i & 3) == 0 ? s4.x : (i & 3) == 1 ? s4.y : (i & 3) == 2 ? s4.z : s4.w;
-                    const float v = xv[i] * sc;
-                    const _Float16 hv = (_Float16)v;
-                    h[i / 8][i % 8] = hv;
-                    l[i / 8][i % 8] = (_Float16)(v - (float)hv);
-                }
-                *(f16x8*)&sa[g][0][r][pk] = h[0];
-                *(f16x8*)&sa[g][0][r][pk + 8] = h[1];
-                *(f16x8*)&sa[g][1][r][pk] = l[0];
-                *(f16x8*)&sa[g][1][r][pk + 8] = l[1];
-            }
-        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_prep(c + 1);
+        __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
 #pragma unroll
         for (int kb = 0; kb < 4; kb++) {
-            const uint32_t word = kb == 0 ? wcur.x : kb == 1 ? wcur.y : kb == 2 ? wcur.z : wcur.w;
-            const f16x8 b = nib_to_f16(word);
+            f16x8 b[kGemmTiles];
+#pragma unroll
+            for (int j = 0; j < kGemmTiles; j++) {
+                const uint32_t word = kb == 0 ? wcur[j].x : kb == 1 ? wcur[j].y
+                                    : kb == 2 ? wcur[j].z : wcur[j].w;
+                b[j] = nib_to_f16(word);
+            }
 #pragma unroll
             for (int rt = 0; rt < RT; rt++) {
                 const int ar = rt * 16 + (lane & 15), ak = 32 * kb + 8 * (lane >> 4);
-                const f16x8 ah = *(const f16x8*)&sa[q][0][ar][ak];
-                const f16x8 al = *(const f16x8*)&sa[q][1][ar][ak];
-                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, acc[rt], 0, 0, 0);
-                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, acc[rt], 0, 0, 0);
+                const f16x8 ah = *(const f16x8*)&sa[ws][0][ar][ak];
+                const f16x8 al = *(const f16x8*)&sa[ws][1][ar][ak];
+#pragma unroll
+                for (int j = 0; j < kGemmTiles; j++) {
+                    acc[j][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b[j], acc[j][rt], 0, 0, 0);
+                    acc[j][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b[j], acc[j][rt], 0, 0, 0);
+                }
             }
         }
-        __syncthreads();
-        wcur = wnxt;
+        __builtin_amdgcn_sched_barrier(0);
+        wload(c + 2, wcur);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int c = c0; c < cend; c += 2) {
+        step(c, wb0);
+        step(c + 1, wb1);
     }
-    // partials: lane holds rows 16 rt + 4 (lane / 16) + v of column lane % 16
+
+    if (!wave_ok) return;
     float* pp = a.part + (size_t)blockIdx.z * a.M * a.N;
-    const int col = lt * 16 + (lane & 15);
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++)
+    for (int j = 0; j < kGemmTiles; j++) {
+        const int col = lcol[ws] + 16 * (4 * (wave & 1) + j) + (lane & 15);
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const int row = row0 + rt * 16 + 4 * (lane >> 4) + v;
-            if (row < a.M) pp[(size_t)row * a.N + col] = acc[rt][v];
-        }
+        for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int r_ = rt * 16 + 4 * (lane >> 4) + v;
+                const int row = row0 + r_;
+                if (row < a.M) pp[(size_t)row * a.N + col] = acc[j][rt][v] * s_unscale[r_];
+            }
+    }
 }
 
-// Per row: RMSNorm rstd (or 1) and the power of two that keeps every
-// x * rstd * nw * s below 2^15 given smax >= every |s|: rowscale = rstd * 2^E,
-// unscale = 2^-E.  One block of 256 threads per row.
-__global__ void k_gemm_rows(const float* __restrict__ x, int ldx, int K, const float* __restrict__ nw,
-                            int rms, float eps, float smax, float* __restrict__ rowscale,
-                            float* __restrict__ unscale) {
+// Row factors of the GEMM's activations: rstd (RMSNorm, else 1) times the
+// power of two 2^E with max|x * nw| * rstd * smax * 2^E < 2^15, and 2^-E.
+// One block per row; every thread's loads are issued together.
+__global__ __launch_bounds__(256) void k_gemm_rows(const float* __restrict__ x, int ldx, int K,
+                                                   const float* __restrict__ nw, int rms,
+                                                   float eps, float smax,
+                                                   float* __restrict__ rowscale,
+                                                   float* __restrict__ unscale) {
     __shared__ float s_a[4], s_s[4];
+    constexpr int U = 12;                   // float4 per thread in one batch (K <= 12288)
     const int m = blockIdx.x, t = threadIdx.x;
     const float* xr = x + (size_t)m * ldx;
+    const int K4 = K / 4;
     float amax = 0.0f, ssq = 0.0f;
-    for (int k = t; k < K; k += blockDim.x) {
-        const float v = xr[k];
-        ssq = fmaf(v, v, ssq);
-        amax = fmaxf(amax, fabsf(nw ? v * nw[k] : v));
+    for (int base = 0; base < K4; base += U * 256) {
+        float4 v[U], w[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = min(base + t + 256 * u, K4 - 1);
+            v[u] = *(const float4*)(xr + 4 * i);
+            w[u] = nw ? *(const float4*)(nw + 4 * i) : make_float4(1.f, 1.f, 1.f, 1.f);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (base + t + 256 * u >= K4) continue;
+            ssq = fmaf(v[u].x, v[u].x, fmaf(v[u].y, v[u].y, fmaf(v[u].z, v[u].z, fmaf(v[u].w, v[u].w, ssq))));
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[u].x * w[u].x), fabsf(v[u].y * w[u].y)),
+                                     fmaxf(fabsf(v[u].z * w[u].z), fabsf(v[u].w * w[u].w))));
+        }
     }
     for (int o = 32; o > 0; o >>= 1) {
         amax = fmaxf(amax, __shfl_xor(amax, o));
@@ -609,9 +704,9 @@ __global__ void k_gemm_rows(const float* __restrict__ x, int ldx, int K, const f
     __syncthreads();
     if (t == 0) {
         float A = 0.0f, S = 0.0f;
-        for (int w = 0; w < 4; w++) {
-            A = fmaxf(A, s_a[w]);
-            S += s_s[w];
+        for (int wv = 0; wv < 4; wv++) {
+            A = fmaxf(A, s_a[wv]);
+            S += s_s[wv];
         }
         const float rstd = rms ? 1.0f / sqrtf(S / (float)K + eps) : 1.0f;
         const float bound = A * rstd * smax;
@@ -623,10 +718,10 @@ __global__ void k_gemm_rows(const float* __restrict__ x, int ldx, int K, const f
     }
 }
 
-// Sum of the K splits in order, times 2^-E, and the epilogue.
+// Sum of the K splits in order, and the epilogue.
 template <int EPI>
 __global__ void k_gemm_reduce(const float* __restrict__ part, int ksplit, int M, int N,
-                              const float* __restrict__ unscale, float* __restrict__ y, int ldy) {
+                              float* __restrict__ y, int ldy) {
     const int Nout = EPI == kEpiSwiGlu ? N / 2 : N;
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (size_t)M * Nout) return;
@@ -634,12 +729,10 @@ __global__ void k_gemm_reduce(const float* __restrict__ part, int ksplit, int M,
     const size_t mn = (size_t)M * N;
     float v = 0.0f;
     for (int z = 0; z < ksplit; z++) v += part[z * mn + (size_t)row * N + col];
-    v *= unscale[row];
     float* yp = y + (size_t)row * ldy + col;
     if (EPI == kEpiSwiGlu) {
         float u = 0.0f;
         for (int z = 0; z < ksplit; z++) u += part[z * mn + (size_t)row * N + Nout + col];
-        u *= unscale[row];
         *yp = v / (1.0f + __expf(-v)) * u;
     } else {
         *yp = EPI == kEpiAccumulate ? *yp + v : v;
@@ -648,7 +741,12 @@ __global__ void k_gemm_reduce(const float* __restrict__ part, int ksplit, int M,
 
 template <int RT, int NG>
 int launch_gemm(const GemmArgs& a, dim3 grid) {
-    hipLaunchKernelGGL((k_gemm_int4<RT, NG>), grid, dim3(64 * kGemmWaves), 0, stream(), a);
+    if (a.nw)
+        hipLaunchKernelGGL((k_gemm_int4<RT, NG, kProRmsNorm>), grid, dim3(64 * kGemmWaves), 0,
+                           stream(), a);
+    else
+        hipLaunchKernelGGL((k_gemm_int4<RT, NG, kProNone>), grid, dim3(64 * kGemmWaves), 0,
+                           stream(), a);
     return launch_check("k_gemm_int4");
 }
 
@@ -736,7 +834,8 @@ extern "C" int cgk_gemv_mfma(const float* x, int ldx, int M, int K, int N, int g
 // 1 when cgk_gemm_int4 takes this product: 8 layout tiles per block within
 // one scale group per A slot.
 extern "C" int cgk_gemm_int4_supported(int M, int K, int N, int gs, int paired) {
-    return M >= 1 && K % kRoundK == 0 && N % 128 == 0 && (paired ? gs % 64 == 0 : gs % 128 == 0);
+    return M >= 1 && K % kChunkK == 0 && N % 128 == 0 && gs % 128 == 0 &&
+           (!paired || (N / 2) % 128 == 0);
 }
 
 extern "C" int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int gs,
@@ -744,43 +843,43 @@ extern "C" int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int g
                              int ldy, int pro, const float* nw, float eps, int epi) {
     const int paired = epi == kEpiSwiGlu;
     if (!cgk_gemm_int4_supported(M, K, N, gs, paired) || ldx < K || (ldx & 3) ||
-        ((uintptr_t)x & 15) || (pro == kProRmsNorm && !nw) || ldy < (paired ? N / 2 : N)) {
+        ((uintptr_t)x & 15) || (pro == kProRmsNorm && (!nw || ((uintptr_t)nw & 15))) ||
+        ldy < (paired ? N / 2 : N)) {
         cgx_set_error("gemm_int4: unsupported shape M=%d K=%d N=%d gs=%d", M, K, N, gs);
         return -1;
     }
-    const int RT = M >= 64 ? (M >= 128 && !paired ? 8 : 4) : (M + 15) / 16;
+    const int RT = M > 64 ? 8 : M > 48 ? 4 : (M + 15) / 16;
     const int BM = 16 * RT;
     const int rowblocks = (M + BM - 1) / BM;
-    const int colblocks = N / 128;
+    const int colblocks = paired ? N / 2 / 128 : (N / 128 + 1) / 2;
     const int nchunks = K / kChunkK;
-    // enough blocks for the chip, splits of at least two chunks
+    // two blocks per CU, splits of at least two chunks
     int ksplit = (512 + colblocks * rowblocks - 1) / (colblocks * rowblocks);
     ksplit = ksplit > nchunks / 2 ? nchunks / 2 : ksplit;
     ksplit = ksplit < 1 ? 1 : (ksplit > 16 ? 16 : ksplit);
     const int ksteps = (nchunks + ksplit - 1) / ksplit;
     ksplit = (nchunks + ksteps - 1) / ksteps;
-    char* ws = (char*)cgx_scratch(CGX_SLOT_WS5, (size_t)M * 8 + 256 + (size_t)ksplit * M * N * 4);
+    const size_t row_bytes = (((size_t)M * 8) + 255) & ~(size_t)255;
+    char* ws = (char*)cgx_scratch(CGX_SLOT_WS5, row_bytes + (size_t)ksplit * M * N * 4);
     if (!ws) return -1;
-    float* rowscale = (float*)ws;
-    float* unscale = rowscale + M;
-    float* part = (float*)(ws + (((size_t)M * 8 + 255) & ~(size_t)255));
-    hipLaunchKernelGGL(k_gemm_rows, dim3(M), dim3(256), 0, stream(), x, ldx, K,
-                       pro == kProRmsNorm ? nw : nullptr, pro == kProRmsNorm, eps, smax,
-                       rowscale, unscale);
-    if (launch_check("k_gemm_rows")) return -1;
     GemmArgs a;
     a.x = x; a.ldx = ldx; a.M = M; a.K = K; a.N = N; a.gs = gs;
     a.w = w; a.scales_t = scales_t;
     a.nw = pro == kProRmsNorm ? nw : nullptr;
-    a.rowscale = rowscale;
-    a.part = part;
+    a.rowscale = (const float*)ws;
+    a.unscale = (const float*)ws + M;
+    a.part = (float*)(ws + row_bytes);
     a.ksteps = ksteps;
     a.ff = N / 2;
+    hipLaunchKernelGGL(k_gemm_rows, dim3(M), dim3(256), 0, stream(), x, ldx, K, a.nw,
+                       pro == kProRmsNorm, eps, smax, (float*)ws, (float*)ws + M);
+    if (launch_check("k_gemm_rows")) return -1;
     dim3 grid(colblocks, rowblocks, ksplit);
     int rc;
     if (paired) {
         rc = RT == 1 ? launch_gemm<1, 2>(a, grid) : RT == 2 ? launch_gemm<2, 2>(a, grid)
-           : RT == 3 ? launch_gemm<3, 2>(a, grid) : launch_gemm<4, 2>(a, grid);
+           : RT == 3 ? launch_gemm<3, 2>(a, grid) : RT == 4 ? launch_gemm<4, 2>(a, grid)
+           : launch_gemm<8, 2>(a, grid);
     } else {
         rc = RT == 1 ? launch_gemm<1, 1>(a, grid) : RT == 2 ? launch_gemm<2, 1>(a, grid)
            : RT == 3 ? launch_gemm<3, 1>(a, grid) : RT == 4 ? launch_gemm<4, 1>(a, grid)
@@ -790,19 +889,18 @@ extern "C" int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int g
     const size_t outs = (size_t)M * (paired ? N / 2 : N);
     const int blocks = (int)((outs + 255) / 256);
     if (epi == kEpiSwiGlu)
-        hipLaunchKernelGGL(k_gemm_reduce<kEpiSwiGlu>, dim3(blocks), dim3(256), 0, stream(), part,
-                           ksplit, M, N, unscale, y, ldy);
+        hipLaunchKernelGGL(k_gemm_reduce<kEpiSwiGlu>, dim3(blocks), dim3(256), 0, stream(),
+                           a.part, ksplit, M, N, y, ldy);
     else if (epi == kEpiAccumulate)
         hipLaunchKernelGGL(k_gemm_reduce<kEpiAccumulate>, dim3(blocks), dim3(256), 0, stream(),
-                           part, ksplit, M, N, unscale, y, ldy);
+                           a.part, ksplit, M, N, y, ldy);
     else
-        hipLaunchKernelGGL(k_gemm_reduce<kEpiStore>, dim3(blocks), dim3(256), 0, stream(), part,
-                           ksplit, M, N, unscale, y, ldy);
+        hipLaunchKernelGGL(k_gemm_reduce<kEpiStore>, dim3(blocks), dim3(256), 0, stream(),
+                           a.part, ksplit, M, N, y, ldy);
     return launch_check("k_gemm_reduce");
 }
 
-// max |s| over a scales array (host result, synchronising): the bound the
-// GEMM's row scaling needs, computed once per weight
+// max |s| over a scales array (host result, synchronising)
 __global__ void k_absmax(const float* __restrict__ s, size_t n, unsigned int* out) {
     float m = 0.0f;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)

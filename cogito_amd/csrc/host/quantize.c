@@ -151,7 +151,8 @@ static cg_tensor_quant* quant_to_device_layout(cg_tensor_quant* q, int want) {
             goto fail;
     }
     {
-        cgx_qinfo info = {layout, K, N, gs, 0};
+        cgx_qinfo info = {layout, K, N, gs, 0, 0.0f};
+        if (layout == CGX_LAYOUT_MFMA && cgk_absmax(d->scales, (size_t)ng, &info.smax)) goto fail;
         cgx_quant_register(d, &info);
     }
     return d;
@@ -265,14 +266,9 @@ int cgx_matmul_int4_dev_kernel(const float* x, int M, cg_tensor_quant* w,
             cgx_set_error("cgx_matmul_int4: MFMA kernels need a layout-3 weight");
             return -1;
         }
-        if (kernel == 4) {
-            /* the GEMM of the batched / tree verify (M >= 32 in the decoder) */
-            float smax;
-            if (cgk_absmax(w->scales, (size_t)info.K * info.N / info.group_size, &smax))
-                return -1;
+        if (kernel == 4)      /* the GEMM of the batched / tree verify (M >= 32) */
             return cgk_gemm_int4(x, info.K, M, info.K, info.N, info.group_size, w->data,
-                                 w->scales, smax, y, info.N, 0, NULL, 0.0f, 0);
-        }
+                                 w->scales, info.smax, y, info.N, 0, NULL, 0.0f, 0);
         return cgk_gemv_mfma(x, info.K, M, info.K, info.N, info.group_size, w->data,
                              w->scales, y, info.N, 0, NULL, 0.0f, 0);
     }
