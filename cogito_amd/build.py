@@ -32,7 +32,7 @@ HIP_FLAGS = [
 ]
 # Files whose arithmetic must round exactly where written (no implicit
 # contraction of a*b+c into fma).
-EXACT_FP = {"accept.hip", "int4.hip", "filter.hip"}
+EXACT_FP = {"accept.hip", "int4.hip", "filter.hip", "tree.hip"}
 C_FLAGS = ["-O2", "-fPIC", "-std=c11", "-Wall", "-Wextra", "-Wno-unused-parameter",
            f"-I{INCLUDE}", f"-I{CSRC}"]
 

@@ -281,6 +281,18 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_spec_batch_step": (I, [VP, VP, VP, VP, VP]),
     "cgx_spec_batch_stats": (None, [VP, C.POINTER(C.c_longlong), C.POINTER(C.c_longlong),
                                     C.POINTER(C.c_longlong)]),
+    "cgx_model_forward_tree_rows": (I, [VP, VP, I, VP, VP, I, VP]),
+    "cgx_tree_spec_new": (VP, [VP, VP, I, I, F, I, F]),
+    "cgx_tree_spec_free": (None, [VP]),
+    "cgx_tree_spec_nodes": (I, [VP]),
+    "cgx_tree_spec_depth": (I, [VP]),
+    "cgx_tree_spec_set_root": (I, [VP, VP]),
+    "cgx_tree_spec_step": (I, [VP, VP, VP, VP]),
+    "cgx_tree_spec_stats": (None, [VP, C.POINTER(C.c_longlong), C.POINTER(C.c_longlong),
+                                   C.POINTER(C.c_longlong)]),
+    "cgx_tree_shape_get": (I, [I, I, VP, VP, VP]),
+    "cgx_topk_lists_dev": (I, [VP, I, I, I, F, VP, VP]),
+    "cgx_tree_accept_dev": (I, [VP, I, I, I, VP, VP, VP, VP, VP, VP, VP]),
 }
 
 # The subset implemented so far; the rest are declared in the headers and

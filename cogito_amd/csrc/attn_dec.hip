@@ -75,7 +75,9 @@ struct DecArgs {
     float* O;                    // [Nq][H][D] when splits == 1
     float* part_o;               // [splits][Nq*H][D]
     float* part_ml;              // [splits][Nq*H][2]
-    unsigned long long anc[64];  // tree: ancestor bits over the last Nq keys
+    unsigned long long anc[64];  // tree: ancestor bits over the last tw keys
+    int tw;                      // tree window: the last tw keys (Nq <= tw <= 64) are
+                                 // visible to a query row only through its anc bits
     // batch: B sequences, each with Nq query rows (Q, O: [B][Nq][H][D]) and
     // its own cache at kc + b * seq_kbytes (scales + b * seq_groups) of
     // nk[b] keys; blockIdx.z = b * chunks + row chunk
@@ -166,7 +168,9 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
     const int k_begin = split * a.keys_per_split;
     const int k_end = min(Nk, k_begin + a.keys_per_split);
     const int ntiles = (k_end - k_begin + kTile - 1) / kTile;
-    const int base = Nk - a.Nq;                      // first of the new positions
+    // first key under the mask's bits: the new positions (chain), or the
+    // tree window (the tree's nodes, of this call and of earlier calls)
+    const int base = Nk - (a.mask_kind == kMaskTree ? a.tw : a.Nq);
 
     float m_run[RT], l_part[RT];
     f32x4 o[RT][8];                                  // O^T tiles t = 0..7
@@ -235,7 +239,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
         // chain: keys up to the query's own position; tree: the cached prefix
         // (plus ancestor bits); no mask: every key
         lim_row[rt] = a.mask_kind == kMaskCausal ? Nk - a.Nq + rq[rt]
-                    : a.mask_kind == kMaskTree ? Nk - a.Nq - 1 : Nk;
+                    : a.mask_kind == kMaskTree ? Nk - a.tw - 1 : Nk;
     }
     {
         // rows are per lane (n); every wave computes the row exponent of its
@@ -516,14 +520,16 @@ extern "C" int cgk_attn_dec_batch(const float* Q, const uint8_t* kc, const uint8
                                   const float* ks, const float* vs, int B, const int* nk,
                                   size_t seq_kbytes, size_t seq_groups, int Nq, int H, int Hk,
                                   int D, float scale, int mask_kind,
-                                  const unsigned long long* anc, float* O) {
+                                  const unsigned long long* anc, int tw, float* O) {
     int nkmax = 0, nkmin = 1 << 30;
     for (int b = 0; b < B; b++) {
         nkmax = nk[b] > nkmax ? nk[b] : nkmax;
         nkmin = nk[b] < nkmin ? nk[b] : nkmin;
     }
+    if (mask_kind == kMaskTree && tw <= 0) tw = Nq;
     if (B < 1 || B > kMaxBatch || Nq <= 0 || nkmin < Nq || Hk <= 0 || H % Hk ||
-        (mask_kind == kMaskTree && (Nq > 64 || !anc)) || (D != 32 && D != 64 && D != 128)) {
+        (mask_kind == kMaskTree && (Nq > 64 || !anc || tw < Nq || tw > 64 || nkmin < tw)) ||
+        (D != 32 && D != 64 && D != 128)) {
         cgx_set_error("attn_dec: unsupported shape B=%d Nq=%d Nk=%d..%d H=%d Hk=%d D=%d", B, Nq,
                       nkmin, nkmax, H, Hk, D);
         return -1;
@@ -537,6 +543,7 @@ extern "C" int cgk_attn_dec_batch(const float* Q, const uint8_t* kc, const uint8
     a.Nq = Nq; a.Nk = nkmax; a.H = H; a.Hk = Hk;
     a.scale = scale;
     a.mask_kind = mask_kind;
+    a.tw = mask_kind == kMaskTree ? tw : Nq;
     for (int i = 0; i < 64; i++) a.anc[i] = (mask_kind == kMaskTree && i < Nq) ? anc[i] : 0ull;
     a.B = B;
     a.seq_kbytes = seq_kbytes;
@@ -588,5 +595,5 @@ extern "C" int cgk_attn_dec(const float* Q, const uint8_t* kc, const uint8_t* vc
                             const float* vs, int Nq, int Nk, int H, int Hk, int D, float scale,
                             int mask_kind, const unsigned long long* anc, float* O) {
     return cgk_attn_dec_batch(Q, kc, vc, ks, vs, 1, &Nk, 0, 0, Nq, H, Hk, D, scale, mask_kind,
-                              anc, O);
+                              anc, Nq, O);
 }

@@ -128,7 +128,7 @@ enum {
     CGK_MASK_CAUSAL_ALIGNED = 1, /* query q sees keys <= Nk - Nq + q */
     CGK_MASK_WINDOW = 2,         /* |key - q| <= window */
     CGK_MASK_CUSTOM = 3,         /* additive fp32 [Nq][Nk] */
-    CGK_MASK_TREE = 4,           /* keys < Nk - Nq, plus ancestor bits */
+    CGK_MASK_TREE = 4,           /* keys < Nk - tw, plus ancestor bits over the last tw */
     CGK_MASK_CAUSAL = 5          /* query q sees keys <= q */
 };
 int cgk_kv_append(const float* k, const float* v, int T, int H, int D, int gs, int pos,
@@ -150,11 +150,58 @@ int cgk_attn_dec(const float* Q, const uint8_t* kc, const uint8_t* vc, const flo
                  const float* vs, int Nq, int Nk, int H, int Hk, int D, float scale,
                  int mask_kind, const unsigned long long* anc, float* O);
 /* Batched decode attention: B sequences of Nq query rows, sequence b's cache
- * at kc + b * seq_kbytes (scales + b * seq_groups) with nk[b] keys. */
+ * at kc + b * seq_kbytes (scales + b * seq_groups) with nk[b] keys.  Tree
+ * mask: the last tw keys (Nq <= tw <= 64; the tree's nodes so far, the query
+ * rows last) are visible to query row i only where bit j of anc[i] is set. */
 int cgk_attn_dec_batch(const float* Q, const uint8_t* kc, const uint8_t* vc, const float* ks,
                        const float* vs, int B, const int* nk, size_t seq_kbytes,
                        size_t seq_groups, int Nq, int H, int Hk, int D, float scale,
-                       int mask_kind, const unsigned long long* anc, float* O);
+                       int mask_kind, const unsigned long long* anc, int tw, float* O);
+
+/* Rows of a tree forward (cgx_model_forward_tree): row i sits at cache slot
+ * len + i and rotary position len + rel[i]; the last tw cached keys are the
+ * tree's nodes, visible to row i through anc[i]. */
+typedef struct {
+    int rel[64];
+    unsigned long long anc[64];
+    int tw;
+} cgx_tree_rows;
+int cgx_model_forward_tree(cgx_model* m, const int* tokens, int M, const cgx_tree_rows* tr,
+                           float* logits, size_t ldl);
+
+/* Static draft tree (tree.hip, host/tree.c): node 0 is the verified root;
+ * nodes are in breadth-first order; kids[i][0..nkids[i]) the children of
+ * node i in rank order (rank r = the draft's (r+1)-th most likely token). */
+typedef struct {
+    int nodes, depth;
+    int parent[64], node_depth[64];
+    int nkids[64];
+    int kids[64][4];
+    int rank[64];
+} cgx_tree_shape;
+int cgk_tree_accept(const cgx_tree_shape* t, int B, int K, const int* lidx, const float* lp,
+                    const int* tok, const float* u, int* out, int* nacc, int* path);
+int cgk_kv_compact(const cgx_tree_shape* t, int B, const int* len0, const int* nacc,
+                   const int* path, int layers, int nb, uint8_t* kc, uint8_t* vc, float* ks,
+                   float* vs, int row_bytes, int row_groups, size_t layer_bytes,
+                   size_t layer_groups);
+int cgk_topk_lists(const float* z, int rows, int V, int top_k, float top_p, int* lidx,
+                   float* lp);
+int cgk_tree_children(const cgx_tree_shape* t, int B, int K, int first, int count, int pfirst,
+                      int pcount, const int* parent_dev, const int* rank_dev, const int* lidx,
+                      int* tok);
+int cgk_tree_gather(int B, int R, int first, int count, const int* tok, int* out);
+/* Moves the accepted path's cache rows (tree.hip k_kv_compact) in every layer
+ * and sets sequence b's length to len0[b] + 1 + nacc_host[b]. */
+int cgx_model_compact_tree(cgx_model* m, const cgx_tree_shape* t, const int* len0,
+                           const int* nacc_dev, const int* path_dev, const int* nacc_host);
+/* The default draft tree: nodes (root included) chosen best-first by a path
+ * score (the product of fixed per-rank weights), at most 4 children and the
+ * given depth; breadth-first numbering. */
+int cgx_tree_shape_default(cgx_tree_shape* t, int nodes, int depth);
+/* A tree from parents (breadth-first, parent[i] < i, parent[0] = -1) and the
+ * rank of each node among its siblings (0 .. 3, distinct, in order). */
+int cgx_tree_shape_from_parents(cgx_tree_shape* t, const int* parent, int nodes);
 int cgk_rope(float* x, int S, int H, int D, int pos0, float theta);
 int cgk_rope_freqs(float* cs, float* sn, int S, int D, float theta);
 int cgk_alibi_slopes(float* slopes, int H);

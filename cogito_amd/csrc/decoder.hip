@@ -48,6 +48,7 @@ __global__ void k_embed(const float* __restrict__ table, const int* __restrict__
 }
 
 constexpr int kMaxBatch = 16;
+constexpr int kMaxTreeRows = 64;
 
 // Token rows of B sequences, M each (row r = b * M + m): sequence b's rows
 // sit at positions pos0[b] + m of its own cache (kc + b * seq_kbytes, scales
@@ -56,6 +57,8 @@ struct RopeBatch {
     int M;
     int pos0[kMaxBatch];
     size_t seq_kbytes, seq_groups;
+    int has_rel;                 // tree rows: rotary position pos0 + rel[row]
+    int rel[kMaxTreeRows];
 };
 
 // One workgroup of D/2 threads per (token row, head): heads [0, H) are query
@@ -68,14 +71,17 @@ __global__ void k_rope_append(const float* __restrict__ qkv, int ld, int H, int 
     __shared__ float sk[256], sv[256];
     const int m = blockIdx.x, head = blockIdx.y, i = threadIdx.x, half = D / 2;
     const int sq = m / rb.M;
+    // cache slot pos0 + row; rotary position the same, or pos0 + rel[row]
+    // for a tree row (its depth below the verified prefix)
     const int pos = rb.pos0[sq] + m % rb.M;
+    const int rpos = rb.has_rel ? rb.pos0[sq] + rb.rel[m % rb.M] : pos;
     kc += (size_t)sq * rb.seq_kbytes;
     vc += (size_t)sq * rb.seq_kbytes;
     ks += (size_t)sq * rb.seq_groups;
     vs += (size_t)sq * rb.seq_groups;
     const float* row = qkv + (size_t)m * ld;
     float freq = __fdiv_rn(1.0f, powf(theta, __fdiv_rn((float)(2 * i), (float)D)));
-    float angle = __fmul_rn((float)pos, freq);
+    float angle = __fmul_rn((float)rpos, freq);
     float c = cosf(angle), s = sinf(angle);
     if (head < H) {
         const float* q = row + head * D;
@@ -174,8 +180,8 @@ extern "C" int cgk_embed(const float* table, const int* tokens, int M, int d, in
 }
 
 extern "C" int cgk_rope_append_batch(const float* qkv, int ld, int B, int M, int H, int Hk,
-                                     int D, int gs, const int* pos0, float theta, float* q_out,
-                                     uint8_t* kc, uint8_t* vc, float* ks, float* vs,
+                                     int D, int gs, const int* pos0, const int* rel, float theta,
+                                     float* q_out, uint8_t* kc, uint8_t* vc, float* ks, float* vs,
                                      size_t seq_kbytes, size_t seq_groups) {
     if (M <= 0) return 0;
     if (D < 2 || D > 256 || (D & 1) || gs <= 0 || (gs & 1) || D % gs) {
@@ -186,7 +192,13 @@ extern "C" int cgk_rope_append_batch(const float* qkv, int ld, int B, int M, int
         cgx_set_error("rope_append: batch %d outside [1, %d]", B, kMaxBatch);
         return -1;
     }
+    if (rel && M > kMaxTreeRows) {
+        cgx_set_error("rope_append: %d tree rows above %d", M, kMaxTreeRows);
+        return -1;
+    }
     RopeBatch rb;
+    rb.has_rel = rel != nullptr;
+    for (int r = 0; r < kMaxTreeRows; r++) rb.rel[r] = rel && r < M ? rel[r] : 0;
     rb.M = M;
     for (int b = 0; b < kMaxBatch; b++) rb.pos0[b] = b < B ? pos0[b] : 0;
     rb.seq_kbytes = seq_kbytes;
@@ -199,8 +211,8 @@ extern "C" int cgk_rope_append_batch(const float* qkv, int ld, int B, int M, int
 extern "C" int cgk_rope_append(const float* qkv, int ld, int M, int H, int Hk, int D, int gs,
                                int pos0, float theta, float* q_out, uint8_t* kc, uint8_t* vc,
                                float* ks, float* vs) {
-    return cgk_rope_append_batch(qkv, ld, 1, M, H, Hk, D, gs, &pos0, theta, q_out, kc, vc, ks,
-                                 vs, 0, 0);
+    return cgk_rope_append_batch(qkv, ld, 1, M, H, Hk, D, gs, &pos0, nullptr, theta, q_out, kc,
+                                 vc, ks, vs, 0, 0);
 }
 
 extern "C" int cgk_spec_tokens(const int* feed, const int* dtok, int B, int gamma, int* ttok,

@@ -289,7 +289,9 @@ __global__ __launch_bounds__(kThreads) void k_top_k(const float* __restrict__ z,
                                                     int kpow2, float top_p,
                                                     const float* __restrict__ u,
                                                     int* __restrict__ tokens,
-                                                    float* __restrict__ dist) {
+                                                    float* __restrict__ dist,
+                                                    int* __restrict__ lidx,
+                                                    float* __restrict__ lp) {
     __shared__ EosShared sh;
     __shared__ unsigned long long cand[kTopKMax];
     __shared__ int hist[256];
@@ -444,6 +446,17 @@ __global__ __launch_bounds__(kThreads) void k_top_k(const float* __restrict__ z,
         if (t == 0) tokens[row] = idx[j];
         return;
     }
+    if (lidx) {
+        // the list itself: entry j of the row is (idx[j], probability); past
+        // the top-p cutoff, and for the (-1e30, 0) fillers, the probability
+        // is 0
+        for (int j = t; j < k; j += kThreads) {
+            float v = j < keep ? (use_p ? __fdiv_rn(pr(j), mass) : pr(j)) : 0.0f;
+            lidx[(size_t)row * k + j] = idx[j];
+            lp[(size_t)row * k + j] = v;
+        }
+        return;
+    }
     float* dr = dist + (size_t)row * V;
     for (int j = t; j < V; j += kThreads) dr[j] = 0.0f;
     __syncthreads();
@@ -458,6 +471,29 @@ __global__ __launch_bounds__(kThreads) void k_top_k(const float* __restrict__ z,
 }  // namespace
 
 // -------------------------------------------------------------- launchers
+
+// Top-k lists of `rows` rows of z [rows][V] (1 <= top_k < V): lidx/lp
+// [rows][top_k], entry j = the j-th of cg_sample_top_k's list (value desc,
+// index asc) and its probability (softmax of the list at T = 1, then the
+// top-p cutoff and renormalisation when top_p < 1; 0 past the cutoff and for
+// the -1e30 fillers).
+extern "C" int cgk_topk_lists(const float* z, int rows, int V, int top_k, float top_p, int* lidx,
+                              float* lp) {
+    if (rows <= 0 || V <= 0 || rows > 65535 || top_k < 1 || top_k >= V || top_k > kTopKMax ||
+        !lidx || !lp) {
+        cgx_set_error("topk_lists: invalid arguments (rows %d, V %d, k %d)", rows, V, top_k);
+        return -1;
+    }
+    if (V > kRound * kMaxRounds) {
+        cgx_set_error("topk_lists: vocabulary size %d above %d", V, kRound * kMaxRounds);
+        return -1;
+    }
+    int kpow2 = 64;
+    while (kpow2 < top_k) kpow2 <<= 1;
+    hipLaunchKernelGGL(k_top_k, dim3(rows), dim3(kThreads), 0, stream(), z, V, top_k, kpow2,
+                       top_p, (const float*)nullptr, (int*)nullptr, (float*)nullptr, lidx, lp);
+    return launch_check("k_top_k");
+}
 
 extern "C" int cgk_scale(const float* x, float* z, size_t n, float T) {
     if (!n) return 0;
@@ -486,7 +522,7 @@ extern "C" int cgk_filter_rows(const float* z, int rows, int V, int top_k, float
         int kpow2 = 64;
         while (kpow2 < top_k) kpow2 <<= 1;
         hipLaunchKernelGGL(k_top_k, dim3(rows), dim3(kThreads), 0, stream(), z, V, top_k,
-                           kpow2, top_p, u, tokens, dist);
+                           kpow2, top_p, u, tokens, dist, (int*)nullptr, (float*)nullptr);
         return launch_check("k_top_k");
     }
     if (V > kSortMax) {

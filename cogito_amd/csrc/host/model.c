@@ -18,8 +18,9 @@
 
 int cgk_embed(const float* table, const int* tokens, int M, int d, int V, float* x);
 int cgk_rope_append_batch(const float* qkv, int ld, int B, int M, int H, int Hk, int D, int gs,
-                          const int* pos0, float theta, float* q_out, uint8_t* kc, uint8_t* vc,
-                          float* ks, float* vs, size_t seq_kbytes, size_t seq_groups);
+                          const int* pos0, const int* rel, float theta, float* q_out,
+                          uint8_t* kc, uint8_t* vc, float* ks, float* vs, size_t seq_kbytes,
+                          size_t seq_groups);
 int cgk_fill_normal(float* out, size_t n, uint64_t seed, uint32_t stream_id, float stddev);
 
 enum { PRO_NONE = 0, PRO_RMSNORM = 1 };
@@ -286,12 +287,18 @@ static int linear(const lin_t* L, const float* x, int ldx, int R, float* y, int 
                          eps, epi);
 }
 
-/* Forward of B sequences (0..B-1), M tokens each. */
+/* Forward of B sequences (0..B-1), M tokens each; tr: the rows are tree
+ * nodes (rotary positions and the tree mask of cgx_tree_rows), else a chain. */
 static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_logits,
-                        float* logits, size_t ldl) {
+                        float* logits, size_t ldl, const cgx_tree_rows* tr) {
     const cgx_model_config* c = &m->c;
     if (!tokens || M < 1 || M > c->max_tokens || n_logits < 0 || n_logits > M) {
         cgx_set_error("cgx_model_forward: invalid argument (M=%d, n_logits=%d)", M, n_logits);
+        return -1;
+    }
+    if (tr && (M > 64 || tr->tw < M || tr->tw > 64)) {
+        cgx_set_error("cgx_model_forward_tree: %d rows in a window of %d (at most 64)", M,
+                      tr->tw);
         return -1;
     }
     cg_kv_cache_int4* kv = m->kv;
@@ -318,7 +325,18 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
     const float eps = c->norm_eps, scale = 1.0f / sqrtf((float)hd);
     if (cgk_embed(m->embed, dtok, R, d, c->vocab, m->x)) return -1;
     const size_t lb = kv_layer_bytes(kv), lg = kv_layer_groups(kv);
-    const int batched = cgk_attn_dec_supported(hd, kv->group_size, 1, CGK_MASK_CAUSAL_ALIGNED);
+    const int mask = tr ? CGK_MASK_TREE : CGK_MASK_CAUSAL_ALIGNED;
+    const int batched = cgk_attn_dec_supported(hd, kv->group_size, 1, mask);
+    if (tr && !batched) {
+        cgx_set_error("cgx_model_forward_tree: head_dim %d / KV group %d not supported", hd,
+                      kv->group_size);
+        return -1;
+    }
+    for (int b = 0; tr && b < B; b++)
+        if (pos0[b] + M < tr->tw) {
+            cgx_set_error("cgx_model_forward_tree: window %d above the cache length", tr->tw);
+            return -1;
+        }
     for (int l = 0; l < c->n_layers; l++) {
         const lin_t* w = m->layers[l].w;
         /* layer l of sequence b: slot l * nb + b */
@@ -330,11 +348,12 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
         if (linear(&w[W_QKV], m->x, d, R, m->qkv, nq, PRO_RMSNORM, m->ones, eps, EPI_STORE,
                    gs) ||
             cgk_rope_append_batch(m->qkv, nq, B, M, H, Hk, hd, kv->group_size, pos0,
-                                  c->rope_theta, m->q, kc, vc, ks, vs, lb, lg))
+                                  tr ? tr->rel : NULL, c->rope_theta, m->q, kc, vc, ks, vs, lb,
+                                  lg))
             return -1;
         if (batched) {
             if (cgk_attn_dec_batch(m->q, kc, vc, ks, vs, B, nk, lb, lg, M, H, Hk, hd, scale,
-                                   CGK_MASK_CAUSAL_ALIGNED, NULL, m->attn))
+                                   mask, tr ? tr->anc : NULL, tr ? tr->tw : M, m->attn))
                 return -1;
         } else {
             for (int b = 0; b < B; b++)
@@ -379,7 +398,7 @@ int cgx_model_forward(cgx_model* m, const int* tokens, int M, int n_logits, floa
         cgx_set_error("cgx_model_forward: NULL model");
         return -1;
     }
-    return forward_rows(m, 1, tokens, M, n_logits, logits, 0);
+    return forward_rows(m, 1, tokens, M, n_logits, logits, 0, NULL);
 }
 
 int cgx_model_forward_batch(cgx_model* m, const int* tokens, int M, int n_logits,
@@ -388,7 +407,7 @@ int cgx_model_forward_batch(cgx_model* m, const int* tokens, int M, int n_logits
         cgx_set_error("cgx_model_forward_batch: NULL model");
         return -1;
     }
-    return forward_rows(m, m->nb, tokens, M, n_logits, logits, 0);
+    return forward_rows(m, m->nb, tokens, M, n_logits, logits, 0, NULL);
 }
 
 int cgx_model_forward_batch_ld(cgx_model* m, const int* tokens, int M, int n_logits,
@@ -397,7 +416,59 @@ int cgx_model_forward_batch_ld(cgx_model* m, const int* tokens, int M, int n_log
         cgx_set_error("cgx_model_forward_batch: NULL model");
         return -1;
     }
-    return forward_rows(m, m->nb, tokens, M, n_logits, logits, ld);
+    return forward_rows(m, m->nb, tokens, M, n_logits, logits, ld, NULL);
+}
+
+/* Tree forward of every sequence: M rows each (device or host tokens
+ * [B][M]), logits of every row at logits + (b * M + i) * vocab (ldl 0) or
+ * with row stride ... : sequence b's rows at logits + b * ldl. */
+int cgx_model_forward_tree(cgx_model* m, const int* tokens, int M, const cgx_tree_rows* tr,
+                           float* logits, size_t ldl) {
+    if (!m || !tr) {
+        cgx_set_error("cgx_model_forward_tree: NULL argument");
+        return -1;
+    }
+    return forward_rows(m, m->nb, tokens, M, logits ? M : 0, logits, ldl, tr);
+}
+
+int cgx_model_forward_tree_rows(cgx_model* m, const int* tokens, int M, const int* rel,
+                                const unsigned long long* anc, int tw, float* logits) {
+    if (!m || !rel || !anc || M < 1 || M > 64) {
+        cgx_set_error("cgx_model_forward_tree_rows: invalid argument");
+        return -1;
+    }
+    cgx_tree_rows tr;
+    memset(&tr, 0, sizeof(tr));
+    for (int i = 0; i < M; i++) {
+        tr.rel[i] = rel[i];
+        tr.anc[i] = anc[i];
+    }
+    tr.tw = tw;
+    return forward_rows(m, m->nb, tokens, M, M, logits, 0, &tr);
+}
+
+int cgx_model_compact_tree(cgx_model* m, const cgx_tree_shape* t, const int* len0,
+                           const int* nacc_dev, const int* path_dev, const int* nacc_host) {
+    if (!m || !t || !len0 || !nacc_host) {
+        cgx_set_error("cgx_model_compact_tree: invalid argument");
+        return -1;
+    }
+    cg_kv_cache_int4* kv = m->kv;
+    const int B = m->nb;
+    for (int b = 0; b < B; b++)
+        if (nacc_host[b] < 0 || nacc_host[b] > t->depth || len0[b] + 1 + nacc_host[b] > m->len[b]) {
+            cgx_set_error("cgx_model_compact_tree: sequence %d: %d accepted past %d + %d cached",
+                          b, nacc_host[b], len0[b], m->len[b] - len0[b]);
+            return -1;
+        }
+    if (cgk_kv_compact(t, B, len0, nacc_dev, path_dev, m->c.n_layers, m->nb, kv->k_cache,
+                       kv->v_cache, kv->k_scales, kv->v_scales,
+                       kv->n_heads * (kv->head_dim / 2), kv->n_heads * (kv->head_dim / kv->group_size),
+                       kv_layer_bytes(kv), kv_layer_groups(kv)))
+        return -1;
+    for (int b = 0; b < B; b++) m->len[b] = len0[b] + 1 + nacc_host[b];
+    kv->current_len = m->len[0];
+    return 0;
 }
 
 int cgx_model_fill_context(cgx_model* m, int len, uint64_t seed) {

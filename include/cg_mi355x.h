@@ -262,6 +262,56 @@ int cgx_spec_batch_step(cgx_spec_batch* s, const float* u_draft, const float* u_
 void cgx_spec_batch_stats(const cgx_spec_batch* s, long long* steps, long long* drafted,
                           long long* accepted);
 
+/* Tree forward of every sequence (M <= 64 rows each, tokens [B][M]): row i
+ * goes to cache slot len + i with rotary position len + rel[i]; of the keys,
+ * the last tw (M <= tw <= 64: the tree's nodes cached so far, these rows
+ * last) are visible to row i only where bit j of anc[i] is set (key
+ * len + M - tw + j).  Logits of every row at logits ([B][M][vocab]) or in the
+ * model's own buffer (logits NULL). */
+int cgx_model_forward_tree_rows(cgx_model* m, const int* tokens, int M, const int* rel,
+                                const unsigned long long* anc, int tw, float* logits);
+
+/* Tree speculation (EAGLE-style), B = max_batch sequences in lockstep.  The
+ * draft tree has `nodes` nodes (node 0 the root: the last emitted token, not
+ * cached yet) to the given depth, chosen best-first with at most 4 children
+ * a node and numbered breadth-first (cgx_tree_shape_get).  A step drafts the
+ * tree level by level (a node's children: the top-c tokens of the draft's
+ * logits at that node), verifies every node in one target forward under the
+ * tree mask, and walks it: at the current node the target distribution p
+ * (top_k list at temperature T, then top_p) accepts candidate x with
+ * probability w[x] / W, a rejected candidate's mass is removed (w[x] = 0),
+ * and when all are rejected (or at a leaf) the next token is drawn from w / W.
+ * No reference counterpart: cogito's EAGLE builder is a stub
+ * (src/inference/speculative.c:244-262).  u: [B][depth + 1][5] draws (slot r
+ * < 4: candidate r's test at that depth, slot 4: the final draw); out_tokens
+ * [B][depth + 2] (the accepted tokens, then the drawn one; -1 after);
+ * n_accepted [B]; returns the total accepted.  Requires max_tokens >= nodes
+ * in both models, 1 <= top_k <= 64. */
+typedef struct cgx_tree_spec cgx_tree_spec;
+cgx_tree_spec* cgx_tree_spec_new(cgx_model* draft, cgx_model* target, int nodes, int depth,
+                                 float temperature, int top_k, float top_p);
+void cgx_tree_spec_free(cgx_tree_spec* s);
+int cgx_tree_spec_nodes(const cgx_tree_spec* s);
+int cgx_tree_spec_depth(const cgx_tree_spec* s);
+int cgx_tree_spec_set_root(cgx_tree_spec* s, const int* root);
+int cgx_tree_spec_step(cgx_tree_spec* s, const float* u, int* out_tokens, int* n_accepted);
+void cgx_tree_spec_stats(const cgx_tree_spec* s, long long* steps, long long* drafted,
+                         long long* accepted);
+/* The default tree's parent, depth and sibling rank per node; returns the
+ * node count. */
+int cgx_tree_shape_get(int nodes, int depth, int* parent, int* node_depth, int* rank);
+/* Device pieces of the step (device pointers): top-k lists of `rows` rows
+ * of z (index and probability per entry, cg_sample_top_k's order), and the
+ * acceptance walk over a tree given by parents (breadth-first, parent[0] =
+ * -1, siblings in rank order) with lists [B * nodes][K], node tokens
+ * [B][nodes] and draws as in cgx_tree_spec_step; out [B][depth + 2], nacc
+ * [B], path [B][depth] (node index of each accepted node). */
+int cgx_topk_lists_dev(const float* z, int rows, int V, int top_k, float top_p, int* lidx,
+                       float* lp);
+int cgx_tree_accept_dev(const int* parent, int nodes, int B, int K, const int* lidx,
+                        const float* lp, const int* tok, const float* u, int* out, int* nacc,
+                        int* path);
+
 #ifdef __cplusplus
 }
 #endif

@@ -641,3 +641,80 @@ void orc_tree_mask_chain(float* mask, int seqlen, int depth) {
         for (int j = 0; j <= i; j++) mask[r * size + seqlen + j] = 0.0f;
     }
 }
+
+/* ------------------------------------------------------------ tree walk */
+
+void orc_topk_lists(const float* z, int V, int k, float top_p, int* lidx, float* lp) {
+    /* the list of cg_sample_top_k (speculative.c:122-146) over z = logits / T:
+     * entry j = (index, probability), the probabilities the softmax of the
+     * list at T = 1 (speculative.c:54-75), then the top-p cutoff of the
+     * filtered verify (list_cutoff) renormalised; 0 past the cutoff */
+    float* vals = (float*)malloc((size_t)k * sizeof(float));
+    float* pr = (float*)malloc((size_t)k * sizeof(float));
+    orc_top_k_list(z, V, k, vals, lidx);
+    orc_temperature_probs(vals, k, 1.0f, pr);
+    int keep = k;
+    float mass = 1.0f;
+    int up = use_top_p(top_p);
+    if (up) keep = list_cutoff(pr, k, top_p, &mass);
+    for (int j = 0; j < k; j++) lp[j] = j < keep ? (up ? pr[j] / mass : pr[j]) : 0.0f;
+    free(vals);
+    free(pr);
+}
+
+int orc_tree_accept(const int* parent, int nodes, int K, const int* lidx, const float* lp,
+                    const int* tok, const float* u, int* out, int* path) {
+    /* No reference counterpart (cogito's EAGLE tree builder is a stub,
+     * speculative.c:244-262).  Recursive rejection with point-mass drafts:
+     * at the current node (target list lidx/lp [nodes][K]) candidate x of
+     * rank r is accepted with probability w[x] / W (u[s][r] < w[x] / W),
+     * else its mass is removed; no candidate left: draw from w / W with
+     * u[s][4] by the scan of speculative.c:66-72 (r = u * W, first running
+     * sum above r); u [depth + 1][5]; returns the accepted count. */
+    int depth = 0, dep[64], nk[64], kids[64][4];
+    memset(nk, 0, sizeof nk);
+    dep[0] = 0;
+    for (int i = 1; i < nodes; i++) {
+        dep[i] = dep[parent[i]] + 1;
+        if (dep[i] > depth) depth = dep[i];
+        kids[parent[i]][nk[parent[i]]++] = i;
+    }
+    float w[64];
+    int node = 0, n = 0;
+    for (int s = 0; s <= depth; s++) {
+        const int* li = lidx + (size_t)node * K;
+        const float* pl = lp + (size_t)node * K;
+        float W = 0.0f;
+        for (int j = 0; j < K; j++) { w[j] = pl[j]; W += w[j]; }
+        int next = -1;
+        for (int r = 0; r < nk[node]; r++) {
+            int c = kids[node][r], x = tok[c], jx = -1;
+            for (int j = 0; j < K; j++)
+                if (w[j] > 0.0f && li[j] == x) { jx = j; break; }
+            float a = jx >= 0 ? w[jx] / W : 0.0f;
+            if (u[s * 5 + r] < a) { next = c; break; }
+            if (jx >= 0) { W -= w[jx]; w[jx] = 0.0f; }
+        }
+        if (next >= 0) {
+            path[n] = next;
+            out[n++] = tok[next];
+            node = next;
+            continue;
+        }
+        if (!(W > 0.0f)) {
+            W = 0.0f;
+            for (int j = 0; j < K; j++) { w[j] = pl[j]; W += w[j]; }
+        }
+        float rr = u[s * 5 + 4] * W, cum = 0.0f;
+        int t = li[0];
+        for (int j = 0; j < K; j++) {
+            if (!(w[j] > 0.0f)) continue;
+            cum += w[j];
+            t = li[j];
+            if (rr < cum) break;
+        }
+        out[n] = t;
+        break;
+    }
+    return n;
+}

@@ -133,6 +133,9 @@ void orc_softmax_rows(const float* x, float* y, int rows, int V);
 
 /* Tree mask of src/inference/speculative.c:197-238 (chain). */
 void orc_tree_mask_chain(float* mask, int seqlen, int depth);
+void orc_topk_lists(const float* z, int V, int k, float top_p, int* lidx, float* lp);
+int orc_tree_accept(const int* parent, int nodes, int K, const int* lidx, const float* lp,
+                    const int* tok, const float* u, int* out, int* path);
 
 #ifdef __cplusplus
 }

@@ -51,6 +51,8 @@ _ORACLE_SIGS = {
     "orc_swiglu": (None, [VP, VP, VP, I]),
     "orc_softmax_rows": (None, [VP, VP, I, I]),
     "orc_tree_mask_chain": (None, [VP, I, I]),
+    "orc_topk_lists": (None, [VP, I, I, F, VP, VP]),
+    "orc_tree_accept": (I, [VP, I, I, VP, VP, VP, VP, VP, VP]),
 }
 
 _oracle = None

@@ -103,7 +103,13 @@ class OracleModel:
         self.orc.orc_rmsnorm(ptr(x), ptr(w), ptr(y), x.shape[0], x.shape[1], self.c.norm_eps)
         return y
 
-    def forward(self, tokens, n_logits=None):
+    def forward_tree(self, tokens, rel, anc, tw):
+        """Tree rows (host/tree.c, cgx_model_forward_tree): row i at cache slot
+        len + i and rotary position len + rel[i]; of the keys, the last tw are
+        visible to row i only where bit (key - (n - tw)) of anc[i] is set."""
+        return self.forward(tokens, None, (rel, anc, tw))
+
+    def forward(self, tokens, n_logits=None, tree=None):
         c, orc = self.c, self.orc
         M = len(tokens)
         pos0 = self.len
@@ -116,8 +122,15 @@ class OracleModel:
             q = np.ascontiguousarray(qkv[:, :H * hd]).reshape(M, H, hd)
             k = np.ascontiguousarray(qkv[:, H * hd:(H + Hk) * hd]).reshape(M, Hk, hd)
             v = np.ascontiguousarray(qkv[:, (H + Hk) * hd:]).reshape(M, Hk, hd)
-            orc.orc_apply_rope(ptr(q), M, H, hd, pos0, c.rope_theta)
-            orc.orc_apply_rope(ptr(k), M, Hk, hd, pos0, c.rope_theta)
+            if tree is None:
+                orc.orc_apply_rope(ptr(q), M, H, hd, pos0, c.rope_theta)
+                orc.orc_apply_rope(ptr(k), M, Hk, hd, pos0, c.rope_theta)
+            else:
+                for m in range(M):
+                    qm, km = np.ascontiguousarray(q[m]), np.ascontiguousarray(k[m])
+                    orc.orc_apply_rope(ptr(qm), 1, H, hd, pos0 + int(tree[0][m]), c.rope_theta)
+                    orc.orc_apply_rope(ptr(km), 1, Hk, hd, pos0 + int(tree[0][m]), c.rope_theta)
+                    q[m], k[m] = qm, km
             for m in range(M):
                 kt, vt = np.ascontiguousarray(k[m]), np.ascontiguousarray(v[m])
                 orc.orc_kv_append(ptr(self.kc[l]), ptr(self.vc[l]), ptr(self.ks[l]),
@@ -129,8 +142,18 @@ class OracleModel:
             orc.orc_kv_get(ptr(self.kc[l]), ptr(self.vc[l]), ptr(self.ks[l]), ptr(self.vs[l]),
                            n, Hk, hd, c.kv_group_size, ptr(K), ptr(V))
             O = np.zeros((1, M, H, hd), np.float32)
-            orc.orc_flash_fwd(ptr(q), ptr(K), ptr(V), ptr(O), None, 1, M, n, H, Hk, hd, scale,
-                              4, 0, None)
+            if tree is None:
+                orc.orc_flash_fwd(ptr(q), ptr(K), ptr(V), ptr(O), None, 1, M, n, H, Hk, hd,
+                                  scale, 4, 0, None)
+            else:
+                _, anc, tw = tree
+                mask = np.zeros((M, n), np.float32)
+                for m in range(M):
+                    for j in range(tw):
+                        if not (int(anc[m]) >> j) & 1:
+                            mask[m, n - tw + j] = -np.finfo(np.float32).max
+                orc.orc_flash_fwd(ptr(q), ptr(K), ptr(V), ptr(O), None, 1, M, n, H, Hk, hd,
+                                  scale, 3, 0, ptr(mask))
             x = x + self.matmul(O.reshape(M, H * hd), wo)
             gu = self.matmul(self.rmsnorm(x), wgu)
             g = np.ascontiguousarray(gu[:, :ff])
