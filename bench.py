@@ -406,6 +406,78 @@ def bench_e2e_batch(lib, name, tgt, drf, ctx, gamma, T, B, steps, warmup, seed=2
             "draft_shares_embed_lm_head": True}
 
 
+def bench_e2e_tree(lib, name, tgt, drf, ctx, nodes, depth, T, top_k, B, steps, warmup,
+                   seed=2027):
+    """The tree loop (cgx_tree_spec_step): B sequences in lockstep, each step
+    drafting a `nodes`-node tree level by level, verifying B x nodes rows in
+    one target forward (the GEMM path) and walking the tree.  Verified tok/s
+    = sum over sequences of (accepted + 1) / wall time."""
+    from cogito_amd.capi import CgxModelConfig, last_error
+
+    max_seq = ctx + (depth + 1) * (steps + warmup + 2) + nodes + 8
+    ct = _model_cfg(*tgt, max_seq=max_seq, max_tokens=nodes, kv_gs=tgt[4])
+    cd = _model_cfg(*drf, max_seq=max_seq, max_tokens=nodes, kv_gs=drf[4])
+    ct.max_batch = B
+    cd.max_batch = B
+    t0 = time.perf_counter()
+    mt = lib.cgx_model_new(C.byref(ct), seed, None)
+    if not mt:
+        raise RuntimeError(last_error(lib))
+    md = lib.cgx_model_new(C.byref(cd), seed + 1, mt)
+    if not md:
+        raise RuntimeError(last_error(lib))
+    if (lib.cgx_model_fill_context(mt, ctx, seed) or
+            lib.cgx_model_fill_context(md, ctx, seed + 7)):
+        raise RuntimeError(last_error(lib))
+    log(f"[bench] {name}: models built and {B} contexts of {ctx} filled in "
+        f"{time.perf_counter() - t0:.1f} s")
+    sp = lib.cgx_tree_spec_new(md, mt, nodes, depth, T, top_k, 1.0)
+    if not sp:
+        raise RuntimeError(last_error(lib))
+    D = lib.cgx_tree_spec_depth(sp)
+    root = np.full(B, 2, np.int32)
+    if lib.cgx_tree_spec_set_root(sp, root.ctypes.data):
+        raise RuntimeError(last_error(lib))
+    rng = np.random.default_rng(seed)
+    out = np.zeros((B, D + 2), np.int32)
+    n = np.zeros(B, np.int32)
+
+    def step():
+        u = rng.random((B, D + 1, 5), dtype=np.float32)
+        tot = lib.cgx_tree_spec_step(sp, u.ctypes.data, out.ctypes.data, n.ctypes.data)
+        if tot < 0:
+            raise RuntimeError(last_error(lib))
+        return tot
+    for _ in range(warmup):
+        step()
+    lib.cgx_synchronize()
+    emitted = 0
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        emitted += step() + B
+    lib.cgx_synchronize()
+    wall = time.perf_counter() - t0
+    lib.cgx_tree_spec_free(sp)
+    lib.cgx_model_free(md)
+    lib.cgx_model_free(mt)
+    tps = emitted / wall
+    acc = (emitted - steps * B) / (steps * B)
+    L, d, H, Hk, hd, ff, V = tgt
+    params = L * (d * (H + 2 * Hk) * hd + H * hd * d + 2 * d * ff + ff * d) + d * V
+    flops = 2.0 * B * nodes * params
+    log(f"[bench] {name}: {tps:.0f} verified tok/s, {wall / steps * 1e3:.3f} ms/step, "
+        f"{acc:.3f} accepted per sequence-step; target {flops / 1e12:.2f} TFLOP per verify")
+    return {"verified_tok_s": round(tps, 1), "ms_per_step": round(wall / steps * 1e3, 4),
+            "accepted_per_seq_step": round(acc, 4), "tokens_per_step": round(emitted / steps, 3),
+            "steps": steps, "tree_nodes": nodes, "tree_depth": D, "temperature": T,
+            "top_k": top_k, "ctx": ctx, "batch": B,
+            "target_flop_per_verify": flops,
+            "target_tflops_over_step": round(flops / (wall / steps) / 1e12, 2),
+            "target": dict(zip(("layers", "d", "H", "Hk", "hd", "ff", "V"), tgt)),
+            "draft": dict(zip(("layers", "d", "H", "Hk", "hd", "ff", "V"), drf)),
+            "draft_shares_embed_lm_head": True}
+
+
 def cpu_baseline_gemv(M, K, N, gs, budget_s=12.0, seed=2024):
     """cogito's cg_matmul_int4 on the host, 1 thread, bounded sample."""
     sys.path.insert(0, str(ROOT / "tests"))
@@ -468,12 +540,14 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=5,
                     help="activation rows M of the headline line (gamma+1 = 5)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--legs", default="valu,shapes,accept,attn,e2e",
+    ap.add_argument("--legs", default="valu,shapes,accept,attn,e2e,tree",
                     help="comma list of legs beside the headline GEMV: valu (the VALU "
                          "GEMV on the headline workload), shapes (7B-stack "
                          "GEMV shapes), accept (acceptance sampling C1 + V=128256 x 64 "
                          "chains), attn (INT4-KV verify attention, 7B shape), e2e "
-                         "(verified tok/s, tiny and 7B-shape stacks)")
+                         "(verified tok/s, tiny and 7B-shape stacks), batch (C4 at "
+                         "batch 8 alone; part of e2e), tree (C5: the "
+                         "EAGLE-style tree loop, 7B shape at V=128256, batch 4)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy (a plain copy kernel "
                          "of known size, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -534,9 +608,14 @@ def main() -> int:
         extra["e2e_7b_c4"] = bench_e2e(
             lib, "C4 7B-shape", (32, 4096, 32, 8, 128, 11008, 32000),
             (1, 4096, 32, 8, 128, 11008, 32000), True, 4096, 4, 1.0, 0, 1.0, 40, 5)
+    if "e2e" in legs or "batch" in legs:
         extra["e2e_7b_c4_b8"] = bench_e2e_batch(
             lib, "C4 7B-shape batch 8", (32, 4096, 32, 8, 128, 11008, 32000),
             (1, 4096, 32, 8, 128, 11008, 32000), 4096, 4, 1.0, 8, 20, 3)
+    if "tree" in legs:
+        extra["e2e_7b_c5_tree"] = bench_e2e_tree(
+            lib, "C5 7B-shape tree", (32, 4096, 32, 8, 128, 11008, 128256),
+            (1, 4096, 32, 8, 128, 11008, 128256), 2048, 64, 6, 0.7, 50, 4, 10, 2)
 
     cpu = None
     if not args.no_cpu:

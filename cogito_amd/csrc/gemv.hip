@@ -479,7 +479,7 @@ struct GemmArgs {
 };
 
 template <int RT, int NG, int PRO>
-__global__ __launch_bounds__(64 * kGemmWaves) void k_gemm_int4(GemmArgs a) {
+__global__ __launch_bounds__(64 * kGemmWaves, 2) void k_gemm_int4(GemmArgs a) {
     constexpr int BM = 16 * RT;
     constexpr int RPT = BM / 8;                 // rows prepared per thread
     __shared__ _Float16 sa[2][2][BM][kGemmRowH];
@@ -848,14 +848,20 @@ extern "C" int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int g
         cgx_set_error("gemm_int4: unsupported shape M=%d K=%d N=%d gs=%d", M, K, N, gs);
         return -1;
     }
-    const int RT = M > 64 ? 8 : M > 48 ? 4 : (M + 15) / 16;
+    // row tiles per block: up to 4 (64 rows), which keeps a wave within 256
+    // registers, so that two blocks share a CU; more rows run as more blocks
+    const int RT = M > 48 ? 4 : (M + 15) / 16;
     const int BM = 16 * RT;
     const int rowblocks = (M + BM - 1) / BM;
     const int colblocks = paired ? N / 2 / 128 : (N / 128 + 1) / 2;
     const int nchunks = K / kChunkK;
-    // two blocks per CU, splits of at least two chunks
+    // two blocks per CU, splits of at least two chunks, and partial sums
+    // (8 M bytes per column and split, written and read) at most about twice
+    // the weight bytes (K / 2 per column): at 40 rows the blocks for every CU
+    // are worth more than the partial traffic (measured), at 256 rows not
     int ksplit = (512 + colblocks * rowblocks - 1) / (colblocks * rowblocks);
     ksplit = ksplit > nchunks / 2 ? nchunks / 2 : ksplit;
+    ksplit = ksplit > K / (4 * M) ? K / (4 * M) : ksplit;
     ksplit = ksplit < 1 ? 1 : (ksplit > 16 ? 16 : ksplit);
     const int ksteps = (nchunks + ksplit - 1) / ksplit;
     ksplit = (nchunks + ksteps - 1) / ksteps;
@@ -878,12 +884,10 @@ extern "C" int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int g
     int rc;
     if (paired) {
         rc = RT == 1 ? launch_gemm<1, 2>(a, grid) : RT == 2 ? launch_gemm<2, 2>(a, grid)
-           : RT == 3 ? launch_gemm<3, 2>(a, grid) : RT == 4 ? launch_gemm<4, 2>(a, grid)
-           : launch_gemm<8, 2>(a, grid);
+           : RT == 3 ? launch_gemm<3, 2>(a, grid) : launch_gemm<4, 2>(a, grid);
     } else {
         rc = RT == 1 ? launch_gemm<1, 1>(a, grid) : RT == 2 ? launch_gemm<2, 1>(a, grid)
-           : RT == 3 ? launch_gemm<3, 1>(a, grid) : RT == 4 ? launch_gemm<4, 1>(a, grid)
-           : launch_gemm<8, 1>(a, grid);
+           : RT == 3 ? launch_gemm<3, 1>(a, grid) : launch_gemm<4, 1>(a, grid);
     }
     if (rc) return rc;
     const size_t outs = (size_t)M * (paired ? N / 2 : N);
