@@ -205,16 +205,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv_mfma(MfmaArgs a) {
             d.x[m] = m < M ? *(const float4*)(a.x + (size_t)m * a.ldx + k0)
                            : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     };
-    ARaw acur;
-    if (my_rounds > 0) load_w(wave, wcur);
-
-    for (int i = 0; i < my_rounds; i++) {
-        const int r = wave + i * kWaves;
-        // activations first: the A-prep waits for them, and loads complete in
-        // issue order, so the next round's weights stay in flight meanwhile
-        load_a(r, acur);
-        if (i + 1 < my_rounds) load_w(r + kWaves, wnxt);
-
+    auto round_body = [&](ARaw& acur, u32x4 (&wcur)[T][2]) {
         // ---- A operands of this round
         float4 xv[MP];
         float amax = 0.0f;
@@ -299,15 +290,41 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv_mfma(MfmaArgs a) {
             tot[j][2] = fmaf(acc[j][2], down, tot[j][2]);
             tot[j][3] = fmaf(acc[j][3], down, tot[j][3]);
         }
-        if (i + 1 < my_rounds) {
-#pragma unroll
-            for (int j = 0; j < T; j++) {
-                wcur[j][0] = wnxt[j][0];
-                wcur[j][1] = wnxt[j][1];
-            }
-        }
         // the next round overwrites this wave's A buffer
         __builtin_amdgcn_wave_barrier();
+    };
+    if (MP <= 8 && my_rounds == 2) {
+        // the usual case at K = 4096: both rounds' weights and activations
+        // are issued at once, so the wave waits for memory once
+        ARaw a0, a1;
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(wave, wcur);
+        load_a(wave, a0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(wave + kWaves, wnxt);
+        load_a(wave + kWaves, a1);
+        __builtin_amdgcn_sched_barrier(0);
+        round_body(a0, wcur);
+        __builtin_amdgcn_sched_barrier(0);
+        round_body(a1, wnxt);
+    } else {
+        ARaw acur;
+        if (my_rounds > 0) load_w(wave, wcur);
+        for (int i = 0; i < my_rounds; i++) {
+            const int r = wave + i * kWaves;
+            // activations first: the A-prep waits for them, and loads complete
+            // in issue order, so the next round's weights stay in flight
+            load_a(r, acur);
+            if (i + 1 < my_rounds) load_w(r + kWaves, wnxt);
+            round_body(acur, wcur);
+            if (i + 1 < my_rounds) {
+#pragma unroll
+                for (int j = 0; j < T; j++) {
+                    wcur[j][0] = wnxt[j][0];
+                    wcur[j][1] = wnxt[j][1];
+                }
+            }
+        }
     }
 
     if (PRO == kProRmsNorm) {
