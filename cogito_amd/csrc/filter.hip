@@ -301,57 +301,78 @@ __global__ __launch_bounds__(kThreads) void k_top_k(const float* __restrict__ z,
     const float* zr = z + (size_t)row * V;
     const uint32_t kfloor = order_key(kTopKFloor);
 
-    // eligible: value > -1e30 (never inserted otherwise; NaN never is)
-    int elig = 0;
-    for (int j = t; j < V; j += kThreads) {
-        float x = zr[j];
-        elig += (x > kTopKFloor);
-    }
-    const int E = block_sum_int(elig, lds);
-    const bool all = E <= k;
-
-    // radix select of the k-th largest key among eligible elements
-    uint32_t prefix = 0, pmask = 0;
-    int need = k;
-    if (!all) {
-        for (int pass = 0; pass < 4; pass++) {
-            const int shift = 24 - 8 * pass;
-            for (int i = t; i < 256; i += kThreads) hist[i] = 0;
-            __syncthreads();
-            for (int j = t; j < V; j += kThreads) {
-                float x = zr[j];
-                uint32_t key = order_key(x);
-                if (x > kTopKFloor && (key & pmask) == prefix)
-                    atomicAdd(&hist[(key >> shift) & 255], 1);
+    // The row is read in coalesced sweeps of kU values per thread, whose loads
+    // are all in flight before any is used.
+    constexpr int kU = 8;
+    auto sweep = [&](auto&& fn) {
+        for (int j0 = t; j0 < V; j0 += kThreads * kU) {
+            float xs[kU];
+#pragma unroll
+            for (int q = 0; q < kU; q++) {
+                const int j = j0 + q * kThreads;
+                xs[q] = j < V ? zr[j] : kTopKFloor;
             }
-            __syncthreads();
-            if (t == 0) {
-                int nd = need, d = 255;
-                for (; d > 0; d--) {
-                    if (nd <= hist[d]) break;
-                    nd -= hist[d];
-                }
-                s_digit = d;
-                s_need = nd;
-            }
-            __syncthreads();
-            prefix |= (uint32_t)s_digit << shift;
-            pmask |= 0xFFu << shift;
-            need = s_need;
-            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < kU; q++) fn(xs[q], j0 + q * kThreads);
         }
+    };
+
+    // radix select of the k-th largest key among eligible elements (value >
+    // -1e30: never inserted otherwise; NaN never is); the first pass also
+    // counts them
+    uint32_t prefix = 0, pmask = 0;
+    int need = k, E = 0, ties = 0;
+    bool all = false;
+    for (int pass = 0; pass < 4; pass++) {
+        const int shift = 24 - 8 * pass;
+        for (int i = t; i < 256; i += kThreads) hist[i] = 0;
+        __syncthreads();
+        int elig = 0;
+        sweep([&](float x, int) {
+            const uint32_t key = order_key(x);
+            if (x > kTopKFloor && (key & pmask) == prefix) {
+                atomicAdd(&hist[(key >> shift) & 255], 1);
+                elig++;
+            }
+        });
+        if (pass == 0) {
+            E = block_sum_int(elig, lds);
+            all = E <= k;
+            if (all) break;
+        }
+        __syncthreads();
+        if (t == 0) {
+            int nd = need, d = 255;
+            for (; d > 0; d--) {
+                if (nd <= hist[d]) break;
+                nd -= hist[d];
+            }
+            s_digit = d;
+            s_need = nd;
+            s_ncand = hist[d];          // after the last pass: the keys equal to T
+        }
+        __syncthreads();
+        prefix |= (uint32_t)s_digit << shift;
+        pmask |= 0xFFu << shift;
+        need = s_need;
+        ties = s_ncand;
+        __syncthreads();
     }
     const uint32_t T = prefix;              // key of the k-th largest
 
-    // collect: every eligible key > T, then the first `need` keys == T by index
+    // collect: every eligible key > T, then the first `need` keys == T by
+    // index.  When every key == T fits next to the others, all of them are
+    // collected and the sort by (value desc, index asc) keeps the first
+    // `need`; otherwise each thread scans its own range in index order.
+    const bool all_ties = all || (k - need) + ties <= kTopKMax;
     if (t == 0) s_ncand = 0;
     __syncthreads();
-    for (int j = t; j < V; j += kThreads) {
-        float x = zr[j];
-        uint32_t key = order_key(x);
-        if (x > kTopKFloor && (all || key > T)) cand[atomicAdd(&s_ncand, 1)] = topk_entry(key, j);
-    }
-    if (!all) {
+    sweep([&](float x, int j) {
+        const uint32_t key = order_key(x);
+        if (x > kTopKFloor && (all || key > T || (all_ties && key == T)))
+            cand[atomicAdd(&s_ncand, 1)] = topk_entry(key, j);
+    });
+    if (!all && !all_ties) {
         const int per = (V + kThreads - 1) / kThreads;
         const int lo = t * per, hi = min(V, lo + per);
         int eq = 0;
@@ -368,13 +389,16 @@ __global__ __launch_bounds__(kThreads) void k_top_k(const float* __restrict__ z,
     }
     __syncthreads();
     const int ncand = s_ncand;
+    // sort size: a power of two holding the list and every candidate
+    int spow2 = kpow2;
+    while (spow2 < ncand) spow2 <<= 1;
     // unfilled slots keep the reference's initial (-1e30, 0); sort padding last
-    for (int i = ncand + t; i < kpow2; i += kThreads)
+    for (int i = ncand + t; i < spow2; i += kThreads)
         cand[i] = i < k ? topk_entry(kfloor, 0) : 0ull;
     __syncthreads();
-    for (int kk = 2; kk <= kpow2; kk <<= 1) {
+    for (int kk = 2; kk <= spow2; kk <<= 1) {
         for (int jj = kk >> 1; jj > 0; jj >>= 1) {
-            for (int p = t; p < kpow2 / 2; p += kThreads) {
+            for (int p = t; p < spow2 / 2; p += kThreads) {
                 int i = 2 * jj * (p / jj) + (p % jj);
                 int l = i + jj;
                 unsigned long long a = cand[i], b = cand[l];
