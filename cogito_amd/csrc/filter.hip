@@ -294,10 +294,13 @@ __global__ __launch_bounds__(kThreads) void k_top_k(const float* __restrict__ z,
                                                     float* __restrict__ lp) {
     __shared__ EosShared sh;
     __shared__ unsigned long long cand[kTopKMax];
-    __shared__ int hist[256];
+    // radix passes: one histogram per wave (fewer same-address atomics), in
+    // the candidate buffer, which is filled only after the passes
+    static_assert(kWaves * 256 * sizeof(int) <= sizeof(cand), "histograms fit in cand");
+    int (*hist)[256] = reinterpret_cast<int (*)[256]>(cand);
     __shared__ int lds[kWaves];
     __shared__ int s_digit, s_need, s_ncand;
-    const int row = blockIdx.x, t = threadIdx.x;
+    const int row = blockIdx.x, t = threadIdx.x, wv = t >> 6;
     const float* zr = z + (size_t)row * V;
     const uint32_t kfloor = order_key(kTopKFloor);
 
@@ -325,13 +328,13 @@ __global__ __launch_bounds__(kThreads) void k_top_k(const float* __restrict__ z,
     bool all = false;
     for (int pass = 0; pass < 4; pass++) {
         const int shift = 24 - 8 * pass;
-        for (int i = t; i < 256; i += kThreads) hist[i] = 0;
+        for (int i = t; i < kWaves * 256; i += kThreads) (&hist[0][0])[i] = 0;
         __syncthreads();
         int elig = 0;
         sweep([&](float x, int) {
             const uint32_t key = order_key(x);
             if (x > kTopKFloor && (key & pmask) == prefix) {
-                atomicAdd(&hist[(key >> shift) & 255], 1);
+                atomicAdd(&hist[wv][(key >> shift) & 255], 1);
                 elig++;
             }
         });
@@ -341,15 +344,20 @@ __global__ __launch_bounds__(kThreads) void k_top_k(const float* __restrict__ z,
             if (all) break;
         }
         __syncthreads();
-        if (t == 0) {
-            int nd = need, d = 255;
-            for (; d > 0; d--) {
-                if (nd <= hist[d]) break;
-                nd -= hist[d];
-            }
-            s_digit = d;
-            s_need = nd;
-            s_ncand = hist[d];          // after the last pass: the keys equal to T
+        // digit of the need-th largest: thread i holds bin 255 - i; an
+        // exclusive scan from the top bin down finds the bin where the count
+        // reaches `need`
+        int h = 0;
+        if (t < 256) {
+#pragma unroll
+            for (int w = 0; w < kWaves; w++) h += hist[w][255 - t];
+        }
+        int above;
+        const int excl = block_excl_scan(h, &above, lds);
+        if (t < 256 && excl < need && need <= excl + h) {
+            s_digit = 255 - t;
+            s_need = need - excl;
+            s_ncand = h;                // after the last pass: the keys equal to T
         }
         __syncthreads();
         prefix |= (uint32_t)s_digit << shift;
