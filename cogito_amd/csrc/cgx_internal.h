@@ -70,11 +70,16 @@ int cgk_int4_repack_mfma(const uint8_t* flat, const float* scales, int K, int N,
 int cgk_int4_dequantize_mfma(const uint8_t* w, const float* scales_t, int K, int N, int gs,
                              int paired, float* out);
 /* INT4 GEMM for M >= 32 rows over layout 3 (gemv.hip): same arguments and
- * epilogues as cgk_gemv_mfma plus smax >= every |scale| of the weight. */
+ * epilogues as cgk_gemv_mfma plus smax >= every |scale| of the weight.
+ * stats_in ([M][nstat_in][2] partial max|x*nw| and sum x^2, from the
+ * producer's stats_out) replaces the row-statistics pass over x; stats_out
+ * ([M][Nout/256][2], Nout % 256 == 0) receives those of the output, with
+ * nw_next the consumer's RMSNorm weights (NULL: 1). */
 int cgk_gemm_int4_supported(int M, int K, int N, int gs, int paired);
 int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int gs, const uint8_t* w,
                   const float* scales_t, float smax, float* y, int ldy, int pro,
-                  const float* nw, float eps, int epi);
+                  const float* nw, float eps, int epi, const float* stats_in, int nstat_in,
+                  float* stats_out, const float* nw_next);
 int cgk_absmax(const float* s, size_t n, float* out_host);
 int cgk_gemv_mfma(const float* x, int ldx, int M, int K, int N, int gs, const uint8_t* w,
                   const float* scales_t, float* y, int ldy, int pro, const float* nw, float eps,

@@ -488,8 +488,11 @@ struct GemmArgs {
     const uint8_t* w;         // layout 3
     const float* scales_t;    // [N/gs][K]
     const float* nw;          // RMSNorm weights [K] or nullptr
-    const float* rowscale;    // [M] rstd * 2^E
-    const float* unscale;     // [M] 2^-E
+    const float* rowscale;    // [M] rstd * 2^E (k_gemm_rows), or
+    const float* unscale;     // [M] 2^-E       ... nullptr with stats:
+    const float* stats;       // [M][nstat][2] partial (max|x*nw|, sum x^2) of x
+    int nstat;                //   per 256 columns, written by the producer's reduction
+    float smax, eps;          // the row factors' scale bound and RMSNorm epsilon
     float* part;              // [ksplit][M][N] partial sums, logical columns
     int ksteps;               // 128-row chunks per split
     int ff;                   // SwiGLU pair: N / 2
@@ -527,13 +530,55 @@ __global__ __launch_bounds__(64 * kGemmWaves, 2) void k_gemm_int4(GemmArgs a) {
     int xrow[RPT];
     uint32_t rowmask[RPT];
     float rsc[RPT];
+    if (a.stats) {
+        // row factors from the producer's partial statistics (fixed order):
+        // the same rule as k_gemm_rows
+        // four lanes per row, each over every fourth partial (loads issued
+        // together), combined by shuffles in a fixed order
+        __shared__ float s_rsc[BM];
+        static_assert(4 * BM <= 64 * kGemmWaves, "four threads per row");
+        float A = 0.0f, S = 0.0f;
+        const int sr = threadIdx.x >> 2, sq = threadIdx.x & 3;
+        if (sr < BM) {
+            const int row = min(row0 + sr, a.M - 1);
+            const float2* st = (const float2*)(a.stats + (size_t)row * a.nstat * 2);
+#pragma unroll 4
+            for (int j = sq; j < a.nstat; j += 4) {
+                const float2 v = st[j];
+                A = fmaxf(A, v.x);
+                S += v.y;
+            }
+        }
+        A = fmaxf(A, __shfl_xor(A, 1));
+        S += __shfl_xor(S, 1);
+        A = fmaxf(A, __shfl_xor(A, 2));
+        S += __shfl_xor(S, 2);
+        if (sr < BM && sq == 0) {
+            const float rstd = PRO == kProRmsNorm ? 1.0f / sqrtf(S / (float)a.K + a.eps) : 1.0f;
+            const float bound = A * rstd * a.smax;
+            int E = 0;
+            if (bound > 0.0f && bound < __builtin_inff()) E = 14 - ilogbf(bound);
+            E = E > 100 ? 100 : (E < -100 ? -100 : E);
+            s_rsc[sr] = rstd * ldexpf(1.0f, E);
+            s_unscale[sr] = ldexpf(1.0f, -E);
+        }
+        __syncthreads();
 #pragma unroll
-    for (int i = 0; i < RPT; i++) {
-        xrow[i] = min(row0 + pr + 8 * i, a.M - 1);
-        rowmask[i] = row0 + pr + 8 * i < a.M ? ~0u : 0u;
-        rsc[i] = a.rowscale[xrow[i]];
+        for (int i = 0; i < RPT; i++) {
+            xrow[i] = min(row0 + pr + 8 * i, a.M - 1);
+            rowmask[i] = row0 + pr + 8 * i < a.M ? ~0u : 0u;
+            rsc[i] = s_rsc[pr + 8 * i];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < RPT; i++) {
+            xrow[i] = min(row0 + pr + 8 * i, a.M - 1);
+            rowmask[i] = row0 + pr + 8 * i < a.M ? ~0u : 0u;
+            rsc[i] = a.rowscale[xrow[i]];
+        }
+        if (threadIdx.x < BM)
+            s_unscale[threadIdx.x] = a.unscale[min(row0 + (int)threadIdx.x, a.M - 1)];
     }
-    if (threadIdx.x < BM) s_unscale[threadIdx.x] = a.unscale[min(row0 + (int)threadIdx.x, a.M - 1)];
     const float* nwp = PRO == kProRmsNorm ? a.nw : a.scales_t;
 
     // ---- this wave's tiles: slot ws, tiles 4 (wave & 1) + j of the slot.  A
@@ -735,24 +780,53 @@ __global__ __launch_bounds__(256) void k_gemm_rows(const float* __restrict__ x, 
     }
 }
 
-// Sum of the K splits in order, and the epilogue.
+// Sum of the K splits in order, and the epilogue.  With stats_out (output
+// width a multiple of 256: a block is 256 outputs of one row), also the
+// block's (max|y * nw_next|, sum y^2) of the stored outputs y: the next
+// GEMM's row statistics without a pass over y.
 template <int EPI>
-__global__ void k_gemm_reduce(const float* __restrict__ part, int ksplit, int M, int N,
-                              float* __restrict__ y, int ldy) {
+__global__ __launch_bounds__(256) void k_gemm_reduce(const float* __restrict__ part, int ksplit,
+                                                     int M, int N, float* __restrict__ y,
+                                                     int ldy, float* __restrict__ stats_out,
+                                                     const float* __restrict__ nw_next) {
+    __shared__ float s_a[4], s_s[4];
     const int Nout = EPI == kEpiSwiGlu ? N / 2 : N;
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t)M * Nout) return;
-    const int row = (int)(i / Nout), col = (int)(i % Nout);
+    if (!stats_out && i >= (size_t)M * Nout) return;
+    const bool live = i < (size_t)M * Nout;
+    const int row = live ? (int)(i / Nout) : 0, col = live ? (int)(i % Nout) : 0;
     const size_t mn = (size_t)M * N;
-    float v = 0.0f;
-    for (int z = 0; z < ksplit; z++) v += part[z * mn + (size_t)row * N + col];
-    float* yp = y + (size_t)row * ldy + col;
-    if (EPI == kEpiSwiGlu) {
-        float u = 0.0f;
-        for (int z = 0; z < ksplit; z++) u += part[z * mn + (size_t)row * N + Nout + col];
-        *yp = v / (1.0f + __expf(-v)) * u;
-    } else {
-        *yp = EPI == kEpiAccumulate ? *yp + v : v;
+    float out = 0.0f;
+    if (live) {
+        float v = 0.0f;
+        for (int z = 0; z < ksplit; z++) v += part[z * mn + (size_t)row * N + col];
+        float* yp = y + (size_t)row * ldy + col;
+        if (EPI == kEpiSwiGlu) {
+            float u = 0.0f;
+            for (int z = 0; z < ksplit; z++) u += part[z * mn + (size_t)row * N + Nout + col];
+            out = v / (1.0f + __expf(-v)) * u;
+        } else {
+            out = EPI == kEpiAccumulate ? *yp + v : v;
+        }
+        *yp = out;
+    }
+    if (!stats_out) return;
+    float am = live ? fabsf(out * (nw_next ? nw_next[col] : 1.0f)) : 0.0f;
+    float ss = live ? out * out : 0.0f;
+    for (int o = 32; o > 0; o >>= 1) {
+        am = fmaxf(am, __shfl_xor(am, o));
+        ss += __shfl_xor(ss, o);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        s_a[threadIdx.x >> 6] = am;
+        s_s[threadIdx.x >> 6] = ss;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0 && live) {
+        const int nblk = Nout / 256, blk = col / 256;
+        stats_out[((size_t)row * nblk + blk) * 2] =
+            fmaxf(fmaxf(s_a[0], s_a[1]), fmaxf(s_a[2], s_a[3]));
+        stats_out[((size_t)row * nblk + blk) * 2 + 1] = ((s_s[0] + s_s[1]) + s_s[2]) + s_s[3];
     }
 }
 
@@ -857,7 +931,9 @@ extern "C" int cgk_gemm_int4_supported(int M, int K, int N, int gs, int paired) 
 
 extern "C" int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int gs,
                              const uint8_t* w, const float* scales_t, float smax, float* y,
-                             int ldy, int pro, const float* nw, float eps, int epi) {
+                             int ldy, int pro, const float* nw, float eps, int epi,
+                             const float* stats_in, int nstat_in, float* stats_out,
+                             const float* nw_next) {
     const int paired = epi == kEpiSwiGlu;
     if (!cgk_gemm_int4_supported(M, K, N, gs, paired) || ldx < K || (ldx & 3) ||
         ((uintptr_t)x & 15) || (pro == kProRmsNorm && (!nw || ((uintptr_t)nw & 15))) ||
@@ -891,12 +967,21 @@ extern "C" int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int g
     a.nw = pro == kProRmsNorm ? nw : nullptr;
     a.rowscale = (const float*)ws;
     a.unscale = (const float*)ws + M;
+    a.stats = stats_in;
+    a.nstat = nstat_in;
+    a.smax = smax;
+    a.eps = eps;
     a.part = (float*)(ws + row_bytes);
     a.ksteps = ksteps;
     a.ff = N / 2;
-    hipLaunchKernelGGL(k_gemm_rows, dim3(M), dim3(256), 0, stream(), x, ldx, K, a.nw,
-                       pro == kProRmsNorm, eps, smax, (float*)ws, (float*)ws + M);
-    if (launch_check("k_gemm_rows")) return -1;
+    if (!stats_in) {
+        hipLaunchKernelGGL(k_gemm_rows, dim3(M), dim3(256), 0, stream(), x, ldx, K, a.nw,
+                           pro == kProRmsNorm, eps, smax, (float*)ws, (float*)ws + M);
+        if (launch_check("k_gemm_rows")) return -1;
+    } else if (nstat_in < 1) {
+        cgx_set_error("gemm_int4: row statistics without entries");
+        return -1;
+    }
     dim3 grid(colblocks, rowblocks, ksplit);
     int rc;
     if (paired) {
@@ -907,17 +992,22 @@ extern "C" int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int g
            : RT == 3 ? launch_gemm<3, 1>(a, grid) : launch_gemm<4, 1>(a, grid);
     }
     if (rc) return rc;
-    const size_t outs = (size_t)M * (paired ? N / 2 : N);
+    const int Nout = paired ? N / 2 : N;
+    const size_t outs = (size_t)M * Nout;
     const int blocks = (int)((outs + 255) / 256);
+    if (stats_out && Nout % 256) {
+        cgx_set_error("gemm_int4: row statistics need an output width multiple of 256");
+        return -1;
+    }
     if (epi == kEpiSwiGlu)
         hipLaunchKernelGGL(k_gemm_reduce<kEpiSwiGlu>, dim3(blocks), dim3(256), 0, stream(),
-                           a.part, ksplit, M, N, y, ldy);
+                           a.part, ksplit, M, N, y, ldy, stats_out, nw_next);
     else if (epi == kEpiAccumulate)
         hipLaunchKernelGGL(k_gemm_reduce<kEpiAccumulate>, dim3(blocks), dim3(256), 0, stream(),
-                           a.part, ksplit, M, N, y, ldy);
+                           a.part, ksplit, M, N, y, ldy, stats_out, nw_next);
     else
         hipLaunchKernelGGL(k_gemm_reduce<kEpiStore>, dim3(blocks), dim3(256), 0, stream(),
-                           a.part, ksplit, M, N, y, ldy);
+                           a.part, ksplit, M, N, y, ldy, stats_out, nw_next);
     return launch_check("k_gemm_reduce");
 }
 

@@ -54,6 +54,7 @@ struct cgx_model {
     cg_kv_cache_int4* kv;
     int* tok;
     float *x, *qkv, *q, *attn, *gu, *logits;
+    float *stats_x, *stats_g;  /* row statistics of x and of the SwiGLU output */
 };
 
 static int nqkv(const cgx_model_config* c) { return (c->n_heads + 2 * c->n_kv_heads) * c->head_dim; }
@@ -146,6 +147,8 @@ void cgx_model_free(cgx_model* m) {
     cgx_free(m->attn);
     cgx_free(m->gu);
     cgx_free(m->logits);
+    cgx_free(m->stats_x);
+    cgx_free(m->stats_g);
     free(m);
 }
 
@@ -210,7 +213,10 @@ cgx_model* cgx_model_new(const cgx_model_config* cfg, uint64_t seed, cgx_model* 
         m->attn = (float*)cgx_malloc((size_t)Mx * c->n_heads * c->head_dim * 4);
         m->gu = (float*)cgx_malloc((size_t)Mx * c->d_ff * 4);      /* SwiGLU output */
         m->logits = (float*)cgx_malloc((size_t)Mx * V * 4);
-        ok = m->kv && m->tok && m->x && m->qkv && m->q && m->attn && m->gu && m->logits;
+        m->stats_x = (float*)cgx_malloc((size_t)Mx * (d / 256 + 1) * 2 * 4);
+        m->stats_g = (float*)cgx_malloc((size_t)Mx * (c->d_ff / 256 + 1) * 2 * 4);
+        ok = m->kv && m->tok && m->x && m->qkv && m->q && m->attn && m->gu && m->logits &&
+             m->stats_x && m->stats_g;
     }
     if (ok) ok = !cgx_synchronize();
     cgx_free(tf);
@@ -276,13 +282,31 @@ static size_t kv_layer_groups(const cg_kv_cache_int4* c) {
     return (size_t)c->max_seq_len * c->n_heads * (c->head_dim / c->group_size);
 }
 
+/* Row statistics handed from one GEMM's reduction to the next GEMM (rows
+ * >= 32): [rows][width / 256][2] partial (max|y * nw|, sum y^2). */
+typedef struct {
+    const float* in;      /* statistics of this linear's input, or NULL */
+    int nin;
+    float* out;           /* statistics of its output for the next linear, or NULL */
+    const float* nw_next; /* the next linear's RMSNorm weights */
+    int produced;         /* set when `out` was written */
+} stats_t;
+
 /* One linear layer over R rows: the GEMM from 32 rows on (one pass over the
  * weight), the GEMV below (it streams the weight once per 16 rows). */
 static int linear(const lin_t* L, const float* x, int ldx, int R, float* y, int ldy, int pro,
-                  const float* nw, float eps, int epi, int gs) {
-    if (R >= 32 && cgk_gemm_int4_supported(R, L->K, L->N, gs, epi == EPI_SWIGLU))
-        return cgk_gemm_int4(x, ldx, R, L->K, L->N, gs, L->tiled, L->scales_t, L->smax, y, ldy,
-                             pro, nw, eps, epi);
+                  const float* nw, float eps, int epi, int gs, stats_t* st) {
+    if (st) st->produced = 0;
+    if (R >= 32 && cgk_gemm_int4_supported(R, L->K, L->N, gs, epi == EPI_SWIGLU)) {
+        const int nout = epi == EPI_SWIGLU ? L->N / 2 : L->N;
+        float* so = st && st->out && nout % 256 == 0 ? st->out : NULL;
+        if (cgk_gemm_int4(x, ldx, R, L->K, L->N, gs, L->tiled, L->scales_t, L->smax, y, ldy,
+                          pro, nw, eps, epi, st ? st->in : NULL, st ? st->nin : 0, so,
+                          st ? st->nw_next : NULL))
+            return -1;
+        if (so) st->produced = 1;
+        return 0;
+    }
     return cgk_gemv_mfma(x, ldx, R, L->K, L->N, gs, L->tiled, L->scales_t, y, ldy, pro, nw,
                          eps, epi);
 }
@@ -325,6 +349,7 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
     const float eps = c->norm_eps, scale = 1.0f / sqrtf((float)hd);
     if (cgk_embed(m->embed, dtok, R, d, c->vocab, m->x)) return -1;
     const size_t lb = kv_layer_bytes(kv), lg = kv_layer_groups(kv);
+    int xs_ok = 0;     /* m->stats_x holds the statistics of m->x */
     const int mask = tr ? CGK_MASK_TREE : CGK_MASK_CAUSAL_ALIGNED;
     const int batched = cgk_attn_dec_supported(hd, kv->group_size, 1, mask);
     if (tr && !batched) {
@@ -345,8 +370,9 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
         uint8_t* vc = kv->v_cache + lb * slot;
         float* ks = kv->k_scales + lg * slot;
         float* vs = kv->v_scales + lg * slot;
+        stats_t sq = {xs_ok ? m->stats_x : NULL, d / 256, NULL, NULL, 0};
         if (linear(&w[W_QKV], m->x, d, R, m->qkv, nq, PRO_RMSNORM, m->ones, eps, EPI_STORE,
-                   gs) ||
+                   gs, &sq) ||
             cgk_rope_append_batch(m->qkv, nq, B, M, H, Hk, hd, kv->group_size, pos0,
                                   tr ? tr->rel : NULL, c->rope_theta, m->q, kc, vc, ks, vs, lb,
                                   lg))
@@ -363,17 +389,29 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
                                   NULL, m->attn + (size_t)b * M * hq, NULL))
                     return -1;
         }
+        /* o -> (x) -> gate|up -> (g) -> down -> (x) -> next qkv / lm_head: each
+         * reduction leaves the row statistics its consumer needs */
+        stats_t so = {NULL, 0, m->stats_x, m->ones, 0};
         if (linear(&w[W_O], m->attn, hq, R, m->x, d, PRO_NONE, NULL, 0.0f, EPI_ACCUMULATE,
-                   gs) ||
-            linear(&w[W_GU], m->x, d, R, m->gu, ff, PRO_RMSNORM, m->ones, eps, EPI_SWIGLU, gs) ||
-            linear(&w[W_DOWN], m->gu, ff, R, m->x, d, PRO_NONE, NULL, 0.0f, EPI_ACCUMULATE, gs))
+                   gs, &so))
             return -1;
+        stats_t sg = {so.produced ? m->stats_x : NULL, d / 256, m->stats_g, NULL, 0};
+        if (linear(&w[W_GU], m->x, d, R, m->gu, ff, PRO_RMSNORM, m->ones, eps, EPI_SWIGLU, gs,
+                   &sg))
+            return -1;
+        stats_t sd = {sg.produced ? m->stats_g : NULL, ff / 256, m->stats_x, m->ones, 0};
+        if (linear(&w[W_DOWN], m->gu, ff, R, m->x, d, PRO_NONE, NULL, 0.0f, EPI_ACCUMULATE, gs,
+                   &sd))
+            return -1;
+        xs_ok = sd.produced;
     }
     float* out = logits ? logits : m->logits;
     if (!ldl) ldl = (size_t)n_logits * c->vocab;
     if (n_logits == M && ldl == (size_t)M * c->vocab) {
         /* every row, sequences in order */
-        if (linear(&m->lm, m->x, d, R, out, c->vocab, PRO_RMSNORM, m->ones, eps, EPI_STORE, gs))
+        stats_t sl = {xs_ok ? m->stats_x : NULL, d / 256, NULL, NULL, 0};
+        if (linear(&m->lm, m->x, d, R, out, c->vocab, PRO_RMSNORM, m->ones, eps, EPI_STORE, gs,
+                   &sl))
             return -1;
     } else if (n_logits == 1) {
         /* the last row of each sequence: rows M-1, 2M-1, ... */

@@ -268,7 +268,8 @@ int cgx_matmul_int4_dev_kernel(const float* x, int M, cg_tensor_quant* w,
         }
         if (kernel == 4)      /* the GEMM of the batched / tree verify (M >= 32) */
             return cgk_gemm_int4(x, info.K, M, info.K, info.N, info.group_size, w->data,
-                                 w->scales, info.smax, y, info.N, 0, NULL, 0.0f, 0);
+                                 w->scales, info.smax, y, info.N, 0, NULL, 0.0f, 0, NULL, 0,
+                                 NULL, NULL);
         return cgk_gemv_mfma(x, info.K, M, info.K, info.N, info.group_size, w->data,
                              w->scales, y, info.N, 0, NULL, 0.0f, 0);
     }
