@@ -241,16 +241,20 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv_mfma(MfmaArgs a) {
 #pragma unroll
             for (int m = 0; m < MP; m++) {
                 if (m < M) {
+                    // hi = v rounded toward zero to fp16 (packed conversion),
+                    // lo = the exact remainder rounded to fp16
                     float v0 = xv[m].x * s0, v1 = xv[m].y * s1, v2 = xv[m].z * s2,
                           v3 = xv[m].w * s3;
-                    _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1, h2 = (_Float16)v2,
-                             h3 = (_Float16)v3;
-                    _Float16 l0 = (_Float16)(v0 - (float)h0), l1 = (_Float16)(v1 - (float)h1),
-                             l2 = (_Float16)(v2 - (float)h2), l3 = (_Float16)(v3 - (float)h3);
-                    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-                    f16x4 hv = {h0, h1, h2, h3}, lv = {l0, l1, l2, l3};
-                    *(f16x4*)(abuf + ((q * 2 + 0) * MP + m) * kRowH + 4 * lane) = hv;
-                    *(f16x4*)(abuf + ((q * 2 + 1) * MP + m) * kRowH + 4 * lane) = lv;
+                    const f16x2 h01 = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(v0, v1));
+                    const f16x2 h23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(v2, v3));
+                    const f16x2 l01 = __builtin_bit_cast(
+                        f16x2, __builtin_amdgcn_cvt_pkrtz(v0 - (float)h01[0], v1 - (float)h01[1]));
+                    const f16x2 l23 = __builtin_bit_cast(
+                        f16x2, __builtin_amdgcn_cvt_pkrtz(v2 - (float)h23[0], v3 - (float)h23[1]));
+                    *(uint2*)(abuf + ((q * 2 + 0) * MP + m) * kRowH + 4 * lane) =
+                        make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
+                    *(uint2*)(abuf + ((q * 2 + 1) * MP + m) * kRowH + 4 * lane) =
+                        make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
                 }
             }
         }
