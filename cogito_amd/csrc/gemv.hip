@@ -168,6 +168,11 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv_mfma(MfmaArgs a) {
     _Float16* abuf = (_Float16*)lds + (size_t)wave * kAHalfs;
     const int mrow = (lane & 15) < M ? (lane & 15) : M - 1;    // A row this lane feeds
     const int g4 = lane >> 4;
+    // with 8 or fewer rows one MFMA takes both parts: A rows 0-7 are the hi
+    // parts of rows 0-7, A rows 8-15 their lo parts; the two halves of D are
+    // summed at the end
+    const int hl8 = (lane >> 3) & 1;
+    const int mrow8 = (lane & 7) < M ? (lane & 7) : M - 1;
 
     f32x4 tot[T];
 #pragma unroll
@@ -273,8 +278,15 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv_mfma(MfmaArgs a) {
             f16x8 ah[NG], al[NG];
 #pragma unroll
             for (int q = 0; q < NG; q++) {
-                ah[q] = *(const f16x8*)(abuf + ((q * 2 + 0) * MP + mrow) * kRowH + 32 * kb + 8 * g4);
-                al[q] = *(const f16x8*)(abuf + ((q * 2 + 1) * MP + mrow) * kRowH + 32 * kb + 8 * g4);
+                if (MP <= 8) {
+                    ah[q] = *(const f16x8*)(abuf + ((q * 2 + hl8) * MP + mrow8) * kRowH + 32 * kb +
+                                            8 * g4);
+                } else {
+                    ah[q] = *(const f16x8*)(abuf + ((q * 2 + 0) * MP + mrow) * kRowH + 32 * kb +
+                                            8 * g4);
+                    al[q] = *(const f16x8*)(abuf + ((q * 2 + 1) * MP + mrow) * kRowH + 32 * kb +
+                                            8 * g4);
+                }
             }
 #pragma unroll
             for (int j = 0; j < T; j++) {
@@ -284,7 +296,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv_mfma(MfmaArgs a) {
                 f16x8 b = nib_to_f16(word);
                 const int q = NG == 1 ? 0 : tq[j];
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], b, acc[j], 0, 0, 0);
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], b, acc[j], 0, 0, 0);
+                if (MP > 8) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], b, acc[j], 0, 0, 0);
             }
         }
 #pragma unroll
@@ -341,6 +353,14 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv_mfma(MfmaArgs a) {
     __syncthreads();                 // every wave is done with its A buffer
     // partials: red[wave][tile][row][col]; lane holds rows 4*g4 .. +3, col lane%16
     float* red = lds;
+    if (MP <= 8) {
+        // row r's hi sum (D row r, lane group g4 < 2) plus its lo sum (D row
+        // r + 8, the lane 32 above)
+#pragma unroll
+        for (int j = 0; j < T; j++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) tot[j][v] += __shfl_down(tot[j][v], 32);
+    }
 #pragma unroll
     for (int j = 0; j < T; j++)
 #pragma unroll
