@@ -120,15 +120,16 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // MP: rows padded (4, 8 or 16); T: column tiles per block; NG: scale groups
 // per block (1, or 2 for a gate|up pair).
-template <int MP, int T, int NG, int PRO, int EPI>
-__global__ __launch_bounds__(64 * kWaves) void k_gemv_mfma(MfmaArgs a) {
+// W: waves per block (8; 16 for deep K, each wave then has fewer rounds)
+template <int MP, int T, int NG, int PRO, int EPI, int W>
+__global__ __launch_bounds__(64 * W) void k_gemv_mfma(MfmaArgs a) {
     // per wave: A operands of one round, [NG][hi|lo][MP][256] halfs
     constexpr int kAHalfs = NG * 2 * MP * kRowH;
-    constexpr int kRedFloats = kWaves * T * MP * 16;
+    constexpr int kRedFloats = W * T * MP * 16;
     constexpr int kLdsFloats =
-        (kWaves * kAHalfs / 2) > kRedFloats ? (kWaves * kAHalfs / 2) : kRedFloats;
+        (W * kAHalfs / 2) > kRedFloats ? (W * kAHalfs / 2) : kRedFloats;
     __shared__ float lds[kLdsFloats];
-    __shared__ float s_ssq[kWaves][MP];
+    __shared__ float s_ssq[W][MP];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int M = a.M;
@@ -163,7 +164,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv_mfma(MfmaArgs a) {
     const int K = a.K;
     const int rounds = K / kRoundK;
     const int nchunks = K / kChunkK;
-    const int my_rounds = (rounds - wave + kWaves - 1) / kWaves;   // may be 0
+    const int my_rounds = (rounds - wave + W - 1) / W;   // may be 0
 
     _Float16* abuf = (_Float16*)lds + (size_t)wave * kAHalfs;
     const int mrow = (lane & 15) < M ? (lane & 15) : M - 1;    // A row this lane feeds
@@ -317,8 +318,8 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv_mfma(MfmaArgs a) {
         load_w(wave, wcur);
         load_a(wave, a0);
         __builtin_amdgcn_sched_barrier(0);
-        load_w(wave + kWaves, wnxt);
-        load_a(wave + kWaves, a1);
+        load_w(wave + W, wnxt);
+        load_a(wave + W, a1);
         __builtin_amdgcn_sched_barrier(0);
         round_body(a0, wcur);
         __builtin_amdgcn_sched_barrier(0);
@@ -327,11 +328,11 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv_mfma(MfmaArgs a) {
         ARaw acur;
         if (my_rounds > 0) load_w(wave, wcur);
         for (int i = 0; i < my_rounds; i++) {
-            const int r = wave + i * kWaves;
+            const int r = wave + i * W;
             // activations first: the A-prep waits for them, and loads complete
             // in issue order, so the next round's weights stay in flight
             load_a(r, acur);
-            if (i + 1 < my_rounds) load_w(r + kWaves, wnxt);
+            if (i + 1 < my_rounds) load_w(r + W, wnxt);
             round_body(acur, wcur);
             if (i + 1 < my_rounds) {
 #pragma unroll
@@ -370,18 +371,18 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv_mfma(MfmaArgs a) {
         }
     __syncthreads();
     constexpr int kOuts = T * MP * 16;
-    for (int o = threadIdx.x; o < kOuts; o += 64 * kWaves) {
+    for (int o = threadIdx.x; o < kOuts; o += 64 * W) {
         const int j = o / (MP * 16), row = (o / 16) % MP, col = o % 16;
         if (row >= M) continue;
         if (EPI == kEpiSwiGlu && (j & 1)) continue;     // the gate thread does the pair
         float v = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kWaves; w++) v += red[((w * T + j) * MP + row) * 16 + col];
+        for (int w = 0; w < W; w++) v += red[((w * T + j) * MP + row) * 16 + col];
         float rs = 1.0f;
         if (PRO == kProRmsNorm) {
             float ss = 0.0f;
 #pragma unroll
-            for (int w = 0; w < kWaves; w++) ss += s_ssq[w][row];
+            for (int w = 0; w < W; w++) ss += s_ssq[w][row];
             rs = 1.0f / sqrtf(ss / (float)a.K + a.eps);
             v *= rs;
         }
@@ -389,7 +390,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_gemv_mfma(MfmaArgs a) {
         if (EPI == kEpiSwiGlu) {
             float u = 0.0f;
 #pragma unroll
-            for (int w = 0; w < kWaves; w++) u += red[((w * T + j + 1) * MP + row) * 16 + col];
+            for (int w = 0; w < W; w++) u += red[((w * T + j + 1) * MP + row) * 16 + col];
             u *= rs;
             float act = v / (1.0f + __expf(-v)) * u;
             a.y[(size_t)row * a.ldy + lt * 16 + col] = act;
@@ -454,9 +455,9 @@ __global__ void k_dequant_mfma(const uint32_t* __restrict__ w, const float* __re
     }
 }
 
-template <int MP, int T, int NG, int PRO, int EPI>
+template <int MP, int T, int NG, int PRO, int EPI, int W = kWaves>
 int launch_t(const MfmaArgs& a, int nblocks) {
-    hipLaunchKernelGGL((k_gemv_mfma<MP, T, NG, PRO, EPI>), dim3(nblocks), dim3(64 * kWaves), 0,
+    hipLaunchKernelGGL((k_gemv_mfma<MP, T, NG, PRO, EPI, W>), dim3(nblocks), dim3(64 * W), 0,
                        stream(), a);
     return launch_check("k_gemv_mfma");
 }
@@ -468,6 +469,15 @@ int launch_mp(const MfmaArgs& a, int T) {
         if (T == 4) return launch_t<MP, 4, 2, PRO, EPI>(a, tiles / 4);
         return launch_t<MP, 2, 2, PRO, EPI>(a, tiles / 2);
     } else {
+        if constexpr (MP <= 8 && PRO == kProNone) {
+            // more than two rounds per wave of 8: 16 waves shorten the chain
+            // of memory waits (the A buffers of 16 waves fit LDS up to 8
+            // rows; with the RMSNorm prologue 128 registers would spill)
+            if (a.K / kRoundK > 2 * kWaves) {
+                if (T == 2) return launch_t<MP, 2, 1, PRO, EPI, 2 * kWaves>(a, tiles / 2);
+                if (T == 1) return launch_t<MP, 1, 1, PRO, EPI, 2 * kWaves>(a, tiles);
+            }
+        }
         if (T == 4) return launch_t<MP, 4, 1, PRO, EPI>(a, tiles / 4);
         if (T == 2) return launch_t<MP, 2, 1, PRO, EPI>(a, tiles / 2);
         return launch_t<MP, 1, 1, PRO, EPI>(a, tiles);

@@ -90,6 +90,23 @@ def test_model_forward_vs_oracle(gpu, oracle, rng):
     gpu.cgx_model_free(m)
 
 
+def test_model_forward_k_split_vs_oracle(gpu, oracle, rng):
+    # K above 4096 splits the GEMV over blocks (at most two 256-row rounds per
+    # wave): d_model 4608 splits wqkv, gate|up and lm_head (RMSNorm prologue,
+    # SwiGLU) and wo (accumulate) in two, d_ff 8448 the down projection in three
+    cfg = Cfg(n_layers=1, d_model=4608, n_heads=36, n_kv_heads=4, head_dim=128, d_ff=8448,
+              vocab=2048, group_size=128, kv_group_size=128, max_seq=64, max_tokens=8,
+              init_std=0.02)
+    m = new_model(gpu, cfg, 9)
+    om = OracleModel(oracle, cfg, 9)
+    for M in (5, 1, 8):
+        toks = rng.integers(0, cfg.vocab, M).astype(np.int32)
+        assert gpu.cgx_model_forward(m, toks.ctypes.data, M, M, None) == 0, last_error(gpu)
+        err = rel_err_rows(logits_np(gpu, m, M, cfg.vocab), om.forward(toks))
+        assert err <= TOL, (M, err)
+    gpu.cgx_model_free(m)
+
+
 @pytest.mark.parametrize("cfg", [TINY, Cfg(n_layers=1, d_model=512, n_heads=8, n_kv_heads=2,
                                             head_dim=128, d_ff=768, vocab=2048, group_size=128,
                                             kv_group_size=128, max_seq=300, max_tokens=5,
