@@ -470,10 +470,14 @@ int launch_mp(const MfmaArgs& a, int T) {
         return launch_t<MP, 2, 2, PRO, EPI>(a, tiles / 2);
     } else {
         if constexpr (MP <= 8 && PRO == kProNone) {
-            // more than two rounds per wave of 8: 16 waves shorten the chain
-            // of memory waits (the A buffers of 16 waves fit LDS up to 8
-            // rows; with the RMSNorm prologue 128 registers would spill)
-            if (a.K / kRoundK > 2 * kWaves) {
+            // 16 waves per block when a wave of 8 would have more than two
+            // 256-row rounds (a shorter chain of memory waits), or two with
+            // at most one block per CU (more waves in flight; with more
+            // blocks the larger blocks lose to the tail).  The A buffers of
+            // 16 waves fit LDS up to 8 rows; with the RMSNorm prologue 128
+            // registers would spill.
+            const int rounds = a.K / kRoundK;
+            if (rounds > 2 * kWaves || (rounds > kWaves && tiles / T <= 256)) {
                 if (T == 2) return launch_t<MP, 2, 1, PRO, EPI, 2 * kWaves>(a, tiles / 2);
                 if (T == 1) return launch_t<MP, 1, 1, PRO, EPI, 2 * kWaves>(a, tiles);
             }
