@@ -545,8 +545,8 @@ def main() -> int:
                          "GEMV on the headline workload), shapes (7B-stack "
                          "GEMV shapes), accept (acceptance sampling C1 + V=128256 x 64 "
                          "chains), attn (INT4-KV verify attention, 7B shape), e2e "
-                         "(verified tok/s, tiny and 7B-shape stacks), batch (C4 at "
-                         "batch 8 alone; part of e2e), tree (C5: the "
+                         "(verified tok/s, tiny and 7B-shape stacks), c4 (C4 at batch 1 alone; "
+                         "part of e2e), batch (C4 at batch 8 alone; part of e2e), tree (C5: the "
                          "EAGLE-style tree loop, 7B shape at V=128256, batch 4)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy (a plain copy kernel "
@@ -605,6 +605,7 @@ def main() -> int:
         extra["e2e_tiny_c3"] = bench_e2e(
             lib, "C3 tiny", (12, 768, 12, 12, 64, 3072, 32000),
             (2, 768, 12, 12, 64, 3072, 32000), False, 1024, 4, 0.8, 0, 0.9, 100, 10)
+    if "e2e" in legs or "c4" in legs:
         extra["e2e_7b_c4"] = bench_e2e(
             lib, "C4 7B-shape", (32, 4096, 32, 8, 128, 11008, 32000),
             (1, 4096, 32, 8, 128, 11008, 32000), True, 4096, 4, 1.0, 0, 1.0, 40, 5)

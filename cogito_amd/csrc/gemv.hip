@@ -118,7 +118,7 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// MP: rows padded (4, 8 or 16); T: column tiles per block; NG: scale groups
+// MP: rows padded (1, 2, 4, 5, 8 or 16); T: column tiles per block; NG: scale groups
 // per block (1, or 2 for a gate|up pair).
 // W: waves per block (8; 16 for deep K, each wave then has fewer rounds)
 template <int MP, int T, int NG, int PRO, int EPI, int W>
@@ -493,6 +493,9 @@ int launch_pe(const MfmaArgs& a, int T) {
     if (a.M == 1) return launch_mp<1, PRO, EPI>(a, T);
     if (a.M == 2) return launch_mp<2, PRO, EPI>(a, T);
     if (a.M <= 4) return launch_mp<4, PRO, EPI>(a, T);
+    // 5 rows (a chain of 4 drafts and the bonus position) keep 3 fewer rows
+    // of activations in registers than 8
+    if (a.M == 5) return launch_mp<5, PRO, EPI>(a, T);
     if constexpr (EPI == kEpiSwiGlu) {
         return launch_mp<8, PRO, EPI>(a, T);
     } else {
