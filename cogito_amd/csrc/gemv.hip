@@ -122,9 +122,9 @@ __device__ __forceinline__ float wave_sum(float v) {
 // per block (1, or 2 for a gate|up pair).
 // W: waves per block (8; 16 for deep K, each wave then has fewer rounds)
 template <int MP, int T, int NG, int PRO, int EPI, int W>
-__global__ __launch_bounds__(64 * W) void k_gemv_mfma(MfmaArgs a) {
-    // per wave: A operands of one round, [NG][hi|lo][MP][256] halfs
-    constexpr int kAHalfs = NG * 2 * MP * kRowH;
+__global__ __launch_bounds__(64 * W, (NG == 2 && T == 2 && MP <= 5) ? 4 : 1) void k_gemv_mfma(MfmaArgs a) {
+    // per wave: A operands of one round and scale group, [hi|lo][MP][256] halfs
+    constexpr int kAHalfs = 2 * MP * kRowH;
     constexpr int kRedFloats = W * T * MP * 16;
     constexpr int kLdsFloats =
         (W * kAHalfs / 2) > kRedFloats ? (W * kAHalfs / 2) : kRedFloats;
@@ -144,21 +144,15 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mfma(MfmaArgs a) {
                        : (int)blockIdx.x;
     const int L0 = sb * T;                         // first layout tile
 
-    // scale rows of the block's groups; tile j uses group slot tq[j]
+    // scale rows of the block's groups: one, or for a gate|up pair (layout
+    // tiles alternate gate / up, and T and L0 are even) the gate group in
+    // slot 0 for the even tiles and the up group in slot 1 for the odd ones
+    static_assert(NG == 1 || T % 2 == 0, "a gate|up block holds whole pairs");
     int grp[NG];
-    int tq[T];
 #pragma unroll
     for (int j = 0; j < T; j++) {
         int lt = logical_tile(L0 + j, paired, ff_tiles);
-        int g = lt * 16 / a.gs;
-        if (NG == 1) {
-            grp[0] = g;
-            tq[j] = 0;
-        } else {
-            // pairs alternate gate / up: slot 0 gate, slot 1 up
-            tq[j] = (L0 + j) & 1;
-            grp[tq[j]] = g;
-        }
+        grp[NG == 1 ? 0 : (j & 1)] = lt * 16 / a.gs;
     }
 
     const int K = a.K;
@@ -240,8 +234,15 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mfma(MfmaArgs a) {
         E = E > 100 ? 100 : (E < -100 ? -100 : E);
         const float up = ldexpf(1.0f, E);
         const float down = ldexpf(1.0f, -E);
+        f32x4 acc[T];
+#pragma unroll
+        for (int j = 0; j < T; j++) acc[j] = (f32x4)(0.0f);
+        // one scale group at a time through the wave's A buffer (a gate|up
+        // pair: the gate group for the even tiles, then the up group for the
+        // odd ones)
 #pragma unroll
         for (int q = 0; q < NG; q++) {
+            if (q > 0) __builtin_amdgcn_wave_barrier();   // group q-1's reads came first
             const float s0 = acur.s[q].x * up, s1 = acur.s[q].y * up, s2 = acur.s[q].z * up,
                         s3 = acur.s[q].w * up;
 #pragma unroll
@@ -257,47 +258,38 @@ __global__ __launch_bounds__(64 * W) void k_gemv_mfma(MfmaArgs a) {
                         f16x2, __builtin_amdgcn_cvt_pkrtz(v0 - (float)h01[0], v1 - (float)h01[1]));
                     const f16x2 l23 = __builtin_bit_cast(
                         f16x2, __builtin_amdgcn_cvt_pkrtz(v2 - (float)h23[0], v3 - (float)h23[1]));
-                    *(uint2*)(abuf + ((q * 2 + 0) * MP + m) * kRowH + 4 * lane) =
+                    *(uint2*)(abuf + (0 * MP + m) * kRowH + 4 * lane) =
                         make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
-                    *(uint2*)(abuf + ((q * 2 + 1) * MP + m) * kRowH + 4 * lane) =
+                    *(uint2*)(abuf + (1 * MP + m) * kRowH + 4 * lane) =
                         make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
                 }
             }
-        }
-        // the A buffer is private to this wave: its own LDS writes must land
-        // before its lanes read each other's rows
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_s_waitcnt(0xc07f);    // lgkmcnt(0)
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-        f32x4 acc[T];
+            // the A buffer is private to this wave: its own LDS writes must
+            // land before its lanes read each other's rows
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_s_waitcnt(0xc07f);    // lgkmcnt(0)
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-        for (int j = 0; j < T; j++) acc[j] = (f32x4)(0.0f);
-#pragma unroll
-        for (int kb = 0; kb < 8; kb++) {
-            f16x8 ah[NG], al[NG];
-#pragma unroll
-            for (int q = 0; q < NG; q++) {
+            for (int kb = 0; kb < 8; kb++) {
+                f16x8 ah, al;
                 if (MP <= 8) {
-                    ah[q] = *(const f16x8*)(abuf + ((q * 2 + hl8) * MP + mrow8) * kRowH + 32 * kb +
-                                            8 * g4);
+                    ah = *(const f16x8*)(abuf + (hl8 * MP + mrow8) * kRowH + 32 * kb + 8 * g4);
                 } else {
-                    ah[q] = *(const f16x8*)(abuf + ((q * 2 + 0) * MP + mrow) * kRowH + 32 * kb +
-                                            8 * g4);
-                    al[q] = *(const f16x8*)(abuf + ((q * 2 + 1) * MP + mrow) * kRowH + 32 * kb +
-                                            8 * g4);
+                    ah = *(const f16x8*)(abuf + (0 * MP + mrow) * kRowH + 32 * kb + 8 * g4);
+                    al = *(const f16x8*)(abuf + (1 * MP + mrow) * kRowH + 32 * kb + 8 * g4);
                 }
-            }
 #pragma unroll
-            for (int j = 0; j < T; j++) {
-                const u32x4 wv = wcur[j][kb >> 2];
-                const uint32_t word = (kb & 3) == 0 ? wv.x : (kb & 3) == 1 ? wv.y
-                                    : (kb & 3) == 2 ? wv.z : wv.w;
-                f16x8 b = nib_to_f16(word);
-                const int q = NG == 1 ? 0 : tq[j];
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[q], b, acc[j], 0, 0, 0);
-                if (MP > 8) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], b, acc[j], 0, 0, 0);
+                for (int j = 0; j < T; j++) {
+                    // T is even for a pair: tile j takes group j & 1
+                    if (NG == 2 && (j & 1) != q) continue;
+                    const u32x4 wv = wcur[j][kb >> 2];
+                    const uint32_t word = (kb & 3) == 0 ? wv.x : (kb & 3) == 1 ? wv.y
+                                        : (kb & 3) == 2 ? wv.z : wv.w;
+                    f16x8 b = nib_to_f16(word);
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, acc[j], 0, 0, 0);
+                    if (MP > 8) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, acc[j], 0, 0, 0);
+                }
             }
         }
 #pragma unroll
