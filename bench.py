@@ -39,7 +39,7 @@ MALL_BYTES = 256 * 1024 * 1024
 # HBM bytes per GEMV launch measured with rocprofv3 FETCH_SIZE + WRITE_SIZE,
 # scaled by a copy kernel of known size (profiles/int4_gemv_4096x4096.md).
 # Measured for k_gemv_mfma (layout 3); re-measure when the kernel changes.
-GEMV_TRAFFIC_BYTES = {1: 9107456, 2: 9274368, 3: 9431040, 4: 9578496, 5: 9741312}
+GEMV_TRAFFIC_BYTES = {1: 9140224, 2: 9291776, 3: 9432064, 4: 9579520, 5: 9740288}
 
 
 def log(msg: str) -> None:
