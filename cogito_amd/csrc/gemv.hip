@@ -302,9 +302,11 @@ __global__ __launch_bounds__(64 * W, (NG == 2 && T == 2 && MP <= 5) ? 4 : 1) voi
         // the next round overwrites this wave's A buffer
         __builtin_amdgcn_wave_barrier();
     };
-    if (MP <= 8 && my_rounds == 2) {
+    if (MP <= 5 && my_rounds == 2) {
         // the usual case at K = 4096: both rounds' weights and activations
-        // are issued at once, so the wave waits for memory once
+        // are issued at once, so the wave waits for memory once (up to 5
+        // rows: with 8 the second round's activations cost the registers of
+        // a second block per CU, measured slower)
         ARaw a0, a1;
         __builtin_amdgcn_sched_barrier(0);
         load_w(wave, wcur);
