@@ -545,7 +545,8 @@ def main() -> int:
                          "GEMV on the headline workload), shapes (7B-stack "
                          "GEMV shapes), accept (acceptance sampling C1 + V=128256 x 64 "
                          "chains), attn (INT4-KV verify attention, 7B shape), e2e "
-                         "(verified tok/s, tiny and 7B-shape stacks), c4 (C4 at batch 1 alone; "
+                         "(verified tok/s, tiny and 7B-shape stacks), c3 (C3 alone; part of e2e), "
+                         "c4 (C4 at batch 1 alone; "
                          "part of e2e), batch (C4 at batch 8 alone; part of e2e), tree (C5: the "
                          "EAGLE-style tree loop, 7B shape at V=128256, batch 4)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -601,7 +602,7 @@ def main() -> int:
     if "attn" in legs:
         extra["attention_7b"] = bench_attention(lib, 4096, 5, 32, 8, 128, 128, args.steps,
                                                 args.warmup)
-    if "e2e" in legs:
+    if "e2e" in legs or "c3" in legs:
         extra["e2e_tiny_c3"] = bench_e2e(
             lib, "C3 tiny", (12, 768, 12, 12, 64, 3072, 32000),
             (2, 768, 12, 12, 64, 3072, 32000), False, 1024, 4, 0.8, 0, 0.9, 100, 10)

@@ -14,7 +14,7 @@
 // lowest-index ties at it are the reference's list, which a bitonic sort in
 // LDS orders by (value desc, index asc).
 //
-// Top-p: probabilities (exact expf and ordered sum), a bitonic sort of the
+// Top-p: probabilities (exact expf and ordered sum), a radix sort of the
 // values in LDS, the exact sequential cumsum over the sorted values for the
 // cutoff and the draw, and the reference's tie order for the one tie group
 // that matters.  The selection sort's order of equal values is not stable
@@ -34,6 +34,8 @@
 #include "cgx_internal.h"
 
 #include "eos.hpp"
+
+#include <rocprim/block/block_radix_sort.hpp>
 
 namespace {
 
@@ -140,30 +142,32 @@ __global__ __launch_bounds__(kThreads) void k_probs_rows(const float* __restrict
     for (int j = threadIdx.x; j < V; j += kThreads) pr[j] = __fdiv_rn(e(j), S);
 }
 
-// Descending bitonic sort of one row of n <= kSortMax non-negative values.
+// Descending sort of one row of n <= kSortMax non-negative values (a block
+// radix sort in LDS, 32 values per thread; rows shorter than kSortMax are
+// padded with -1, which sorts last).  Only the sorted values are used: the
+// order of equal values is fixed afterwards by the tie rule.
 __global__ __launch_bounds__(kThreads) void k_sort_desc(const float* __restrict__ in, int n,
-                                                        int npow2, float* __restrict__ out) {
-    __shared__ float buf[kSortMax];
+                                                        float* __restrict__ out) {
+    constexpr int kItems = kSortMax / kThreads;
+    // 4-bit digits with the basic ranking keep the fewest values spilled
+    // (32 keys per thread under the 128 registers of a 1024-thread block)
+    using Sort = rocprim::block_radix_sort<float, kThreads, kItems, rocprim::empty_type, 1, 1, 4,
+                                           rocprim::block_radix_rank_algorithm::basic>;
+    __shared__ typename Sort::storage_type storage;
     const float* src = in + (size_t)blockIdx.x * n;
-    for (int i = threadIdx.x; i < npow2; i += kThreads) buf[i] = i < n ? src[i] : -1.0f;
-    __syncthreads();
-    for (int k = 2; k <= npow2; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int p = threadIdx.x; p < npow2 / 2; p += kThreads) {
-                int i = 2 * j * (p / j) + (p % j);
-                int l = i + j;
-                float a = buf[i], b = buf[l];
-                bool desc = (i & k) == 0;
-                if (desc ? (a < b) : (a > b)) {
-                    buf[i] = b;
-                    buf[l] = a;
-                }
-            }
-            __syncthreads();
-        }
+    float keys[kItems];
+#pragma unroll
+    for (int i = 0; i < kItems; i++) {
+        const int j = i * kThreads + (int)threadIdx.x;
+        keys[i] = j < n ? src[j] : -1.0f;
     }
+    Sort().sort_desc_to_striped(keys, storage);
     float* dst = out + (size_t)blockIdx.x * n;
-    for (int i = threadIdx.x; i < n; i += kThreads) dst[i] = buf[i];
+#pragma unroll
+    for (int i = 0; i < kItems; i++) {
+        const int j = i * kThreads + (int)threadIdx.x;
+        if (j < n) dst[j] = keys[i];
+    }
 }
 
 // The tie group {j : p[j] == v} in index order: member indices -> wi[0..m),
@@ -567,12 +571,9 @@ extern "C" int cgk_filter_rows(const float* z, int rows, int V, int top_k, float
     float* probs = (float*)w;
     float* sorted = probs + n;
     int* ws = (int*)(sorted + n);
-    int npow2 = 64;
-    while (npow2 < V) npow2 <<= 1;
     hipLaunchKernelGGL(k_probs_rows, dim3(rows), dim3(kThreads), 0, stream(), z, V, probs);
     if (launch_check("k_probs_rows")) return -1;
-    hipLaunchKernelGGL(k_sort_desc, dim3(rows), dim3(kThreads), 0, stream(), probs, V, npow2,
-                       sorted);
+    hipLaunchKernelGGL(k_sort_desc, dim3(rows), dim3(kThreads), 0, stream(), probs, V, sorted);
     if (launch_check("k_sort_desc")) return -1;
     hipLaunchKernelGGL(k_top_p_finish, dim3(rows), dim3(kThreads), 0, stream(), probs, sorted,
                        V, top_p, u, tokens, dist, ws);
