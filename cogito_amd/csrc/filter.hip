@@ -137,9 +137,14 @@ __global__ __launch_bounds__(kThreads) void k_probs_rows(const float* __restrict
     RowSrc src{z + (size_t)blockIdx.x * V};
     float m = gen_max(src, V, sh);
     ExpGen<RowSrc> e{src, m, 1.0f};
-    float S = eos_sum(e, V, sh);
+    // the exponentials are evaluated once, into the output row, and summed
+    // from there
     float* pr = probs + (size_t)blockIdx.x * V;
-    for (int j = threadIdx.x; j < V; j += kThreads) pr[j] = __fdiv_rn(e(j), S);
+    for (int j = threadIdx.x; j < V; j += kThreads) pr[j] = e(j);
+    __threadfence_block();
+    __syncthreads();
+    float S = eos_sum(RowSrc{pr}, V, sh);
+    for (int j = threadIdx.x; j < V; j += kThreads) pr[j] = __fdiv_rn(pr[j], S);
 }
 
 // Descending sort of one row of n <= kSortMax non-negative values (a block
