@@ -120,7 +120,9 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // MP: rows padded (1, 2, 4, 5, 8 or 16); T: column tiles per block; NG: scale groups
 // per block (1, or 2 for a gate|up pair).
-// W: waves per block (8; 16 for deep K, each wave then has fewer rounds)
+// W: waves per block (8; 16 for deep K, each wave then has fewer rounds).
+// The gate|up pair at up to 5 rows asks for 4 waves per SIMD (at most 128
+// VGPRs), so that two 8-wave blocks share a CU; unconstrained it takes 138.
 template <int MP, int T, int NG, int PRO, int EPI, int W>
 __global__ __launch_bounds__(64 * W, (NG == 2 && T == 2 && MP <= 5) ? 4 : 1) void k_gemv_mfma(MfmaArgs a) {
     // per wave: A operands of one round and scale group, [hi|lo][MP][256] halfs
