@@ -555,10 +555,17 @@ extern "C" int cgk_attn_dec_batch(const float* Q, const uint8_t* kc, const uint8
     const int RT = 1;
     const int chunks = (R + 16 * RT - 1) / (16 * RT);
     a.chunks = chunks;
-    // keys per split: whole block rounds, about 24 splits at most (measured
-    // at the 7B verify shape: 256-key splits beat 128 and 512); the splits
-    // follow the longest sequence, shorter ones leave their last splits empty
-    const int rounds = (nkmax + kSplitKeys * 24 - 1) / (kSplitKeys * 24);
+    // keys per split: whole block rounds; splits until the grid has about
+    // 512 blocks (two per CU), at most about 24 (measured on the 7B shape:
+    // at batch 1, 16 blocks per split, 256-key splits beat 128 and 512; at
+    // batch 8 and on the 64-node tree, where one split already has 128 and
+    // 512 blocks, fewer and longer splits won: 6.82 -> 6.49 and 18.5 -> 15.9
+    // ms/step against the fixed 24); the splits follow the longest sequence,
+    // shorter ones leave their last splits empty
+    const int nrb = Hk * B * (((H / Hk) * Nq + 15) / 16);    // blocks of one split
+    int maxsp = 512 / nrb;
+    maxsp = maxsp < 1 ? 1 : (maxsp > 24 ? 24 : maxsp);
+    const int rounds = (nkmax + kSplitKeys * maxsp - 1) / (kSplitKeys * maxsp);
     int kps = kSplitKeys * (rounds > 1 ? rounds : 1);
     while ((nkmax + kps - 1) / kps > 128) kps += kSplitKeys;
     const int splits = (nkmax + kps - 1) / kps;
