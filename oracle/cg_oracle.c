@@ -15,6 +15,17 @@
 #include <stdlib.h>
 #include <string.h>
 
+/* Planted mistakes for the tests that prove the law checks have power
+ * (tests/test_verify_law.py builds one library per value; the product
+ * oracle is built with 0):
+ *   1  the correction draw reuses the accept test's uniform u[i];
+ *   2  the acceptance ratio takes p and q swapped;
+ *   3  top-p keeps the cut probabilities without renormalising them;
+ *   4  the bonus draw reuses the last accept test's uniform u[gamma-1]. */
+#ifndef ORC_MUTANT
+#define ORC_MUTANT 0
+#endif
+
 /* ---------------------------------------------------------------- A1, A2 */
 
 uint32_t orc_lcg_next_state(uint32_t state) {
@@ -215,6 +226,9 @@ int orc_filtered_dist(const float* logits, int V, float T, int top_k,
         int keep = top_k;
         float mass = 1.0f;
         if (up) keep = list_cutoff(pr, top_k, top_p, &mass);
+#if ORC_MUTANT == 3
+        mass = 1.0f;
+#endif
         for (int j = 0; j < keep; j++) {
             float v = up ? pr[j] / mass : pr[j];
             if (v != 0.0f) { dist[idx[j]] = v; nz++; }
@@ -225,6 +239,9 @@ int orc_filtered_dist(const float* logits, int V, float T, int top_k,
         int* si = (int*)malloc((size_t)V * sizeof(int));
         float mass;
         int keep = orc_top_p_sorted(z, V, top_p, sp, si, &mass);
+#if ORC_MUTANT == 3
+        mass = 1.0f;
+#endif
         for (int j = 0; j < keep; j++) {
             float v = sp[j] / mass;
             if (v != 0.0f) { dist[si[j]] = v; nz++; }
@@ -278,24 +295,51 @@ int orc_verify_chain(const float* target_logits, const float* draft_logits,
         orc_filtered_dist(target_logits + (size_t)i * V, V, T, top_k, top_p, p);
         orc_filtered_dist(draft_logits + (size_t)i * V, V, T, top_k, top_p, q);
         int x = draft_tokens[i];
+#if ORC_MUTANT == 2
+        float a = orc_acceptance_prob(p[x], q[x]);
+#else
         float a = orc_acceptance_prob(q[x], p[x]);
+#endif
         if (accept_prob) accept_prob[i] = a;
         if (n >= 0) continue;              /* decisions stop at the first reject */
         if (u[i] < a) {
             out_tokens[i] = x;
         } else {
+#if ORC_MUTANT == 1
+            out_tokens[i] = orc_sample_corrected(q, p, V, u[i]);
+#else
             out_tokens[i] = orc_sample_corrected(q, p, V, u[i + 1]);
+#endif
             n = i;
         }
     }
     if (n < 0) {
         n = gamma;
+#if ORC_MUTANT == 4
+        float ub = u[gamma - 1];
+#else
+        float ub = u[gamma];
+#endif
         out_tokens[gamma] = orc_sample_filtered(
-            target_logits + (size_t)gamma * V, V, T, top_k, top_p, u[gamma]);
+            target_logits + (size_t)gamma * V, V, T, top_k, top_p, ub);
     }
     free(p);
     free(q);
     return n;
+}
+
+void orc_verify_chain_many(const float* target_logits, const float* draft_logits,
+                           const int* draft_tokens, const float* u, int N, int gamma,
+                           int V, float T, int top_k, float top_p, int* out_tokens,
+                           int* n_accepted) {
+    /* N independent calls of orc_verify_chain on the same logits: draw set k
+     * is draft_tokens[k][gamma] and u[k][gamma + 1].  A loop only, so that
+     * the law tests can afford 10^5 draws per case. */
+    for (int k = 0; k < N; k++)
+        n_accepted[k] = orc_verify_chain(target_logits, draft_logits,
+                                         draft_tokens + (size_t)k * gamma,
+                                         u + (size_t)k * (gamma + 1), gamma, V, T, top_k,
+                                         top_p, out_tokens + (size_t)k * (gamma + 1), NULL);
 }
 
 /* ------------------------------------------------------------ A9 .. A12 */

@@ -12,9 +12,12 @@
  * Pinning (see tests/): each function is checked against the compiled
  * reference (oracle/_ref, where /root/reference is present), against the
  * committed golden fixtures made from it (tests/golden/), and against closed
- * forms.  Functions that go beyond the reference (the verify composition,
- * the corrected KV cache, the aligned causal mask) are composed from pinned
- * primitives and say so below.
+ * forms.  Functions that go beyond the reference are pinned by what the
+ * mathematics fixes: the verify composition and the filtered distribution by
+ * the losslessness of speculative sampling and a float64 recomputation
+ * (tests/test_verify_law.py, with planted mistakes that the checks catch),
+ * the tree walk likewise (tests/test_tree_oracle.py); the corrected KV cache
+ * and the aligned causal mask by closed forms.
  */
 #ifndef CG_ORACLE_H
 #define CG_ORACLE_H
@@ -80,6 +83,14 @@ int orc_verify_chain(const float* target_logits, const float* draft_logits,
                      const int* draft_tokens, const float* u, int gamma, int V,
                      float T, int top_k, float top_p,
                      int* out_tokens, float* accept_prob);
+
+/* orc_verify_chain over N draw sets on the same logits (a plain loop, for
+ * the law tests): draft_tokens [N][gamma], u [N][gamma+1], out_tokens
+ * [N][gamma+1], n_accepted [N]. */
+void orc_verify_chain_many(const float* target_logits, const float* draft_logits,
+                           const int* draft_tokens, const float* u, int N, int gamma,
+                           int V, float T, int top_k, float top_p, int* out_tokens,
+                           int* n_accepted);
 
 /* A9-A12: include/cg_quantize.h:155-175, src/quantize/int4.c:10-114. */
 void orc_quantize_int4(const float* x, int n, int group_size,

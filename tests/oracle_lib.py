@@ -35,6 +35,7 @@ _ORACLE_SIGS = {
     "orc_filtered_dist": (I, [VP, I, F, I, F, VP]),
     "orc_sample_filtered": (I, [VP, I, F, I, F, F]),
     "orc_verify_chain": (I, [VP, VP, VP, VP, I, I, F, I, F, VP, VP]),
+    "orc_verify_chain_many": (None, [VP, VP, VP, VP, I, I, I, F, I, F, VP, VP]),
     "orc_quantize_int4": (None, [VP, I, I, VP, VP]),
     "orc_dequantize_int4": (None, [VP, VP, I, I, VP]),
     "orc_matmul_int4": (None, [VP, I, I, VP, VP, I, I, VP]),
@@ -59,17 +60,26 @@ _oracle = None
 _ref = None
 
 
+def _open_oracle(path: Path) -> C.CDLL:
+    if not path.exists():
+        raise RuntimeError(f"{path} missing: run `make -C oracle`")
+    lib = C.CDLL(str(path), mode=C.RTLD_LOCAL)
+    for name, (res, args) in _ORACLE_SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = res, args
+    return lib
+
+
 def load_oracle() -> C.CDLL:
     global _oracle
     if _oracle is None:
-        if not ORACLE_SO.exists():
-            raise RuntimeError(f"{ORACLE_SO} missing: run `make -C oracle`")
-        lib = C.CDLL(str(ORACLE_SO), mode=C.RTLD_LOCAL)
-        for name, (res, args) in _ORACLE_SIGS.items():
-            fn = getattr(lib, name)
-            fn.restype, fn.argtypes = res, args
-        _oracle = lib
+        _oracle = _open_oracle(ORACLE_SO)
     return _oracle
+
+
+def load_oracle_mutant(n: int) -> C.CDLL:
+    """The oracle built with planted mistake n (ORC_MUTANT in cg_oracle.c)."""
+    return _open_oracle(ORACLE_SO.with_name(f"liboracle_mut{n}.so"))
 
 
 class RefTensor(C.Structure):
