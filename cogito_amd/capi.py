@@ -245,6 +245,8 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_sample_top_p_u": (I, [VP, I, F, F]),
     "cgx_sample_corrected_u": (I, [VP, VP, I, F]),
     "cgx_filtered_dist": (I, [VP, I, F, I, F, VP]),
+    "cgx_last_verify_token": (I, []),
+    "cgx_tree_attention_mask_parents": (PT, [VP, I, I]),
     "cgx_exact_expf_dev": (I, [VP, VP, I]),
     "cgx_ordered_sum_dev": (I, [VP, I, VP]),
     "cgx_exp_fast_maxerr_dev": (I, [F, F, VP]),

@@ -118,6 +118,12 @@ int cgk_verify_chain(const float* target, const float* draft, const int* tokens,
 int cgk_verify_chain_dist(const float* p, const float* q, const int* tokens, const float* u,
                           int batch, int gamma, int V, const int* bonus, float* accept_prob,
                           int* correction, int* out_tokens, int* n_accepted);
+/* One token from a device logits row with the verify filters (host/sampling.c):
+ * draw at du (device), the same value uh on the host; z: V-float workspace. */
+int cgx_sample_row_dev(const float* row, int V, float T, int top_k, float top_p,
+                       const float* du, float uh, float* z, int* out);
+/* The global LCG of the drop-in samplers (host/speculative.c). */
+float cgx_lcg_draw(void);
 /* z = x / T elementwise. */
 int cgk_scale(const float* x, float* z, size_t n, float T);
 /* Top-k (0 < top_k < V) or top-p over rows of z [rows][V]: a token per row
@@ -173,6 +179,15 @@ typedef struct {
 } cgx_tree_rows;
 int cgx_model_forward_tree(cgx_model* m, const int* tokens, int M, const cgx_tree_rows* tr,
                            float* logits, size_t ldl);
+/* The same for sequence 0 only (tokens [M]; every row's logits, or none). */
+int cgx_model_forward_tree1(cgx_model* m, const int* tokens, int M, const cgx_tree_rows* tr,
+                            float* logits);
+/* The model behind a void* handle, or NULL when p is no live model. */
+cgx_model* cgx_model_from_handle(const void* p);
+/* Changes with every forward, truncation, context fill or compaction. */
+uint64_t cgx_model_epoch(const cgx_model* m);
+/* The driver (host/driver.c) drops what it knows about a freed model. */
+void cgx_driver_forget_model(const cgx_model* m);
 
 /* Static draft tree (tree.hip, host/tree.c): node 0 is the verified root;
  * nodes are in breadth-first order; kids[i][0..nkids[i]) the children of

@@ -43,6 +43,7 @@ typedef struct {
 
 struct cgx_model {
     cgx_model_config c;
+    uint64_t epoch;          /* bumped by every change of the cached positions */
     int nb;                  /* sequences (max_batch, at least 1) */
     int len[CGX_MAX_BATCH];  /* KV length of each sequence */
     uint64_t seed;
@@ -127,8 +128,44 @@ static int check_config(const cgx_model_config* c) {
     return 0;
 }
 
+/* ------------------------------------------------------ live handles */
+/* The reference's decoder holds its models as void* (cg_speculative.h:33-34);
+ * the driver accepts a pointer as a model only when it is a live handle. */
+static cgx_model** g_live;
+static int g_nlive, g_cap_live;
+
+static int live_add(cgx_model* m) {
+    if (g_nlive == g_cap_live) {
+        int cap = g_cap_live ? 2 * g_cap_live : 16;
+        cgx_model** p = (cgx_model**)realloc(g_live, (size_t)cap * sizeof(*p));
+        if (!p) return -1;
+        g_live = p;
+        g_cap_live = cap;
+    }
+    g_live[g_nlive++] = m;
+    return 0;
+}
+
+static void live_remove(const cgx_model* m) {
+    for (int i = 0; i < g_nlive; i++)
+        if (g_live[i] == m) {
+            g_live[i] = g_live[--g_nlive];
+            return;
+        }
+}
+
+cgx_model* cgx_model_from_handle(const void* p) {
+    for (int i = 0; p && i < g_nlive; i++)
+        if (g_live[i] == p) return g_live[i];
+    return NULL;
+}
+
+uint64_t cgx_model_epoch(const cgx_model* m) { return m ? m->epoch : 0; }
+
 void cgx_model_free(cgx_model* m) {
     if (!m) return;
+    live_remove(m);
+    cgx_driver_forget_model(m);
     if (m->layers) {
         for (int l = 0; l < m->c.n_layers; l++)
             for (int w = 0; w < 4; w++) free_lin(&m->layers[l].w[w]);
@@ -222,6 +259,10 @@ cgx_model* cgx_model_new(const cgx_model_config* cfg, uint64_t seed, cgx_model* 
     cgx_free(tf);
     cgx_free(tq);
     cgx_free(ts);
+    if (ok && live_add(m)) {
+        cgx_set_error("cgx_model_new: out of memory");
+        ok = 0;
+    }
     if (!ok) {
         cgx_model_free(m);
         return NULL;
@@ -261,6 +302,7 @@ int cgx_model_truncate_seq(cgx_model* m, int seq, int len) {
     }
     m->len[seq] = len;
     if (seq == 0) m->kv->current_len = len;
+    m->epoch++;
     return 0;
 }
 
@@ -271,6 +313,7 @@ int cgx_model_truncate(cgx_model* m, int len) {
     }
     if (cgx_kv_cache_int4_truncate(m->kv, len)) return -1;
     m->len[0] = len;
+    m->epoch++;
     return 0;
 }
 
@@ -428,6 +471,7 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
     }
     for (int b = 0; b < B; b++) m->len[b] = pos0[b] + M;
     kv->current_len = m->len[0];
+    m->epoch++;
     return 0;
 }
 
@@ -469,6 +513,15 @@ int cgx_model_forward_tree(cgx_model* m, const int* tokens, int M, const cgx_tre
     return forward_rows(m, m->nb, tokens, M, logits ? M : 0, logits, ldl, tr);
 }
 
+int cgx_model_forward_tree1(cgx_model* m, const int* tokens, int M, const cgx_tree_rows* tr,
+                            float* logits) {
+    if (!m || !tr) {
+        cgx_set_error("cgx_model_forward_tree1: NULL argument");
+        return -1;
+    }
+    return forward_rows(m, 1, tokens, M, logits ? M : 0, logits, 0, tr);
+}
+
 int cgx_model_forward_tree_rows(cgx_model* m, const int* tokens, int M, const int* rel,
                                 const unsigned long long* anc, int tw, float* logits) {
     if (!m || !rel || !anc || M < 1 || M > 64) {
@@ -491,6 +544,7 @@ int cgx_model_compact_tree(cgx_model* m, const cgx_tree_shape* t, const int* len
         cgx_set_error("cgx_model_compact_tree: invalid argument");
         return -1;
     }
+    m->epoch++;
     cg_kv_cache_int4* kv = m->kv;
     const int B = m->nb;
     for (int b = 0; b < B; b++)
@@ -515,6 +569,7 @@ int cgx_model_fill_context(cgx_model* m, int len, uint64_t seed) {
         return -1;
     }
     cg_kv_cache_int4* kv = m->kv;
+    m->epoch++;
     if (!len) {
         for (int b = 0; b < m->nb; b++) m->len[b] = 0;
         return cgx_kv_cache_int4_set_len(kv, 0);

@@ -34,6 +34,22 @@ static int read_token(const int* dev) {
     return tok;
 }
 
+/* One token from a device logits row with the verify filters (D5): the
+ * reference sampler of that filter (A3 / A4 / A5, or the kept-list scan when
+ * both filters are on) over z = row / T.  The draw is at du (device); uh is
+ * the same value on the host, for the single-block fallback.  z is a V-float
+ * device workspace; out a device int. */
+int cgx_sample_row_dev(const float* row, int V, float T, int top_k, float top_p,
+                       const float* du, float uh, float* z, int* out) {
+    if (!uses_filters(V, top_k, top_p)) {
+        if (cgk_verify_pipe_supported(1, 0, V, T))
+            return cgk_sample_temperature_pipe(row, 1, V, T, du, out, (size_t)V);
+        return cgk_sample_temperature(row, V, T, uh, out);
+    }
+    if (cgk_scale(row, z, (size_t)V, T)) return -1;
+    return cgk_filter_rows(z, 1, V, top_k, top_p, du, out, NULL);
+}
+
 /* ------------------------------------------------ explicit-uniform forms */
 
 int cgx_sample_temperature_u(const float* logits, int V, float T, float u) {

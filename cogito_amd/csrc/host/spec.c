@@ -23,7 +23,6 @@ struct cgx_spec {
     float T;
     int top_k;
     float top_p;
-    int filtered;
     int* d_tokens;        /* [gamma + 1]: last, d_1 .. d_gamma */
     int* d_pending;       /* [2]: draft inputs not yet in the draft cache */
     float* d_draft_logits;
@@ -74,7 +73,6 @@ cgx_spec* cgx_spec_new(cgx_model* draft, cgx_model* target, int gamma, float tem
     s->T = temperature;
     s->top_k = top_k;
     s->top_p = top_p;
-    s->filtered = (top_k > 0 && top_k < s->V) || top_p < 1.0f;
     size_t V = (size_t)s->V;
     s->d_tokens = (int*)cgx_malloc((size_t)(gamma + 1) * 4);
     s->d_pending = (int*)cgx_malloc(2 * 4);
@@ -141,16 +139,8 @@ int cgx_spec_prefill(cgx_spec* s, const int* prompt, int n) {
 
 /* Draft token i + 1 from the draft logits row i, written to d_tokens[i + 1]. */
 static int draft_sample(cgx_spec* s, int i, float u_host) {
-    const float* row = s->d_draft_logits + (size_t)i * s->V;
-    int* out = s->d_tokens + i + 1;
-    if (!s->filtered) {
-        if (cgk_verify_pipe_supported(1, 0, s->V, s->T))
-            return cgk_sample_temperature_pipe(row, 1, s->V, s->T, s->d_u + i, out,
-                                               (size_t)s->V);
-        return cgk_sample_temperature(row, s->V, s->T, u_host, out);
-    }
-    if (cgk_scale(row, s->d_z, (size_t)s->V, s->T)) return -1;
-    return cgk_filter_rows(s->d_z, 1, s->V, s->top_k, s->top_p, s->d_u + i, out, NULL);
+    return cgx_sample_row_dev(s->d_draft_logits + (size_t)i * s->V, s->V, s->T, s->top_k,
+                              s->top_p, s->d_u + i, u_host, s->d_z, s->d_tokens + i + 1);
 }
 
 int cgx_spec_step(cgx_spec* s, const float* u_draft, const float* u_verify, int* out_tokens) {

@@ -73,44 +73,22 @@ cg_token_tree* cg_token_tree_new(int depth) {
 }
 
 void cg_token_tree_free(cg_token_tree* t) {
+    /* reference speculative.c:22-30: branch_points is not the tree's */
     if (!t) return;
     free(t->tokens);
     free(t->draft_probs);
     free(t->target_probs);
     free(t->accepted);
-    free(t->branch_points);
     cg_tensor_free(t->hidden_states);
     free(t);
 }
 
 void cg_token_tree_add_token(cg_token_tree* t, int token, float* probs) {
-    /* The reference body is empty (speculative.c:184-187).  Here a token is
-     * appended as the child of the last node (chain growth); `probs`, when
-     * given, is stored as that node's draft row only if the tree already
-     * owns a draft_probs buffer. */
+    /* reference speculative.c:184-187: the body is empty (the tree is a
+     * fixed-depth chain filled through tokens[]) */
+    (void)t;
+    (void)token;
     (void)probs;
-    if (!t) return;
-    int n = t->depth + 1;
-    int* tok = (int*)realloc(t->tokens, (size_t)n * sizeof(int));
-    bool* acc = (bool*)realloc(t->accepted, (size_t)n * sizeof(bool));
-    if (!tok || !acc) {
-        if (tok) t->tokens = tok;
-        if (acc) t->accepted = acc;
-        cgx_set_error("cg_token_tree_add_token: out of memory");
-        return;
-    }
-    t->tokens = tok;
-    t->accepted = acc;
-    tok[n - 1] = token;
-    acc[n - 1] = false;
-    if (t->branch_points) {
-        int* bp = (int*)realloc(t->branch_points, (size_t)n * sizeof(int));
-        if (bp) {
-            t->branch_points = bp;
-            bp[n - 1] = n - 2;
-        }
-    }
-    t->depth = n;
 }
 
 cg_tensor* cg_token_tree_to_tensor(cg_token_tree* t) {
@@ -126,38 +104,55 @@ cg_tensor* cg_token_tree_to_tensor(cg_token_tree* t) {
     return out;
 }
 
-cg_tensor* cg_tree_attention_mask(cg_token_tree* t, int seqlen) {
-    /* reference speculative.c:197-238: [1,1,S,S] additive mask (0 / -1e9),
-     * causal prefix, nodes see the prefix and their ancestors.  The
-     * reference assumes a chain; with branch_points (parent per node) the
-     * ancestor set follows the tree. */
-    if (!t || seqlen < 0) {
-        cgx_set_error("cg_tree_attention_mask: invalid argument");
+/* [1,1,S,S] additive mask (0 / -1e9), S = seqlen + nodes: causal prefix;
+ * node i sees the prefix and the nodes j with anc(i, j). */
+static cg_tensor* tree_mask(int seqlen, int nodes, const int* parents, const char* who) {
+    if (seqlen < 0 || nodes < 0 || seqlen + nodes <= 0) {
+        cgx_set_error("%s: empty mask", who);
         return NULL;
     }
-    int n = t->depth, size = seqlen + n;
-    if (size <= 0) {
-        cgx_set_error("cg_tree_attention_mask: empty mask");
-        return NULL;
-    }
+    const int size = seqlen + nodes;
     int shape[4] = {1, 1, size, size};
     cg_tensor* m = cg_tensor_new(shape, 4, false);
     if (!m) return NULL;
     for (int i = 0; i < m->size; i++) m->data[i] = -1e9f;
     for (int i = 0; i < seqlen; i++)
         for (int j = 0; j <= i; j++) m->data[(size_t)i * size + j] = 0.0f;
-    for (int i = 0; i < n; i++) {
+    for (int i = 0; i < nodes; i++) {
         size_t r = (size_t)(seqlen + i) * size;
         for (int j = 0; j < seqlen; j++) m->data[r + j] = 0.0f;
-        if (t->branch_points) {
-            for (int a = i, guard = 0; a >= 0 && a < n && guard <= n;
-                 a = t->branch_points[a], guard++)
-                m->data[r + seqlen + a] = 0.0f;
+        if (parents) {
+            for (int a = i; a >= 0; a = parents[a]) m->data[r + seqlen + a] = 0.0f;
         } else {
             for (int j = 0; j <= i; j++) m->data[r + seqlen + j] = 0.0f;
         }
     }
     return m;
+}
+
+cg_tensor* cg_tree_attention_mask(cg_token_tree* t, int seqlen) {
+    /* reference speculative.c:197-238: the nodes form a chain (the reference
+     * reads no parent links); tree parents go through
+     * cgx_tree_attention_mask_parents */
+    if (!t) {
+        cgx_set_error("cg_tree_attention_mask: NULL tree");
+        return NULL;
+    }
+    return tree_mask(seqlen, t->depth, NULL, "cg_tree_attention_mask");
+}
+
+cg_tensor* cgx_tree_attention_mask_parents(const int* parents, int nodes, int seqlen) {
+    if (!parents || nodes < 1) {
+        cgx_set_error("cgx_tree_attention_mask_parents: parents of at least one node required");
+        return NULL;
+    }
+    for (int i = 0; i < nodes; i++)
+        if (parents[i] < -1 || parents[i] >= i) {
+            cgx_set_error("cgx_tree_attention_mask_parents: node %d has parent %d (need -1 <= "
+                          "parent < node)", i, parents[i]);
+            return NULL;
+        }
+    return tree_mask(seqlen, nodes, parents, "cgx_tree_attention_mask_parents");
 }
 
 /* ---------------------------------------------------------------- EAGLE */
@@ -169,7 +164,7 @@ cg_eagle_draft* cg_eagle_draft_new(void* base_draft) {
 }
 
 void cg_eagle_draft_free(cg_eagle_draft* e) {
-    if (!e) return;
-    free(e->feature_cache);
+    /* reference speculative.c:264-267: the struct only (feature_cache is
+     * never allocated by the library) */
     free(e);
 }

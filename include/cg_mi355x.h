@@ -112,6 +112,15 @@ int cgx_sample_top_p_u(const float* logits, int V, float top_p, float u);
 int cgx_sample_corrected_u(const float* draft_probs, const float* target_probs,
                            int V, float u);
 
+/* The token that followed the accepted drafts (correction or bonus) in the
+ * last cg_target_verify / cg_speculative_step; -1 before any. */
+int cgx_last_verify_token(void);
+
+/* cg_tree_attention_mask for a tree: nodes[0..nodes) with parents[i] < i
+ * (-1: child of the prefix); node i sees the prefix, itself and its
+ * ancestors.  New host tensor [1, 1, seqlen + nodes, seqlen + nodes]. */
+cg_tensor* cgx_tree_attention_mask_parents(const int* parents, int nodes, int seqlen);
+
 /* Probability vector the verify composition uses for one row (host or
  * device logits; dist_out host or device, V floats). */
 int cgx_filtered_dist(const float* logits, int V, float T, int top_k,

@@ -24,11 +24,14 @@
 extern "C" {
 #endif
 
-/* Draft chain / tree under verification (reference :15-25).
- * tokens[depth]; draft_probs/target_probs [depth, vocab] when filled;
- * accepted[depth].  In this library `branch_points`, when non-NULL, holds a
- * parent index per node (-1 = child of the verified prefix), which turns the
- * chain into a tree for cg_tree_attention_mask / tree verification. */
+/* Draft chain under verification (reference :15-25).  tokens[depth],
+ * accepted[depth].  In this library draft_probs holds the draft LOGITS
+ * [depth][vocab] and target_probs the target LOGITS [depth + 1][vocab] (row
+ * depth scores the token after the last draft); both are host buffers owned
+ * by the tree (cg_token_tree_free frees them).  branch_points / num_branches
+ * are the caller's, as in the reference: the library neither reads nor frees
+ * them.  Trees with parent links go through cgx_tree_attention_mask_parents
+ * and the cgx_tree_spec_* loop (cg_mi355x.h). */
 typedef struct {
     int* tokens;
     float* draft_probs;
@@ -62,9 +65,22 @@ cg_speculative_decoder* cg_speculative_decoder_new(
     void* draft_model, void* target_model, int gamma
 );
 
-/* Generation driver.  draft_model/target_model must be cgx_model handles
- * (cg_mi355x.h) for these to run; otherwise they set the last error and
- * return NULL / -1. */
+/* Generation driver (declared only in the reference).  draft_model and
+ * target_model must be cgx_model handles (cg_mi355x.h); otherwise the calls
+ * set the last error and return NULL / -1.
+ *
+ * input_ids holds the sequence so far as float token ids ([1, n] or [n],
+ * host or device).  Each model's KV cache is cut to the longest prefix it
+ * shares with input_ids and the rest is run, so any input_ids is served and
+ * a growing sequence reuses the cache.  Draws come from the global LCG in the
+ * order of a sequential implementation: one per drafted token (the
+ * decoder's temperature / top_k / top_p filter, as cg_sample_temperature /
+ * cg_sample_top_k / cg_sample_top_p draw), then one per accept test and one
+ * for the token after the accepted drafts.
+ *
+ * cg_speculative_generate sets decoder->temperature / top_p from its
+ * arguments and steps until max_new_tokens are out (or a cache is full);
+ * returns a new host tensor [1, n + generated] of float token ids. */
 cg_tensor* cg_speculative_generate(
     cg_speculative_decoder* decoder,
     cg_tensor* input_ids,
@@ -73,25 +89,33 @@ cg_tensor* cg_speculative_generate(
     float top_p
 );
 
+/* One step with a chain of tree->depth drafts: fills tree->tokens and the
+ * tree's draft / target logits, then verifies as cg_target_verify. */
 int cg_speculative_step(
     cg_speculative_decoder* decoder,
     cg_tensor* input_ids,
     cg_token_tree* tree
 );
 
+/* A new tree of decoder->gamma drafted tokens after input_ids, with their
+ * draft logits in draft_probs. */
 cg_token_tree* cg_draft_generate(
     cg_speculative_decoder* decoder,
     cg_tensor* input_ids
 );
 
-/* Verification of a filled token tree (chain when branch_points == NULL).
- * With tree->target_probs [depth+1, vocab] holding TARGET LOGITS and
- * tree->draft_probs [depth, vocab] holding DRAFT LOGITS (either host or
- * device memory), runs the acceptance kernel with the decoder's temperature /
- * top_k / top_p, writes tree->accepted[], updates the decoder statistics, and
- * returns the number of accepted draft tokens n (0..depth).  The token that
- * follows them (correction or bonus) is written to tree->tokens[n] when
- * n < depth, and is otherwise available from cgx_last_verify_token(). */
+/* Verification of the chain tree->tokens[0..depth) against the draft
+ * logits in tree->draft_probs [depth][vocab] (host or device).  The target
+ * logits [depth + 1][vocab] are tree->target_probs when set (host or
+ * device); when NULL the target model scores [last input token, drafts] and
+ * target_probs receives them, and its cache keeps the accepted drafts.  The
+ * verify kernels run with the decoder's temperature / top_k / top_p and LCG
+ * draws; the call writes tree->accepted[], updates total_draft_tokens,
+ * accepted_draft_tokens, avg_acceptance_rate and num_steps, and returns the
+ * number n of accepted drafts (0..depth).  The token that follows them (the
+ * correction, or the bonus when all are accepted) is written to
+ * tree->tokens[n] when n < depth and is always returned by
+ * cgx_last_verify_token() (cg_mi355x.h).  vocab is the target model's. */
 int cg_target_verify(
     cg_speculative_decoder* decoder,
     cg_tensor* input_ids,
@@ -108,13 +132,25 @@ void cg_token_tree_free(cg_token_tree* tree);
 
 /* Tree attention (reference :123-130).  cg_tree_attention_mask returns the
  * additive [1,1,S,S] mask (0 / -1e9) with S = seqlen + depth: causal prefix,
- * every node sees the prefix, itself and its ancestors. */
+ * every node sees the prefix and the nodes up to itself (the reference's
+ * chain; cgx_tree_attention_mask_parents builds it for a tree).
+ * cg_forward_tree_attention runs a cgx_model over input (float token ids,
+ * [S]) under such a mask: a causal prefix followed by at most 64 tree rows,
+ * each seeing the whole prefix, itself and any of the other tree rows, at
+ * rotary position prefix + (visible tree rows - 1).  Mask entries must be 0
+ * (visible) or <= -1e4 (hidden).  Returns the logits of every row as a new
+ * host tensor [1, S, vocab]; the model's cache is the workspace and keeps the
+ * causal prefix. */
 cg_tensor* cg_tree_attention_mask(cg_token_tree* tree, int seqlen);
 cg_tensor* cg_forward_tree_attention(
     void* model, cg_tensor* input, cg_tensor* tree_mask
 );
 
-/* EAGLE draft (reference :136-162). */
+/* EAGLE draft (reference :136-162).  cg_eagle_generate_tree with a
+ * cgx_model as base_draft drafts the most likely token at each depth (ties:
+ * the lower id) after input (float token ids), with the draft logits in
+ * draft_probs; with any other base_draft it returns the reference's
+ * placeholder tree (every token 1, src/inference/speculative.c:244-262). */
 typedef struct {
     void* base_draft;
     void* feature_proj;

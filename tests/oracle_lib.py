@@ -135,6 +135,7 @@ _REF_SIGS = {
     "cg_tree_attention_mask": (C.POINTER(RefTensor), [VP, I]),
     "cg_token_tree_new": (VP, [I]),
     "cg_token_tree_free": (None, [VP]),
+    "cg_token_tree_to_tensor": (C.POINTER(RefTensor), [VP]),
     "cg_flash_attention_forward_cuda": (None, [VP]),
     "cg_flash_attention_forward_cpu": (None, [VP]),
     "cg_apply_rope": (None, [VP, VP, I, I, I, I, F]),
