@@ -96,6 +96,15 @@ int cgk_verify_pipe(const float* target, const float* draft, const int* tokens, 
                     int* n_accepted);
 int cgk_sample_temperature_pipe(const float* logits, int rows, int V, float T, const float* u,
                                 int* out, size_t ld);
+/* The verify pipeline on the static workspace of `device` (verify.hip): no
+ * allocation; the address is resolved once per device by
+ * cgk_verify_static_init (cgx_init calls it). */
+int cgk_verify_static_init(int device);
+int cgk_verify_pipe_static(int device, const float* target, const float* draft,
+                           const int* tokens, const float* u, int batch, int gamma, int V,
+                           float T, float* accept_prob, int* out_tokens, int* n_accepted);
+/* The device the library is bound to (-1 before cgx_init). */
+int cgx_device_id(void);
 /* The loop's token rows: ttok[b] = last_b, d_1 .. d_gamma and vtok[b] = d_1 .. d_gamma from
  * feed [B][2] (prev, last) and the drafted tokens dtok [gamma][B]. */
 int cgk_spec_tokens(const int* feed, const int* dtok, int B, int gamma, int* ttok, int* vtok);

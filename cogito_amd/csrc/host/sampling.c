@@ -253,6 +253,33 @@ int cgx_verify_chain_batch_dev(const float* target_logits, const float* draft_lo
                             temperature, ap, corr, bonus, out_tokens, n_accepted);
 }
 
+int cgx_verify_chain_batch_dev_noalloc(const float* target_logits, const float* draft_logits,
+                                       const int* draft_tokens, const float* u, int batch,
+                                       int gamma, int V, float temperature, int top_k,
+                                       float top_p, int* out_tokens, int* n_accepted,
+                                       float* accept_prob) {
+    if (!target_logits || !draft_logits || !draft_tokens || !u || !out_tokens ||
+        !n_accepted || batch <= 0 || gamma <= 0 || V <= 0) {
+        cgx_set_error("cgx_verify_chain_batch_dev_noalloc: invalid argument");
+        return -1;
+    }
+    if (uses_filters(V, top_k, top_p)) {
+        cgx_set_error("cgx_verify_chain_batch_dev_noalloc: top-k / top-p verification needs "
+                      "cgx_verify_chain_batch_dev");
+        return -1;
+    }
+    if (!cgk_verify_pipe_supported(batch, gamma, V, temperature)) {
+        cgx_set_error("cgx_verify_chain_batch_dev_noalloc: batch %d, gamma %d, V %d, "
+                      "temperature %g outside the verify pipeline", batch, gamma, V,
+                      (double)temperature);
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    return cgk_verify_pipe_static(cgx_device_id(), target_logits, draft_logits, draft_tokens, u,
+                                  batch, gamma, V, temperature, accept_prob, out_tokens,
+                                  n_accepted);
+}
+
 int cgx_verify_chain(const float* target_logits, const float* draft_logits,
                      const int* draft_tokens, const float* u, int gamma, int V,
                      float temperature, int top_k, float top_p, int* out_tokens,

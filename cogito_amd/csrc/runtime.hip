@@ -87,8 +87,12 @@ extern "C" int cgx_init(int device) {
     for (int i = 0; i < 8; i++) CGX_TRY(hipEventCreate(&g_rt.events[i]));
     g_rt.device = device;
     g_rt.initialized = true;
+    // the allocation-free verify's workspace address on this device
+    if (cgk_verify_static_init(device)) return -1;
     return 0;
 }
+
+extern "C" int cgx_device_id(void) { return g_rt.initialized ? g_rt.device : -1; }
 
 extern "C" int cgx_ensure_init(void) {
     return g_rt.initialized ? 0 : cgx_init(0);

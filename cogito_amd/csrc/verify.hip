@@ -1117,9 +1117,39 @@ extern "C" int cgk_verify_pipe_supported(int batch, int gamma, int V, float T) {
            V <= kRound * kMaxRounds && T > 0.0f && T <= FLT_MAX;
 }
 
+// Workspace of the allocation-free entry point (cgk_verify_pipe_static): a
+// file-scope device array.  Every GPU the library runs on holds its own copy
+// at its own address until the process ends; host code reaches it only
+// through the address hipGetSymbolAddress returns for that device.
+constexpr size_t kStaticWsBytes = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticWsBytes];
+constexpr int kMaxDevices = 64;
+static void* g_static_ws[kMaxDevices];
+
+extern "C" int cgk_verify_static_init(int device) {
+    if (device < 0 || device >= kMaxDevices) {
+        cgx_set_error("verify workspace: device %d outside 0..%d", device, kMaxDevices - 1);
+        return -1;
+    }
+    if (g_static_ws[device]) return 0;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        (void)hipGetLastError();
+        cgx_set_error("verify workspace: hipGetSymbolAddress failed on device %d: %s", device,
+                      hipGetErrorString(e));
+        return -1;
+    }
+    g_static_ws[device] = p;
+    return 0;
+}
+
+// ws_fixed: a caller-provided workspace of ws_cap bytes instead of the
+// library's grow-only scratch.
 static int verify_pipe(const float* target, size_t ldt, const float* draft, const int* tokens,
                        const float* u, int batch, int gamma, int V, float T, float* accept_prob,
-                       int* out_tokens, int* n_accepted) {
+                       int* out_tokens, int* n_accepted, char* ws_fixed = nullptr,
+                       size_t ws_cap = 0) {
     using namespace vp;
     if (!cgk_verify_pipe_supported(batch, gamma, V, T)) {
         cgx_set_error("verify: batch %d, gamma %d, V %d, T %g outside the pipeline's range",
@@ -1151,7 +1181,12 @@ static int verify_pipe(const float* target, size_t ldt, const float* draft, cons
     const size_t o_flags = take((size_t)batch * 4);
     const size_t o_ap = take((size_t)batch * gamma * 4);
     const size_t o_n = take((size_t)batch * 4);
-    char* ws = (char*)cgx_scratch(CGX_SLOT_WS4, off);
+    if (ws_fixed && off > ws_cap) {
+        cgx_set_error("verify: batch %d, gamma %d, V %d needs %zu bytes of workspace, above "
+                      "the static maximum of %zu", batch, gamma, V, off, ws_cap);
+        return -1;
+    }
+    char* ws = ws_fixed ? ws_fixed : (char*)cgx_scratch(CGX_SLOT_WS4, off);
     if (!ws) return -1;
     Work w;
     w.R1 = R1;
@@ -1202,6 +1237,17 @@ extern "C" int cgk_verify_pipe(const float* target, const float* draft, const in
                                float* accept_prob, int* out_tokens, int* n_accepted) {
     return verify_pipe(target, (size_t)V, draft, tokens, u, batch, gamma, V, T, accept_prob,
                        out_tokens, n_accepted);
+}
+
+// The same pipeline with its workspace in the static array of the current
+// device: no allocation, every call on one GPU shares the array.
+extern "C" int cgk_verify_pipe_static(int device, const float* target, const float* draft,
+                                      const int* tokens, const float* u, int batch, int gamma,
+                                      int V, float T, float* accept_prob, int* out_tokens,
+                                      int* n_accepted) {
+    if (cgk_verify_static_init(device)) return -1;
+    return verify_pipe(target, (size_t)V, draft, tokens, u, batch, gamma, V, T, accept_prob,
+                       out_tokens, n_accepted, (char*)g_static_ws[device], kStaticWsBytes);
 }
 
 // cg_sample_temperature on `rows` rows at once through the same pipeline: a

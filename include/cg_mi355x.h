@@ -104,6 +104,27 @@ int cgx_verify_chain_batch_dev(const float* target_logits,
                                int top_k, float top_p, int* out_tokens,
                                int* n_accepted, float* accept_prob);
 
+/* Allocation-free form of cgx_verify_chain_batch_dev.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as cgx_verify_chain_batch_dev for
+ * unfiltered verification (top_k <= 0 or >= V, top_p >= 1, temperature > 0);
+ * filtered calls are rejected.  The workspace is a static 32 MiB device array
+ * per GPU, held from library load until the process ends, which covers
+ * 16 chains of gamma 4 at V = 32000 or 4 chains at V = 128256; larger calls
+ * fail with an error naming the bytes needed.  Nothing is allocated or
+ * freed (the array's address is resolved once per device by cgx_init).
+ * Every call on one GPU uses the same array and leaves its contents behind;
+ * calls issued on the library stream run in order, but calls that overlap on
+ * one GPU (graph replays or other threads running concurrently) race. */
+int cgx_verify_chain_batch_dev_noalloc(const float* target_logits,
+                                       const float* draft_logits,
+                                       const int* draft_tokens, const float* u,
+                                       int batch, int gamma, int V,
+                                       float temperature, int top_k, float top_p,
+                                       int* out_tokens, int* n_accepted,
+                                       float* accept_prob);
+
 /* Single samplers with an explicit uniform (same arithmetic as the
  * reference samplers; logits host or device). */
 int cgx_sample_temperature_u(const float* logits, int V, float T, float u);
