@@ -250,6 +250,7 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_tree_attention_mask_parents": (PT, [VP, I, I]),
     "cgx_exact_expf_dev": (I, [VP, VP, I]),
     "cgx_ordered_sum_dev": (I, [VP, I, VP]),
+    "cgx_sort_rows_dev": (I, [VP, VP, I, I, I, VP, VP]),
     "cgx_exp_fast_maxerr_dev": (I, [F, F, VP]),
     "cgx_kv_cache_int4_truncate": (I, [PKV, I]),
     "cgx_kv_cache_int4_write": (I, [PKV, I, I, VP, VP, I]),

@@ -133,6 +133,12 @@ int cgx_sample_row_dev(const float* row, int V, float T, int top_k, float top_p,
                        const float* du, float uh, float* z, int* out);
 /* The global LCG of the drop-in samplers (host/speculative.c). */
 float cgx_lcg_draw(void);
+/* Stable radix sort of rows of 32-bit keys (rowsort.hip), descending or
+ * ascending; with pout, payloads travel with their keys (pin NULL: the key's
+ * index in its row).  ws: cgk_row_sort_ws(rows, n, pout != NULL) bytes. */
+size_t cgk_row_sort_ws(int rows, int n, int with_payload);
+int cgk_row_sort(const uint32_t* kin, const uint32_t* pin, int rows, int n, int desc,
+                 uint32_t* kout, uint32_t* pout, void* ws, size_t ws_bytes);
 /* z = x / T elementwise. */
 int cgk_scale(const float* x, float* z, size_t n, float T);
 /* Top-k (0 < top_k < V) or top-p over rows of z [rows][V]: a token per row

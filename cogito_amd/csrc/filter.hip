@@ -15,8 +15,8 @@
 // LDS orders by (value desc, index asc).
 //
 // Top-p: probabilities (exact expf and ordered sum), a radix sort of the
-// values in LDS, the exact sequential cumsum over the sorted values for the
-// cutoff and the draw, and the reference's tie order for the one tie group
+// values (rowsort.hip), the exact sequential cumsum over the sorted values for
+// the cutoff and the draw, and the reference's tie order for the one tie group
 // that matters.  The selection sort's order of equal values is not stable
 // but follows a rule that depends only on counts: let the members of the
 // group of value v be i_1 < ... < i_n and g_t the number of elements > v
@@ -35,7 +35,6 @@
 
 #include "eos.hpp"
 
-#include <rocprim/block/block_radix_sort.hpp>
 
 namespace {
 
@@ -50,7 +49,6 @@ int launch_check(const char* what) {
     return 0;
 }
 
-constexpr int kSortMax = 32768;        // top-p: values sorted in LDS
 constexpr int kTopKMax = 4096;         // top-k: list held in LDS
 constexpr float kTopKFloor = -1e30f;   // speculative.c:128
 
@@ -145,34 +143,6 @@ __global__ __launch_bounds__(kThreads) void k_probs_rows(const float* __restrict
     __syncthreads();
     float S = eos_sum(RowSrc{pr}, V, sh);
     for (int j = threadIdx.x; j < V; j += kThreads) pr[j] = __fdiv_rn(pr[j], S);
-}
-
-// Descending sort of one row of n <= kSortMax non-negative values (a block
-// radix sort in LDS, 32 values per thread; rows shorter than kSortMax are
-// padded with -1, which sorts last).  Only the sorted values are used: the
-// order of equal values is fixed afterwards by the tie rule.
-__global__ __launch_bounds__(kThreads) void k_sort_desc(const float* __restrict__ in, int n,
-                                                        float* __restrict__ out) {
-    constexpr int kItems = kSortMax / kThreads;
-    // 4-bit digits with the basic ranking keep the fewest values spilled
-    // (32 keys per thread under the 128 registers of a 1024-thread block)
-    using Sort = rocprim::block_radix_sort<float, kThreads, kItems, rocprim::empty_type, 1, 1, 4,
-                                           rocprim::block_radix_rank_algorithm::basic>;
-    __shared__ typename Sort::storage_type storage;
-    const float* src = in + (size_t)blockIdx.x * n;
-    float keys[kItems];
-#pragma unroll
-    for (int i = 0; i < kItems; i++) {
-        const int j = i * kThreads + (int)threadIdx.x;
-        keys[i] = j < n ? src[j] : -1.0f;
-    }
-    Sort().sort_desc_to_striped(keys, storage);
-    float* dst = out + (size_t)blockIdx.x * n;
-#pragma unroll
-    for (int i = 0; i < kItems; i++) {
-        const int j = i * kThreads + (int)threadIdx.x;
-        if (j < n) dst[j] = keys[i];
-    }
 }
 
 // The tie group {j : p[j] == v} in index order: member indices -> wi[0..m),
@@ -566,20 +536,23 @@ extern "C" int cgk_filter_rows(const float* z, int rows, int V, int top_k, float
                            kpow2, top_p, u, tokens, dist, (int*)nullptr, (float*)nullptr);
         return launch_check("k_top_k");
     }
-    if (V > kSortMax) {
-        cgx_set_error("top-p: vocabulary size %d above the supported %d", V, kSortMax);
-        return -1;
-    }
+    // the descending sort of each row's probabilities (rowsort.hip, on the
+    // values' bit patterns, monotone for non-negative floats) shares its
+    // workspace with the finish's
     size_t n = (size_t)rows * V;
-    char* w = (char*)cgx_scratch(CGX_SLOT_WS0, n * (4 + 4 + 8));
+    size_t wsb = n * 8;
+    const size_t sb = cgk_row_sort_ws(rows, V, 0);
+    if (sb > wsb) wsb = sb;
+    char* w = (char*)cgx_scratch(CGX_SLOT_WS0, n * 8 + wsb);
     if (!w) return -1;
     float* probs = (float*)w;
     float* sorted = probs + n;
     int* ws = (int*)(sorted + n);
     hipLaunchKernelGGL(k_probs_rows, dim3(rows), dim3(kThreads), 0, stream(), z, V, probs);
     if (launch_check("k_probs_rows")) return -1;
-    hipLaunchKernelGGL(k_sort_desc, dim3(rows), dim3(kThreads), 0, stream(), probs, V, sorted);
-    if (launch_check("k_sort_desc")) return -1;
+    if (cgk_row_sort((const uint32_t*)probs, nullptr, rows, V, 1, (uint32_t*)sorted, nullptr, ws,
+                     wsb))
+        return -1;
     hipLaunchKernelGGL(k_top_p_finish, dim3(rows), dim3(kThreads), 0, stream(), probs, sorted,
                        V, top_p, u, tokens, dist, ws);
     return launch_check("k_top_p_finish");

@@ -128,6 +128,20 @@ int cgx_exp_fast_maxerr_dev(float lo, float hi, unsigned int* out_dev) {
     return cgk_exp_fast_maxerr(lo, hi, out_dev);
 }
 
+int cgx_sort_rows_dev(const uint32_t* keys, const uint32_t* payload, int rows, int n,
+                      int descending, uint32_t* keys_out, uint32_t* payload_out) {
+    if (!keys || !keys_out || rows <= 0 || n <= 0) {
+        cgx_set_error("cgx_sort_rows_dev: invalid argument");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    const size_t wb = cgk_row_sort_ws(rows, n, payload_out != NULL);
+    void* ws = cgx_scratch(CGX_SLOT_WS5, wb);
+    if (!ws || cgk_row_sort(keys, payload, rows, n, descending, keys_out, payload_out, ws, wb))
+        return -1;
+    return cgx_synchronize();
+}
+
 int cgx_ordered_sum_dev(const float* x, int n, float* out_dev) {
     if (!x || !out_dev || n <= 0) {
         cgx_set_error("cgx_ordered_sum_dev: invalid argument");

@@ -1,0 +1,239 @@
+// rowsort.hip -- stable radix sort of rows of 32-bit keys, optionally
+// carrying a 32-bit payload, with several workgroups per row (gfx950).
+//
+// The samplers that order a whole vocabulary row (top-p by probability,
+// typical sampling by score) sort with it, so no row size is bounded by LDS.
+// Least-significant-digit first, 8-bit digits, four passes.  Each pass is two
+// launches over tiles of 4096 keys (grid: tiles x rows):
+//   k_rs_hist     the tile's digit counts -> hist[row][tile][256];
+//   k_rs_scatter  the tile's output offsets (counts of every tile before it,
+//                 and of the digits before its own in the sort order), the
+//                 stable rank of each key among the tile's keys of its digit,
+//                 and the scatter.
+// Ranks come from wave-level digit matching: eight ballots give each lane the
+// mask of lanes holding the same digit, so one lane per digit group touches
+// the LDS counters (no atomics, no contention when most keys share a digit,
+// as the high byte of probabilities does).  A tile's keys are ordered (wave,
+// item, lane), which is their order in the row, so every pass is stable.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "cgx_internal.h"
+
+namespace {
+
+constexpr int kT = 256;                 // threads per block (4 waves)
+constexpr int kWv = kT / 64;
+constexpr int kItems = 16;              // keys per thread
+constexpr int kTile = kT * kItems;      // keys per block
+constexpr int kBins = 256;
+constexpr int kMaxTiles = 1024;         // rows up to 4 M keys
+
+inline hipStream_t stream() { return (hipStream_t)cgx_stream(); }
+
+int launch_check(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        cgx_set_error("%s launch failed: %s", what, hipGetErrorString(e));
+        return -1;
+    }
+    return 0;
+}
+
+// Lanes (among the valid ones) whose 8-bit digit equals this lane's.
+__device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid) {
+    uint64_t m = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+        const bool bit = (d >> b) & 1u;
+        const uint64_t v = __ballot(bit);
+        m &= bit ? v : ~v;
+    }
+    return m;
+}
+
+// Position of item q of lane `lane` in wave w of tile `tile`.
+__device__ __forceinline__ int tile_pos(int tile, int w, int q, int lane) {
+    return tile * kTile + w * (kItems * 64) + q * 64 + lane;
+}
+
+__global__ __launch_bounds__(kT) void k_rs_hist(const uint32_t* __restrict__ keys, int n,
+                                                int shift, int ntiles,
+                                                uint32_t* __restrict__ hist) {
+    __shared__ uint32_t h[kBins];
+    const int row = blockIdx.y, tile = blockIdx.x, t = threadIdx.x;
+    const int lane = t & 63, w = t >> 6;
+    h[t] = 0;
+    __syncthreads();
+    const uint32_t* src = keys + (size_t)row * n;
+    uint32_t kk[kItems];
+#pragma unroll
+    for (int q = 0; q < kItems; q++) {
+        const int p = tile_pos(tile, w, q, lane);
+        kk[q] = p < n ? src[p] : 0u;
+    }
+#pragma unroll
+    for (int q = 0; q < kItems; q++) {
+        const bool valid = tile_pos(tile, w, q, lane) < n;
+        const uint32_t d = (kk[q] >> shift) & 255u;
+        const uint64_t m = match_digit(d, valid);
+        if (valid && lane == __ffsll((unsigned long long)m) - 1)
+            atomicAdd(&h[d], (uint32_t)__popcll(m));
+    }
+    __syncthreads();
+    hist[((size_t)row * ntiles + tile) * kBins + t] = h[t];
+}
+
+// Exclusive sum over the 256 threads of the block (one value each).
+__device__ __forceinline__ uint32_t block_excl_256(uint32_t v, uint32_t* part) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    uint32_t x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    if (lane == 63) part[w] = x;
+    __syncthreads();
+    uint32_t off = 0;
+#pragma unroll
+    for (int i = 0; i < kWv; i++) off += i < w ? part[i] : 0u;
+    __syncthreads();
+    return off + x - v;
+}
+
+template <bool kDesc, bool kPay>
+__global__ __launch_bounds__(kT) void k_rs_scatter(const uint32_t* __restrict__ kin,
+                                                   const uint32_t* __restrict__ pin, int n,
+                                                   int shift, int ntiles,
+                                                   const uint32_t* __restrict__ hist,
+                                                   uint32_t* __restrict__ kout,
+                                                   uint32_t* __restrict__ pout) {
+    __shared__ uint32_t wcnt[kWv][kBins];
+    __shared__ uint32_t goff[kBins];
+    __shared__ uint32_t ord[kBins];
+    __shared__ uint32_t part[kWv];
+    const int row = blockIdx.y, tile = blockIdx.x, t = threadIdx.x;
+    const int lane = t & 63, w = t >> 6;
+    const size_t rb = (size_t)row * n;
+
+    // keys first, so their loads are in flight during the offset arithmetic
+    uint32_t kk[kItems], pp[kItems], rk[kItems];
+#pragma unroll
+    for (int q = 0; q < kItems; q++) {
+        const int p = tile_pos(tile, w, q, lane);
+        kk[q] = p < n ? kin[rb + p] : 0u;
+        if (kPay) pp[q] = p < n ? (pin ? pin[rb + p] : (uint32_t)p) : 0u;
+    }
+
+    // digit d = t: keys of d in earlier tiles, and in the whole row
+    const uint32_t* hr = hist + (size_t)row * ntiles * kBins;
+    uint32_t pre = 0, tot = 0;
+    for (int b = 0; b < ntiles; b++) {
+        const uint32_t c = hr[(size_t)b * kBins + t];
+        tot += c;
+        pre += b < tile ? c : 0u;
+    }
+    // digits in sort order: position o(d) = d (ascending) or 255 - d
+    ord[kDesc ? 255 - t : t] = tot;
+    for (int i = 0; i < kWv; i++) wcnt[i][t] = 0;
+    __syncthreads();
+    const uint32_t before = block_excl_256(ord[t], part);
+    ord[t] = before;
+    __syncthreads();
+    goff[t] = ord[kDesc ? 255 - t : t] + pre;
+
+    // stable rank of each key among the tile's keys of its digit, per wave
+    const uint64_t lt = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int q = 0; q < kItems; q++) {
+        const bool valid = tile_pos(tile, w, q, lane) < n;
+        const uint32_t d = (kk[q] >> shift) & 255u;
+        const uint64_t m = match_digit(d, valid);
+        rk[q] = 0;
+        if (valid) {
+            const uint32_t c = wcnt[w][d];
+            rk[q] = c + (uint32_t)__popcll(m & lt);
+            if (lane == __ffsll((unsigned long long)m) - 1) wcnt[w][d] = c + (uint32_t)__popcll(m);
+        }
+    }
+    __syncthreads();
+    // earlier waves' counts per digit
+    {
+        uint32_t r = 0;
+#pragma unroll
+        for (int i = 0; i < kWv; i++) {
+            const uint32_t c = wcnt[i][t];
+            wcnt[i][t] = r;
+            r += c;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kItems; q++) {
+        if (tile_pos(tile, w, q, lane) >= n) continue;
+        const uint32_t d = (kk[q] >> shift) & 255u;
+        const uint32_t pos = goff[d] + wcnt[w][d] + rk[q];
+        if (pos >= (uint32_t)n) continue;   // unreachable with consistent counts
+        kout[rb + pos] = kk[q];
+        if (kPay) pout[rb + pos] = pp[q];
+    }
+}
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+}  // namespace
+
+extern "C" size_t cgk_row_sort_ws(int rows, int n, int with_payload) {
+    const size_t ntiles = ((size_t)n + kTile - 1) / kTile;
+    const size_t buf = align256((size_t)rows * n * 4);
+    return (with_payload ? 4 : 2) * buf + align256((size_t)rows * ntiles * kBins * 4);
+}
+
+extern "C" int cgk_row_sort(const uint32_t* kin, const uint32_t* pin, int rows, int n, int desc,
+                            uint32_t* kout, uint32_t* pout, void* ws, size_t ws_bytes) {
+    if (rows <= 0 || rows > 65535 || n <= 0 || !kin || !kout || !ws) {
+        cgx_set_error("row sort: invalid arguments (rows %d, n %d)", rows, n);
+        return -1;
+    }
+    const int ntiles = (n + kTile - 1) / kTile;
+    const int pay = pout != nullptr;
+    if (ntiles > kMaxTiles || ws_bytes < cgk_row_sort_ws(rows, n, pay)) {
+        cgx_set_error("row sort: %d keys per row need %d tiles (at most %d) or the workspace "
+                      "is too small", n, ntiles, kMaxTiles);
+        return -1;
+    }
+    const size_t buf = align256((size_t)rows * n * 4);
+    char* w = (char*)ws;
+    uint32_t* kb[2] = {(uint32_t*)w, (uint32_t*)(w + buf)};
+    uint32_t* pb[2] = {pay ? (uint32_t*)(w + 2 * buf) : nullptr,
+                       pay ? (uint32_t*)(w + 3 * buf) : nullptr};
+    uint32_t* hist = (uint32_t*)(w + (pay ? 4 : 2) * buf);
+    const dim3 grid(ntiles, rows);
+    const uint32_t* ks = kin;
+    const uint32_t* ps = pin;
+    for (int pass = 0; pass < 4; pass++) {
+        const int shift = 8 * pass;
+        uint32_t* kd = pass == 3 ? kout : kb[pass & 1];
+        uint32_t* pd = pass == 3 ? pout : pb[pass & 1];
+        hipLaunchKernelGGL(k_rs_hist, grid, dim3(kT), 0, stream(), ks, n, shift, ntiles, hist);
+        if (launch_check("k_rs_hist")) return -1;
+        if (desc && pay)
+            hipLaunchKernelGGL((k_rs_scatter<true, true>), grid, dim3(kT), 0, stream(), ks, ps, n,
+                               shift, ntiles, hist, kd, pd);
+        else if (desc)
+            hipLaunchKernelGGL((k_rs_scatter<true, false>), grid, dim3(kT), 0, stream(), ks, ps,
+                               n, shift, ntiles, hist, kd, pd);
+        else if (pay)
+            hipLaunchKernelGGL((k_rs_scatter<false, true>), grid, dim3(kT), 0, stream(), ks, ps,
+                               n, shift, ntiles, hist, kd, pd);
+        else
+            hipLaunchKernelGGL((k_rs_scatter<false, false>), grid, dim3(kT), 0, stream(), ks, ps,
+                               n, shift, ntiles, hist, kd, pd);
+        if (launch_check("k_rs_scatter")) return -1;
+        ks = kd;
+        ps = pd;
+    }
+    return 0;
+}

@@ -152,6 +152,12 @@ int cgx_filtered_dist(const float* logits, int V, float T, int top_k,
  * non-negative values. */
 int cgx_exact_expf_dev(const float* x, float* y, int n);
 int cgx_ordered_sum_dev(const float* x, int n, float* out_dev);
+/* Test hook of the samplers' row sort: rows [rows][n] of 32-bit keys sorted
+ * stably (descending when `descending`), payloads carried along when
+ * payload_out is given (payload NULL: each key's index in its row).  Device
+ * pointers; synchronous. */
+int cgx_sort_rows_dev(const uint32_t* keys, const uint32_t* payload, int rows, int n,
+                      int descending, uint32_t* keys_out, uint32_t* payload_out);
 /* Largest relative distance between the samplers' fast exponential and the
  * exact one over every fp32 in [lo, hi] (-104 <= lo < hi <= 0), folded with
  * an unsigned max into *out_dev as the float's bits (caller zeroes it).  The

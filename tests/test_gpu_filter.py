@@ -73,6 +73,86 @@ def test_sample_top_p_bitexact(gpu, oracle, rng, V, p, kind):
             assert got == exp, (trial, u, got, exp)
 
 
+SORT_CASES = [(1, 1, "full"), (3, 100, "dups"), (2, 4096, "full"), (2, 4097, "dups"),
+              (4, 40000, "probs"), (1, 128256, "probs"), (2, 70001, "dups")]
+
+
+@pytest.mark.parametrize("rows,n,kind", SORT_CASES)
+def test_row_sort_matches_numpy(gpu, rng, rows, n, kind):
+    # the multi-workgroup radix sort of rows (rowsort.hip): keys and the
+    # payload of a stable sort, both directions
+    print(f"row sort rows={rows} n={n} {kind}", flush=True)
+    if kind == "full":
+        keys = rng.integers(0, 2**32, (rows, n), dtype=np.uint64).astype(np.uint32)
+    elif kind == "dups":
+        keys = rng.integers(0, 40, (rows, n)).astype(np.uint32) * np.uint32(0x01010101)
+    else:
+        x = rng.normal(0, 2, (rows, n))
+        keys = (np.exp(x - x.max()) / np.exp(x - x.max()).sum()).astype(np.float32).view(np.uint32)
+    dk = DeviceArray.from_numpy(gpu, keys)
+    pay = rng.integers(0, 2**31, (rows, n)).astype(np.uint32)
+    dp = DeviceArray.from_numpy(gpu, pay)
+    ok_, op_ = DeviceArray(gpu, keys.nbytes), DeviceArray(gpu, keys.nbytes)
+    for desc in (1, 0):
+        order = np.argsort(-keys.astype(np.int64) if desc else keys, axis=1, kind="stable")
+        for payload in (None, dp):
+            rc = gpu.cgx_sort_rows_dev(dk.ptr, payload.ptr if payload else None, rows, n, desc,
+                                       ok_.ptr, op_.ptr)
+            assert rc == 0, last_error(gpu)
+            np.testing.assert_array_equal(ok_.numpy(np.uint32, (rows, n)),
+                                          np.take_along_axis(keys, order, 1))
+            exp_pay = order if payload is None else np.take_along_axis(pay, order, 1)
+            np.testing.assert_array_equal(op_.numpy(np.uint32, (rows, n)), exp_pay)
+        # keys only
+        rc = gpu.cgx_sort_rows_dev(dk.ptr, None, rows, n, desc, ok_.ptr, None)
+        assert rc == 0, last_error(gpu)
+        np.testing.assert_array_equal(ok_.numpy(np.uint32, (rows, n)),
+                                      np.take_along_axis(keys, order, 1))
+    for a in (dk, dp, ok_, op_):
+        a.free()
+
+
+@pytest.mark.parametrize("V,p,kind", [(40000, 0.9, "flat"), (40000, 0.7, "ties"),
+                                      (40000, 0.95, "normal")])
+def test_sample_top_p_beyond_lds_sort(gpu, oracle, rng, V, p, kind):
+    # rows longer than the LDS sort's 32768 take the multi-workgroup sort
+    print(f"top-p V={V} p={p} {kind}", flush=True)
+    x = logits_case(rng, V, kind)
+    for u in (float(rng.uniform()), 0.0):
+        got = gpu.cgx_sample_top_p_u(x.ctypes.data, V, p, u)
+        assert got >= 0, last_error(gpu)
+        assert got == oracle.orc_sample_top_p(ptr(x), V, p, u), u
+
+
+def test_top_p_7b_vocabulary(gpu, oracle, rng):
+    # V = 128256 (config 5's vocabulary), near-uniform logits: the cutoff
+    # falls deep in the sorted row and fp32 ties are everywhere.  One O(V^2)
+    # oracle sort gives the sorted probabilities, indices and cutoff; the
+    # draws and the distribution follow from them by the reference's scan
+    # (speculative.c:102-115).
+    V, p = 128256, 0.9
+    x = logits_case(rng, V, "flat")
+    sp = np.zeros(V, np.float32)
+    si = np.zeros(V, np.int32)
+    import ctypes as C
+    mass = C.c_float(0)
+    cut = oracle.orc_top_p_sorted(ptr(x), V, p, ptr(sp), ptr(si), C.byref(mass))
+    assert cut > V // 2
+    cum = np.add.accumulate(sp[:cut], dtype=np.float32)
+    for u in (0.0, 0.3141, 0.9999):
+        r = np.float32(u) * np.float32(mass.value)
+        hit = np.flatnonzero(r < cum)
+        exp = int(si[hit[0]]) if hit.size else int(si[0])
+        got = gpu.cgx_sample_top_p_u(x.ctypes.data, V, p, u)
+        assert got == exp, (u, got, exp, last_error(gpu))
+    got = np.full(V, 7.0, np.float32)
+    assert gpu.cgx_filtered_dist(x.ctypes.data, V, 1.0, 0, p, got.ctypes.data) == 0, \
+        last_error(gpu)
+    dist = np.zeros(V, np.float32)
+    dist[si[:cut]] = sp[:cut] / np.float32(mass.value)
+    np.testing.assert_array_equal(_bits(got), _bits(dist))
+
+
 def test_top_p_tie_order_dense_draws(gpu, oracle, rng):
     # many draws on one row with large tie groups: every rank inside the
     # groups is exercised against the literal sort
@@ -89,6 +169,7 @@ FILTER_CASES = [
     (32000, 0.8, 0, 0.9, "normal"),
     (4000, 0.8, 0, 0.9, "ties"),
     (4000, 1.0, 0, 0.5, "flat"),
+    (40000, 0.8, 0, 0.9, "ties"),
     (128256, 0.7, 50, 1.0, "normal"),
     (128256, 0.7, 50, 0.9, "normal"),
     (2000, 1.3, 300, 0.8, "halves"),
@@ -190,8 +271,9 @@ def test_dropin_top_k_top_p_follow_reference_lcg(gpu, oracle, rng):
 def test_filter_limits_report_errors(gpu, rng):
     x = rng.normal(0, 1, 40000).astype(np.float32)
     gpu.cgx_clear_error()
-    assert gpu.cgx_sample_top_p_u(x.ctypes.data, 40000, 0.9, 0.5) == -1
-    assert "top-p" in last_error(gpu)
+    big = np.zeros(262145, np.float32)
+    assert gpu.cgx_sample_top_p_u(big.ctypes.data, big.size, 0.9, 0.5) == -1
+    assert "vocabulary size" in last_error(gpu)
     gpu.cgx_clear_error()
     assert gpu.cgx_sample_top_k_u(x.ctypes.data, 40000, 5000, 0.5) == -1
     assert "top-k" in last_error(gpu)
