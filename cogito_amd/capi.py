@@ -246,11 +246,14 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_sample_top_p_u": (I, [VP, I, F, F]),
     "cgx_sample_corrected_u": (I, [VP, VP, I, F]),
     "cgx_filtered_dist": (I, [VP, I, F, I, F, VP]),
+    "cgx_sample_typical_u": (I, [VP, I, F, F]),
+    "cgx_typical_dist": (I, [VP, I, F, VP]),
     "cgx_last_verify_token": (I, []),
     "cgx_tree_attention_mask_parents": (PT, [VP, I, I]),
     "cgx_exact_expf_dev": (I, [VP, VP, I]),
     "cgx_ordered_sum_dev": (I, [VP, I, VP]),
     "cgx_sort_rows_dev": (I, [VP, VP, I, I, I, VP, VP]),
+    "cgx_typ_log_dev": (I, [VP, VP, I]),
     "cgx_exp_fast_maxerr_dev": (I, [F, F, VP]),
     "cgx_kv_cache_int4_truncate": (I, [PKV, I]),
     "cgx_kv_cache_int4_write": (I, [PKV, I, I, VP, VP, I]),

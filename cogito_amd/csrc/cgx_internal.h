@@ -133,6 +133,12 @@ int cgx_sample_row_dev(const float* row, int V, float T, int top_k, float top_p,
                        const float* du, float uh, float* z, int* out);
 /* The global LCG of the drop-in samplers (host/speculative.c). */
 float cgx_lcg_draw(void);
+/* Typical sampling (decision D16) over rows of logits at T = 1: tokens drawn
+ * with u (device), or dense distributions.  Uses scratch slot WS0. */
+int cgk_typical_rows(const float* logits, int rows, int V, float typical_p, const float* u,
+                     int* tokens, float* dist);
+/* The typical sampler's binary64 log of positive floats, elementwise. */
+int cgk_typ_log(const float* x, double* y, int n);
 /* Stable radix sort of rows of 32-bit keys (rowsort.hip), descending or
  * ascending; with pout, payloads travel with their keys (pin NULL: the key's
  * index in its row).  ws: cgk_row_sort_ws(rows, n, pout != NULL) bytes. */

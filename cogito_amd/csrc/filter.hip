@@ -479,9 +479,153 @@ __global__ __launch_bounds__(kThreads) void k_top_k(const float* __restrict__ z,
     }
 }
 
+// ----------------------------------------------------- typical sampling
+//
+// cg_sample_typical is declared by cogito (include/cg_speculative.h:186)
+// and never defined; this build defines it (decision D16) in the reference
+// samplers' style: the softmax of cg_sample_top_p; L_i = (float)log p_i;
+// H = sum_i fl(p_i * -L_i) left to right in fp32; tokens ordered by
+// (|fl(-L_i - H)| ascending, index ascending); the first tokens of that order
+// up to cumsum >= typical_p; the draw r = u * (kept mass) scans them.
+
+// log of a positive finite float in binary64 by a fixed sequence of IEEE
+// operations (no FMA; this file is built without contraction): x = m 2^k,
+// m in [sqrt(1/2), sqrt(2)), log m = 2 atanh((m - 1) / (m + 1)) by the odd
+// series to s^25.  The CPU restatement evaluates the same sequence, so both
+// give the same bits.
+__device__ double typ_log(float x) {
+    const double kLn2 = 0x1.62e42fefa39efp-1;
+    const double kSqrt2 = 0x1.6a09e667f3bcdp+0;
+    const double kC[13] = {1.0,        1.0 / 3.0,  1.0 / 5.0,  1.0 / 7.0,  1.0 / 9.0,
+                           1.0 / 11.0, 1.0 / 13.0, 1.0 / 15.0, 1.0 / 17.0, 1.0 / 19.0,
+                           1.0 / 21.0, 1.0 / 23.0, 1.0 / 25.0};
+    const unsigned long long b = (unsigned long long)__double_as_longlong((double)x);
+    int k = (int)((b >> 52) & 0x7ff) - 1023;
+    double m = __longlong_as_double(
+        (long long)((b & 0x000fffffffffffffull) | 0x3ff0000000000000ull));
+    if (m > kSqrt2) {
+        m = __dmul_rn(m, 0.5);
+        k += 1;
+    }
+    const double s = __ddiv_rn(__dsub_rn(m, 1.0), __dadd_rn(m, 1.0));
+    const double s2 = __dmul_rn(s, s);
+    double q = kC[12];
+#pragma unroll
+    for (int j = 11; j >= 0; j--) q = __dadd_rn(kC[j], __dmul_rn(s2, q));
+    return __dadd_rn(__dmul_rn((double)k, kLn2), __dmul_rn(2.0, __dmul_rn(s, q)));
+}
+
+__global__ void k_typ_log(const float* __restrict__ x, double* __restrict__ y, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = typ_log(x[i]);
+}
+
+// Per row: -L_i and the entropy terms, H by the exact ordered sum, then the
+// sort key of each token (its score's bits; +inf for p_i = 0).
+__global__ __launch_bounds__(kThreads) void k_typ_scores(const float* __restrict__ probs, int V,
+                                                         float* __restrict__ nl,
+                                                         float* __restrict__ terms,
+                                                         uint32_t* __restrict__ keys) {
+    __shared__ EosShared sh;
+    const size_t rb = (size_t)blockIdx.x * V;
+    const float* pr = probs + rb;
+    for (int j = threadIdx.x; j < V; j += kThreads) {
+        const float x = pr[j];
+        const float n = x > 0.0f ? -(float)typ_log(x) : 0.0f;
+        nl[rb + j] = n;
+        terms[rb + j] = x > 0.0f ? __fmul_rn(x, n) : 0.0f;
+    }
+    __threadfence_block();
+    __syncthreads();
+    const float H = eos_sum(RowSrc{terms + rb}, V, sh);
+    for (int j = threadIdx.x; j < V; j += kThreads) {
+        const float sc = pr[j] > 0.0f ? fabsf(__fsub_rn(nl[rb + j], H)) : __builtin_inff();
+        keys[rb + j] = __float_as_uint(sc);
+    }
+}
+
+struct PermSrc {                 // probabilities in the typical order
+    const float* p;
+    const uint32_t* o;
+    __device__ float operator()(int j) const { return p[o[j]]; }
+};
+
+// Cutoff over the typical order, then the draw (tokens) or the filtered
+// distribution (dist, dense rows).
+__global__ __launch_bounds__(kThreads) void k_typ_finish(const float* __restrict__ probs,
+                                                         const uint32_t* __restrict__ perm,
+                                                         int V, float typical_p,
+                                                         const float* __restrict__ u,
+                                                         int* __restrict__ tokens,
+                                                         float* __restrict__ dist) {
+    __shared__ EosShared sh;
+    const int row = blockIdx.x;
+    const size_t rb = (size_t)row * V;
+    PermSrc g{probs + rb, perm + rb};
+    const float total = eos_sum(g, V, sh);
+    float C;
+    const int ci = gen_find_val(g, V, float_below(typical_p), -1, total, &C, sh);
+    const int cutoff = ci < 0 ? V : ci + 1;
+    if (tokens) {
+        // speculative.c:109-115's scan over the kept tokens
+        int pos = gen_find(g, V, __fmul_rn(u[row], C), 0, sh);
+        if (pos >= cutoff) pos = 0;
+        if (threadIdx.x == 0) tokens[row] = (int)perm[rb + pos];
+        return;
+    }
+    float* dr = dist + rb;
+    for (int j = threadIdx.x; j < V; j += kThreads) dr[j] = 0.0f;
+    __threadfence_block();
+    __syncthreads();
+    for (int j = threadIdx.x; j < cutoff; j += kThreads) {
+        const int i = (int)perm[rb + j];
+        dr[i] = __fdiv_rn(probs[rb + i], C);
+    }
+}
+
 }  // namespace
 
 // -------------------------------------------------------------- launchers
+
+extern "C" int cgk_typ_log(const float* x, double* y, int n) {
+    hipLaunchKernelGGL(k_typ_log, dim3((n + 255) / 256), dim3(256), 0, stream(), x, y, n);
+    return launch_check("k_typ_log");
+}
+
+// Typical sampling of `rows` rows of logits [rows][V] (T = 1): tokens[row]
+// drawn with u[row], or dense distributions.  Uses scratch slot WS0.
+extern "C" int cgk_typical_rows(const float* logits, int rows, int V, float typical_p,
+                                const float* u, int* tokens, float* dist) {
+    if (rows <= 0 || V <= 0 || rows > 65535 || (!tokens == !dist)) {
+        cgx_set_error("typical: invalid arguments");
+        return -1;
+    }
+    if (V > kRound * kMaxRounds) {
+        cgx_set_error("typical: vocabulary size %d above %d", V, kRound * kMaxRounds);
+        return -1;
+    }
+    const size_t n = (size_t)rows * V;
+    const size_t a = (n * 4 + 255) & ~(size_t)255;
+    const size_t sb = cgk_row_sort_ws(rows, V, 1);
+    char* w = (char*)cgx_scratch(CGX_SLOT_WS0, 6 * a + sb);
+    if (!w) return -1;
+    float* probs = (float*)w;
+    float* nl = (float*)(w + a);
+    float* terms = (float*)(w + 2 * a);
+    uint32_t* keys = (uint32_t*)(w + 3 * a);
+    uint32_t* skeys = (uint32_t*)(w + 4 * a);
+    uint32_t* perm = (uint32_t*)(w + 5 * a);
+    void* sws = w + 6 * a;
+    hipLaunchKernelGGL(k_probs_rows, dim3(rows), dim3(kThreads), 0, stream(), logits, V, probs);
+    if (launch_check("k_probs_rows")) return -1;
+    hipLaunchKernelGGL(k_typ_scores, dim3(rows), dim3(kThreads), 0, stream(), probs, V, nl, terms,
+                       keys);
+    if (launch_check("k_typ_scores")) return -1;
+    if (cgk_row_sort(keys, nullptr, rows, V, 0, skeys, perm, sws, sb)) return -1;
+    hipLaunchKernelGGL(k_typ_finish, dim3(rows), dim3(kThreads), 0, stream(), probs, perm, V,
+                       typical_p, u, tokens, dist);
+    return launch_check("k_typ_finish");
+}
 
 // Top-k lists of `rows` rows of z [rows][V] (1 <= top_k < V): lidx/lp
 // [rows][top_k], entry j = the j-th of cg_sample_top_k's list (value desc,

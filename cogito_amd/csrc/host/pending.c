@@ -15,9 +15,3 @@
 int* cg_eagle_compute_branching(cg_eagle_draft* e, cg_tensor* f) {
     (void)e; (void)f; PENDING("cg_eagle_compute_branching"); return NULL;
 }
-
-/* cg_speculative.h: typical sampling (declared only in the reference,
- * include/cg_speculative.h:186) */
-int cg_sample_typical(float* l, int V, float p) {
-    (void)l; (void)V; (void)p; PENDING("cg_sample_typical"); return -1;
-}

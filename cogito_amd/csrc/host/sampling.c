@@ -6,6 +6,8 @@
  *   cg_sample_corrected    reference src/inference/speculative.c:148-172
  *   cg_sample_top_p        reference src/inference/speculative.c:77-120
  *   cg_sample_top_k        reference src/inference/speculative.c:122-146
+ *   cg_sample_typical      declared only (include/cg_speculative.h:186);
+ *                          decision D16
  *   cgx_verify_chain       composition of those with cg_acceptance_prob
  *                          (:49-52); the reference only declares
  *                          cg_target_verify (include/cg_speculative.h:99-103)
@@ -21,8 +23,6 @@
 #include "cg_mi355x.h"
 #include "cg_speculative.h"
 #include "cgx_internal.h"
-
-float cgx_lcg_draw(void);
 
 static int uses_filters(int V, int top_k, float top_p) {
     return (top_k > 0 && top_k < V) || top_p < 1.0f;
@@ -119,6 +119,15 @@ int cgx_exact_expf_dev(const float* x, float* y, int n) {
     return n ? cgk_exact_expf(x, y, n) : 0;
 }
 
+int cgx_typ_log_dev(const float* x, double* y, int n) {
+    if (!x || !y || n < 0) {
+        cgx_set_error("cgx_typ_log_dev: invalid argument");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    return n ? cgk_typ_log(x, y, n) : 0;
+}
+
 int cgx_exp_fast_maxerr_dev(float lo, float hi, unsigned int* out_dev) {
     if (!out_dev) {
         cgx_set_error("cgx_exp_fast_maxerr_dev: invalid argument");
@@ -195,6 +204,42 @@ int cgx_sample_top_p_u(const float* logits, int V, float top_p, float u) {
         cgk_filter_rows(d, 1, V, 0, top_p, du, out, NULL))
         return -1;
     return read_token(out);
+}
+
+/* cg_sample_typical (declared only in the reference, include/
+ * cg_speculative.h:186): decision D16, the typical kernels of filter.hip. */
+int cgx_sample_typical_u(const float* logits, int V, float typical_p, float u) {
+    if (!logits || V <= 0) {
+        cgx_set_error("cgx_sample_typical_u: invalid argument");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    const float* d = (const float*)cgx_dev_in(logits, (size_t)V * 4, CGX_SLOT_IN0);
+    float* du = (float*)cgx_scratch(CGX_SLOT_IN1, sizeof(float));
+    int* out = (int*)cgx_scratch(CGX_SLOT_OUT1, sizeof(int));
+    if (!d || !du || !out || cgx_memcpy_h2d(du, &u, sizeof(float)) ||
+        cgk_typical_rows(d, 1, V, typical_p, du, out, NULL))
+        return -1;
+    return read_token(out);
+}
+
+int cg_sample_typical(float* logits, int vocab_size, float typical_p) {
+    float u = cgx_lcg_draw();
+    return cgx_sample_typical_u(logits, vocab_size, typical_p, u);
+}
+
+int cgx_typical_dist(const float* logits, int V, float typical_p, float* dist_out) {
+    if (!logits || !dist_out || V <= 0) {
+        cgx_set_error("cgx_typical_dist: invalid argument");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    const float* d = (const float*)cgx_dev_in(logits, (size_t)V * 4, CGX_SLOT_IN0);
+    int out_dev = cgx_is_device_ptr(dist_out);
+    float* o = out_dev ? dist_out : (float*)cgx_scratch(CGX_SLOT_OUT0, (size_t)V * 4);
+    if (!d || !o || cgk_typical_rows(d, 1, V, typical_p, NULL, NULL, o)) return -1;
+    if (!out_dev) return cgx_memcpy_d2h(dist_out, o, (size_t)V * 4);
+    return cgx_synchronize();
 }
 
 int cg_sample_top_k(float* logits, int vocab_size, int top_k) {

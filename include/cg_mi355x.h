@@ -133,6 +133,11 @@ int cgx_sample_top_p_u(const float* logits, int V, float top_p, float u);
 int cgx_sample_corrected_u(const float* draft_probs, const float* target_probs,
                            int V, float u);
 
+/* Typical sampling with an explicit uniform, and its distribution (logits
+ * host or device; dist_out host or device, V floats): see cg_sample_typical. */
+int cgx_sample_typical_u(const float* logits, int V, float typical_p, float u);
+int cgx_typical_dist(const float* logits, int V, float typical_p, float* dist_out);
+
 /* The token that followed the accepted drafts (correction or bonus) in the
  * last cg_target_verify / cg_speculative_step; -1 before any. */
 int cgx_last_verify_token(void);
@@ -152,6 +157,9 @@ int cgx_filtered_dist(const float* logits, int V, float T, int top_k,
  * non-negative values. */
 int cgx_exact_expf_dev(const float* x, float* y, int n);
 int cgx_ordered_sum_dev(const float* x, int n, float* out_dev);
+/* Test hook: the typical sampler's binary64 log of positive floats
+ * (device pointers), the same bits as the CPU restatement's. */
+int cgx_typ_log_dev(const float* x, double* y, int n);
 /* Test hook of the samplers' row sort: rows [rows][n] of 32-bit keys sorted
  * stably (descending when `descending`), payloads carried along when
  * payload_out is given (payload NULL: each key's index in its row).  Device

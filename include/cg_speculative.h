@@ -168,7 +168,12 @@ int* cg_eagle_compute_branching(cg_eagle_draft* eagle, cg_tensor* features);
 void cg_eagle_draft_free(cg_eagle_draft* eagle);
 
 /* Samplers (reference :171-196).  `logits` may be host or device memory.
- * Each draws one uniform from the global LCG. */
+ * Each draws one uniform from the global LCG.  cg_sample_typical, declared
+ * only in the reference, is locally typical sampling in the style of
+ * cg_sample_top_p: probabilities p (softmax at T = 1), L_i = log p_i (a
+ * binary64 log rounded to float), entropy H = sum fl(p_i * -L_i) left to
+ * right in fp32, tokens ordered by (|-L_i - H| ascending, index ascending),
+ * kept up to the first cumsum >= typical_p, drawn by r = u * kept mass. */
 int cg_sample_temperature(float* logits, int vocab_size, float temperature);
 int cg_sample_top_p(float* logits, int vocab_size, float top_p);
 int cg_sample_top_k(float* logits, int vocab_size, int top_k);

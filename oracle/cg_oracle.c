@@ -342,6 +342,119 @@ void orc_verify_chain_many(const float* target_logits, const float* draft_logits
                                          top_p, out_tokens + (size_t)k * (gamma + 1), NULL);
 }
 
+/* ------------------------------------------------------ typical sampling */
+
+/* Natural log of a positive finite float in binary64 by a fixed sequence of
+ * IEEE operations (no FMA), the same bits on any conforming host or device:
+ * x = m 2^k with m in [sqrt(1/2), sqrt(2)); log m = 2 atanh(s) with
+ * s = (m - 1) / (m + 1), |s| <= 0.1716, and atanh(s) = s (1 + s^2/3 + s^4/5
+ * + ... + s^24/25) (truncation below 2^-60). */
+double orc_typ_log(float x) {
+    static const double kLn2 = 0x1.62e42fefa39efp-1;
+    static const double kSqrt2 = 0x1.6a09e667f3bcdp+0;
+    static const double kC[13] = {1.0,        1.0 / 3.0,  1.0 / 5.0,  1.0 / 7.0,  1.0 / 9.0,
+                                  1.0 / 11.0, 1.0 / 13.0, 1.0 / 15.0, 1.0 / 17.0, 1.0 / 19.0,
+                                  1.0 / 21.0, 1.0 / 23.0, 1.0 / 25.0};
+    double d = (double)x;
+    uint64_t b;
+    memcpy(&b, &d, sizeof(b));
+    int k = (int)((b >> 52) & 0x7ff) - 1023;
+    b = (b & 0x000fffffffffffffull) | 0x3ff0000000000000ull;
+    double m;
+    memcpy(&m, &b, sizeof(m));
+    if (m > kSqrt2) {
+        m = m * 0.5;
+        k += 1;
+    }
+    const double s = (m - 1.0) / (m + 1.0);
+    const double s2 = s * s;
+    double q = kC[12];
+    for (int j = 11; j >= 0; j--) q = kC[j] + s2 * q;
+    return (double)k * kLn2 + 2.0 * (s * q);
+}
+
+typedef struct {
+    float score;
+    int idx;
+} typ_key;
+
+static int typ_cmp(const void* a, const void* b) {
+    const typ_key* x = (const typ_key*)a;
+    const typ_key* y = (const typ_key*)b;
+    if (x->score < y->score) return -1;
+    if (x->score > y->score) return 1;
+    return (x->idx > y->idx) - (x->idx < y->idx);
+}
+
+int orc_typical_sorted(const float* logits, int V, float typical_p, float* probs, int* order,
+                       float* mass) {
+    /* Decision D16 (cg_sample_typical is declared only in the reference,
+     * include/cg_speculative.h:186; locally typical sampling, Meister et al.
+     * 2023), written in the reference samplers' style: the softmax of
+     * cg_sample_top_p (speculative.c:81-90); L_i = (float)log p_i;
+     * H = sum_i fl(p_i * -L_i) left to right in fp32 (p_i = 0 adds 0);
+     * score_i = |fl(-L_i - H)| (+inf for p_i = 0); tokens ordered by (score
+     * ascending, index ascending); the first `cutoff` of that order with the
+     * cumsum >= typical_p rule of speculative.c:102-107. */
+    orc_temperature_probs(logits, V, 1.0f, probs);
+    float* L = (float*)malloc((size_t)V * sizeof(float));
+    float H = 0.0f;
+    for (int i = 0; i < V; i++) {
+        L[i] = probs[i] > 0.0f ? (float)orc_typ_log(probs[i]) : 0.0f;
+        if (probs[i] > 0.0f) H += probs[i] * -L[i];
+    }
+    typ_key* key = (typ_key*)malloc((size_t)V * sizeof(typ_key));
+    for (int i = 0; i < V; i++) {
+        key[i].score = probs[i] > 0.0f ? fabsf(-L[i] - H) : INFINITY;
+        key[i].idx = i;
+    }
+    qsort(key, (size_t)V, sizeof(typ_key), typ_cmp);
+    float cumsum = 0.0f;
+    int cutoff = V;
+    for (int j = 0; j < V; j++) {
+        order[j] = key[j].idx;
+        if (cutoff == V) {
+            cumsum += probs[key[j].idx];
+            if (cumsum >= typical_p) cutoff = j + 1;
+        }
+    }
+    *mass = cumsum;
+    free(L);
+    free(key);
+    return cutoff;
+}
+
+int orc_sample_typical(const float* logits, int V, float typical_p, float u) {
+    float* probs = (float*)malloc((size_t)V * sizeof(float));
+    int* order = (int*)malloc((size_t)V * sizeof(int));
+    float mass;
+    const int cutoff = orc_typical_sorted(logits, V, typical_p, probs, order, &mass);
+    /* the draw of speculative.c:109-115 over the kept tokens */
+    float r = u * mass, cumsum = 0.0f;
+    int token = order[0];
+    for (int j = 0; j < cutoff; j++) {
+        cumsum += probs[order[j]];
+        if (r < cumsum) {
+            token = order[j];
+            break;
+        }
+    }
+    free(probs);
+    free(order);
+    return token;
+}
+
+void orc_typical_dist(const float* logits, int V, float typical_p, float* dist) {
+    float* probs = (float*)malloc((size_t)V * sizeof(float));
+    int* order = (int*)malloc((size_t)V * sizeof(int));
+    float mass;
+    const int cutoff = orc_typical_sorted(logits, V, typical_p, probs, order, &mass);
+    memset(dist, 0, (size_t)V * sizeof(float));
+    for (int j = 0; j < cutoff; j++) dist[order[j]] = probs[order[j]] / mass;
+    free(probs);
+    free(order);
+}
+
 /* ------------------------------------------------------------ A9 .. A12 */
 
 static uint8_t orc_pack(int8_t a, int8_t b) {

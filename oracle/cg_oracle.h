@@ -92,6 +92,19 @@ void orc_verify_chain_many(const float* target_logits, const float* draft_logits
                            int V, float T, int top_k, float top_p, int* out_tokens,
                            int* n_accepted);
 
+/* Typical sampling (decision D16 of the build; the reference declares
+ * cg_sample_typical, include/cg_speculative.h:186, without a definition).
+ * orc_typ_log: log of a positive float in binary64 by a fixed IEEE sequence
+ * (shared bit for bit with the device).  orc_typical_sorted: probabilities
+ * (probs[V]), the typical order (order[V]) and the kept count; *mass gets
+ * the kept mass.  Pinned by closed forms and brute force in
+ * tests/test_typical_oracle.py. */
+double orc_typ_log(float x);
+int orc_typical_sorted(const float* logits, int V, float typical_p, float* probs, int* order,
+                       float* mass);
+int orc_sample_typical(const float* logits, int V, float typical_p, float u);
+void orc_typical_dist(const float* logits, int V, float typical_p, float* dist);
+
 /* A9-A12: include/cg_quantize.h:155-175, src/quantize/int4.c:10-114. */
 void orc_quantize_int4(const float* x, int n, int group_size,
                        uint8_t* data, float* scales);

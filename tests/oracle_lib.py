@@ -36,6 +36,10 @@ _ORACLE_SIGS = {
     "orc_sample_filtered": (I, [VP, I, F, I, F, F]),
     "orc_verify_chain": (I, [VP, VP, VP, VP, I, I, F, I, F, VP, VP]),
     "orc_verify_chain_many": (None, [VP, VP, VP, VP, I, I, I, F, I, F, VP, VP]),
+    "orc_typ_log": (C.c_double, [F]),
+    "orc_typical_sorted": (I, [VP, I, F, VP, VP, C.POINTER(F)]),
+    "orc_sample_typical": (I, [VP, I, F, F]),
+    "orc_typical_dist": (None, [VP, I, F, VP]),
     "orc_quantize_int4": (None, [VP, I, I, VP, VP]),
     "orc_dequantize_int4": (None, [VP, VP, I, I, VP]),
     "orc_matmul_int4": (None, [VP, I, I, VP, VP, I, I, VP]),
