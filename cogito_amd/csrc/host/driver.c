@@ -8,6 +8,7 @@
  *   cg_speculative_generate    include/cg_speculative.h:71-77    (declared only)
  *   cg_forward_tree_attention  include/cg_speculative.h:128-130  (declared only)
  *   cg_eagle_generate_tree     src/inference/speculative.c:244-262 (a stub there)
+ *   cg_eagle_compute_branching include/cg_speculative.h:160       (declared only)
  *
  * Sequences.  input_ids holds the token ids so far as floats (the form
  * cg_token_tree_to_tensor produces), in host or device memory.  The driver
@@ -691,4 +692,75 @@ cg_token_tree* cg_eagle_generate_tree(cg_eagle_draft* eagle, cg_tensor* input, i
 fail:
     cg_token_tree_free(tree);
     return NULL;
+}
+
+/* Decision D17: the branching factor of a draft node is the number of its
+ * most likely tokens (1..4, cg_sample_top_k's order: probability descending,
+ * ties to the lower id) whose probabilities, summed in that order in fp32,
+ * first reach kBranchMass; a confident draft branches once, an uncertain one
+ * up to four times.  Probabilities are the draft's softmax at T = 1
+ * (cg_sample_temperature's). */
+static const float kBranchMass = 0.8f;
+
+int* cg_eagle_compute_branching(cg_eagle_draft* eagle, cg_tensor* features) {
+    static const char* who = "cg_eagle_compute_branching";
+    if (!eagle || !features || !features->data || features->ndim < 1) {
+        cgx_set_error("%s: an EAGLE draft and a [rows][vocab] tensor of draft logits are "
+                      "required", who);
+        return NULL;
+    }
+    const int V = features->shape[features->ndim - 1];
+    cgx_model* dm = cgx_model_from_handle(eagle->base_draft);
+    if (dm) {
+        cgx_model_config c;
+        cgx_model_get_config(dm, &c);
+        if (c.vocab != V) {
+            cgx_set_error("%s: features have %d columns, the draft's vocabulary is %d", who, V,
+                          c.vocab);
+            return NULL;
+        }
+    }
+    if (V < 2 || features->size % V) {
+        cgx_set_error("%s: features must be [rows][vocab] with vocab >= 2", who);
+        return NULL;
+    }
+    if (cgx_ensure_init()) return NULL;
+    const int rows = features->size / V, K = V < 4 ? V - 1 : 4;
+    const float* x = (const float*)cgx_dev_in(features->data, (size_t)features->size * 4,
+                                              CGX_SLOT_IN0);
+    float* probs = (float*)dbuf(B_TL, (size_t)V * sizeof(float));
+    int* lidx = (int*)dbuf(B_TOK, 4 * sizeof(int));
+    float* lp = (float*)dbuf(B_U, 4 * sizeof(float));
+    int* out = (int*)malloc((size_t)rows * sizeof(int));
+    if (!x || !probs || !lidx || !lp || !out) {
+        free(out);
+        if (x && probs && lidx && lp) cgx_set_error("%s: out of memory", who);
+        return NULL;
+    }
+    for (int r = 0; r < rows; r++) {
+        int idx[4];
+        float pk[4];
+        if (cgk_temperature_probs(x + (size_t)r * V, V, 1.0f, probs) ||
+            cgk_topk_lists(probs, 1, V, K, 1.0f, lidx, lp) ||
+            cgx_memcpy_d2h(idx, lidx, (size_t)K * sizeof(int))) {
+            free(out);
+            return NULL;
+        }
+        for (int j = 0; j < K; j++)
+            if (cgx_memcpy_d2h(&pk[j], probs + idx[j], sizeof(float))) {
+                free(out);
+                return NULL;
+            }
+        int b = K;
+        float mass = 0.0f;
+        for (int j = 0; j < K; j++) {
+            mass += pk[j];
+            if (mass >= kBranchMass) {
+                b = j + 1;
+                break;
+            }
+        }
+        out[r] = b;
+    }
+    return out;
 }

@@ -150,7 +150,11 @@ cg_tensor* cg_forward_tree_attention(
  * cgx_model as base_draft drafts the most likely token at each depth (ties:
  * the lower id) after input (float token ids), with the draft logits in
  * draft_probs; with any other base_draft it returns the reference's
- * placeholder tree (every token 1, src/inference/speculative.c:244-262). */
+ * placeholder tree (every token 1, src/inference/speculative.c:244-262).
+ * cg_eagle_compute_branching takes draft logits [rows][vocab] (host or
+ * device) and returns a malloc'd int[rows] (free with free()): per row the
+ * number of most likely tokens (1..4, top-k order) whose softmax
+ * probabilities, summed in that order, first reach 0.8. */
 typedef struct {
     void* base_draft;
     void* feature_proj;

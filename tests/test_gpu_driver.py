@@ -14,7 +14,9 @@ declared only in the reference) through the C ABI.
 * cg_forward_tree_attention: rows of the causal prefix and of a tree under
   cgx_tree_attention_mask_parents match the oracle stack run over the
   prefix plus each node's ancestor path.
-* cg_eagle_generate_tree: the draft's most likely token at each depth.
+* cg_eagle_generate_tree: the draft's most likely token at each depth;
+  cg_eagle_compute_branching: the number of top tokens reaching 0.8 of the
+  draft's softmax mass (decision D17).
 """
 from __future__ import annotations
 
@@ -307,4 +309,34 @@ def test_eagle_generate_tree(gpu, oracle, rng):
     gpu.cg_token_tree_free(t2)
     gpu.cg_eagle_draft_free(e2)
     gpu.cg_tensor_free(ids)
+    gpu.cgx_model_free(dm)
+
+
+def test_eagle_compute_branching(gpu, oracle, rng):
+    # decision D17: per row, the number of most likely tokens (1..4) whose
+    # softmax probabilities first sum to 0.8, against the oracle's softmax
+    V = DRAFT.vocab
+    x = rng.normal(0, 1, (6, V)).astype(np.float32)
+    x[0, 17] = 20.0                              # confident: one branch
+    x[1, [3, 4]] = 12.0                          # two equal peaks: two
+    x[2] = 0.0                                   # flat: four
+    x[3, [5, 6, 7]] = [9.0, 8.5, 8.0]
+    exp = []
+    for row in x:
+        p = np.zeros(V, np.float32)
+        oracle.orc_temperature_probs(ptr(np.ascontiguousarray(row)), V, 1.0, ptr(p))
+        top = p[np.argsort(-p, kind="stable")[:4]]
+        c = np.add.accumulate(top, dtype=np.float32)
+        hit = np.flatnonzero(c >= np.float32(0.8))
+        exp.append(int(hit[0]) + 1 if hit.size else 4)
+    assert exp[:3] == [1, 2, 4]
+    dm = new_model(gpu, DRAFT, 21)
+    e = gpu.cg_eagle_draft_new(dm)
+    t = host_tensor(gpu, x)
+    out = gpu.cg_eagle_compute_branching(e, t)
+    assert out, last_error(gpu)
+    assert [out[i] for i in range(6)] == exp
+    C.CDLL(None).free(C.cast(out, C.c_void_p))
+    gpu.cg_tensor_free(t)
+    gpu.cg_eagle_draft_free(e)
     gpu.cgx_model_free(dm)
