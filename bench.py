@@ -13,7 +13,10 @@ events on the library stream around the K timed launches.
 Also reported (same JSON line): the GEMV at every M in 1..5, and the CPU
 baseline -- cogito's own cg_matmul_int4 compiled from the reference sources
 (oracle/_ref) or, when that is absent, the C restatement (oracle/), timed on
-this host's cores, single-threaded, on a bounded sample.
+one pinned core of this host on a bounded sample.  The legs carry CPU
+figures of their own: config 1's verify from cogito's softmax and samplers,
+and per-step estimates of configs 3-5 composed from timed pieces (see
+cpu_verify_step).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--rows M]
 """
@@ -75,17 +78,23 @@ def bench_gemv(lib, M_list, K, N, gs, steps, warmup, seed=2024, layout=3):
             raise RuntimeError(f"weight upload failed: {last_error(lib)}")
         dws.append(dq)
     results = {}
+    # one rotation index over every warm-up and timed launch of every M: a
+    # launch reads the copy the previous `copies - 1` launches (> 2x the MALL)
+    # did not touch, whatever --steps is
+    rot = 0
     for M in M_list:
         x = rng.normal(0, 1, (M, K)).astype(np.float32)
         dx = DeviceArray.from_numpy(lib, x)
         dy = DeviceArray(lib, M * N * 4)
-        for i in range(warmup):
-            if lib.cgx_matmul_int4_dev(dx.ptr, M, dws[i % copies], dy.ptr):
+        for _ in range(warmup):
+            if lib.cgx_matmul_int4_dev(dx.ptr, M, dws[rot % copies], dy.ptr):
                 raise RuntimeError(last_error(lib))
+            rot += 1
         lib.cgx_synchronize()
         lib.cgx_event_record(0)
-        for i in range(steps):
-            lib.cgx_matmul_int4_dev(dx.ptr, M, dws[i % copies], dy.ptr)
+        for _ in range(steps):
+            lib.cgx_matmul_int4_dev(dx.ptr, M, dws[rot % copies], dy.ptr)
+            rot += 1
         lib.cgx_event_record(1)
         if lib.cgx_synchronize():
             raise RuntimeError(last_error(lib))
@@ -129,13 +138,16 @@ def bench_gemv_shapes(lib, shapes, M, steps, warmup, gs=128, seed=77):
         del keep, data, scales
         dx = DeviceArray.from_numpy(lib, rng.normal(0, 1, (M, K)).astype(np.float32))
         dy = DeviceArray(lib, M * N * 4)
-        for i in range(warmup):
-            lib.cgx_matmul_int4_dev(dx.ptr, M, dws[i % copies], dy.ptr)
+        rot = 0
+        for _ in range(warmup):
+            lib.cgx_matmul_int4_dev(dx.ptr, M, dws[rot % copies], dy.ptr)
+            rot += 1
         if lib.cgx_synchronize():
             raise RuntimeError(last_error(lib))
         lib.cgx_event_record(0)
-        for i in range(steps):
-            lib.cgx_matmul_int4_dev(dx.ptr, M, dws[i % copies], dy.ptr)
+        for _ in range(steps):
+            lib.cgx_matmul_int4_dev(dx.ptr, M, dws[rot % copies], dy.ptr)
+            rot += 1
         lib.cgx_event_record(1)
         if lib.cgx_synchronize():
             raise RuntimeError(last_error(lib))
@@ -478,58 +490,255 @@ def bench_e2e_tree(lib, name, tgt, drf, ctx, nodes, depth, T, top_k, B, steps, w
             "draft_shares_embed_lm_head": True}
 
 
-def cpu_baseline_gemv(M, K, N, gs, budget_s=12.0, seed=2024):
-    """cogito's cg_matmul_int4 on the host, 1 thread, bounded sample."""
-    sys.path.insert(0, str(ROOT / "tests"))
-    import oracle_lib
-    rng = np.random.default_rng(seed)
-    data, scales = make_config2_weight(rng, K, N, gs)
-    x = rng.normal(0, 1, (M, K)).astype(np.float32)
-    y = np.zeros((M, N), np.float32)
-    ref = oracle_lib.load_ref()
-    if ref is not None:
-        kind = "reference"
-        # build a reference cg_tensor_quant around the arrays
-        q = oracle_lib.RefQuant()
-        shape = (C.c_int * 2)(K, N)
-        zeros = np.zeros_like(scales)
-        q.data = data.ctypes.data_as(C.POINTER(C.c_uint8))
-        q.scales = scales.ctypes.data_as(C.POINTER(C.c_float))
-        q.zeros = zeros.ctypes.data_as(C.POINTER(C.c_float))
-        q.shape = C.cast(shape, C.POINTER(C.c_int))
-        q.ndim, q.size, q.group_size = 2, K * N, gs
-        q.num_groups = K * N // gs
-        tx = oracle_lib.ref_tensor(ref, x)
-        ty = oracle_lib.ref_tensor(ref, y)
+# ------------------------------------------------------------ CPU side
 
-        def run():
-            ref.cg_matmul_int4(tx, C.byref(q), ty)
-    else:
-        kind = "port"
-        orc = oracle_lib.load_oracle()
+def cpu_info() -> dict:
+    """The host's CPU model (lscpu's "Model name", from /proc/cpuinfo), the
+    logical CPUs it has and the ones this process may use."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"model": model or platform.processor() or platform.machine(),
+            "nproc": os.cpu_count(), "usable": len(os.sched_getaffinity(0))}
 
-        def run():
-            orc.orc_matmul_int4(x.ctypes.data, M, K, data.ctypes.data,
-                                scales.ctypes.data, N, gs, y.ctypes.data)
-    run()  # warm-up
+
+class one_core:
+    """Pins the calling thread (the one timing the CPU baseline) to one core
+    of those it may use, and restores its affinity afterwards."""
+
+    def __enter__(self):
+        self.saved = os.sched_getaffinity(0)
+        self.core = max(self.saved)
+        os.sched_setaffinity(0, {self.core})
+        return self.core
+
+    def __exit__(self, *exc):
+        os.sched_setaffinity(0, self.saved)
+        return False
+
+
+def _median_time(run, budget_s, max_runs=50, min_runs=3, warm=True):
+    if warm:
+        run()
     times = []
     t_start = time.perf_counter()
-    while time.perf_counter() - t_start < budget_s or len(times) < 3:
+    while time.perf_counter() - t_start < budget_s or len(times) < min_runs:
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
-        if len(times) >= 50:
+        if len(times) >= max_runs:
             break
-    if kind == "reference":
-        # the reference reports unfreed tensors on stdout at exit
-        ref.cg_tensor_free(tx)
-        ref.cg_tensor_free(ty)
-    med = float(np.median(times))
+    return float(np.median(times)), len(times)
+
+
+def _oracle_libs():
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib
+    return oracle_lib, oracle_lib.load_ref(), oracle_lib.load_oracle()
+
+
+class _RefMatmul:
+    """cogito's cg_matmul_int4 (oracle/_ref) on a random INT4 weight
+    [K, N] with rows x [M, K]; the C restatement when the reference build is
+    absent."""
+
+    def __init__(self, K, N, gs, M, seed=11):
+        self.olib, self.ref, self.orc = _oracle_libs()
+        rng = np.random.default_rng(seed)
+        self.data = rng.integers(0, 256, K * N // 2, dtype=np.uint8)
+        self.scales = rng.uniform(0.005, 0.02, K * N // gs).astype(np.float32)
+        self.x = rng.normal(0, 1, (M, K)).astype(np.float32)
+        self.y = np.zeros((M, N), np.float32)
+        self.K, self.N, self.gs, self.M = K, N, gs, M
+        self.kind = "reference" if self.ref is not None else "port"
+        if self.ref is not None:
+            q = self.olib.RefQuant()
+            self.shape = (C.c_int * 2)(K, N)
+            self.zeros = np.zeros_like(self.scales)
+            q.data = self.data.ctypes.data_as(C.POINTER(C.c_uint8))
+            q.scales = self.scales.ctypes.data_as(C.POINTER(C.c_float))
+            q.zeros = self.zeros.ctypes.data_as(C.POINTER(C.c_float))
+            q.shape = C.cast(self.shape, C.POINTER(C.c_int))
+            q.ndim, q.size, q.group_size = 2, K * N, gs
+            q.num_groups = K * N // gs
+            self.q = q
+            self.tx = self.olib.ref_tensor(self.ref, self.x)
+            self.ty = self.olib.ref_tensor(self.ref, self.y)
+
+    def __call__(self):
+        if self.ref is not None:
+            self.ref.cg_matmul_int4(self.tx, C.byref(self.q), self.ty)
+        else:
+            self.orc.orc_matmul_int4(self.x.ctypes.data, self.M, self.K, self.data.ctypes.data,
+                                     self.scales.ctypes.data, self.N, self.gs,
+                                     self.y.ctypes.data)
+
+    def close(self):
+        if self.ref is not None:
+            self.ref.cg_tensor_free(self.tx)
+            self.ref.cg_tensor_free(self.ty)
+
+
+def cpu_baseline_gemv(M, K, N, gs, budget_s=6.0):
+    """cogito's cg_matmul_int4 on the host, one pinned core, bounded sample."""
+    mm = _RefMatmul(K, N, gs, M, seed=2024)
+    with one_core() as core:
+        med, runs = _median_time(mm, budget_s)
+    mm.close()
     nbytes = gemv_bytes(M, K, N, gs)
+    return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": 1, "kind": mm.kind,
+            "sample": f"cg_matmul_int4 M={M} K={K} N={N} gs={gs}, median of {runs} runs "
+                      f"({med * 1e3:.1f} ms each), 1 thread pinned to core {core}",
+            "cpu": cpu_info()}
+
+
+def cpu_baseline_accept(V=32000, gamma=4, budget_s=3.0, seed=5):
+    """Config 1's verify on the host from cogito's own compiled functions
+    (oracle/_ref): cg_cuda_softmax_forward for the gamma + 1 target and gamma
+    draft rows (src/cuda/tensor_kernels.c:699-740), cg_acceptance_prob per
+    drafted token, then cg_sample_corrected at the first reject or
+    cg_sample_temperature of target row gamma (src/inference/speculative.c:
+    49-75,148-172).  Accept draws are pre-drawn; the samplers draw from the
+    reference's own LCG."""
+    olib, ref, orc = _oracle_libs()
+    rng = np.random.default_rng(seed)
+    t = rng.normal(0, 2, (gamma + 1, V)).astype(np.float32)
+    d = rng.normal(0, 2, (gamma, V)).astype(np.float32)
+    x = _draft_tokens_from(d, rng.random(gamma, dtype=np.float32)).astype(np.int32)
+    u = rng.random(gamma, dtype=np.float32)
+    if ref is None:
+        uu = rng.random(gamma + 1, dtype=np.float32)
+        out = np.zeros(gamma + 1, np.int32)
+
+        def run():
+            orc.orc_verify_chain(t.ctypes.data, d.ctypes.data, x.ctypes.data, uu.ctypes.data,
+                                 gamma, V, 1.0, 0, 1.0, out.ctypes.data, None)
+        kind = "port"
+    else:
+        kind = "reference"
+        tt, td = olib.ref_tensor(ref, t), olib.ref_tensor(ref, d)
+        tp = olib.ref_tensor(ref, np.zeros_like(t))
+        tq = olib.ref_tensor(ref, np.zeros_like(d))
+        P = np.ctypeslib.as_array(tp.contents.data, shape=(gamma + 1, V))
+        Q = np.ctypeslib.as_array(tq.contents.data, shape=(gamma, V))
+
+        def run():
+            ref.cg_cuda_softmax_forward(tt, tp, 1)
+            ref.cg_cuda_softmax_forward(td, tq, 1)
+            for i in range(gamma):
+                a = ref.cg_acceptance_prob(float(Q[i, x[i]]), float(P[i, x[i]]))
+                if not u[i] < a:
+                    ref.cg_sample_corrected(Q[i:].ctypes.data, P[i:].ctypes.data, V)
+                    return
+            ref.cg_sample_temperature(t[gamma:].ctypes.data, V, 1.0)
+    with one_core() as core:
+        med, runs = _median_time(run, budget_s, max_runs=400)
+    if kind == "reference":
+        for tt_ in (tt, td, tp, tq):
+            ref.cg_tensor_free(tt_)
+    nbytes = (2 * gamma + 1) * V * 4
     return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
-            "sample": f"cg_matmul_int4 M={M} K={K} N={N} gs={gs}, median of "
-                      f"{len(times)} runs ({med * 1e3:.1f} ms each), 1 thread",
-            "cpu": platform.processor() or platform.machine()}
+            "us_per_call": round(med * 1e6, 2),
+            "sample": f"config 1 verify (V={V}, gamma={gamma}, T=1) from cogito's softmax, "
+                      f"acceptance ratio and samplers, median of {runs} runs, 1 thread pinned "
+                      f"to core {core}"}
+
+
+_ROW_TIMES: dict = {}   # cg_matmul_int4 seconds per row, by weight shape
+
+
+def cpu_verify_step(tgt, drf, ctx, target_rows, draft_rows, batch, T, top_k, top_p,
+                    tokens_per_step, sampler_rows, budget_s=0.6):
+    """Host time of one speculative step of a synthetic stack, composed from
+    timed pieces (the full step is minutes of single-core work at these
+    shapes; the pieces are timed once and scaled):
+      - every linear shape of the target and the draft through cogito's
+        cg_matmul_int4 at one row, scaled by the rows of the step (the
+        reference loop is O(M K N): each row re-reads and dequantises W) and
+        by the layer count;
+      - one layer of attention (the C restatement of cogito's GQA flash
+        forward, src/cuda/flash_attn_kernels.c:261-396) at the step's query
+        rows and context, scaled by the layer count;
+      - the samplers the step runs, as cogito's own (cg_sample_temperature,
+        or cg_sample_top_p with its O(V^2) sort when top-p is on), one call
+        timed and scaled by the number of rows sampled.
+    RMSNorm, SwiGLU, RoPE and the KV writes (O(rows * d)) are left out.
+    Returns the estimate and its parts; "verified tok/s" uses the GPU leg's
+    tokens per step, so both sides are compared at the same acceptance."""
+    olib, ref, orc = _oracle_libs()
+    parts = {}
+    M_t = target_rows * batch           # target rows per step (one forward)
+    M_d = draft_rows * batch            # draft rows per step
+
+    def linears(cfg):
+        L, d, H, Hk, hd, ff, V = cfg
+        return [("qkv", d, (H + 2 * Hk) * hd), ("o", H * hd, d), ("gate_up", d, 2 * ff),
+                ("down", ff, d)], ("lm_head", d, V)
+
+    total = 0.0
+    with one_core() as core:
+        for who, cfg, M in (("target", tgt, M_t), ("draft", drf, M_d)):
+            lin, head = linears(cfg)
+            L = cfg[0]
+            for name, K, N in lin + [head]:
+                if (K, N) not in _ROW_TIMES:
+                    mm = _RefMatmul(K, N, 128, 1)
+                    _ROW_TIMES[(K, N)] = _median_time(mm, budget_s, max_runs=5, min_runs=1,
+                                                      warm=K * N < 1 << 26)[0]
+                    mm.close()
+                t1 = _ROW_TIMES[(K, N)]
+                reps = M * (L if name != "lm_head" else 1)
+                parts[f"{who}.{name} {K}x{N}"] = {"s_one_row": round(t1, 6), "rows": reps}
+                total += t1 * reps
+            L, d, H, Hk, hd, ff, V = cfg
+            Nq = target_rows if who == "target" else 1
+            Nk = ctx + Nq
+            rng = np.random.default_rng(3)
+            Q = rng.normal(0, 1, (Nq, H, hd)).astype(np.float32)
+            Kc = rng.normal(0, 1, (Nk, Hk, hd)).astype(np.float32)
+            Vc = rng.normal(0, 1, (Nk, Hk, hd)).astype(np.float32)
+            O = np.zeros_like(Q)
+            sc = 1.0 / np.sqrt(hd)
+
+            def attn():
+                orc.orc_flash_fwd(Q.ctypes.data, Kc.ctypes.data, Vc.ctypes.data, O.ctypes.data,
+                                  None, 1, Nq, Nk, H, Hk, hd, sc, 4, 0, None)
+            big = Nq * Nk * H * hd > 1 << 26
+            ta, _ = _median_time(attn, 0.0 if big else budget_s, max_runs=5, min_runs=1,
+                                 warm=not big)
+            reps = L * (batch if who == "target" else M_d)
+            parts[f"{who}.attention Nq={Nq} Nk={Nk}"] = {"s_one": round(ta, 6), "count": reps}
+            total += ta * reps
+        V = tgt[6]
+        rng = np.random.default_rng(4)
+        row = rng.normal(0, 2, V).astype(np.float32)
+        f32p = row.ctypes.data
+        if top_p < 1.0 and (top_k <= 0 or top_k >= V):
+            fn, name = (lambda: ref.cg_sample_top_p(f32p, V, top_p)), "cg_sample_top_p"
+        elif 0 < top_k < V:
+            fn, name = (lambda: ref.cg_sample_top_k(f32p, V, top_k)), "cg_sample_top_k"
+        else:
+            fn, name = (lambda: ref.cg_sample_temperature(f32p, V, T)), "cg_sample_temperature"
+        if ref is None:
+            fn, name = (lambda: orc.orc_sample_filtered(f32p, V, T, top_k, top_p, 0.5)), \
+                "orc_sample_filtered"
+        ts, _ = _median_time(fn, 0.0, max_runs=1, min_runs=1, warm=False)
+        parts[f"sampler {name} V={V}"] = {"s_one": round(ts, 6), "rows": sampler_rows}
+        total += ts * sampler_rows
+    return {"value": round(tokens_per_step / total, 4), "unit": "verified tok/s", "cores": 1,
+            "kind": "reference" if ref is not None else "port",
+            "s_per_step": round(total, 3), "parts": parts,
+            "sample": f"one step composed from pieces timed once on 1 thread pinned to core "
+                      f"{core} and scaled by their counts (cg_matmul_int4 per row and layer, "
+                      f"attention per layer, the sampler per sampled row); RMSNorm, SwiGLU, "
+                      f"RoPE and KV writes left out; the GPU leg's {tokens_per_step} tokens "
+                      f"per step"}
 
 
 def main() -> int:
@@ -596,31 +805,56 @@ def main() -> int:
             lib, [("qkv", d, (32 + 2 * 8) * hd), ("o", d, d), ("gate_up", d, 2 * ff),
                   ("down", ff, d), ("lm_head", d, 32000), ("lm_head_128k", d, 128256)],
             args.rows, max(50, args.steps // 4), 10)
+    cpu_on = not args.no_cpu
     if "accept" in legs:
         extra["accept_c1"] = bench_accept(lib, 32000, 1, 4, 1.0, args.steps, args.warmup)
         extra["accept_roofline"] = bench_accept(lib, 128256, 64, 4, 1.0, 50, 5, sets=2)
+        if cpu_on:
+            extra["accept_c1"]["cpu_baseline"] = cpu_baseline_accept()
+            log(f"[bench] CPU C1 verify: {extra['accept_c1']['cpu_baseline']['us_per_call']} "
+                f"us/call")
     if "attn" in legs:
         extra["attention_7b"] = bench_attention(lib, 4096, 5, 32, 8, 128, 128, args.steps,
                                                 args.warmup)
     if "e2e" in legs or "c3" in legs:
-        extra["e2e_tiny_c3"] = bench_e2e(
-            lib, "C3 tiny", (12, 768, 12, 12, 64, 3072, 32000),
-            (2, 768, 12, 12, 64, 3072, 32000), False, 1024, 4, 0.8, 0, 0.9, 100, 10)
+        c3t, c3d = (12, 768, 12, 12, 64, 3072, 32000), (2, 768, 12, 12, 64, 3072, 32000)
+        extra["e2e_tiny_c3"] = bench_e2e(lib, "C3 tiny", c3t, c3d, False, 1024, 4, 0.8, 0,
+                                         0.9, 100, 10)
+        if cpu_on:
+            # top-p sorts: the 4 draft draws and the 9 verified rows
+            extra["e2e_tiny_c3"]["cpu_baseline"] = cpu_verify_step(
+                c3t, c3d, 1024, 5, 4, 1, 0.8, 0, 0.9,
+                extra["e2e_tiny_c3"]["tokens_per_step"], 13)
     if "e2e" in legs or "c4" in legs:
-        extra["e2e_7b_c4"] = bench_e2e(
-            lib, "C4 7B-shape", (32, 4096, 32, 8, 128, 11008, 32000),
-            (1, 4096, 32, 8, 128, 11008, 32000), True, 4096, 4, 1.0, 0, 1.0, 40, 5)
+        c4t, c4d = (32, 4096, 32, 8, 128, 11008, 32000), (1, 4096, 32, 8, 128, 11008, 32000)
+        extra["e2e_7b_c4"] = bench_e2e(lib, "C4 7B-shape", c4t, c4d, True, 4096, 4, 1.0, 0,
+                                       1.0, 40, 5)
+        if cpu_on:
+            # softmax-sized passes: 4 draft draws, 9 verified rows, the last draw
+            extra["e2e_7b_c4"]["cpu_baseline"] = cpu_verify_step(
+                c4t, c4d, 4096, 5, 4, 1, 1.0, 0, 1.0,
+                extra["e2e_7b_c4"]["tokens_per_step"], 14)
     if "e2e" in legs or "batch" in legs:
-        extra["e2e_7b_c4_b8"] = bench_e2e_batch(
-            lib, "C4 7B-shape batch 8", (32, 4096, 32, 8, 128, 11008, 32000),
-            (1, 4096, 32, 8, 128, 11008, 32000), 4096, 4, 1.0, 8, 20, 3)
+        c4t, c4d = (32, 4096, 32, 8, 128, 11008, 32000), (1, 4096, 32, 8, 128, 11008, 32000)
+        extra["e2e_7b_c4_b8"] = bench_e2e_batch(lib, "C4 7B-shape batch 8", c4t, c4d, 4096,
+                                                4, 1.0, 8, 20, 3)
+        if cpu_on:
+            extra["e2e_7b_c4_b8"]["cpu_baseline"] = cpu_verify_step(
+                c4t, c4d, 4096, 5, 4, 8, 1.0, 0, 1.0,
+                extra["e2e_7b_c4_b8"]["tokens_per_step"], 14 * 8)
     if "tree" in legs:
-        extra["e2e_7b_c5_tree"] = bench_e2e_tree(
-            lib, "C5 7B-shape tree", (32, 4096, 32, 8, 128, 11008, 128256),
-            (1, 4096, 32, 8, 128, 11008, 128256), 2048, 64, 6, 0.7, 50, 4, 10, 2)
+        c5t, c5d = (32, 4096, 32, 8, 128, 11008, 128256), (1, 4096, 32, 8, 128, 11008, 128256)
+        extra["e2e_7b_c5_tree"] = bench_e2e_tree(lib, "C5 7B-shape tree", c5t, c5d, 2048, 64,
+                                                 6, 0.7, 50, 4, 10, 2)
+        if cpu_on:
+            # every node drafted and verified; top-k lists of 64 draft and 64
+            # target rows per sequence
+            extra["e2e_7b_c5_tree"]["cpu_baseline"] = cpu_verify_step(
+                c5t, c5d, 2048, 64, 64, 4, 0.7, 50, 1.0,
+                extra["e2e_7b_c5_tree"]["tokens_per_step"], 128 * 4)
 
     cpu = None
-    if not args.no_cpu:
+    if cpu_on:
         log("[bench] CPU baseline (cogito cg_matmul_int4, 1 thread) ...")
         cpu = cpu_baseline_gemv(args.rows, K, N, gs)
         log(f"[bench] CPU: {cpu['value']:.3f} GB/s ({cpu['kind']})")
