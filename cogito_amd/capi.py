@@ -259,6 +259,7 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_kv_cache_int4_write": (I, [PKV, I, I, VP, VP, I]),
     "cgx_kv_cache_int4_set_len": (I, [PKV, I]),
     "cgx_attention_int4_kv_dev": (I, [VP, I, I, PKV, I, I, VP, VP]),
+    "cgx_attention_int4_kv_batch_dev": (I, [VP, I, I, I, PKV, I, VP, I, VP, I, VP]),
     # synthetic decoder and the speculative loop
     "cgx_model_new": (VP, [C.POINTER(CgxModelConfig), C.c_uint64, VP]),
     "cgx_model_free": (None, [VP]),

@@ -166,6 +166,35 @@ void cg_kv_cache_int4_get(cg_kv_cache_int4* c, int layer, cg_tensor* k_out,
 
 /* ------------------------------------------------------------ attention */
 
+int cgx_attention_int4_kv_batch_dev(const float* Q, int B, int Nq, int H, cg_kv_cache_int4* c,
+                                    int slot0, const int* nk, int mask_kind,
+                                    const unsigned long long* anc, int tw, float* O) {
+    if (!Q || !O || !c || !nk || B < 1 || Nq <= 0 || H <= 0 || slot0 < 0 ||
+        slot0 + B > c->num_layers || (mask_kind != 0 && mask_kind != 1) ||
+        (mask_kind == 1 && !anc)) {
+        cgx_set_error("cgx_attention_int4_kv_batch_dev: invalid argument");
+        return -1;
+    }
+    for (int b = 0; b < B; b++)
+        if (nk[b] < Nq || nk[b] > c->max_seq_len) {
+            cgx_set_error("cgx_attention_int4_kv_batch_dev: sequence %d has %d keys (need %d.."
+                          "%d)", b, nk[b], Nq, c->max_seq_len);
+            return -1;
+        }
+    if (c->group_size != c->head_dim) {
+        cgx_set_error("cgx_attention_int4_kv_batch_dev: the batched kernel needs one scale per "
+                      "head row (group_size == head_dim)");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    const size_t lb = layer_bytes(c), lg = layer_groups(c);
+    return cgk_attn_dec_batch(Q, c->k_cache + lb * slot0, c->v_cache + lb * slot0,
+                              c->k_scales + lg * slot0, c->v_scales + lg * slot0, B, nk, lb, lg,
+                              Nq, H, c->n_heads, c->head_dim, 1.0f / sqrtf((float)c->head_dim),
+                              mask_kind == 1 ? CGK_MASK_TREE : CGK_MASK_CAUSAL_ALIGNED, anc, tw,
+                              O);
+}
+
 int cgx_attention_int4_kv_dev(const float* Q, int Nq, int H, cg_kv_cache_int4* c,
                               int layer, int mask_kind, const int* parents, float* O) {
     if (!Q || !O || !c || Nq <= 0 || H <= 0 || layer < 0 || layer >= c->num_layers) {

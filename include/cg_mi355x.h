@@ -189,6 +189,17 @@ int cgx_attention_int4_kv_dev(const float* Q, int Nq, int H,
                               cg_kv_cache_int4* cache, int layer_idx,
                               int mask_kind, const int* parents, float* O);
 
+/* The batched decode/verify attention of the decoder (test hook): B
+ * sequences, sequence b's keys in cache layer slot slot0 + b (the batched
+ * models' layout), nk[b] keys each (host array), Q/O [B][Nq][H][D] device.
+ * mask_kind 0: chain (query i sees keys < nk[b] - Nq + i + 1); 1: tree, the
+ * last tw keys (Nq <= tw <= 64) visible to query i where bit j of anc[i]
+ * (host array of Nq masks) is set.  Needs group_size == head_dim. */
+int cgx_attention_int4_kv_batch_dev(const float* Q, int B, int Nq, int H,
+                                    cg_kv_cache_int4* cache, int slot0, const int* nk,
+                                    int mask_kind, const unsigned long long* anc, int tw,
+                                    float* O);
+
 /* ------------------------------------------------- synthetic decoder */
 /* Decoder-only transformer with INT4 weights resident in HBM, the model the
  * verify stack runs (reference src/layers/transformer.c:26-149 block order,

@@ -267,6 +267,66 @@ def test_attention_int4_tree(gpu, oracle, rng, H, Hk, D, ctx, Nq, gs):
     gpu.cg_kv_cache_int4_free(c)
 
 
+BATCH_CASES = [
+    # B, Nq, tree, keys per sequence: uneven lengths, empty trailing splits
+    (8, 5, False, [4101, 3000, 4096, 17, 2048, 4101, 5, 3333]),     # 4 key splits
+    (8, 64, True, [1200, 64, 700, 1500, 90, 1024, 333, 1100]),      # one split
+    (4, 64, True, [2112, 2112, 2112, 2112]),                        # config 5 shape
+    (2, 5, False, [4101, 1000]),
+]
+
+
+@pytest.mark.parametrize("B,Nq,tree,nks", BATCH_CASES)
+def test_attention_int4_batch(gpu, oracle, rng, B, Nq, tree, nks):
+    # the decoder's batched kernel (sequence b in cache slot b, nk[b] keys)
+    # against the oracle on each sequence, 7B head shape
+    print(f"batch attention B={B} Nq={Nq} tree={tree} nk={nks}", flush=True)
+    H, Hk, D, gs = 32, 8, 128, 128
+    S = max(nks)
+    c = gpu.cg_kv_cache_int4_new(B, S, Hk, D, gs)
+    assert c, last_error(gpu)
+    refs = []
+    for b, n in enumerate(nks):
+        k = rng.normal(0, 1, (n, Hk, D)).astype(np.float32)
+        v = rng.normal(0, 1, (n, Hk, D)).astype(np.float32)
+        assert gpu.cgx_kv_cache_int4_write(c, b, 0, k.ctypes.data, v.ctypes.data, n) == 0, \
+            last_error(gpu)
+        ko, vo = oracle_kv_get(oracle, *oracle_kv_fill(oracle, k, v, Hk, D, gs, n), n, Hk, D,
+                               gs)
+        refs.append((ko[None], vo[None]))
+    anc = np.zeros(Nq, np.uint64)
+    if tree:
+        parents = random_tree(rng, Nq)
+        for i in range(Nq):
+            anc[i] = (1 << i) | (int(anc[parents[i]]) if parents[i] >= 0 else 0)
+    Q = rng.normal(0, 1, (B, Nq, H, D)).astype(np.float32)
+    dq = DeviceArray.from_numpy(gpu, Q)
+    do = DeviceArray.from_numpy(gpu, np.zeros_like(Q))
+    nk = np.array(nks, np.int32)
+    assert gpu.cgx_attention_int4_kv_batch_dev(dq.ptr, B, Nq, H, c, 0, nk.ctypes.data,
+                                               1 if tree else 0,
+                                               anc.ctypes.data if tree else None, Nq,
+                                               do.ptr) == 0, last_error(gpu)
+    got = do.numpy(np.float32, Q.shape)
+    scale = float(np.float32(1.0 / np.sqrt(D)))
+    for b, n in enumerate(nks):
+        K, V = refs[b]
+        if tree:
+            mask = np.zeros((Nq, n), np.float32)
+            for i in range(Nq):
+                for j in range(Nq):
+                    if not (int(anc[i]) >> j) & 1:
+                        mask[i, n - Nq + j] = -np.inf
+            exp, _ = orc_attention(oracle, Q[b:b + 1], K, V, H, Hk, scale, 3, mask=mask)
+        else:
+            exp, _ = orc_attention(oracle, Q[b:b + 1], K, V, H, Hk, scale, 4)
+        err = rel_err_rows(got[b].reshape(-1, D), exp.reshape(-1, D))
+        assert err <= TOL, (b, n, err)
+    dq.free()
+    do.free()
+    gpu.cg_kv_cache_int4_free(c)
+
+
 def test_attention_int4_errors(gpu, rng):
     c = gpu.cg_kv_cache_int4_new(1, 8, 2, 32, 32)
     Q = DeviceArray.from_numpy(gpu, np.zeros((3, 2, 32), np.float32))
