@@ -34,6 +34,9 @@ HIP_FLAGS = [
 # contraction of a*b+c into fma).
 EXACT_FP = {"accept.hip", "int4.hip", "filter.hip", "tree.hip"}
 C_FLAGS = ["-O2", "-fPIC", "-std=c11", "-Wall", "-Wextra", "-Wno-unused-parameter",
+           # a call to an undeclared function (e.g. POSIX strdup under C11)
+           # would truncate a returned pointer to int
+           "-Werror=implicit-function-declaration",
            f"-I{INCLUDE}", f"-I{CSRC}"]
 
 

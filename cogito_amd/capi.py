@@ -210,6 +210,10 @@ SIGNATURES: dict[str, tuple] = {
     "cg_rope_precompute_freqs": (None, [VP, VP, I, I, F]),
     "cg_alibi_bias": (None, [VP, I, I, I, VP]),
     "cg_alibi_slopes": (None, [VP, I]),
+    # cg_serialization.h
+    "cg_save_model": (None, [C.c_char_p, C.POINTER(PT), C.POINTER(C.c_char_p), I]),
+    "cg_load_model": (None, [C.c_char_p, C.POINTER(C.POINTER(PT)),
+                             C.POINTER(C.POINTER(C.c_char_p)), C.POINTER(I)]),
     # cg_mi355x.h
     "cgx_init": (I, [I]),
     "cgx_last_error": (C.c_char_p, []),
@@ -255,6 +259,9 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_sort_rows_dev": (I, [VP, VP, I, I, I, VP, VP]),
     "cgx_typ_log_dev": (I, [VP, VP, I]),
     "cgx_exp_fast_maxerr_dev": (I, [F, F, VP]),
+    "cgx_save_quantized": (I, [C.c_char_p, C.POINTER(PQ), C.POINTER(C.c_char_p), I]),
+    "cgx_load_quantized": (I, [C.c_char_p, C.POINTER(C.POINTER(PQ)),
+                               C.POINTER(C.POINTER(C.c_char_p)), C.POINTER(I)]),
     "cgx_kv_cache_int4_truncate": (I, [PKV, I]),
     "cgx_kv_cache_int4_write": (I, [PKV, I, I, VP, VP, I]),
     "cgx_kv_cache_int4_set_len": (I, [PKV, I]),

@@ -21,6 +21,7 @@
 #include "cg_quantize.h"
 #include "cg_speculative.h"
 #include "cg_flash_attn.h"
+#include "cg_serialization.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -171,6 +172,20 @@ int cgx_sort_rows_dev(const uint32_t* keys, const uint32_t* payload, int rows, i
  * an unsigned max into *out_dev as the float's bits (caller zeroes it).  The
  * certified sampler paths assume it stays within 2^-20 on [-87, 0]. */
 int cgx_exp_fast_maxerr_dev(float lo, float hi, unsigned int* out_dev);
+
+/* ------------------------------------------------ INT4 tensors on disk */
+/* COG1 files (cg_serialization.h) holding INT4 tensors: each tensor is an
+ * entry "<name>" of the reference's INT4 dtype 2 (shape[0..ndim) the logical
+ * shape, shape[7] the group size, data the reference's packed nibbles) and
+ * an fp32 entry "<name>.scales" of num_groups values.  Tensors may be host
+ * or flat device tensors (cgx_quant_to_device_flat); names up to 56
+ * characters.  The loader returns host tensors (free each with
+ * cg_tensor_quant_free, the arrays and names with free()); other entries of
+ * the file are skipped. */
+int cgx_save_quantized(const char* filename, cg_tensor_quant* const* tensors,
+                       const char* const* names, int count);
+int cgx_load_quantized(const char* filename, cg_tensor_quant*** out_tensors,
+                       char*** out_names, int* out_count);
 
 /* ----------------------------------------------------------- KV cache */
 /* Drops positions >= new_len (rollback after a rejected draft). */

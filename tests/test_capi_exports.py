@@ -11,7 +11,7 @@ from cogito_amd import capi
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADERS = ["cg_tensor.h", "cg_quantize.h", "cg_speculative.h", "cg_flash_attn.h",
-           "cg_mi355x.h"]
+           "cg_serialization.h", "cg_mi355x.h"]
 
 
 def declared_functions() -> set[str]:
