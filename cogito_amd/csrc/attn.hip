@@ -500,7 +500,9 @@ extern "C" int cgk_attention(const float* Q, int int4, const uint8_t* kc, const 
         cgx_set_error("attention: tree mask needs ancestor bits for at most 64 new tokens");
         return -1;
     }
-    if (int4 && !lse && cgk_attn_dec_supported(D, gs, B, mask_kind))
+    // the decode kernel reads Q and the K cache and writes O in 16-byte units
+    const int aligned = !(((uintptr_t)Q | (uintptr_t)O | (uintptr_t)kc) & 15);
+    if (int4 && !lse && aligned && cgk_attn_dec_supported(D, gs, B, mask_kind))
         return cgk_attn_dec(Q, kc, vc, ks, vs, Nq, Nk, H, Hk, D, scale, mask_kind, anc, O);
     AttnArgs a;
     a.Q = Q; a.int4 = int4; a.kc = kc; a.vc = vc; a.ks = ks; a.vs = vs; a.gs = gs;

@@ -19,10 +19,14 @@
 // fp32 score of its key.
 //
 // Work split.  Block = (key split, KV head, chunk of 16*RT query rows), 4
-// waves; wave w takes the 32-key tiles w, w+4, ... of the split (a split is
-// one round of 128 keys unless the context is very long, so the 7B verify
-// shape runs ~260 blocks); the first tile's loads are issued before the Q
-// operands are built.  In the
+// waves; wave w takes the 32-key tiles w, w+4, ... of the split.  The launch
+// picks RT (16 or 32 rows per block) and the split length from the shape
+// (see cgk_attn_dec_batch).  A block loads its Q rows, then issues its first
+// tile, and builds the Q operands while the tile is in flight (the barrier
+// that publishes them orders LDS only); every tile is loaded by the same
+// branch-free sequence (keys past the split's end are clamped and masked),
+// the loop prefetches the next tile, and the last tile is peeled off so no
+// load is issued past the split.  In the
 // S^T orientation a lane holds one query row and 8 keys of a tile -- exactly
 // the B operand of the P^T side, so P never moves.  V^T needs each lane to
 // hold 8 keys of one head-dim column: the lane loads one u32 (8 columns) of
@@ -47,6 +51,11 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kWaves = 4;
 constexpr int kTile = 32;                  // keys per wave tile
 constexpr int kSplitKeys = kWaves * kTile; // keys per block round
+// launch shape: about this many blocks with 16 / 32 query rows per block,
+// at most this many key splits (the combine reads every split's partial rows)
+constexpr int kTargetBlocks1 = 256;
+constexpr int kTargetBlocks2 = 384;
+constexpr int kMaxSplits = 40;
 
 inline hipStream_t stream() { return (hipStream_t)cgx_stream(); }
 
@@ -130,20 +139,31 @@ __device__ __forceinline__ void split16(float v, _Float16& hi, _Float16& lo) {
     lo = (_Float16)(v - (float)hi);
 }
 
+// Workgroup barrier that orders LDS accesses only: global loads in flight
+// stay in flight (__syncthreads() would wait for every one of them).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // key of MFMA position pos (0..31) of a tile: positions 8g..8g+3 are keys
 // 4g..4g+3, positions 8g+4..8g+7 are keys 16+4g..16+4g+3 (the S^T rows a
 // lane of group g holds)
 __device__ __forceinline__ int key_of_pos(int g, int p) { return p < 4 ? 4 * g + p : 16 + 4 * g + p - 4; }
 
 template <int D, int RT>
-__global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
+__global__ __launch_bounds__(64 * kWaves, 2) void k_attn_dec(DecArgs a) {
     constexpr int NC = D / 32;          // QK MFMAs per 16 keys (32 head-dim values each)
     constexpr int DPL = D / 4;          // head-dim values per lane group
     constexpr int ROWS = 16 * RT;
     // LDS: the Q^T operands (read back per tile, which keeps them out of
-    // the register file), and the waves' partial O at the end
-    __shared__ float s_o[kWaves][ROWS][D + 4];
-    __shared__ f16x8 s_q[RT][NC][2][64];
+    // the register file), then, in the same bytes, the waves' partial O
+    constexpr int kQBytes = RT * NC * 2 * 64 * (int)sizeof(f16x8);
+    constexpr int kOBytes = kWaves * ROWS * (D + 4) * (int)sizeof(float);
+    __shared__ __attribute__((aligned(16))) unsigned char s_raw[kOBytes > kQBytes ? kOBytes : kQBytes];
+    f16x8 (*s_q)[NC][2][64] = (f16x8 (*)[NC][2][64])s_raw;
+    float (*s_o)[ROWS][D + 4] = (float (*)[ROWS][D + 4])s_raw;
     __shared__ float s_m[kWaves][ROWS], s_l[kWaves][ROWS];
     __shared__ float s_w[kWaves][ROWS], s_M[ROWS], s_L[ROWS];
 
@@ -191,15 +211,29 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
         uint32_t vw[8];
         float sk[8], sv[8];
     };
+    // one load sequence for every tile (a single code path keeps the
+    // compiler's load counters exact, so a wait for one tile never waits for
+    // the next): keys past k_end read the last key (its values are masked),
+    // addresses are 32-bit offsets (key * row bytes) from uniform bases.
+    // Lane (n, g) reads K rows n and 16 + n (head-dim part g), and the V word
+    // and K / V scales of its keys 4g + koff(p), koff = {0, 1, 2, 3, 16, 17,
+    // 18, 19} (key_of_pos); lanes n >= D/8 read V column block 0, whose O^T
+    // rows are never stored.
+    const int nb = n < D / 8 ? n : 0;
+    const uint8_t* __restrict__ kbase = kcache + (size_t)hk * (D / 2);
+    const uint8_t* __restrict__ vbase = vcache + (size_t)hk * (D / 2);
+    const float* __restrict__ ksb = kscale + hk;
+    const float* __restrict__ vsb = vscale + hk;
+    const uint32_t krow32 = (uint32_t)krow;
+    const int klast = k_end - 1;
     auto load_tile = [&](int kt, TileData& t) {
 #pragma unroll
         for (int kh = 0; kh < 2; kh++) {
-            int key = kt + 16 * kh + n;
-            key = key < k_end ? key : k_end - 1;
-            const uint8_t* p = kcache + (size_t)key * krow + (size_t)hk * (D / 2) + (D / 8) * g;
+            const uint32_t key = (uint32_t)min(kt + 16 * kh + n, klast);
+            const uint8_t* p = kbase + (key * krow32 + (uint32_t)((D / 8) * g));
             if (NC == 4) {
                 u32x4 v = *(const u32x4*)p;
-                t.kw[kh][0] = v.x; t.kw[kh][1] = v.y; t.kw[kh][2 % NC] = v.z; t.kw[kh][3 % NC] = v.w;
+                t.kw[kh][0] = v.x; t.kw[kh][1 % NC] = v.y; t.kw[kh][2 % NC] = v.z; t.kw[kh][3 % NC] = v.w;
             } else if (NC == 2) {
                 u32x2 v = *(const u32x2*)p;
                 t.kw[kh][0] = v.x; t.kw[kh][1 % NC] = v.y;
@@ -207,24 +241,19 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
                 t.kw[kh][0] = *(const uint32_t*)p;
             }
         }
+        const int kl = kt + 4 * g;
 #pragma unroll
         for (int p = 0; p < 8; p++) {
-            int key = kt + key_of_pos(g, p);
-            key = key < k_end ? key : k_end - 1;
-            // lanes n >= D/8 have no column block: they read block 0 and the
-            // O^T rows they produce are never stored
-            const int nb = n < D / 8 ? n : 0;
-            t.vw[p] = *(const uint32_t*)(vcache + (size_t)key * krow + (size_t)hk * (D / 2) + 4 * nb);
-            t.sk[p] = kscale[(size_t)key * Hk + hk];
-            t.sv[p] = vscale[(size_t)key * Hk + hk];
+            const uint32_t key = (uint32_t)min(kl + (p < 4 ? p : 12 + p), klast);
+            t.vw[p] = *(const uint32_t*)(vbase + (key * krow32 + (uint32_t)(4 * nb)));
+            const uint32_t so = key * (uint32_t)Hk;
+            t.sk[p] = ksb[so];
+            t.sv[p] = vsb[so];
         }
     };
-    TileData td;
-    if (wave < ntiles) load_tile(k_begin + wave * kTile, td);
 
     // ---- Q^T operands of the block's rows (B operand: row n, 8 positions per
-    //      MFMA), built once per block: wave w prepares row tile w % RT's
-    //      head-dim part (w / RT) ... and all waves read them back from LDS
+    //      MFMA), built once per block and read back from LDS by every wave
     float qinv[RT];
     int rq[RT];
     bool rok[RT];
@@ -235,12 +264,32 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
         const int r = row0 + 16 * rt + n;
         rok[rt] = r < R;
         rq[rt] = rok[rt] ? r % a.Nq : 0;
-        anc_row[rt] = a.mask_kind == kMaskTree ? a.anc[rq[rt]] : 0ull;
+        anc_row[rt] = a.anc[rq[rt]];     // zero unless a tree mask
         // chain: keys up to the query's own position; tree: the cached prefix
         // (plus ancestor bits); no mask: every key
         lim_row[rt] = a.mask_kind == kMaskCausal ? Nk - a.Nq + rq[rt]
                     : a.mask_kind == kMaskTree ? Nk - a.tw - 1 : Nk;
     }
+    // the Q rows are loaded first (the previous kernel just wrote them, they
+    // come from cache), then the first tile: the operand preparation below
+    // waits for Q only and overlaps the tile's HBM latency.  Rows past R read
+    // row 0 (valid memory) and are zeroed, so the loads are unconditional.
+    float qv[RT][DPL];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const int r = row0 + 16 * rt + n;
+        const int h = h0 + (rok[rt] ? r / a.Nq : 0), q = rq[rt];
+        const float* qp = Qs + ((size_t)q * a.H + h) * D + DPL * g;
+#pragma unroll
+        for (int i = 0; i < DPL; i += 4) {
+            const float4 t = *(const float4*)(qp + i);
+            qv[rt][i] = t.x; qv[rt][i + 1] = t.y; qv[rt][i + 2] = t.z; qv[rt][i + 3] = t.w;
+        }
+    }
+    // unconditional, like the prefetch below: a wave without a tile reads the
+    // split's last key (k_end >= 1 whenever the block runs)
+    TileData td;
+    load_tile(k_begin + wave * kTile, td);
     {
         // rows are per lane (n); every wave computes the row exponent of its
         // lanes' rows for all RT (cheap), the fp16 splits are divided: wave w
@@ -248,21 +297,13 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
         // (rt * NC + c) % kWaves == w
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
-            const int r = row0 + 16 * rt + n;
-            // rows past R read row 0 (valid memory) and are zeroed: the loads
-            // stay unconditional so they issue together
-            const int h = h0 + (rok[rt] ? r / a.Nq : 0), q = rq[rt];
-            const float* qp = Qs + ((size_t)q * a.H + h) * D + DPL * g;
             const float keep = rok[rt] ? 1.0f : 0.0f;
-            float qv[DPL];
-#pragma unroll
-            for (int i = 0; i < DPL; i += 4) {
-                const float4 t = *(const float4*)(qp + i);
-                qv[i] = t.x * keep; qv[i + 1] = t.y * keep; qv[i + 2] = t.z * keep; qv[i + 3] = t.w * keep;
-            }
             float qmax = 0.0f;
 #pragma unroll
-            for (int i = 0; i < DPL; i++) qmax = fmaxf(qmax, fabsf(qv[i]));
+            for (int i = 0; i < DPL; i++) {
+                qv[rt][i] *= keep;
+                qmax = fmaxf(qmax, fabsf(qv[rt][i]));
+            }
             qmax *= a.scale;
             qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
             qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
@@ -277,7 +318,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
                 f16x8 hv, lv;
 #pragma unroll
                 for (int p = 0; p < 8; p++) {
-                    const float v = qv[8 * c + slot_of(p)] * up;
+                    const float v = qv[rt][8 * c + slot_of(p)] * up;
                     _Float16 hi, lo;
                     split16(v, hi, lo);
                     hv[p] = hi;
@@ -288,12 +329,21 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
             }
         }
     }
-    __syncthreads();
+    // the Q^T operands are in LDS; the first tile's loads stay in flight
+    lds_barrier();
 
-    TileData tn;                     // the next tile, loaded while this one computes
-    for (int tile = wave; tile < ntiles; tile += kWaves) {
+    // keys below open_end are visible to every row: the chain's cached
+    // prefix, the tree's prefix below its window, every key without a mask
+    const int open_end = a.mask_kind == kMaskNone ? Nk : base;
+    // one tile: scores, online softmax, O update.  The loop prefetches the
+    // next tile while it computes; the last tile is peeled off so that no
+    // load is issued past the split (each path keeps exact load counters).
+    auto process = [&](TileData& td, const int tile) {
         const int kt = k_begin + tile * kTile;
-        if (tile + kWaves < ntiles) load_tile(kt + kWaves * kTile, tn);
+        // wave-uniform: the wave's first tile (O and l are still zero), and a
+        // whole tile under no mask
+        const bool first = tile == wave;
+        const bool open = kt + kTile <= k_end && kt + kTile <= open_end;
         uint32_t (&kw)[2][NC] = td.kw;
         uint32_t (&vw)[8] = td.vw;
         float (&sk)[8] = td.sk;
@@ -330,9 +380,9 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
         int ev = 0;
         if (svmax > 0.0f && svmax < __builtin_inff()) ev = 14 - ilogbf(svmax);
         ev = ev > 60 ? 60 : (ev < -60 ? -60 : ev);
-        if (tile != wave && ev > ev_cur) ev = ev_cur;
+        if (!first && ev > ev_cur) ev = ev_cur;
         const float evup = ldexpf(1.0f, ev);
-        const float evshift = tile == wave ? 1.0f : ldexpf(1.0f, ev - ev_cur);
+        const float evshift = first ? 1.0f : ldexpf(1.0f, ev - ev_cur);
         ev_cur = ev;
         float svup[8];
 #pragma unroll
@@ -346,18 +396,27 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
             // scores, mask, online softmax for row (rt, n)
             float val[8];
             float tmax = -__builtin_inff();
+            if (open) {
+                // rows past R score 0 against their zeroed Q and are never stored
 #pragma unroll
-            for (int p = 0; p < 8; p++) {
-                const int kk = kt + key_of_pos(g, p);
-                const bool exists = kk < k_end;
-                // keys <= lim_row are visible; a tree row also sees its
-                // ancestors among the new keys
-                const unsigned rel = (unsigned)(kk - base);
-                const bool anc_bit = rel < 64u && ((anc_row[rt] >> (rel & 63u)) & 1ull);
-                const bool vis = rok[rt] && (kk <= lim_row[rt] || anc_bit);
-                const float sc = s[rt][p >> 2][p & 3] * qinv[rt] * sk[p];
-                val[p] = !exists ? -__builtin_inff() : (vis ? sc : -FLT_MAX);
-                tmax = fmaxf(tmax, val[p]);
+                for (int p = 0; p < 8; p++) {
+                    val[p] = s[rt][p >> 2][p & 3] * qinv[rt] * sk[p];
+                    tmax = fmaxf(tmax, val[p]);
+                }
+            } else {
+#pragma unroll
+                for (int p = 0; p < 8; p++) {
+                    const int kk = kt + key_of_pos(g, p);
+                    const bool exists = kk < k_end;
+                    // keys <= lim_row are visible; a tree row also sees its
+                    // ancestors among the new keys
+                    const unsigned rel = (unsigned)(kk - base);
+                    const bool anc_bit = rel < 64u && ((anc_row[rt] >> (rel & 63u)) & 1ull);
+                    const bool vis = rok[rt] && (kk <= lim_row[rt] || anc_bit);
+                    const float sc = s[rt][p >> 2][p & 3] * qinv[rt] * sk[p];
+                    val[p] = !exists ? -__builtin_inff() : (vis ? sc : -FLT_MAX);
+                    tmax = fmaxf(tmax, val[p]);
+                }
             }
             tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
             tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
@@ -374,10 +433,14 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
                 ph[rt][p] = hi;
                 pl[rt][p] = lo;
             }
-            l_part[rt] = l_part[rt] * alpha + psum;
-            const float oscale = alpha * evshift;
+            if (first) {
+                l_part[rt] = psum;           // O is zero: nothing to rescale
+            } else {
+                l_part[rt] = l_part[rt] * alpha + psum;
+                const float oscale = alpha * evshift;
 #pragma unroll
-            for (int t = 0; t < 8; t++) o[rt][t] *= oscale;
+                for (int t = 0; t < 8; t++) o[rt][t] *= oscale;
+            }
         }
         // -- O^T += V^T P^T (tile t: head-dim columns 8m + t); the V^T operand
         //    of a tile serves every row tile
@@ -396,11 +459,22 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
                 o[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[rt], o[rt][t], 0, 0, 0);
             }
         }
+    };
+    TileData tn;
+    int tile = wave;
+    for (; tile + kWaves < ntiles; tile += kWaves) {
+        load_tile(k_begin + (tile + kWaves) * kTile, tn);
+        process(td, tile);
         td = tn;
     }
+    if (tile < ntiles) process(td, tile);
 
-    // ---- per wave: true-unit O, row max and sum -> LDS
+    // ---- per wave: true-unit O, row max and sum -> LDS (s_o reuses the
+    // bytes of s_q: every wave is past its last read of the Q operands)
+    __syncthreads();
     const float oun = ldexpf(1.0f, -ev_cur);
+    // rows of this block that exist (R may end inside it)
+    const int nvalid = min(ROWS, R - row0);
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
         float l = l_part[rt];
@@ -411,17 +485,24 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
             s_m[wave][row] = m_run[rt];
             s_l[wave][row] = l;
         }
-        // lane holds O^T[m = 4g + i][row] for tile t: head-dim 8m + t
-#pragma unroll
-        for (int t = 0; t < 8; t++)
+        // lane holds O^T[m = 4g + i][row] of tile t: head-dim 8m + t, so for
+        // each i its 8 tiles are 8 consecutive columns
+        if (row < nvalid) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int d = 8 * (4 * g + i) + t;
-                if (d < D) s_o[wave][row][d] = o[rt][t][i] * oun;
+                const int d0 = 8 * (4 * g + i);
+                if (d0 < D) {
+                    float4* dst = (float4*)&s_o[wave][row][d0];
+                    dst[0] = make_float4(o[rt][0][i] * oun, o[rt][1][i] * oun, o[rt][2][i] * oun,
+                                         o[rt][3][i] * oun);
+                    dst[1] = make_float4(o[rt][4][i] * oun, o[rt][5][i] * oun, o[rt][6][i] * oun,
+                                         o[rt][7][i] * oun);
+                }
             }
+        }
     }
     __syncthreads();
-    if (threadIdx.x < ROWS) {
+    if (threadIdx.x < nvalid) {
         const int row = threadIdx.x;
         float M = -__builtin_inff();
 #pragma unroll
@@ -437,54 +518,59 @@ __global__ __launch_bounds__(64 * kWaves) void k_attn_dec(DecArgs a) {
         s_L[row] = L;
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < ROWS * D; e += 64 * kWaves) {
-        const int row = e / D, d = e % D;
+    // four consecutive columns per thread
+    constexpr int kQuads = D / 4;
+    const size_t nrow = (size_t)a.B * a.Nq * a.H;
+    for (int e = threadIdx.x; e < nvalid * kQuads; e += 64 * kWaves) {
+        const int row = e / kQuads, d = 4 * (e % kQuads);
         const int r = row0 + row;
-        if (r >= R) continue;
-        float acc = 0.0f;
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-        for (int w = 0; w < kWaves; w++) acc += s_o[w][row][d] * s_w[w][row];
+        for (int w = 0; w < kWaves; w++) {
+            const float4 v = *(const float4*)&s_o[w][row][d];
+            const float wg = s_w[w][row];
+            acc.x += v.x * wg; acc.y += v.y * wg; acc.z += v.z * wg; acc.w += v.w * wg;
+        }
         const int h = h0 + r / a.Nq, q = r % a.Nq;
         const size_t orow = orow0 + (size_t)q * a.H + h;
         if (a.splits == 1) {
-            a.O[orow * D + d] = s_L[row] > 0.0f ? acc / s_L[row] : 0.0f;
+            const float L = s_L[row];
+            const float4 out = L > 0.0f ? make_float4(acc.x / L, acc.y / L, acc.z / L, acc.w / L)
+                                        : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            *(float4*)&a.O[orow * D + d] = out;
         } else {
-            const size_t nrow = (size_t)a.B * a.Nq * a.H;
-            a.part_o[((size_t)split * nrow + orow) * D + d] = acc;
+            *(float4*)&a.part_o[((size_t)split * nrow + orow) * D + d] = acc;
             if (d == 0) {
-                a.part_ml[((size_t)split * nrow + orow) * 2] = s_M[row];
-                a.part_ml[((size_t)split * nrow + orow) * 2 + 1] = s_L[row];
+                *(float2*)&a.part_ml[((size_t)split * nrow + orow) * 2] =
+                    make_float2(s_M[row], s_L[row]);
             }
         }
     }
 }
 
 // Merge the splits: one block per output row, one thread per head-dim value.
-// The (max, sum) pairs go through LDS; the partial rows are read eight
-// splits at a time with independent loads.
+// Every split's (max, sum) pair is loaded at once into LDS; each thread then
+// forms the maximum, the weights and the weighted sum in split order (the
+// same fixed order for every column), and reads the partial rows eight splits
+// at a time with independent loads.
 __global__ void k_attn_dec_combine(const float* __restrict__ part_o,
                                    const float* __restrict__ part_ml, int splits, int nrow,
                                    int D, float* __restrict__ O) {
     const int row = blockIdx.x, d = threadIdx.x;
-    __shared__ float s_m[128], s_w[128];
-    __shared__ float s_M, s_L;
-    for (int s = d; s < splits; s += blockDim.x) s_m[s] = part_ml[((size_t)s * nrow + row) * 2];
-    __syncthreads();
-    if (d == 0) {
-        float M = -__builtin_inff();
-        for (int s = 0; s < splits; s++) M = fmaxf(M, s_m[s]);
-        s_M = M;
+    __shared__ float s_m[128], s_l[128], s_w[128];
+    for (int s = d; s < splits; s += blockDim.x) {
+        const float2 ml = *(const float2*)(part_ml + ((size_t)s * nrow + row) * 2);
+        s_m[s] = ml.x;
+        s_l[s] = ml.y;
     }
     __syncthreads();
-    const float M = s_M;
+    float M = -__builtin_inff();
+    for (int s = 0; s < splits; s++) M = fmaxf(M, s_m[s]);
     for (int s = d; s < splits; s += blockDim.x)
         s_w[s] = s_m[s] == -__builtin_inff() ? 0.0f : __expf(s_m[s] - M);
     __syncthreads();
-    if (d == 0) {
-        float L = 0.0f;
-        for (int s = 0; s < splits; s++) L += part_ml[((size_t)s * nrow + row) * 2 + 1] * s_w[s];
-        s_L = L;
-    }
+    float L = 0.0f;
+    for (int s = 0; s < splits; s++) L += s_l[s] * s_w[s];
     float acc = 0.0f;
     int s = 0;
     for (; s + 8 <= splits; s += 8) {
@@ -495,8 +581,7 @@ __global__ void k_attn_dec_combine(const float* __restrict__ part_o,
         for (int j = 0; j < 8; j++) acc += v[j] * s_w[s + j];
     }
     for (; s < splits; s++) acc += part_o[((size_t)s * nrow + row) * D + d] * s_w[s];
-    __syncthreads();
-    O[(size_t)row * D + d] = s_L > 0.0f ? acc / s_L : 0.0f;
+    O[(size_t)row * D + d] = L > 0.0f ? acc / L : 0.0f;
 }
 
 template <int D, int RT>
@@ -534,8 +619,8 @@ extern "C" int cgk_attn_dec_batch(const float* Q, const uint8_t* kc, const uint8
                       nkmin, nkmax, H, Hk, D);
         return -1;
     }
-    if (((uintptr_t)Q & 15) || ((uintptr_t)kc & 15) || (seq_kbytes & 15)) {
-        cgx_set_error("attn_dec: Q and the K cache must be 16-byte aligned");
+    if (((uintptr_t)Q & 15) || ((uintptr_t)O & 15) || ((uintptr_t)kc & 15) || (seq_kbytes & 15)) {
+        cgx_set_error("attn_dec: Q, O and the K cache must be 16-byte aligned");
         return -1;
     }
     DecArgs a;
@@ -550,23 +635,29 @@ extern "C" int cgk_attn_dec_batch(const float* Q, const uint8_t* kc, const uint8
     a.seq_groups = seq_groups;
     for (int b = 0; b < kMaxBatch; b++) a.nk[b] = b < B ? nk[b] : 0;
     const int R = (H / Hk) * Nq;
-    // one 16-row tile per block keeps a wave's registers low enough for two
-    // waves per SIMD; more rows run as more blocks (they re-read K/V from cache)
-    const int RT = 1;
+    // rows per block: 32 (RT = 2) dequantises each K/V tile once for both
+    // 16-row halves, 16 (RT = 1) gives twice the blocks.  RT = 2 when RT = 1
+    // would have more than 1024 block rounds of work.  Measured on the 7B head
+    // shape (H 32, Hk 8, D 128), attention plus combine per call: the 5-row
+    // chain at batch 1 (528 rounds) 14.1 us at RT = 1 against 16.6 at RT = 2;
+    // batch 8 (4224) 33.6 against 39.8; the 64-node tree at batch 4 (8704)
+    // 47.4 against 51.4.  The block targets were measured the same way.
+    const int total_rounds = (nkmax + kSplitKeys - 1) / kSplitKeys;
+    const long rounds1 = (long)total_rounds * Hk * B * ((R + 15) / 16);
+    const int RT = (R > 16 && rounds1 > 1024) ? 2 : 1;
+    const int target_blocks = RT == 2 ? kTargetBlocks2 : kTargetBlocks1;
     const int chunks = (R + 16 * RT - 1) / (16 * RT);
     a.chunks = chunks;
-    // keys per split: whole block rounds; splits until the grid has about
-    // 512 blocks (two per CU), at most about 24 (measured on the 7B shape:
-    // at batch 1, 16 blocks per split, 256-key splits beat 128 and 512; at
-    // batch 8 and on the 64-node tree, where one split already has 128 and
-    // 512 blocks, fewer and longer splits won: 6.82 -> 6.49 and 18.5 -> 15.9
-    // ms/step against the fixed 24); the splits follow the longest sequence,
-    // shorter ones leave their last splits empty
-    const int nrb = Hk * B * (((H / Hk) * Nq + 15) / 16);    // blocks of one split
-    int maxsp = 512 / nrb;
-    maxsp = maxsp < 1 ? 1 : (maxsp > 24 ? 24 : maxsp);
-    const int rounds = (nkmax + kSplitKeys * maxsp - 1) / (kSplitKeys * maxsp);
-    int kps = kSplitKeys * (rounds > 1 ? rounds : 1);
+    // keys per split: whole block rounds; about target_blocks blocks, at most
+    // kMaxSplits splits before a split takes more rounds (rounded down, so a
+    // context just past a multiple of the split size adds a split rather than
+    // doubling every split); the splits follow the longest sequence, shorter
+    // ones leave their last splits empty
+    const int nrb = Hk * B * chunks;    // blocks of one split
+    int maxsp = target_blocks / nrb;
+    maxsp = maxsp < 1 ? 1 : (maxsp > kMaxSplits ? kMaxSplits : maxsp);
+    const int rps = total_rounds / maxsp > 1 ? total_rounds / maxsp : 1;
+    int kps = kSplitKeys * rps;
     while ((nkmax + kps - 1) / kps > 128) kps += kSplitKeys;
     const int splits = (nkmax + kps - 1) / kps;
     a.splits = splits;
@@ -582,9 +673,15 @@ extern "C" int cgk_attn_dec_batch(const float* Q, const uint8_t* kc, const uint8
     }
     dim3 grid(splits, Hk, chunks * B);
     int rc;
-    if (D == 128) rc = launch<128, 1>(a, grid);
-    else if (D == 64) rc = launch<64, 1>(a, grid);
-    else rc = launch<32, 1>(a, grid);
+    if (RT == 2) {
+        if (D == 128) rc = launch<128, 2>(a, grid);
+        else if (D == 64) rc = launch<64, 2>(a, grid);
+        else rc = launch<32, 2>(a, grid);
+    } else {
+        if (D == 128) rc = launch<128, 1>(a, grid);
+        else if (D == 64) rc = launch<64, 1>(a, grid);
+        else rc = launch<32, 1>(a, grid);
+    }
     if (rc) return rc;
     if (splits > 1) {
         if (splits > 128) {
