@@ -181,6 +181,32 @@ __device__ __forceinline__ int tie_gap(const int* wc, int m, int gtt, int t) {
     return (t < m ? wc[t] : gtt) - wc[t - 1];
 }
 
+// Length of the shortest prefix of the non-negative values s[0..V) (whole
+// chunks of kCh, V <= kRound) whose sequential fp32 sum certainly exceeds
+// thr, V when none: the fp64 sum P through chunk t bounds the fp32 running
+// sum from below by P (1 - delta_t), the bound of the exact sum's guide for
+// (t + 1) kCh additions of non-negative values.
+__device__ int certified_prefix(const float* s, int V, float thr, EosShared& sh) {
+    const int t = threadIdx.x;
+    float x[kCh];
+    load_vals(RowSrc{s}, V, 0.0f, x);
+    double gs = 0.0;
+#pragma unroll
+    for (int k = 0; k < kCh; k++) gs += (double)x[k];
+    const double inc = wave_incl_sum_d(gs);
+    if (t == 0) sh.result = kThreads;
+    if (lane_id() == 63) sh.wsum[wave_id()] = inc;
+    __syncthreads();
+    double wpre = 0.0;
+    for (int w = 0; w < wave_id(); w++) wpre += sh.wsum[w];
+    const double delta = (double)(t * kCh + kCh + 1) * 0x1p-24 * (1.0 + 0x1p-7) + 0x1p-40;
+    if (t * kCh < V && (wpre + inc) * (1.0 - delta) > (double)thr) atomicMin(&sh.result, t);
+    __syncthreads();
+    const int first = sh.result;
+    __syncthreads();
+    return first >= kThreads ? V : min(V, (first + 1) * kCh);
+}
+
 // Cutoff, draw and (optionally) the filtered distribution of top-p over
 // one row: `probs` (index order) and `sorted` (descending).  ws holds 2V
 // ints per row.
@@ -197,17 +223,37 @@ __global__ __launch_bounds__(kThreads) void k_top_p_finish(
     int* wi = ws + (size_t)row * 2 * V;
     int* wc = wi + V;
     RowSrc s{sr};
-    const float total = eos_sum(s, V, sh);
+    // The cumsum of the descending values: a sequential sum is a prefix of
+    // the longer one, so only the certified prefix that passes the threshold
+    // is summed (the cutoff and the draw lie inside it); this also keeps the
+    // exact sum away from the binade boundary at 1 that the whole row's sum
+    // approaches.  The whole row when no prefix is certified (or V > kRound).
+    const float thr = float_below(top_p);       // cumsum >= top_p <=> thr < cumsum
+    int n = V <= kRound ? certified_prefix(sr, V, thr, sh) : V;
+    float total = eos_sum(s, n, sh);
+    if (n < V && !(thr < total)) {              // excluded by the bound; kept as a guard
+        n = V;
+        total = eos_sum(s, n, sh);
+    }
     float C;
-    const int ci = gen_find_val(s, V, float_below(top_p), -1, total, &C, sh);
+    const int ci = gen_find_val(s, n, thr, -1, total, &C, sh);
     const int cutoff = ci < 0 ? V : ci + 1;
 
     if (tokens) {
         // speculative.c:109-115: r = u * cumsum; first i < cutoff with r < cumsum
         float r = __fmul_rn(u[row], C);
-        int pos = gen_find(s, V, r, 0, sh);
+        int pos = gen_find(s, n, r, 0, sh);
         if (pos >= cutoff) pos = 0;
         float v = sr[pos];
+        // a value held by one element (its sorted neighbours differ): the
+        // token is that element, found by one coalesced pass
+        if ((pos == 0 || sr[pos - 1] != v) && (pos == V - 1 || sr[pos + 1] != v)) {
+            for (int j = threadIdx.x; j < V; j += kThreads)
+                if (pr[j] == v) s_tok = j;
+            __syncthreads();
+            if (threadIdx.x == 0) tokens[row] = s_tok;
+            return;
+        }
         int rank = pos - count_above_sorted(sr, V, v);
         int gtt;
         int m = tie_members(pr, V, v, wi, wc, &gtt, lds);

@@ -26,6 +26,10 @@ def logits_case(rng, V, kind):
         return rng.integers(-3, 3, V).astype(np.float32)
     if kind == "flat":                      # near-uniform, fp32 probability ties
         return rng.normal(0, 0.01, V).astype(np.float32)
+    if kind == "peaked":                    # a few tokens hold almost all the mass
+        return rng.normal(0, 8, V).astype(np.float32)
+    if kind == "spread":                    # the cutoff falls deep in the sorted row
+        return rng.normal(0, 1, V).astype(np.float32)
     if kind == "halves":
         return (np.round(rng.normal(0, 2, V) * 2) / 2).astype(np.float32)
     if kind == "floor":                     # most values at/below -1e30
@@ -57,7 +61,11 @@ def test_sample_top_k_bitexact(gpu, oracle, rng, V, k, kind):
 
 TOPP_CASES = [(1000, 0.9, "ties"), (1000, 0.5, "halves"), (3000, 0.9, "flat"),
               (2000, 1.0, "normal"), (2000, 0.0, "normal"), (500, 0.95, "ties"),
-              (32000, 0.9, "normal"), (32000, 0.9, "flat")]
+              (32000, 0.9, "normal"), (32000, 0.9, "flat"),
+              # the summed prefix of the sorted row: cut after a few tokens, deep in
+              # the row, and top_p close to 1 (the running sum near the binade at 1)
+              (8000, 0.9, "peaked"), (8000, 0.3, "peaked"), (8000, 0.9, "spread"),
+              (8000, 0.999, "normal"), (8000, 0.99999, "peaked")]
 
 
 @pytest.mark.parametrize("V,p,kind", TOPP_CASES)
@@ -174,6 +182,8 @@ FILTER_CASES = [
     (128256, 0.7, 50, 0.9, "normal"),
     (2000, 1.3, 300, 0.8, "halves"),
     (64, 1.0, 20, 1.0, "floor"),
+    (8000, 1.0, 0, 0.999, "peaked"),
+    (8000, 0.8, 0, 0.9, "spread"),
 ]
 
 
