@@ -539,6 +539,32 @@ __device__ __forceinline__ float eos_round(const float (&x)[kCh], const G& g, in
     return eos_tail(own, clean, b, g, rd, n, s_round, sh);
 }
 
+// This thread's chunk g(base .. base + kCh - 1), zero past n.
+template <class G>
+__device__ __forceinline__ void chunk_vals(const G& g, int base, int n, float (&x)[kCh]) {
+#pragma unroll
+    for (int k = 0; k < kCh; k++) x[k] = (base + k < n) ? g(base + k) : 0.0f;
+}
+
+// raw rows: 16-byte loads when the chunk is whole and aligned (a lane's 32
+// consecutive values in 8 loads rather than 32 strided ones)
+__device__ __forceinline__ void chunk_vals(const RowSrc& g, int base, int n, float (&x)[kCh]) {
+    if (base + kCh <= n && ((uintptr_t)(g.p + base) & 15u) == 0) {
+        const float4* q = reinterpret_cast<const float4*>(g.p + base);
+#pragma unroll
+        for (int j = 0; j < kCh / 4; j++) {
+            const float4 v = q[j];
+            x[4 * j] = v.x;
+            x[4 * j + 1] = v.y;
+            x[4 * j + 2] = v.z;
+            x[4 * j + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < kCh; k++) x[k] = (base + k < n) ? g.p[base + k] : 0.0f;
+    }
+}
+
 // Exact ordered sum of g(0..n-1).  Leaves the exact running value at every
 // chunk boundary in sh.cstart / sh.cend (rounds x threads) for gen_find.
 template <class G>
@@ -547,10 +573,8 @@ __device__ __forceinline__ float eos_sum(const G& g, int n, EosShared& sh) {
     const int rounds = (n + kRound - 1) / kRound;
     float s_round = 0.0f;
     for (int rd = 0; rd < rounds; rd++) {
-        const int base = rd * kRound + t * kCh;
         float x[kCh];
-#pragma unroll
-        for (int k = 0; k < kCh; k++) x[k] = (base + k < n) ? g(base + k) : 0.0f;
+        chunk_vals(g, rd * kRound + t * kCh, n, x);
         s_round = eos_round(x, g, rd, n, s_round, sh);
     }
     return s_round;

@@ -133,11 +133,24 @@ __global__ __launch_bounds__(kThreads) void k_probs_rows(const float* __restrict
                                                          float* __restrict__ probs) {
     __shared__ EosShared sh;
     RowSrc src{z + (size_t)blockIdx.x * V};
+    float* pr = probs + (size_t)blockIdx.x * V;
+    if (V <= kRound) {
+        // one round: the row and its exponentials stay in registers
+        float x[kCh], e[kCh];
+        load_vals(src, V, -__builtin_inff(), x);
+        const float m = vals_max(x, sh);
+        vals_exp(x, m, 1.0f, V, e);
+        const float S = eos_sum_vals(e, ExpGen<RowSrc>{src, m, 1.0f}, V, sh);
+        const int base = threadIdx.x * kCh;
+#pragma unroll
+        for (int k = 0; k < kCh; k++)
+            if (base + k < V) pr[base + k] = __fdiv_rn(e[k], S);
+        return;
+    }
     float m = gen_max(src, V, sh);
     ExpGen<RowSrc> e{src, m, 1.0f};
     // the exponentials are evaluated once, into the output row, and summed
     // from there
-    float* pr = probs + (size_t)blockIdx.x * V;
     for (int j = threadIdx.x; j < V; j += kThreads) pr[j] = e(j);
     __threadfence_block();
     __syncthreads();
