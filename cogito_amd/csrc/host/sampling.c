@@ -37,12 +37,16 @@ static int read_token(const int* dev) {
 /* One token from a device logits row with the verify filters (D5): the
  * reference sampler of that filter (A3 / A4 / A5, or the kept-list scan when
  * both filters are on) over z = row / T.  The draw is at du (device); uh is
- * the same value on the host, for the single-block fallback.  z is a V-float
+ * the same value on the host, for the single-block sampler.  z is a V-float
  * device workspace; out a device int. */
 int cgx_sample_row_dev(const float* row, int V, float T, int top_k, float top_p,
                        const float* du, float uh, float* z, int* out) {
     if (!uses_filters(V, top_k, top_p)) {
-        if (cgk_verify_pipe_supported(1, 0, V, T))
+        /* one row of up to 32768 values: the single-workgroup exact sampler
+         * (one launch, the row in registers) beats the chunk-parallel
+         * pipeline's nine launches (C4's draft draws: 3.07 -> 2.93 ms a
+         * step); longer rows take the pipeline */
+        if (V > 32768 && cgk_verify_pipe_supported(1, 0, V, T))
             return cgk_sample_temperature_pipe(row, 1, V, T, du, out, (size_t)V);
         return cgk_sample_temperature(row, V, T, uh, out);
     }
