@@ -111,6 +111,51 @@ def bench_gemv(lib, M_list, K, N, gs, steps, warmup, seed=2024, layout=3):
     return results
 
 
+def bench_floor(lib, nbytes, steps, warmup, seed=31):
+    """A plain streaming read of the headline's algorithmic bytes
+    (cgx_stream_read), rotated over copies like the GEMV: the floor of any
+    kernel that has to read those bytes on this GPU.  The first copy's XOR
+    fold is checked on the host."""
+    from cogito_amd.capi import DeviceArray, last_error
+
+    nbytes = (nbytes + 15) // 16 * 16
+    copies = max(4, -(-2 * MALL_BYTES // nbytes) + 1)
+    rng = np.random.default_rng(seed)
+    host = rng.integers(0, 2**32, nbytes // 4, dtype=np.uint64).astype(np.uint32)
+    bufs = [DeviceArray.from_numpy(lib, host) for _ in range(copies)]
+    blocks = -(-(nbytes // 16) // 512)
+    out = DeviceArray(lib, blocks * 4 * 4)
+    for i in range(warmup):
+        if lib.cgx_stream_read(bufs[i % copies].ptr, nbytes, out.ptr):
+            raise RuntimeError(last_error(lib))
+    got = out.numpy(np.uint32, (blocks * 4,))
+    words = np.zeros(blocks * 512 * 4, np.uint32)
+    words[:host.size] = host
+    exp = np.bitwise_xor.reduce(words.reshape(blocks, 2, 4, 64, 4), axis=(1, 3, 4)).ravel()
+    if not np.array_equal(got, exp):
+        raise RuntimeError("cgx_stream_read: fold mismatch")
+    rot = warmup
+    lib.cgx_synchronize()
+    lib.cgx_event_record(0)
+    for _ in range(steps):
+        lib.cgx_stream_read(bufs[rot % copies].ptr, nbytes, out.ptr)
+        rot += 1
+    lib.cgx_event_record(1)
+    if lib.cgx_synchronize():
+        raise RuntimeError(last_error(lib))
+    us = lib.cgx_event_elapsed_ms(0, 1) / steps * 1e3
+    for b in bufs:
+        b.free()
+    out.free()
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"[bench] plain read of {nbytes} B: {us:.2f} us, {gbs:.0f} GB/s "
+        f"({gbs / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+    return {"bytes": nbytes, "us": round(us, 3), "GB/s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies,
+            "what": "cgx_stream_read: 256-thread blocks, two 16-byte loads per thread, "
+                    "rotated like the headline GEMV; the floor of a kernel reading these bytes"}
+
+
 def _rotations(per_copy: int, floor: int = 2) -> int:
     """Copies needed so one pass over them streams >= 2x the MALL."""
     return max(floor, -(-2 * MALL_BYTES // per_copy) + 1)
@@ -749,8 +794,9 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=5,
                     help="activation rows M of the headline line (gamma+1 = 5)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--legs", default="valu,shapes,accept,attn,e2e,tree",
-                    help="comma list of legs beside the headline GEMV: valu (the VALU "
+    ap.add_argument("--legs", default="floor,valu,shapes,accept,attn,e2e,tree",
+                    help="comma list of legs beside the headline GEMV: floor (a plain read "
+                         "of the headline's bytes, rotated the same way), valu (the VALU "
                          "GEMV on the headline workload), shapes (7B-stack "
                          "GEMV shapes), accept (acceptance sampling C1 + V=128256 x 64 "
                          "chains), attn (INT4-KV verify attention, 7B shape), e2e "
@@ -793,6 +839,9 @@ def main() -> int:
     res = bench_gemv(lib, M_list, K, N, gs, args.steps, args.warmup, layout=3)
     head = res[args.rows]
     extra = {}
+    if "floor" in legs:
+        extra["read_floor"] = bench_floor(lib, gemv_bytes(args.rows, K, N, gs), args.steps,
+                                          args.warmup)
     if "valu" in legs:
         # the VALU GEMV (weight layout 2) on the same workload, for comparison
         rv = bench_gemv(lib, M_list, K, N, gs, args.steps, args.warmup, layout=2)

@@ -231,6 +231,7 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_is_device_ptr": (I, [VP]),
     "cgx_event_record": (I, [I]),
     "cgx_event_elapsed_ms": (F, [I, I]),
+    "cgx_stream_read": (I, [VP, SZ, VP]),
     "cgx_tensor_device_new": (PT, [C.POINTER(I), I]),
     "cgx_tensor_to_device": (PT, [PT]),
     "cgx_tensor_to_host": (I, [PT, C.POINTER(F)]),

@@ -48,6 +48,14 @@ int cgx_is_device_ptr(const void* p);  /* 1 device, 0 host */
 int cgx_event_record(int slot);      /* slot 0..7 */
 float cgx_event_elapsed_ms(int slot_begin, int slot_end);
 
+/* A plain streaming read of `bytes` (a multiple of 16, 16-byte aligned) of
+ * device memory, the floor of any kernel that reads the same bytes: out
+ * (device, 4 * ceil(bytes / 8192) words) receives, for block b and wave w,
+ * the XOR of the 32-bit words of the 16-byte words b*512 + 64w + l and
+ * b*512 + 256 + 64w + l, l = 0..63.  No counterpart in the reference: a
+ * measurement aid for bench.py's roofline figures. */
+int cgx_stream_read(const void* buf, size_t bytes, unsigned int* out);
+
 /* ------------------------------------------------- device-resident data */
 /* Tensor whose data lives in HBM (zero-filled).  Free with cg_tensor_free. */
 cg_tensor* cgx_tensor_device_new(int* shape, int ndim);
