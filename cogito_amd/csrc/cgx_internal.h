@@ -23,7 +23,8 @@ int cgx_ensure_init(void);
  * names the same slot. */
 enum { CGX_SLOT_IN0 = 0, CGX_SLOT_IN1, CGX_SLOT_IN2, CGX_SLOT_IN3,
        CGX_SLOT_OUT0, CGX_SLOT_OUT1, CGX_SLOT_WS0, CGX_SLOT_WS1,
-       CGX_SLOT_WS2, CGX_SLOT_WS3, CGX_SLOT_WS4, CGX_SLOT_WS5, CGX_NUM_SLOTS };
+       CGX_SLOT_WS2, CGX_SLOT_WS3, CGX_SLOT_WS4, CGX_SLOT_WS5, CGX_SLOT_WS6,
+       CGX_NUM_SLOTS };
 void* cgx_scratch(int slot, size_t bytes);
 /* Zero-initialised counters that kernels reset themselves after use. */
 unsigned int* cgx_counters(size_t count);

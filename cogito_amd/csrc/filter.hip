@@ -329,7 +329,9 @@ __global__ __launch_bounds__(kThreads) void k_top_k(const float* __restrict__ z,
                                                     int* __restrict__ tokens,
                                                     float* __restrict__ dist,
                                                     int* __restrict__ lidx,
-                                                    float* __restrict__ lp) {
+                                                    float* __restrict__ lp,
+                                                    const unsigned long long* __restrict__ gcand,
+                                                    const int* __restrict__ gstate) {
     __shared__ EosShared sh;
     __shared__ unsigned long long cand[kTopKMax];
     // radix passes: one histogram per wave (fewer same-address atomics), in
@@ -358,80 +360,90 @@ __global__ __launch_bounds__(kThreads) void k_top_k(const float* __restrict__ z,
         }
     };
 
-    // radix select of the k-th largest key among eligible elements (value >
-    // -1e30: never inserted otherwise; NaN never is); the first pass also
-    // counts them
-    uint32_t prefix = 0, pmask = 0;
-    int need = k, E = 0, ties = 0;
-    bool all = false;
-    for (int pass = 0; pass < 4; pass++) {
-        const int shift = 24 - 8 * pass;
-        for (int i = t; i < kWaves * 256; i += kThreads) (&hist[0][0])[i] = 0;
-        __syncthreads();
-        int elig = 0;
-        sweep([&](float x, int) {
-            const uint32_t key = order_key(x);
-            if (x > kTopKFloor && (key & pmask) == prefix) {
-                atomicAdd(&hist[wv][(key >> shift) & 255], 1);
-                elig++;
+    // candidates gathered by the multi-workgroup pass (k_topk_hist /
+    // k_topk_collect): every eligible key in or above the k-th largest key's
+    // 12-bit bin, in any order (the sort below orders them)
+    const int gn = gcand ? gstate[4 * row] : -1;
+    if (gn >= 0) {
+        for (int i = t; i < gn; i += kThreads) cand[i] = gcand[(size_t)row * kTopKMax + i];
+        if (t == 0) s_ncand = gn;
+    } else {
+        // radix select of the k-th largest key among eligible elements (value >
+        // -1e30: never inserted otherwise; NaN never is); the first pass also
+        // counts them
+        uint32_t prefix = 0, pmask = 0;
+        int need = k, E = 0, ties = 0;
+        bool all = false;
+        for (int pass = 0; pass < 4; pass++) {
+            const int shift = 24 - 8 * pass;
+            for (int i = t; i < kWaves * 256; i += kThreads) (&hist[0][0])[i] = 0;
+            __syncthreads();
+            int elig = 0;
+            sweep([&](float x, int) {
+                const uint32_t key = order_key(x);
+                if (x > kTopKFloor && (key & pmask) == prefix) {
+                    atomicAdd(&hist[wv][(key >> shift) & 255], 1);
+                    elig++;
+                }
+            });
+            if (pass == 0) {
+                E = block_sum_int(elig, lds);
+                all = E <= k;
+                if (all) break;
             }
-        });
-        if (pass == 0) {
-            E = block_sum_int(elig, lds);
-            all = E <= k;
-            if (all) break;
+            __syncthreads();
+            // digit of the need-th largest: thread i holds bin 255 - i; an
+            // exclusive scan from the top bin down finds the bin where the count
+            // reaches `need`
+            int h = 0;
+            if (t < 256) {
+    #pragma unroll
+                for (int w = 0; w < kWaves; w++) h += hist[w][255 - t];
+            }
+            int above;
+            const int excl = block_excl_scan(h, &above, lds);
+            if (t < 256 && excl < need && need <= excl + h) {
+                s_digit = 255 - t;
+                s_need = need - excl;
+                s_ncand = h;                // after the last pass: the keys equal to T
+            }
+            __syncthreads();
+            prefix |= (uint32_t)s_digit << shift;
+            pmask |= 0xFFu << shift;
+            need = s_need;
+            ties = s_ncand;
+            __syncthreads();
         }
-        __syncthreads();
-        // digit of the need-th largest: thread i holds bin 255 - i; an
-        // exclusive scan from the top bin down finds the bin where the count
-        // reaches `need`
-        int h = 0;
-        if (t < 256) {
-#pragma unroll
-            for (int w = 0; w < kWaves; w++) h += hist[w][255 - t];
-        }
-        int above;
-        const int excl = block_excl_scan(h, &above, lds);
-        if (t < 256 && excl < need && need <= excl + h) {
-            s_digit = 255 - t;
-            s_need = need - excl;
-            s_ncand = h;                // after the last pass: the keys equal to T
-        }
-        __syncthreads();
-        prefix |= (uint32_t)s_digit << shift;
-        pmask |= 0xFFu << shift;
-        need = s_need;
-        ties = s_ncand;
-        __syncthreads();
-    }
-    const uint32_t T = prefix;              // key of the k-th largest
+        const uint32_t T = prefix;              // key of the k-th largest
 
-    // collect: every eligible key > T, then the first `need` keys == T by
-    // index.  When every key == T fits next to the others, all of them are
-    // collected and the sort by (value desc, index asc) keeps the first
-    // `need`; otherwise each thread scans its own range in index order.
-    const bool all_ties = all || (k - need) + ties <= kTopKMax;
-    if (t == 0) s_ncand = 0;
-    __syncthreads();
-    sweep([&](float x, int j) {
-        const uint32_t key = order_key(x);
-        if (x > kTopKFloor && (all || key > T || (all_ties && key == T)))
-            cand[atomicAdd(&s_ncand, 1)] = topk_entry(key, j);
-    });
-    if (!all && !all_ties) {
-        const int per = (V + kThreads - 1) / kThreads;
-        const int lo = t * per, hi = min(V, lo + per);
-        int eq = 0;
-        for (int j = lo; j < hi; j++) eq += (zr[j] > kTopKFloor && order_key(zr[j]) == T);
-        int tot;
-        int r = block_excl_scan(eq, &tot, lds);
-        for (int j = lo; j < hi && r < need; j++) {
-            float x = zr[j];
-            if (x > kTopKFloor && order_key(x) == T) {
-                cand[atomicAdd(&s_ncand, 1)] = topk_entry(order_key(x), j);
-                r++;
+        // collect: every eligible key > T, then the first `need` keys == T by
+        // index.  When every key == T fits next to the others, all of them are
+        // collected and the sort by (value desc, index asc) keeps the first
+        // `need`; otherwise each thread scans its own range in index order.
+        const bool all_ties = all || (k - need) + ties <= kTopKMax;
+        if (t == 0) s_ncand = 0;
+        __syncthreads();
+        sweep([&](float x, int j) {
+            const uint32_t key = order_key(x);
+            if (x > kTopKFloor && (all || key > T || (all_ties && key == T)))
+                cand[atomicAdd(&s_ncand, 1)] = topk_entry(key, j);
+        });
+        if (!all && !all_ties) {
+            const int per = (V + kThreads - 1) / kThreads;
+            const int lo = t * per, hi = min(V, lo + per);
+            int eq = 0;
+            for (int j = lo; j < hi; j++) eq += (zr[j] > kTopKFloor && order_key(zr[j]) == T);
+            int tot;
+            int r = block_excl_scan(eq, &tot, lds);
+            for (int j = lo; j < hi && r < need; j++) {
+                float x = zr[j];
+                if (x > kTopKFloor && order_key(x) == T) {
+                    cand[atomicAdd(&s_ncand, 1)] = topk_entry(order_key(x), j);
+                    r++;
+                }
             }
         }
+
     }
     __syncthreads();
     const int ncand = s_ncand;
@@ -536,6 +548,143 @@ __global__ __launch_bounds__(kThreads) void k_top_k(const float* __restrict__ z,
         float v = use_p ? __fdiv_rn(pr(j), mass) : pr(j);
         if (v != 0.0f) dr[idx[j]] = v;
     }
+}
+
+// ------------------------------------------ top-k over many workgroups
+// Rows of 16384 values and more: each row is cut into tiles of kTK values,
+// one 256-thread workgroup per (tile, row).  k_topk_hist adds the tile's
+// histogram of the top kHBits bits of the eligible keys into the row's;
+// k_topk_collect finds, from the row's histogram, the bin of the k-th
+// largest key and appends every eligible key of its tile in or above that
+// bin to the row's candidate list (the sort in k_top_k orders them); a row
+// whose bin would overflow the list (kTopKMax) is marked and k_top_k selects
+// from the row itself.
+
+constexpr int kTK = 4096;                 // values per tile
+constexpr int kTKThreads = 256;
+constexpr int kHBits = 12, kHBins = 1 << kHBits;
+constexpr int kTKState = 4;               // per row: candidates (-1: select in k_top_k)
+
+__global__ void k_topk_zero(int* __restrict__ p, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+__global__ __launch_bounds__(kTKThreads) void k_topk_hist(const float* __restrict__ z, int V,
+                                                         int* __restrict__ hist) {
+    __shared__ int h[kHBins];
+    const int row = blockIdx.y, tile = blockIdx.x, t = threadIdx.x;
+    for (int i = t; i < kHBins; i += kTKThreads) h[i] = 0;
+    __syncthreads();
+    const float* zr = z + (size_t)row * V + (size_t)tile * kTK;
+    const int n = min(kTK, V - tile * kTK);
+    float xs[kTK / kTKThreads];
+#pragma unroll
+    for (int q = 0; q < kTK / kTKThreads; q++) {
+        const int j = q * kTKThreads + t;
+        xs[q] = j < n ? zr[j] : kTopKFloor;
+    }
+#pragma unroll
+    for (int q = 0; q < kTK / kTKThreads; q++)
+        if (xs[q] > kTopKFloor) atomicAdd(&h[order_key(xs[q]) >> (32 - kHBits)], 1);
+    __syncthreads();
+    int* gh = hist + (size_t)row * kHBins;
+    for (int i = t; i < kHBins; i += kTKThreads)
+        if (h[i]) atomicAdd(&gh[i], h[i]);
+}
+
+__global__ __launch_bounds__(kTKThreads) void k_topk_collect(const float* __restrict__ z, int V,
+                                                            int k, const int* __restrict__ hist,
+                                                            int* __restrict__ state,
+                                                            unsigned long long* __restrict__ gcand) {
+    constexpr int kPer = kHBins / kTKThreads;          // bins per thread
+    constexpr int kW = kTKThreads / 64;
+    __shared__ int s_w[kW];
+    __shared__ int s_bin, s_fast;
+    const int row = blockIdx.y, tile = blockIdx.x, t = threadIdx.x, lane = t & 63;
+    const int* gh = hist + (size_t)row * kHBins;
+    // thread t holds bins kHBins-1-kPer*t downwards; the exclusive scan in
+    // thread order counts the keys above them
+    int hb[kPer], hs = 0;
+#pragma unroll
+    for (int q = 0; q < kPer; q++) {
+        hb[q] = gh[kHBins - 1 - kPer * t - q];
+        hs += hb[q];
+    }
+    int x = hs;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    if (lane == 63) s_w[t >> 6] = x;
+    if (t == 0) {
+        s_bin = 0;                                     // at most k eligible: take them all
+        s_fast = 1;
+    }
+    __syncthreads();
+    int excl = x - hs, tot = 0;
+    for (int w = 0; w < kW; w++) {
+        if (w < (t >> 6)) excl += s_w[w];
+        tot += s_w[w];
+    }
+    if (tot > k) {
+#pragma unroll
+        for (int q = 0; q < kPer; q++) {
+            if (excl < k && k <= excl + hb[q]) {
+                s_bin = kHBins - 1 - kPer * t - q;
+                s_fast = excl + hb[q] <= kTopKMax;
+            }
+            excl += hb[q];
+        }
+    }
+    __syncthreads();
+    if (!s_fast) {
+        if (tile == 0 && t == 0) state[(size_t)row * kTKState] = -1;
+        return;
+    }
+    const uint32_t bin = (uint32_t)s_bin;
+    const float* zr = z + (size_t)row * V + (size_t)tile * kTK;
+    const int n = min(kTK, V - tile * kTK);
+#pragma unroll
+    for (int q = 0; q < kTK / kTKThreads; q++) {
+        const int j = q * kTKThreads + t;
+        if (j >= n) continue;
+        const float v = zr[j];
+        const uint32_t key = order_key(v);
+        if (v > kTopKFloor && (key >> (32 - kHBits)) >= bin) {
+            const int pos = atomicAdd(&state[(size_t)row * kTKState], 1);
+            gcand[(size_t)row * kTopKMax + pos] = topk_entry(key, tile * kTK + j);
+        }
+    }
+}
+
+// Launch of k_top_k, through the multi-workgroup candidate pass for long rows.
+int launch_top_k(const float* z, int rows, int V, int k, int kpow2, float top_p, const float* u,
+                 int* tokens, float* dist, int* lidx, float* lp) {
+    const unsigned long long* gcand = nullptr;
+    const int* gstate = nullptr;
+    if (V >= 4 * kTK) {
+        const size_t hn = (size_t)rows * (kHBins + kTKState);
+        char* w = (char*)cgx_scratch(CGX_SLOT_WS6, hn * 4 + (size_t)rows * kTopKMax * 8 + 256);
+        if (!w) return -1;
+        int* hist = (int*)w;
+        int* state = hist + (size_t)rows * kHBins;
+        unsigned long long* cand =
+            (unsigned long long*)(((uintptr_t)(w + hn * 4) + 255) & ~(uintptr_t)255);
+        hipLaunchKernelGGL(k_topk_zero, dim3((unsigned)((hn + 255) / 256)), dim3(256), 0,
+                           stream(), hist, hn);
+        const dim3 grid((V + kTK - 1) / kTK, rows);
+        hipLaunchKernelGGL(k_topk_hist, grid, dim3(kTKThreads), 0, stream(), z, V, hist);
+        hipLaunchKernelGGL(k_topk_collect, grid, dim3(kTKThreads), 0, stream(), z, V, k, hist,
+                           state, cand);
+        if (launch_check("k_topk_collect")) return -1;
+        gcand = cand;
+        gstate = state;
+    }
+    hipLaunchKernelGGL(k_top_k, dim3(rows), dim3(kThreads), 0, stream(), z, V, k, kpow2, top_p,
+                       u, tokens, dist, lidx, lp, gcand, gstate);
+    return launch_check("k_top_k");
 }
 
 // ----------------------------------------------------- typical sampling
@@ -704,9 +853,7 @@ extern "C" int cgk_topk_lists(const float* z, int rows, int V, int top_k, float 
     }
     int kpow2 = 64;
     while (kpow2 < top_k) kpow2 <<= 1;
-    hipLaunchKernelGGL(k_top_k, dim3(rows), dim3(kThreads), 0, stream(), z, V, top_k, kpow2,
-                       top_p, (const float*)nullptr, (int*)nullptr, (float*)nullptr, lidx, lp);
-    return launch_check("k_top_k");
+    return launch_top_k(z, rows, V, top_k, kpow2, top_p, nullptr, nullptr, nullptr, lidx, lp);
 }
 
 extern "C" int cgk_scale(const float* x, float* z, size_t n, float T) {
@@ -735,9 +882,7 @@ extern "C" int cgk_filter_rows(const float* z, int rows, int V, int top_k, float
         }
         int kpow2 = 64;
         while (kpow2 < top_k) kpow2 <<= 1;
-        hipLaunchKernelGGL(k_top_k, dim3(rows), dim3(kThreads), 0, stream(), z, V, top_k,
-                           kpow2, top_p, u, tokens, dist, (int*)nullptr, (float*)nullptr);
-        return launch_check("k_top_k");
+        return launch_top_k(z, rows, V, top_k, kpow2, top_p, u, tokens, dist, nullptr, nullptr);
     }
     // the descending sort of each row's probabilities (rowsort.hip, on the
     // values' bit patterns, monotone for non-negative floats) shares its

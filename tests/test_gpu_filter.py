@@ -44,7 +44,12 @@ def logits_case(rng, V, kind):
 
 TOPK_CASES = [(32000, 50, "normal"), (128256, 50, "normal"), (1000, 1, "ties"),
               (5000, 4096, "halves"), (2000, 300, "ties"), (64, 20, "floor"),
-              (32000, 50, "flat"), (100, 99, "normal")]
+              (32000, 50, "flat"), (100, 99, "normal"),
+              # rows of 16384 values and more gather their candidates over many
+              # workgroups: a k-th largest bin too large for the list (ties) falls
+              # back to the single-workgroup select; a large k; a floor-heavy row
+              (40000, 3000, "ties"), (70000, 4096, "normal"), (20000, 7, "floor"),
+              (16384, 1000, "halves")]
 
 
 @pytest.mark.parametrize("V,k,kind", TOPK_CASES)
