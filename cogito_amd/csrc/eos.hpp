@@ -565,10 +565,36 @@ __device__ __forceinline__ void chunk_vals(const RowSrc& g, int base, int n, flo
     }
 }
 
+// Exact ordered sum of at most two chunks (n <= 64): one wave evaluates the
+// elements (lane j: element j) and adds them in order with real fp32
+// additions -- the reference's sum itself -- leaving the chunk boundaries as
+// the general path does.
+template <class G>
+__device__ float eos_sum_small(const G& g, int n, EosShared& sh) {
+    if (wave_id() == 0) {
+        const int l = lane_id();
+        const float x = l < n ? g(l) : 0.0f;
+        float s = 0.0f;
+        for (int c = 0; c * kCh < n; c++) {
+            if (l == 0) sh.cstart[0][c] = s;
+            const int end = min(n, (c + 1) * kCh);
+            for (int j = c * kCh; j < end; j++)
+                s = __fadd_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), j)));
+            if (l == 0) sh.cend[0][c] = s;
+        }
+        if (l == 0) sh.total = s;
+    }
+    __syncthreads();
+    const float total = sh.total;
+    __syncthreads();
+    return total;
+}
+
 // Exact ordered sum of g(0..n-1).  Leaves the exact running value at every
 // chunk boundary in sh.cstart / sh.cend (rounds x threads) for gen_find.
 template <class G>
 __device__ __forceinline__ float eos_sum(const G& g, int n, EosShared& sh) {
+    if (n <= 2 * kCh) return eos_sum_small(g, n, sh);
     const int t = threadIdx.x;
     const int rounds = (n + kRound - 1) / kRound;
     float s_round = 0.0f;
@@ -584,6 +610,7 @@ __device__ __forceinline__ float eos_sum(const G& g, int n, EosShared& sh) {
 template <class G>
 __device__ __forceinline__ float eos_sum_vals(const float (&x)[kCh], const G& g, int n,
                                               EosShared& sh) {
+    if (n <= 2 * kCh) return eos_sum_small(g, n, sh);
     return eos_round(x, g, 0, n, 0.0f, sh);
 }
 
