@@ -140,8 +140,11 @@ __device__ __forceinline__ int binade_bits(float s) {
 }
 
 __device__ __forceinline__ float mi_apply(float s, const MI& m) {
+    // branch-free choice of the increment (a select here became a
+    // dynamically indexed pair in scratch memory inside the walk's loop)
     const unsigned int u = __float_as_uint(s);
-    return __uint_as_float(u + (unsigned int)((u & 1u) ? m.q1 : m.q0));
+    const unsigned int q0 = (unsigned int)m.q0, q1 = (unsigned int)m.q1;
+    return __uint_as_float(u + (q0 ^ ((q0 ^ q1) & (0u - (u & 1u)))));
 }
 
 // ------------------------------------------------------------- workspace
@@ -746,67 +749,112 @@ __device__ float replay_exact(const Eval<KIND>& ev, int j0, int j1, float s) {
     return s;
 }
 
+constexpr int kWalkStaged = kDirtyCap * kC;   // walk: staged values held in LDS per batch
+
+// 16 bytes a lane from global memory straight into LDS: lane i's bytes land
+// at dst + 16 i (dst wave-uniform), no registers and no wait at issue
+__device__ __forceinline__ void load_lds16(const void* src, void* dst) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+}
+
 struct WalkShared {
-    Item items[kWalkItems];
-    int ioff[kMaxSegs + 1];
-    int doff[kMaxSegs];
+    alignas(16) Item items[kWalkItems];
+    alignas(16) float staged[kWalkStaged];
+    int ioff[kMaxSegs + 1];    // prefix counts over the row's segments: runs
+    int soff[kMaxSegs + 1];    // staged values
     int over[kMaxSegs];
 };
 
-// Replay n staged chunks (exact values at dv, global memory) from s: fp32
-// additions in order, the next 64 values loaded while the current ones are
-// added; the exact value at each chunk start goes to out[chunk].
-__device__ __forceinline__ float replay_staged(const float* __restrict__ dv, int n, float s,
-                                               float* __restrict__ out) {
-    const int tot = n * kC;
-    float x = lane_id() < tot ? dv[lane_id()] : 0.0f;
-    for (int i = 0; i < tot; i += 64) {
-        const float xn = i + 64 + lane_id() < tot ? dv[i + 64 + lane_id()] : 0.0f;
-        // chunk starts of this batch (4 chunks of 16) gathered in lanes 0..3
-        float cs = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 64; k++) {
-            if ((k & (kC - 1)) == 0) cs = lane_id() == k / kC ? s : cs;   // s is wave-uniform
-            s = __fadd_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k)));
-        }
-        if (lane_id() < 4 && i + lane_id() * kC < tot) out[i / kC + lane_id()] = cs;
-        x = xn;
+typedef float vf4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float add4(float s, vf4 v) {
+    s = __fadd_rn(s, v.x);
+    s = __fadd_rn(s, v.y);
+    s = __fadd_rn(s, v.z);
+    return __fadd_rn(s, v.w);
+}
+
+// Replay n staged chunks (exact values at sv, in LDS) from s: fp32 additions
+// in order.  Every lane reads the whole chunk (one address: a broadcast) and
+// runs the same additions in its own registers, so the serial chain has no
+// cross-lane moves; the next chunk's read is in flight meanwhile.  The exact
+// value at each chunk start goes to out[chunk].
+__device__ __forceinline__ float replay_lds(const float* sv, int n, float s,
+                                            float* __restrict__ out) {
+    const vf4* p = (const vf4*)sv;
+    vf4 a = p[0], b = p[1], c = p[2], d = p[3];
+    for (int k = 0; k < n; k++) {
+        const int kn = k + 1 < n ? k + 1 : k;
+        const vf4 an = p[4 * kn], bn = p[4 * kn + 1], cn = p[4 * kn + 2], dn = p[4 * kn + 3];
+        if (lane_id() == 0) out[k] = s;
+        s = add4(add4(add4(add4(s, a), b), c), d);
+        a = an;
+        b = bn;
+        c = cn;
+        d = dn;
     }
     return s;
 }
 
 // One wave per row: exact value at every segment and item start, row sum.
-// The runs of a batch of segments are gathered in LDS first (all loads in
-// flight together); staged values stream from global memory.
+// Segments are walked in batches; a batch's runs and staged values are
+// gathered into LDS first, all loads in flight together, so the serial chain
+// of additions waits on global memory once per batch, not once per staged run.
 template <int KIND>
 __device__ void walk_row(const Eval<KIND>& ev, const Work& w, int row, WalkShared& sh) {
     const int l = lane_id();
     // every segment's counts (nseg <= 64), and their prefix sums
-    int c = 0;
-    if (l < w.nseg) c = w.cnt[2 * segi(w, row, l)];
-    int io = c > 0 ? c : 0;
+    int c = 0, dc = 0;
+    if (l < w.nseg) {
+        c = w.cnt[2 * segi(w, row, l)];
+        dc = w.cnt[2 * segi(w, row, l) + 1];
+    }
+    int io = c > 0 ? c : 0, so = c >= 0 && dc > 0 ? dc * kC : 0;
     for (int o = 1; o < 64; o <<= 1) {
-        const int a = __shfl_up(io, o);
-        if (l >= o) io += a;
+        const int a = __shfl_up(io, o), b = __shfl_up(so, o);
+        if (l >= o) {
+            io += a;
+            so += b;
+        }
     }
     if (l < w.nseg) {
         sh.ioff[l + 1] = io;
+        sh.soff[l + 1] = so;
         sh.over[l] = c < 0;
     }
-    if (l == 0) sh.ioff[0] = 0;
+    if (l == 0) sh.ioff[0] = sh.soff[0] = 0;
     __syncthreads();
+    const float* rdirty = w.dirty + segi(w, row, 0) * kDirtyCap * kC;
+    const Item* ritems = w.items + segi(w, row, 0) * kItemCap;
     float s = 0.0f;
     int g0 = 0;
     while (g0 < w.nseg) {
-        // batch [g0, g1): as many segments as fit
-        int g1 = g0 + 1;
-        while (g1 < w.nseg && sh.ioff[g1 + 1] - sh.ioff[g0] <= kWalkItems) g1++;
-        const int i0 = sh.ioff[g0], ni = sh.ioff[g1] - i0;
-        for (int i = l; i < ni; i += 64) {     // one round trip for up to 64 runs
-            int sg = g0;
-            while (sg + 1 < g1 && sh.ioff[sg + 1] <= i0 + i) sg++;
-            sh.items[i] = w.items[segi(w, row, sg) * kItemCap + (i0 + i - sh.ioff[sg])];
+        // batch [g0, g1): as many segments as fit (lane l holds the prefix
+        // counts through segment l, so the fitting segments form a ballot)
+        const int ib = g0 > 0 ? __builtin_amdgcn_readlane(io, g0 - 1) : 0;
+        const int sb = g0 > 0 ? __builtin_amdgcn_readlane(so, g0 - 1) : 0;
+        const unsigned long long fit = __ballot(l >= g0 && l < w.nseg && io - ib <= kWalkItems &&
+                                                so - sb <= kWalkStaged);
+        const int g1 = max(g0 + 1, 64 - __clzll(fit));
+        const int i0 = ib, s0 = sb;
+        // gather the batch's runs and staged values into LDS, every load in
+        // flight together (counts from the lanes' prefix sums: no LDS read
+        // between the loads)
+        for (int seg = g0; seg < g1; seg++) {
+            const int sa = seg > 0 ? __builtin_amdgcn_readlane(so, seg - 1) : 0;
+            const int sz = __builtin_amdgcn_readlane(so, seg) - sa;         // floats
+            const float* ssrc = rdirty + (size_t)seg * kDirtyCap * kC;
+            float* sdst = sh.staged + (sa - s0);
+            for (int f = 0; f < sz; f += 256)
+                if (f + 4 * l < sz) load_lds16(ssrc + f + 4 * l, sdst + f);
+            const int ia = seg > 0 ? __builtin_amdgcn_readlane(io, seg - 1) : 0;
+            const int iz = (__builtin_amdgcn_readlane(io, seg) - ia) * (int)(sizeof(Item) / 4);
+            const int* isrc = (const int*)(ritems + (size_t)seg * kItemCap);
+            int* idst = (int*)(sh.items + (ia - i0));
+            for (int f = 0; f < iz; f += 256)
+                if (f + 4 * l < iz) load_lds16(isrc + f + 4 * l, idst + f);
         }
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         for (int seg = g0; seg < g1; seg++) {
             const size_t si = segi(w, row, seg);
@@ -818,7 +866,7 @@ __device__ void walk_row(const Eval<KIND>& ev, const Work& w, int row, WalkShare
             }
             const int n = sh.ioff[seg + 1] - sh.ioff[seg];
             const Item* its = sh.items + (sh.ioff[seg] - i0);
-            const float* dv = w.dirty + si * kDirtyCap * kC;
+            const float* sv = sh.staged + (sh.soff[seg] - s0);
             Item nx = n > 0 ? its[0] : Item{};
             for (int i = 0; i < n; i++) {
                 const Item it = nx;
@@ -826,8 +874,8 @@ __device__ void walk_row(const Eval<KIND>& ev, const Work& w, int row, WalkShare
                 const int cend = i + 1 < n ? nx.chunk : kT;
                 if (l == 0) w.item_start[si * kItemCap + i] = s;
                 if (it.binade == kDirty) {
-                    s = replay_staged(dv + it.slot * kC, cend - it.chunk, s,
-                                      w.dirty_start + si * kDirtyCap + it.slot);
+                    s = replay_lds(sv + it.slot * kC, cend - it.chunk, s,
+                                   w.dirty_start + si * kDirtyCap + it.slot);
                 } else if (binade_bits(s) != it.binade) {
                     // the run's start is not in the binade its chunks assumed
                     // (excluded by the bounds; replayed exactly anyway)
