@@ -239,14 +239,15 @@ struct Eval {
         const float B = KIND == kKindRes ? arg(b[j], mb) : 0.0f;
         return exact(A, B);
     }
-    // this thread's chunk: exact arguments
+    // this thread's chunk: raw values, exact arguments from them, or both
+    __device__ __forceinline__ void raw(int base, float (&X)[kC], float (&Y)[kC]) const;
+    __device__ __forceinline__ void args_of(int base, const float (&X)[kC], const float (&Y)[kC],
+                                            float (&A)[kC], float (&B)[kC]) const;
     __device__ __forceinline__ void args(int base, float (&A)[kC], float (&B)[kC]) const;
 };
 
-// exact args of this thread's chunk (-inf past V: value 0)
-__device__ __forceinline__ void load_args(const float* p, float m, float T, int base, int V,
-                                          float (&A)[kC]) {
-    float x[kC];
+// this thread's chunk of a row as stored (-inf past V)
+__device__ __forceinline__ void load_raw(const float* p, int base, int V, float (&x)[kC]) {
     if (base + kC <= V && ((uintptr_t)(p + base) & 15u) == 0) {
         const float4* q = reinterpret_cast<const float4*>(p + base);
 #pragma unroll
@@ -261,6 +262,11 @@ __device__ __forceinline__ void load_args(const float* p, float m, float T, int 
 #pragma unroll
         for (int k = 0; k < kC; k++) x[k] = base + k < V ? p[base + k] : -__builtin_inff();
     }
+}
+
+// exact args of a chunk from its raw values (-inf past V: value 0)
+__device__ __forceinline__ void make_args(const float (&x)[kC], float m, float T, int base,
+                                          int V, float (&A)[kC]) {
     if (T == 1.0f) {
 #pragma unroll
         for (int k = 0; k < kC; k++)
@@ -273,9 +279,24 @@ __device__ __forceinline__ void load_args(const float* p, float m, float T, int 
 }
 
 template <int KIND>
+__device__ __forceinline__ void Eval<KIND>::raw(int base, float (&X)[kC], float (&Y)[kC]) const {
+    load_raw(a, base, V, X);
+    if constexpr (KIND == kKindRes) load_raw(b, base, V, Y);
+}
+
+template <int KIND>
+__device__ __forceinline__ void Eval<KIND>::args_of(int base, const float (&X)[kC],
+                                                    const float (&Y)[kC], float (&A)[kC],
+                                                    float (&B)[kC]) const {
+    make_args(X, ma, T, base, V, A);
+    if constexpr (KIND == kKindRes) make_args(Y, mb, T, base, V, B);
+}
+
+template <int KIND>
 __device__ __forceinline__ void Eval<KIND>::args(int base, float (&A)[kC], float (&B)[kC]) const {
-    load_args(a, ma, T, base, V, A);
-    if constexpr (KIND == kKindRes) load_args(b, mb, T, base, V, B);
+    float X[kC], Y[kC];
+    raw(base, X, Y);
+    args_of(base, X, Y, A, B);
 }
 
 // Summary of one chunk in binade b from its approximations (v, bound er) and
@@ -459,14 +480,36 @@ __global__ __launch_bounds__(kT) void k_seg_stats(Rows rows, float T, Work w) {
     const float ms = block_max256(mx, s_f);
     float g = 0.0f, h = 0.0f;
     if (ms > -__builtin_inff()) {
+        // exp_cert without a branch per element: exp_fast on the clamped
+        // argument everywhere (arguments are <= 0), exp_glibc afterwards for
+        // the rare arguments below exp_fast's range
+        float a[kC], e[kC];
+        bool slow = false;
+        if (T == 1.0f) {
+#pragma unroll
+            for (int k = 0; k < kC; k++) a[k] = __fsub_rn(x[k], ms);
+        } else {
+#pragma unroll
+            for (int k = 0; k < kC; k++) a[k] = __fdiv_rn(__fsub_rn(x[k], ms), T);
+        }
 #pragma unroll
         for (int k = 0; k < kC; k++) {
-            if (x[k] > -__builtin_inff()) {
-                const float a = T == 1.0f ? __fsub_rn(x[k], ms) : __fdiv_rn(__fsub_rn(x[k], ms), T);
-                const float e = exp_cert(a);
-                g += e;
-                h += e * fabsf(a);
-            }
+            const bool live = x[k] > -__builtin_inff();
+            const float f = exp_fast(fmaxf(a[k], kExpFastMin));
+            e[k] = live ? f : 0.0f;
+            a[k] = live ? a[k] : 0.0f;
+            slow |= live && !(a[k] >= kExpFastMin && a[k] <= 0.0f);
+        }
+        if (slow) {
+#pragma unroll
+            for (int k = 0; k < kC; k++)
+                if (x[k] > -__builtin_inff() && !(a[k] >= kExpFastMin && a[k] <= 0.0f))
+                    e[k] = exp_glibc(a[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < kC; k++) {
+            g += e[k];
+            h += e[k] * fabsf(a[k]);
         }
     }
     const double G = block_sum256_d((double)g, s_d);
@@ -481,34 +524,22 @@ __global__ __launch_bounds__(kT) void k_seg_stats(Rows rows, float T, Work w) {
     }
 }
 
-// row maximum of a pass-1 row from its segment maxima
-__device__ __forceinline__ float row_max(const Work& w, int r, float* s_f) {
-    float m = -__builtin_inff();
-    for (int s = threadIdx.x; s < w.nseg; s += kT) m = fmaxf(m, w.seg_m[segi(w, r, s)]);
-    return block_max256(m, s_f);
-}
-
-// guide of pass-1 row r over segments [0, seg): sum of c G and its bound.
-// seg < 64, so wave 0 holds every term; c = exp(-D) with exp_fast on the
-// fp32-rounded D (relative error 2^-20 + 2^-24 D), or 0 below 2^-125.
-__device__ __forceinline__ void exp_prefix(const Work& w, int r, int seg, float m, float T,
-                                           double* s_d, double* P, double* E) {
+// guide of a pass-1 row over segments [0, seg) from its segment stats: sum of
+// c G and its bound.  seg < 64, so wave 0 holds every term (lane s: segment
+// s's G, H and maximum ms, loaded by the caller); c = exp(-D) with exp_fast on
+// the fp32-rounded D (relative error 2^-20 + 2^-24 D), or 0 below 2^-125.
+__device__ __forceinline__ void exp_prefix(double G, double H, float ms, bool mine, float m,
+                                           float T, double* s_d, double* P, double* E) {
     if (wave_id() == 0) {
         double cg = 0.0, eb = 0.0;
-        const int s = threadIdx.x;
-        if (s < seg) {
-            const size_t i = segi(w, r, s);
-            const double G = w.seg_gh[2 * i], H = w.seg_gh[2 * i + 1];
-            const float ms = w.seg_m[i];
-            if (G > 0.0) {
-                const double D = ((double)m - (double)ms) / (double)T;
-                const bool ok = D <= 87.0;
-                const double c = ok ? (double)exp_fast(-(float)D) : 0.0;
-                cg = c * G;
-                const double cu = ok ? c * (1.0 + 0x1p-19 + 0x1p-23 * D) : 0x1p-125;
-                eb = cu * (0x1p-22 * 1.01 * H + (0x1p-23 * 1.01 * D + 0x1p-18) * G) +
-                     (cu - c) * G + 0x1p-136;
-            }
+        if (mine && G > 0.0) {
+            const double D = ((double)m - (double)ms) / (double)T;
+            const bool ok = D <= 87.0;
+            const double c = ok ? (double)exp_fast(-(float)D) : 0.0;
+            cg = c * G;
+            const double cu = ok ? c * (1.0 + 0x1p-19 + 0x1p-23 * D) : 0x1p-125;
+            eb = cu * (0x1p-22 * 1.01 * H + (0x1p-23 * 1.01 * D + 0x1p-18) * G) +
+                 (cu - c) * G + 0x1p-136;
         }
         for (int o = 32; o > 0; o >>= 1) {
             cg += __shfl_xor(cg, o);
@@ -525,6 +556,23 @@ __device__ __forceinline__ void exp_prefix(const Work& w, int r, int seg, float 
     __syncthreads();
 }
 
+// the stats of segment t of pass-1 row r (thread t < nseg)
+struct SegStats {
+    float m;
+    double G, H;
+};
+
+__device__ __forceinline__ SegStats seg_stats_of(const Work& w, int r) {
+    SegStats st{-__builtin_inff(), 0.0, 0.0};
+    if ((int)threadIdx.x < w.nseg) {
+        const size_t i = segi(w, r, threadIdx.x);
+        st.m = w.seg_m[i];
+        st.G = w.seg_gh[2 * i];
+        st.H = w.seg_gh[2 * i + 1];
+    }
+    return st;
+}
+
 // ------------------------------------------------------------ the fold
 
 struct FoldShared {
@@ -538,14 +586,16 @@ struct FoldShared {
 };
 
 // One segment of a row through the certified fold: items and staged chunks
-// for the walk.  P0/E0: guide of the row before this segment and its bound.
+// for the walk.  X/Y: this thread's chunk as loaded (raw); P0/E0: guide of
+// the row before this segment and its bound.
 template <int KIND>
-__device__ void fold_segment(const Eval<KIND>& ev, const Work& w, int row, int seg, double P0,
-                             double E0, FoldShared& sh) {
+__device__ void fold_segment(const Eval<KIND>& ev, const Work& w, int row, int seg,
+                             const float (&X)[kC], const float (&Y)[kC], double P0, double E0,
+                             FoldShared& sh) {
     const int t = threadIdx.x;
     const int base = seg * kSeg + t * kC;
     float A[kC], B[kC];
-    ev.args(base, A, B);
+    ev.args_of(base, X, Y, A, B);
     float v[kC], er[kC];
     float gs = 0.0f, ge = 0.0f;
 #pragma unroll
@@ -660,14 +710,19 @@ __device__ __forceinline__ Eval<KIND> task_eval(const Rows& rows, const Work& w,
     return ev;
 }
 
+// Every global load of the block is issued first (the chunk and the row's
+// segment stats), so their latencies overlap.
 __global__ __launch_bounds__(kT) void k_seg_fold1(Rows rows, float T, Work w) {
     __shared__ FoldShared sh;
     const int seg = blockIdx.x, r = blockIdx.y;
-    const float m = row_max(w, r, sh.f);
+    float X[kC], Y[kC];
+    load_raw(rows.row(r), seg * kSeg + threadIdx.x * kC, rows.V, X);
+    const SegStats st = seg_stats_of(w, r);
+    const float m = block_max256(st.m, sh.f);        // the row maximum
     if (seg == 0 && threadIdx.x == 0) w.row_m[r] = m;
     double P0, E0;
-    exp_prefix(w, r, seg, m, T, sh.d, &P0, &E0);
-    fold_segment(pass1_eval(rows, r, m, T), w, r, seg, P0, E0, sh);
+    exp_prefix(st.G, st.H, st.m, (int)threadIdx.x < seg, m, T, sh.d, &P0, &E0);
+    fold_segment(pass1_eval(rows, r, m, T), w, r, seg, X, Y, P0, E0, sh);
 }
 
 // residual guide sums of the first-reject row pairs (pass-2 stats)
@@ -702,16 +757,21 @@ __global__ __launch_bounds__(kT) void k_seg_fold2(Rows rows, float T, Work w) {
     const int seg = blockIdx.x, c = blockIdx.y;
     const Task tk = w.task[c];
     if (tk.kind < 0) return;
+    const int base = seg * kSeg + threadIdx.x * kC;
+    float X[kC], Y[kC];
     if (tk.kind == kKindProb) {
         // p_i = e_i / S: the pass-1 guide of row ra, divided by S
         const Eval<kKindProb> ev = task_eval<kKindProb>(rows, w, tk, T);
+        ev.raw(base, X, Y);
+        const SegStats st = seg_stats_of(w, tk.ra);
         double P, E;
-        exp_prefix(w, tk.ra, seg, ev.ma, T, sh.d, &P, &E);
+        exp_prefix(st.G, st.H, st.m, (int)threadIdx.x < seg, ev.ma, T, sh.d, &P, &E);
         const double P0 = P / (double)ev.Sa;
         const double E0 = E / (double)ev.Sa + P0 * 0x1p-22;
-        fold_segment(ev, w, w.R1 + c, seg, P0, E0, sh);
+        fold_segment(ev, w, w.R1 + c, seg, X, Y, P0, E0, sh);
     } else {
         const Eval<kKindRes> ev = task_eval<kKindRes>(rows, w, tk, T);
+        ev.raw(base, X, Y);
         double g = 0.0, e = 0.0;
         if ((int)threadIdx.x < seg) {
             const size_t i = (size_t)c * w.nseg + threadIdx.x;
@@ -720,7 +780,7 @@ __global__ __launch_bounds__(kT) void k_seg_fold2(Rows rows, float T, Work w) {
         }
         const double P0 = block_sum256_d(g, sh.d);
         const double E0 = block_sum256_d(e, sh.d);
-        fold_segment(ev, w, w.R1 + c, seg, P0, E0, sh);
+        fold_segment(ev, w, w.R1 + c, seg, X, Y, P0, E0, sh);
     }
 }
 
