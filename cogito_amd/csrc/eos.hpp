@@ -42,9 +42,14 @@ __constant__ uint64_t kExp2Tab[32] = {
     0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
+// Branch-free: the main path runs on the argument clamped into the range
+// where it applies and the out-of-range results are selected afterwards, so
+// several evaluations can be in flight in one thread.
 __device__ __forceinline__ float exp_glibc(float x) {
-    if (!(x <= 0x1.62e42ep6f)) return x != x ? x + x : __builtin_inff();
-    if (x < -0x1.9fe368p6f) return 0.0f;
+    const bool over = !(x <= 0x1.62e42ep6f);       // NaN included
+    const bool under = x < -0x1.9fe368p6f;
+    const float special = x != x ? x + x : (over ? __builtin_inff() : 0.0f);
+    x = fminf(fmaxf(x, -0x1.9fe368p6f), 0x1.62e42ep6f);
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
     const double shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
@@ -62,7 +67,7 @@ __device__ __forceinline__ float exp_glibc(float x) {
     double y = fma(c2, r, 1.0);
     y = fma(z, r2, y);
     y = y * s;
-    return (float)y;
+    return over || under ? special : (float)y;
 }
 
 // ------------------------------------------------- fast, certified expf

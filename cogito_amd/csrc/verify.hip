@@ -55,6 +55,7 @@ constexpr int kDirtyCap = kT;            // staged chunks per segment (all of th
 constexpr int kWalkItems = 512;          // walk: runs held in LDS per batch
 constexpr int kMaxGamma = 64;
 constexpr int kMaxSegs = 64;             // segments per row (V <= 262144)
+constexpr int kExactBatch = 4;           // exact element evaluations in flight per thread
 
 enum { kKindExp = 0, kKindProb = 1, kKindRes = 2 };
 
@@ -322,10 +323,26 @@ __device__ __forceinline__ MI fold_chunk16(const Eval<KIND>& ev, const float (&A
         const int q = (int)Q;
         return MI{q, q, (q & 1) | (((q & 1) ^ 1) << 1)};
     }
+    // exact values four at a time: four independent evaluation chains in
+    // flight instead of one long dependent chain per element
 #pragma unroll
-    for (int k = 0; k < kC; k++) {
-        const float y = ldexpf(v[k], e);
-        if (fabsf(y - rintf(y)) + ldexpf(er[k], e) >= 0.5f) v[k] = ev.exact(A[k], B[k]);
+    for (int k0 = 0; k0 < kC; k0 += kExactBatch) {
+        bool need[kExactBatch];
+        bool any = false;
+#pragma unroll
+        for (int j = 0; j < kExactBatch; j++) {
+            const float y = ldexpf(v[k0 + j], e);
+            need[j] = fabsf(y - rintf(y)) + ldexpf(er[k0 + j], e) >= 0.5f;
+            any |= need[j];
+        }
+        if (any) {
+            float ex[kExactBatch];
+#pragma unroll
+            for (int j = 0; j < kExactBatch; j++) ex[j] = ev.exact(A[k0 + j], B[k0 + j]);
+#pragma unroll
+            for (int j = 0; j < kExactBatch; j++) v[k0 + j] = need[j] ? ex[j] : v[k0 + j];
+        }
+        __builtin_amdgcn_sched_barrier(0);
     }
     int q0 = 0, q1 = 0, c0 = 0, c1 = 1;
 #pragma unroll
@@ -667,10 +684,15 @@ __device__ void fold_segment(const Eval<KIND>& ev, const Work& w, int row, int s
         }
         if (!clean) {
             float* dv = w.dirty + (si * kDirtyCap + slot) * kC;
+            // four exact elements live at a time
 #pragma unroll
-            for (int k = 0; k < kC; k++) {
-                dv[k] = base + k < ev.V ? ev.exact(A[k], B[k]) : 0.0f;
-                __builtin_amdgcn_sched_barrier(0);   // one exact element live at a time
+            for (int k0 = 0; k0 < kC; k0 += kExactBatch) {
+                float ex[kExactBatch];
+#pragma unroll
+                for (int j = 0; j < kExactBatch; j++)   // 0 past V (argument -inf)
+                    ex[j] = ev.exact(A[k0 + j], B[k0 + j]);
+                *(float4*)(dv + k0) = make_float4(ex[0], ex[1], ex[2], ex[3]);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
