@@ -216,7 +216,7 @@ struct EosShared {
     int wcount[kWaves];
     int n_items;
     int dirty_slot[kThreads];    // staging slot of a dirty chunk (-1: none)
-    float dirty_vals[kDirtySlots][kCh];
+    alignas(16) float dirty_vals[kDirtySlots][kCh];
     float total;
     int result;
     float fval;
@@ -326,14 +326,29 @@ __device__ __forceinline__ SegMono wave_incl_seg(SegMono v) {
 }
 
 // Staged values of a dirty chunk, or the generator when it was not staged.
+typedef float vf4 __attribute__((ext_vector_type(4)));
+
+// s + v.x + v.y + v.z + v.w, in order (fp32)
+__device__ __forceinline__ float add4(float s, vf4 v) {
+    s = __fadd_rn(s, v.x);
+    s = __fadd_rn(s, v.y);
+    s = __fadd_rn(s, v.z);
+    return __fadd_rn(s, v.w);
+}
+
+// A staged chunk: every lane reads all of it (one address: a broadcast) and
+// runs the same additions in its own registers, so the serial chain carries
+// no cross-lane moves.
 template <class G>
 __device__ __forceinline__ float replay_chunk_staged(const G& g, int slot, int base, int n,
                                                      float s, EosShared& sh) {
     if (slot < 0) return replay_chunk_wave(g, base, n, s);
-    const float x = lane_id() < kCh ? sh.dirty_vals[slot][lane_id()] : 0.0f;
+    const vf4* p = (const vf4*)sh.dirty_vals[slot];
+    vf4 v[kCh / 4];
 #pragma unroll
-    for (int k = 0; k < kCh; k++)
-        s = __fadd_rn(s, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), k)));
+    for (int i = 0; i < kCh / 4; i++) v[i] = p[i];
+#pragma unroll
+    for (int i = 0; i < kCh / 4; i++) s = add4(s, v[i]);
     return s;
 }
 

@@ -847,15 +847,6 @@ struct WalkShared {
     int over[kMaxSegs];
 };
 
-typedef float vf4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ float add4(float s, vf4 v) {
-    s = __fadd_rn(s, v.x);
-    s = __fadd_rn(s, v.y);
-    s = __fadd_rn(s, v.z);
-    return __fadd_rn(s, v.w);
-}
-
 // Replay n staged chunks (exact values at sv, in LDS) from s: fp32 additions
 // in order.  Every lane reads the whole chunk (one address: a broadcast) and
 // runs the same additions in its own registers, so the serial chain has no
