@@ -137,11 +137,12 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
 struct Mono {                    // effect of a run of additions on (n, parity)
-    double q0, q1;               // increment (in ulps) for input parity 0 / 1
+    int q0, q1;                  // increment (in ulps) for input parity 0 / 1; a run
+                                 // stays in one binade, so under 2^24
     int c0, c1;                  // output parity for input parity 0 / 1
 };
 
-__device__ __forceinline__ Mono mono_id() { return Mono{0.0, 0.0, 0, 1}; }
+__device__ __forceinline__ Mono mono_id() { return Mono{0, 0, 0, 1}; }
 
 __device__ __forceinline__ Mono mono_then(const Mono& a, const Mono& b) {
     Mono r;
@@ -206,6 +207,7 @@ __device__ __forceinline__ int parity_of(float s, int b) {
 struct EosShared {
     double wsum[kWaves];
     SegMono wseg[kWaves];
+    SegMono wpre[kWaves];        // wave w: aggregate of waves 0..w-1
     Mono incl[kThreads];
     int binade[kThreads];
     int head[kThreads];
@@ -305,8 +307,8 @@ __device__ __forceinline__ double wave_incl_sum_d(double x) {
 template <int CTRL, int RMASK>
 __device__ __forceinline__ SegMono dpp_seg(const SegMono& v) {
     SegMono o;
-    o.m.q0 = dpp_d<CTRL, RMASK>(v.m.q0);
-    o.m.q1 = dpp_d<CTRL, RMASK>(v.m.q1);
+    o.m.q0 = dpp_i<CTRL, RMASK>(v.m.q0);
+    o.m.q1 = dpp_i<CTRL, RMASK>(v.m.q1);
     o.m.c0 = dpp_i<CTRL, RMASK>(v.m.c0);
     o.m.c1 = dpp_i<CTRL, RMASK>(v.m.c1);
     o.head = dpp_i<CTRL, RMASK>(v.head);
@@ -380,7 +382,7 @@ __device__ __forceinline__ Mono fold_chunk(XF xk, int b) {
             c1 ^= qo;
         }
     }
-    return Mono{(double)q0, (double)q1, c0, c1};
+    return Mono{q0, q1, c0, c1};
 }
 
 // Segmented scan, walk and exact chunk boundaries of one round, shared by the
@@ -400,11 +402,25 @@ __device__ __forceinline__ float eos_tail(const Mono& own, bool clean, int b, co
     v = wave_incl_seg(v);
     if (lane_id() == 63) sh.wseg[wave_id()] = v;
     __syncthreads();
-    if (wave_id() > 0) {
-        SegMono pre = sh.wseg[0];
-        for (int w = 1; w < wave_id(); w++) pre = seg_then(pre, sh.wseg[w]);
-        v = seg_then(pre, v);
+    // the waves' aggregates scanned by wave 0 (lane w: waves 0..w), so each
+    // wave combines one exclusive prefix instead of looping over the waves
+    // before it (chunk 0 heads wave 0's range: every prefix has a head)
+    if (wave_id() == 0) {
+        SegMono a{mono_id(), 0, 0};
+        if (lane_id() < kWaves) {
+            const SegMono& src = sh.wseg[lane_id()];
+            a.m.q0 = src.m.q0;
+            a.m.q1 = src.m.q1;
+            a.m.c0 = src.m.c0;
+            a.m.c1 = src.m.c1;
+            a.head = src.head;
+            a.flag = src.flag;
+        }
+        a = wave_incl_seg(a);
+        if (lane_id() < kWaves - 1) sh.wpre[lane_id() + 1] = a;
     }
+    __syncthreads();
+    if (wave_id() > 0) v = seg_then(sh.wpre[wave_id()], v);
     sh.incl[t] = v.m;
     sh.head[t] = v.head;
     const bool is_last = t == kThreads - 1 || sh.binade[t + 1] != sh.binade[t] ||
@@ -441,7 +457,7 @@ __device__ __forceinline__ float eos_tail(const Mono& own, bool clean, int b, co
             const int my_b = sh.binade[my_c];
             const int my_e = my_b != kDirty ? sh.seg_last[my_c] : my_c;
             const int my_slot = sh.dirty_slot[my_c];
-            double my_q0 = 0.0, my_q1 = 0.0;
+            int my_q0 = 0, my_q1 = 0;
             if (my_b != kDirty) {
                 my_q0 = sh.incl[my_e].q0;
                 my_q1 = sh.incl[my_e].q1;
@@ -470,7 +486,8 @@ __device__ __forceinline__ float eos_tail(const Mono& own, bool clean, int b, co
                     }
                 } else {
                     if (lane_id() == 0) sh.cstart[rd][c] = s;
-                    const double q0 = readlane_f64(my_q0, k), q1 = readlane_f64(my_q1, k);
+                    const double q0 = __builtin_amdgcn_readlane(my_q0, k),
+                                 q1 = __builtin_amdgcn_readlane(my_q1, k);
                     const double q = parity_of(s, bc) ? q1 : q0;
                     s = (float)((double)s + q * ulp_of(bc));
                 }
@@ -486,7 +503,13 @@ __device__ __forceinline__ float eos_tail(const Mono& own, bool clean, int b, co
         const int h = sh.head[t];
         const float sh0 = sh.cstart[rd][h];
         const int par = parity_of(sh0, bt);
-        const Mono ex = (t == h) ? mono_id() : sh.incl[t - 1];
+        Mono ex = mono_id();
+        if (t != h) {
+            ex.q0 = sh.incl[t - 1].q0;
+            ex.q1 = sh.incl[t - 1].q1;
+            ex.c0 = sh.incl[t - 1].c0;
+            ex.c1 = sh.incl[t - 1].c1;
+        }
         const double u = ulp_of(bt);
         const double s0 = (double)sh0 + (par ? ex.q1 : ex.q0) * u;
         const int par2 = par ? ex.c1 : ex.c0;
@@ -546,7 +569,8 @@ __device__ __forceinline__ float eos_round(const float (&x)[kCh], const G& g, in
         if (lane_id() == 0) sh.wcount[wave_id()] = __popcll(bal);
         __syncthreads();
         int off = 0;
-        for (int w = 0; w < wave_id(); w++) off += sh.wcount[w];
+#pragma unroll
+        for (int w = 0; w < kWaves - 1; w++) off += w < wave_id() ? sh.wcount[w] : 0;
         const int slot = off + below;
         const bool staged = !clean && slot < kDirtySlots;
         sh.dirty_slot[t] = staged ? slot : -1;
