@@ -38,6 +38,35 @@ def model(gpu, vocab, max_seq, max_tokens, seed, batch=0, layers=32, share=None)
     return m
 
 
+def test_c4_stack_logits_finite_and_row_count_independent(gpu):
+    """The 32-layer stack after a 4096-token context: the logits of 5 tokens
+    forwarded at once are finite, spread out, and equal (to the fp32
+    accumulation tolerance) to those of the same tokens forwarded one at a
+    time -- the M = 5 kernels (GEMV rows, 5-row attention) against the M = 1
+    ones at the full shape.  (Acceptance-only checks pass on NaN logits: the
+    acceptance ratio of NaN probabilities is 1.)"""
+    print("C4 stack logits, 5 rows at once vs one at a time", flush=True)
+    V, ctx = 32000, 4096
+    m = model(gpu, V, ctx + 16, 5, 7)
+    assert gpu.cgx_model_fill_context(m, ctx, 99) == 0, last_error(gpu)
+    toks = np.array([11, 222, 3333, 4444, 31999], np.int32)
+    assert gpu.cgx_model_forward(m, toks.ctypes.data, 5, 5, None) == 0, last_error(gpu)
+    all5 = np.zeros((5, V), np.float32)
+    assert gpu.cgx_memcpy_d2h(all5.ctypes.data, gpu.cgx_model_logits(m), all5.nbytes) == 0
+    assert np.isfinite(all5).all()
+    assert all5.std(axis=1).min() > 1e-3, all5.std(axis=1)
+    assert gpu.cgx_model_truncate(m, ctx) == 0
+    one = np.zeros((5, V), np.float32)
+    for i in range(5):
+        assert gpu.cgx_model_forward(m, toks[i:i + 1].ctypes.data, 1, 1, None) == 0, \
+            last_error(gpu)
+        assert gpu.cgx_memcpy_d2h(one[i].ctypes.data, gpu.cgx_model_logits(m), V * 4) == 0
+    scale = float(np.abs(all5).max())
+    err = float(np.abs(one - all5).max())
+    assert err <= 2e-3 * scale, (err, scale)
+    gpu.cgx_model_free(m)
+
+
 def test_c4_batch1_identical_draft_accepts_everything(gpu):
     print("C4 batch 1, identical draft", flush=True)
     g, ctx, steps = 4, 4096, 3
