@@ -184,6 +184,7 @@ struct Work {
     float* item_start;   // [Rall][nseg][kItemCap]
     float* dirty_start;  // [Rall][nseg][kDirtyCap] exact value at each staged chunk start
     double* task_ge;     // [chains][nseg][2] residual guide sums, bounds
+    MI* chunk_mi;        // [chains][nseg][kT] pass-2 chunk summaries (identity if staged)
     Task* task;          // [chains]
     int* flags;          // [chains] 1: non-finite row, 2: residual mass < 1e-10
 };
@@ -640,6 +641,8 @@ __device__ void fold_segment(const Eval<KIND>& ev, const Work& w, int row, int s
     const int b = binade_of(lo);
     const bool clean = binade_of(hi) == b;
     const MI own = clean ? fold_chunk16(ev, A, B, v, er, b) : mi_id();
+    if constexpr (KIND != kKindExp)   // pass 2: the find resolves a clean run from these
+        w.chunk_mi[((size_t)(row - w.R1) * w.nseg + seg) * kT + t] = own;
     sh.bin[t] = clean ? b : kDirty;
     __syncthreads();
     const bool head = t == 0 || sh.bin[t - 1] != sh.bin[t];
@@ -1049,12 +1052,12 @@ __global__ __launch_bounds__(64) void k_decide(Rows rows, const int* __restrict_
 struct FindShared {
     FoldShared fold;
     int item;
+    float sst[kMaxSegs], send[kMaxSegs];   // segment starts and ends
+    int scnt[kMaxSegs];                      // runs per segment (-1: replayed exactly)
+    Item it[kItemCap];                       // the segment's runs,
+    float ist[kItemCap], iend[kItemCap];     // their starts and ends
+    float dst[kT];                           // a staged run's chunk starts
 };
-
-// end value of item i of a segment (start of the next item, or of the next segment)
-__device__ __forceinline__ float iend_of(const float* is, int i, int n, const float* ss, int seg) {
-    return i + 1 < n ? is[i + 1] : ss[seg + 1];
-}
 
 // First element i of the row with thr < (running value after i), from the
 // walk's exact starts; dflt when the row sum does not exceed thr.
@@ -1063,68 +1066,73 @@ __device__ int find_row(const Eval<KIND>& ev, const Work& w, int row, float thr,
                         FindShared& sh) {
     const int t = threadIdx.x;
     const float* ss = w.seg_start + (size_t)row * (w.nseg + 1);
-    const int seg = block_first256(t < w.nseg && thr < ss[t + 1], sh.fold.i);
+    // each search step loads everything its successor needs from the step's
+    // answer in one round trip: the segments' starts, ends and run counts,
+    // then the segment's runs with their starts and ends, then a staged
+    // run's chunk starts (the choices travel through LDS)
+    if (t < w.nseg) {
+        sh.sst[t] = ss[t];
+        sh.send[t] = ss[t + 1];
+        sh.scnt[t] = w.cnt[2 * segi(w, row, t)];
+    }
+    const int seg = block_first256(t < w.nseg && thr < sh.send[t < w.nseg ? t : 0], sh.fold.i);
     if (seg >= w.nseg) return dflt;
     const size_t si = segi(w, row, seg);
-    const int n = w.cnt[2 * si];
+    const int n = sh.scnt[seg];
     const int segbase = seg * kSeg;
     int j0 = segbase, j1 = min(segbase + kSeg, ev.V);
-    float s0 = ss[seg];
+    float s0 = sh.sst[seg];
     if (n >= 0) {
         const Item* its = w.items + si * kItemCap;
         const float* is = w.item_start + si * kItemCap;
-        const float iend = t < n ? (t + 1 < n ? is[t + 1] : ss[seg + 1]) : 0.0f;
-        const int i = block_first256(t < n && thr < iend, sh.fold.i);
+        const float segend = sh.send[seg];
+        if (t < n) {
+            sh.it[t] = its[t];
+            sh.ist[t] = is[t];
+            sh.iend[t] = t + 1 < n ? is[t + 1] : segend;
+        }
+        const int i = block_first256(t < n && thr < sh.iend[t < n ? t : 0], sh.fold.i);
         if (i >= n) return dflt;
-        const Item it = its[i];
-        s0 = is[i];
+        const Item it = sh.it[i];
+        const int cnext = i + 1 < n ? sh.it[i + 1].chunk : kT;
+        s0 = sh.ist[i];
         if (it.binade == kDirty) {
             // staged run: the walk left the exact start of each of its chunks
-            const int nc = (i + 1 < n ? its[i + 1].chunk : kT) - it.chunk;
+            const int nc = cnext - it.chunk;
             const float* ds = w.dirty_start + si * kDirtyCap + it.slot;
-            const float cend = t < nc ? (t + 1 < nc ? ds[t + 1] : iend_of(is, i, n, ss, seg)) : 0.0f;
+            float cend = 0.0f;
+            if (t < nc) {
+                sh.dst[t] = ds[t];
+                cend = t + 1 < nc ? ds[t + 1] : sh.iend[i];
+            }
             const int ch = block_first256(t < nc && thr < cend, sh.fold.i);
             if (ch >= nc) return dflt;
-            s0 = ds[ch];
+            s0 = sh.dst[ch];
             j0 = segbase + (it.chunk + ch) * kC;
             j1 = min(j0 + kC, ev.V);
         } else {
             // clean run [c0, c1): exact chunk ends from the chunk summaries
-            const int c0 = it.chunk, c1 = i + 1 < n ? its[i + 1].chunk : kT;
-            const int b = it.binade;
+            // that the fold left (the same summaries the run's total came from)
+            const int c0 = it.chunk, c1 = cnext;
             const bool mine = t >= c0 && t < c1;
-            MI own = mi_id();
-            if (mine) {
-                float A[kC], B[kC], v[kC], er[kC];
-                ev.args(segbase + t * kC, A, B);
-#pragma unroll
-                for (int k = 0; k < kC; k++) {
-                    const float2 q = ev.approx(A[k], B[k]);
-                    v[k] = q.x;
-                    er[k] = q.y;
-                }
-                own = fold_chunk16(ev, A, B, v, er, b);
-            }
+            const MI own = mine ? w.chunk_mi[((size_t)(row - w.R1) * w.nseg + seg) * kT + t]
+                                : mi_id();
             SMI sv{own, 0};
             sv = wave_incl_smi(sv);
             __syncthreads();
             if (lane_id() == 63) sh.fold.wagg[wave_id()] = sv;
             __syncthreads();
             MI pre = mi_id();
-            for (int ww = 0; ww < wave_id(); ww++) pre = mi_then(pre, sh.fold.wagg[ww].m);
+#pragma unroll
+            for (int ww = 0; ww < kW - 1; ww++)
+                if (ww < wave_id()) pre = mi_then(pre, sh.fold.wagg[ww].m);
             const MI incl = mi_then(pre, sv.m);
             const float cend = mine ? mi_apply(s0, incl) : 0.0f;
+            sh.dst[t] = cend;
             const int ch = block_first256(mine && thr < cend, sh.fold.i);
             if (ch >= c1) return dflt;
-            // start of chunk ch: the run start advanced by chunks [c0, ch)
-            SMI bv{(t >= c0 && t < ch) ? own : mi_id(), 0};
-            bv = wave_incl_smi(bv);
-            __syncthreads();
-            if (lane_id() == 63) sh.fold.wagg[wave_id()] = bv;
-            __syncthreads();
-            MI tot = mi_id();
-            for (int ww = 0; ww < kW; ww++) tot = mi_then(tot, sh.fold.wagg[ww].m);
-            s0 = mi_apply(s0, tot);
+            // start of chunk ch: the end of chunk ch - 1, or the run's start
+            s0 = ch > c0 ? sh.dst[ch - 1] : s0;
             j0 = segbase + ch * kC;
             j1 = min(j0 + kC, ev.V);
         }
@@ -1298,6 +1306,7 @@ static int verify_pipe(const float* target, size_t ldt, const float* draft, cons
     const size_t o_ist = take((size_t)Rall * nseg * kItemCap * 4);
     const size_t o_dst = take((size_t)Rall * nseg * kDirtyCap * 4);
     const size_t o_tge = take((size_t)batch * nseg * 16);
+    const size_t o_cmi = take((size_t)batch * nseg * kT * sizeof(MI));
     const size_t o_task = take((size_t)batch * sizeof(Task));
     const size_t o_flags = take((size_t)batch * 4);
     const size_t o_ap = take((size_t)batch * gamma * 4);
@@ -1324,6 +1333,7 @@ static int verify_pipe(const float* target, size_t ldt, const float* draft, cons
     w.seg_start = (float*)(ws + o_sst);
     w.item_start = (float*)(ws + o_ist);
     w.dirty_start = (float*)(ws + o_dst);
+    w.chunk_mi = (MI*)(ws + o_cmi);
     w.task_ge = (double*)(ws + o_tge);
     w.task = (Task*)(ws + o_task);
     w.flags = (int*)(ws + o_flags);
