@@ -919,7 +919,9 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4xfp32->fp32",
+        # INT4 weights (exact in fp16) times the fp32 activation*scale carried
+        # as hi + lo fp16 (22 significant bits) on the matrix cores, fp32 sums
+        "dtype": "int4 x fp32(as fp16 hi+lo, 22 bits) -> fp32",
         "data": "synthetic (BASELINE config 2: uniform nibbles, fp16-valued scales, "
                 "x~N(0,1)); weights rotated over >2x MALL",
         "config": {"workload": f"int4_gemv K={K} N={N} g={gs} M={args.rows}",
