@@ -97,22 +97,36 @@ struct DecArgs {
 
 __device__ __forceinline__ int head_begin(int hk, int H, int Hk) { return (hk * H + Hk - 1) / Hk; }
 
+// Nibble-decode constants: the masks in SGPRs and the fp16 exponent bits in
+// a VGPR, produced where the compiler does not see them as constants.  It
+// then forms (w & m) | c as one v_and_or_b32; with literal masks it emits a
+// separate AND and OR, because VOP3 takes no literal operand on this target.
+struct NibConst {
+    uint32_t mlo, mhi, mag;
+};
+
+__device__ __forceinline__ NibConst nib_consts() {
+    NibConst k;
+    asm volatile("s_mov_b32 %0, 0x000f000f" : "=s"(k.mlo));
+    asm volatile("s_mov_b32 %0, 0x00f000f0" : "=s"(k.mhi));
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(k.mag));
+    return k;
+}
+
 // nibble slot of MFMA position p inside a u32 of 8 nibbles (see nib_pairs)
 __device__ __forceinline__ int slot_of(int p) { return (p >> 1) + 4 * (p & 1); }
 
 // Eight offset-binary nibbles of w as exact fp16 (o - 8), in position order
 // p -> slot {0,4,1,5,2,6,3,7}[p].
-__device__ __forceinline__ f16x8 nib_to_f16(uint32_t w) {
+__device__ __forceinline__ f16x8 nib_to_f16(uint32_t w, const NibConst& nk) {
     const uint32_t w8 = w >> 8;
     const f16x2 m1032 = {(_Float16)-1032.0f, (_Float16)-1032.0f};
     const f16x2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
     const f16x2 m72 = {(_Float16)-72.0f, (_Float16)-72.0f};
-    f16x2 p0 = __builtin_bit_cast(f16x2, (w & 0x000F000Fu) | 0x64006400u) + m1032;
-    f16x2 p1 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (w & 0x00F000F0u) | 0x64006400u),
-                                         s16, m72);
-    f16x2 p2 = __builtin_bit_cast(f16x2, (w8 & 0x000F000Fu) | 0x64006400u) + m1032;
-    f16x2 p3 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (w8 & 0x00F000F0u) | 0x64006400u),
-                                         s16, m72);
+    f16x2 p0 = __builtin_bit_cast(f16x2, (w & nk.mlo) | nk.mag) + m1032;
+    f16x2 p1 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (w & nk.mhi) | nk.mag), s16, m72);
+    f16x2 p2 = __builtin_bit_cast(f16x2, (w8 & nk.mlo) | nk.mag) + m1032;
+    f16x2 p3 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (w8 & nk.mhi) | nk.mag), s16, m72);
     f16x8 r;
     r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
     r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
@@ -120,18 +134,17 @@ __device__ __forceinline__ f16x8 nib_to_f16(uint32_t w) {
 }
 
 // Nibble t (0..7) of two offset-binary words as an exact fp16 pair (o - 8).
-__device__ __forceinline__ f16x2 nib_pair(uint32_t wlo, uint32_t whi, int t) {
+__device__ __forceinline__ f16x2 nib_pair(uint32_t wlo, uint32_t whi, int t, const NibConst& nk) {
     const uint32_t b = (uint32_t)(t >> 1);
     const uint32_t sel = 0x0C000C00u | ((4u + b) << 16) | b;
     const uint32_t v = __builtin_amdgcn_perm(whi, wlo, sel);
     if (t & 1) {
         const f16x2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
         const f16x2 m72 = {(_Float16)-72.0f, (_Float16)-72.0f};
-        return __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (v & 0x00F000F0u) | 0x64006400u),
-                                         s16, m72);
+        return __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (v & nk.mhi) | nk.mag), s16, m72);
     }
     const f16x2 m1032 = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-    return __builtin_bit_cast(f16x2, (v & 0x000F000Fu) | 0x64006400u) + m1032;
+    return __builtin_bit_cast(f16x2, (v & nk.mlo) | nk.mag) + m1032;
 }
 
 __device__ __forceinline__ void split16(float v, _Float16& hi, _Float16& lo) {
@@ -168,6 +181,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_dec(DecArgs a) {
     __shared__ float s_w[kWaves][ROWS], s_M[ROWS], s_L[ROWS];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const NibConst nk = nib_consts();
     const int n = lane & 15, g = lane >> 4;
     const int split = blockIdx.x, hk = blockIdx.y;
     const int h0 = head_begin(hk, a.H, a.Hk), h1 = head_begin(hk + 1, a.H, a.Hk);
@@ -361,7 +375,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_dec(DecArgs a) {
         for (int kh = 0; kh < 2; kh++)
 #pragma unroll
             for (int c = 0; c < NC; c++) {
-                const f16x8 ka = nib_to_f16(kw[kh][c] ^ 0x88888888u);
+                const f16x8 ka = nib_to_f16(kw[kh][c] ^ 0x88888888u, nk);
 #pragma unroll
                 for (int rt = 0; rt < RT; rt++) {
                     s[rt][kh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, s_q[rt][c][0][ql], s[rt][kh], 0, 0, 0);
@@ -449,7 +463,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_dec(DecArgs a) {
             f16x8 va;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                f16x2 pr = nib_pair(vw[2 * j], vw[2 * j + 1], t);
+                f16x2 pr = nib_pair(vw[2 * j], vw[2 * j + 1], t, nk);
                 va[2 * j] = pr[0];
                 va[2 * j + 1] = pr[1];
             }

@@ -78,18 +78,32 @@ __device__ __forceinline__ int logical_tile(int L, int paired, int ff_tiles) {
     return paired ? ((L & 1) ? ff_tiles + (L >> 1) : (L >> 1)) : L;
 }
 
+// Nibble-decode constants: the masks in SGPRs and the fp16 exponent bits in
+// a VGPR, produced where the compiler does not see them as constants.  It
+// then forms (w & m) | c as one v_and_or_b32; with literal masks it emits a
+// separate AND and OR, because VOP3 takes no literal operand on this target.
+struct NibConst {
+    uint32_t mlo, mhi, mag;
+};
+
+__device__ __forceinline__ NibConst nib_consts() {
+    NibConst k;
+    asm volatile("s_mov_b32 %0, 0x000f000f" : "=s"(k.mlo));
+    asm volatile("s_mov_b32 %0, 0x00f000f0" : "=s"(k.mhi));
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(k.mag));
+    return k;
+}
+
 // Four MFMA B operands (one per k-block of a chunk) from the lane's 16 bytes.
-__device__ __forceinline__ f16x8 nib_to_f16(uint32_t w) {
-    const uint32_t lo = w & 0x000F000Fu, hi4 = w & 0x00F000F0u;
+__device__ __forceinline__ f16x8 nib_to_f16(uint32_t w, const NibConst& nk) {
     const uint32_t w8 = w >> 8;
-    const uint32_t lo8 = w8 & 0x000F000Fu, hi8 = w8 & 0x00F000F0u;
     const f16x2 m1032 = {(_Float16)-1032.0f, (_Float16)-1032.0f};
     const f16x2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
     const f16x2 m72 = {(_Float16)-72.0f, (_Float16)-72.0f};
-    f16x2 p0 = __builtin_bit_cast(f16x2, lo | 0x64006400u) + m1032;
-    f16x2 p1 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, hi4 | 0x64006400u), s16, m72);
-    f16x2 p2 = __builtin_bit_cast(f16x2, lo8 | 0x64006400u) + m1032;
-    f16x2 p3 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, hi8 | 0x64006400u), s16, m72);
+    f16x2 p0 = __builtin_bit_cast(f16x2, (w & nk.mlo) | nk.mag) + m1032;
+    f16x2 p1 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (w & nk.mhi) | nk.mag), s16, m72);
+    f16x2 p2 = __builtin_bit_cast(f16x2, (w8 & nk.mlo) | nk.mag) + m1032;
+    f16x2 p3 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (w8 & nk.mhi) | nk.mag), s16, m72);
     f16x8 r;
     r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
     r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
@@ -134,6 +148,7 @@ __global__ __launch_bounds__(64 * W, (NG == 2 && T == 2 && MP <= 5) ? 4 : 1) voi
     __shared__ float s_ssq[W][MP];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const NibConst nk = nib_consts();
     const int M = a.M;
     const int paired = EPI == kEpiSwiGlu;
     const int ff_tiles = a.ff / 16;
@@ -288,7 +303,7 @@ __global__ __launch_bounds__(64 * W, (NG == 2 && T == 2 && MP <= 5) ? 4 : 1) voi
                     const u32x4 wv = wcur[j][kb >> 2];
                     const uint32_t word = (kb & 3) == 0 ? wv.x : (kb & 3) == 1 ? wv.y
                                         : (kb & 3) == 2 ? wv.z : wv.w;
-                    f16x8 b = nib_to_f16(word);
+                    f16x8 b = nib_to_f16(word, nk);
                     acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, acc[j], 0, 0, 0);
                     if (MP > 8) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, acc[j], 0, 0, 0);
                 }
@@ -542,6 +557,7 @@ __global__ __launch_bounds__(64 * kGemmWaves, 2) void k_gemm_int4(GemmArgs a) {
     __shared__ _Float16 sa[2][2][BM][kGemmRowH];
     __shared__ float s_unscale[BM];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const NibConst nk = nib_consts();
     const int paired = NG == 2;
     const int nchunks = a.K / kChunkK;
     const int bx = blockIdx.x;
@@ -723,7 +739,7 @@ __global__ __launch_bounds__(64 * kGemmWaves, 2) void k_gemm_int4(GemmArgs a) {
             for (int j = 0; j < kGemmTiles; j++) {
                 const uint32_t word = kb == 0 ? wcur[j].x : kb == 1 ? wcur[j].y
                                     : kb == 2 ? wcur[j].z : wcur[j].w;
-                b[j] = nib_to_f16(word);
+                b[j] = nib_to_f16(word, nk);
             }
 #pragma unroll
             for (int rt = 0; rt < RT; rt++) {
