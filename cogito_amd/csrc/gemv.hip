@@ -531,6 +531,7 @@ int launch_pe(const MfmaArgs& a, int T) {
 // gate|up pair).
 
 constexpr int kGemmWaves = 4;
+constexpr int kBufWord3 = 0x00020000;    // buffer resource word 3 (raw dword access)
 constexpr int kGemmTiles = 4;            // column tiles per wave
 constexpr int kGemmRowH = kChunkK + 8;   // LDS pitch (halfs) of an A row
 
@@ -632,28 +633,38 @@ __global__ __launch_bounds__(64 * kGemmWaves, 2) void k_gemm_int4(GemmArgs a) {
         if (threadIdx.x < BM)
             s_unscale[threadIdx.x] = a.unscale[min(row0 + (int)threadIdx.x, a.M - 1)];
     }
-    const float* nwp = PRO == kProRmsNorm ? a.nw : a.scales_t;
 
     // ---- this wave's tiles: slot ws, tiles 4 (wave & 1) + j of the slot.  A
     // wave of a missing slot (odd number of 128-column slots) runs on tile 0
     // and stores nothing, so that every wave takes the same path.
     const int ws = wave >> 1;
     const int wave_ok = slot_ok[ws];
-    const uint8_t* wp[kGemmTiles];
+    // loads through buffer resources: a lane's 32-bit offset is fixed, the
+    // step's advance is a uniform SGPR offset, so a step's loads take no
+    // address arithmetic (the resources bound every access to its array)
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.w, (short)0, (int)((size_t)a.N / 16 * nchunks * kChunkBytes), kBufWord3);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.x, (short)0, (int)((size_t)a.M * a.ldx * 4), kBufWord3);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.scales_t, (short)0, (int)((size_t)(a.N / a.gs) * a.K * 4), kBufWord3);
+    const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(PRO == kProRmsNorm ? a.nw : a.scales_t), (short)0, a.K * 4, kBufWord3);
+    int wo[kGemmTiles];
 #pragma unroll
     for (int j = 0; j < kGemmTiles; j++) {
         const int t = 4 * (wave & 1) + j;               // tile within the slot
         const int L = paired ? 2 * (8 * bx + t) + ws : 8 * (2 * bx + ws) + t;
-        wp[j] = a.w + ((size_t)(wave_ok ? L : 0) * nchunks) * kChunkBytes + 16 * lane;
+        wo[j] = (wave_ok ? L : 0) * nchunks * kChunkBytes + 16 * lane;
     }
     // steps run in pairs; a step at or past c1 (odd count) prepares zeros and
     // reads the split's last chunk again
     const int cend = c0 + ((c1 - c0 + 1) & ~1);
     auto wload = [&](int c, u32x4 (&d)[kGemmTiles]) {
-        const size_t off = (size_t)min(c, c1 - 1) * kChunkBytes;
+        const int off = min(c, c1 - 1) * kChunkBytes;
 #pragma unroll
         for (int j = 0; j < kGemmTiles; j++)
-            d[j] = __builtin_nontemporal_load((const u32x4*)(wp[j] + off));
+            d[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo[j], off, 2));
     };
     u32x4 wb0[kGemmTiles], wb1[kGemmTiles];
     __builtin_amdgcn_sched_barrier(0);
@@ -668,14 +679,22 @@ __global__ __launch_bounds__(64 * kGemmWaves, 2) void k_gemm_int4(GemmArgs a) {
     // prefetched preparation inputs
     float4 px[RPT], ps[2], pn = make_float4(1.f, 1.f, 1.f, 1.f);
     uint32_t plive;
+    int xo[RPT], so[2];
+#pragma unroll
+    for (int i = 0; i < RPT; i++) xo[i] = (xrow[i] * a.ldx + pk) * 4;
+#pragma unroll
+    for (int s_ = 0; s_ < 2; s_++) so[s_] = (grp[s_] * a.K + pk) * 4;
+    auto ld4 = [](const __amdgpu_buffer_rsrc_t& r, int vo, int so_) {
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so_, 0));
+    };
     auto load_prep = [&](int c) {
         const int cc = min(c, c1 - 1);
-        const int k = cc * kChunkK + pk;
-        if (PRO == kProRmsNorm) pn = *(const float4*)(nwp + k);
+        const int kb = cc * kChunkK * 4;
+        if (PRO == kProRmsNorm) pn = ld4(rn, pk * 4, kb);
 #pragma unroll
-        for (int s_ = 0; s_ < 2; s_++) ps[s_] = *(const float4*)(a.scales_t + (size_t)grp[s_] * a.K + k);
+        for (int s_ = 0; s_ < 2; s_++) ps[s_] = ld4(rs, so[s_], kb);
 #pragma unroll
-        for (int i = 0; i < RPT; i++) px[i] = *(const float4*)(a.x + (size_t)xrow[i] * a.ldx + k);
+        for (int i = 0; i < RPT; i++) px[i] = ld4(rx, xo[i], kb);
         plive = c < c1 ? ~0u : 0u;
     };
     // the same load order as at the end of a step pair, so that the loop
