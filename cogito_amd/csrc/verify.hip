@@ -750,11 +750,94 @@ __global__ __launch_bounds__(kT) void k_seg_fold1(Rows rows, float T, Work w) {
     fold_segment(pass1_eval(rows, r, m, T), w, r, seg, X, Y, P0, E0, sh);
 }
 
-// residual guide sums of the first-reject row pairs (pass-2 stats)
-__global__ __launch_bounds__(kT) void k_res_stats(Rows rows, float T, Work w) {
+// The decisions of chain c, by one wave: non-finite rows (NaN, +inf, all
+// -inf) go to the exact single-block path; otherwise the accept tests of the
+// drafted tokens, the first reject j and the chain's pass-2 task (the
+// residual of pair j, or the bonus from target row gamma).  Every caller
+// computes the same decisions for a finite chain; the one with `write`
+// stores them (the others' task for a chain with non-finite rows is not used:
+// the kernels after this one read the stored task).
+__device__ Task decide_chain(const Rows& rows, const int* __restrict__ tokens,
+                             const float* __restrict__ u, float T, const Work& w, int c,
+                             bool write, float* __restrict__ accept_prob,
+                             int* __restrict__ out_tokens, int* __restrict__ n_accepted) {
+    const int l = lane_id(), gamma = rows.gamma, V = rows.V;
+    const int per = 2 * gamma + 1;
+    // only the storing caller checks for non-finite rows: a chain that has
+    // them is finished by the fallback whatever the others compute for it
+    int bad = 0;
+    if (write) {
+        for (int r = l; r < per; r += 64) {
+            const int rr = c * per + r;
+            bad |= !(w.row_m[rr] > -__builtin_inff()) || !(w.row_S[rr] <= FLT_MAX);
+            for (int s = 0; s < w.nseg; s++) bad |= w.seg_bad[segi(w, rr, s)];
+        }
+        bad = __any(bad);
+    }
+    const float* uu = u + (size_t)c * (gamma + 1);
+    bool reject = false;
+    if (l < gamma) {
+        const int x = tokens[(size_t)c * gamma + l];
+        float a = 0.0f;   // a draft token outside [0, V) is rejected
+        if (x >= 0 && x < V) {
+            const int rt = c * per + l, rd = c * per + gamma + 1 + l;
+            const float at = __fdiv_rn(__fsub_rn(rows.row(rt)[x], w.row_m[rt]), T);
+            const float ad = __fdiv_rn(__fsub_rn(rows.row(rd)[x], w.row_m[rd]), T);
+            const float px = __fdiv_rn(exp_glibc(at), w.row_S[rt]);
+            const float qx = __fdiv_rn(exp_glibc(ad), w.row_S[rd]);
+            a = qx < 1e-10f ? 1.0f : fminf(1.0f, __fdiv_rn(px, qx));
+        }
+        if (write && !bad) accept_prob[(size_t)c * gamma + l] = a;
+        reject = !(uu[l] < a);
+    }
+    const unsigned long long rb = __ballot(reject);
+    const int j = rb ? __builtin_ctzll(rb) : gamma;
+    Task tk;
+    tk.kind = bad ? -1 : (j < gamma ? kKindRes : kKindProb);
+    tk.ra = c * per + j;
+    tk.rb = c * per + gamma + 1 + (j < gamma ? j : 0);
+    tk.j = j;
+    tk.u = uu[j < gamma ? j + 1 : gamma];
+    tk.pad[0] = tk.pad[1] = tk.pad[2] = 0;
+    if (!write) return tk;
+    if (bad) {
+        if (l == 0) {
+            w.flags[c] = 1;
+            w.task[c].kind = -1;
+        }
+        return tk;
+    }
+    int* out = out_tokens + (size_t)c * (gamma + 1);
+    for (int i = l; i <= gamma; i += 64) {
+        if (i < j) out[i] = tokens[(size_t)c * gamma + i];
+        else if (i > j) out[i] = -1;
+    }
+    if (l == 0) {
+        n_accepted[c] = j;
+        w.flags[c] = 0;
+        w.task[c] = tk;
+    }
+    return tk;
+}
+
+// residual guide sums of the first-reject row pairs (pass-2 stats).  Each
+// block first takes its chain's decisions (the segment-0 block stores them
+// for the kernels after this one), so no separate launch decides.
+__global__ __launch_bounds__(kT) void k_res_stats(Rows rows, const int* __restrict__ tokens,
+                                                  const float* __restrict__ u, float T, Work w,
+                                                  float* __restrict__ accept_prob,
+                                                  int* __restrict__ out_tokens,
+                                                  int* __restrict__ n_accepted) {
     __shared__ double s_d[kW];
+    __shared__ Task s_task;
     const int seg = blockIdx.x, c = blockIdx.y;
-    const Task tk = w.task[c];
+    if (wave_id() == 0) {
+        const Task t0 = decide_chain(rows, tokens, u, T, w, c, seg == 0, accept_prob, out_tokens,
+                                     n_accepted);
+        if (lane_id() == 0) s_task = t0;
+    }
+    __syncthreads();
+    const Task tk = s_task;
     if (tk.kind != kKindRes) return;
     const Eval<kKindRes> ev = task_eval<kKindRes>(rows, w, tk, T);
     const int base = seg * kSeg + threadIdx.x * kC;
@@ -876,6 +959,15 @@ __device__ __forceinline__ float replay_lds(const float* sv, int n, float s,
 // Segments are walked in batches; a batch's runs and staged values are
 // gathered into LDS first, all loads in flight together, so the serial chain
 // of additions waits on global memory once per batch, not once per staged run.
+// The walk runs in one wave: its LDS traffic (and the LDS-bound loads,
+// waited for with s_waitcnt) needs ordering inside the wave only, so the walk
+// also runs as one wave of a larger block.
+__device__ __forceinline__ void walk_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <int KIND>
 __device__ void walk_row(const Eval<KIND>& ev, const Work& w, int row, WalkShared& sh) {
     const int l = lane_id();
@@ -899,7 +991,7 @@ __device__ void walk_row(const Eval<KIND>& ev, const Work& w, int row, WalkShare
         sh.over[l] = c < 0;
     }
     if (l == 0) sh.ioff[0] = sh.soff[0] = 0;
-    __syncthreads();
+    walk_sync();
     const float* rdirty = w.dirty + segi(w, row, 0) * kDirtyCap * kC;
     const Item* ritems = w.items + segi(w, row, 0) * kItemCap;
     float s = 0.0f;
@@ -931,7 +1023,7 @@ __device__ void walk_row(const Eval<KIND>& ev, const Work& w, int row, WalkShare
                 if (f + 4 * l < iz) load_lds16(isrc + f + 4 * l, idst + f);
         }
         __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+        walk_sync();
         for (int seg = g0; seg < g1; seg++) {
             const size_t si = segi(w, row, seg);
             if (l == 0) w.seg_start[(size_t)row * (w.nseg + 1) + seg] = s;
@@ -961,7 +1053,7 @@ __device__ void walk_row(const Eval<KIND>& ev, const Work& w, int row, WalkShare
                 }
             }
         }
-        __syncthreads();
+        walk_sync();
         g0 = g1;
     }
     if (l == 0) {
@@ -976,76 +1068,9 @@ __global__ __launch_bounds__(64) void k_walk1(Rows rows, float T, Work w) {
     walk_row(pass1_eval(rows, r, w.row_m[r], T), w, r, sh);
 }
 
-__global__ __launch_bounds__(64) void k_walk2(Rows rows, float T, Work w) {
-    __shared__ WalkShared sh;
-    const int c = blockIdx.x;
-    const Task tk = w.task[c];
-    if (tk.kind == kKindProb) walk_row(task_eval<kKindProb>(rows, w, tk, T), w, w.R1 + c, sh);
-    else if (tk.kind == kKindRes) walk_row(task_eval<kKindRes>(rows, w, tk, T), w, w.R1 + c, sh);
-}
 
 // ----------------------------------------------------------- decisions
 
-// One wave per chain: acceptance ratios (lane i: position i), first reject,
-// the accepted tokens, and the pass-2 task.
-__global__ __launch_bounds__(64) void k_decide(Rows rows, const int* __restrict__ tokens,
-                                               const float* __restrict__ u, float T, Work w,
-                                               float* __restrict__ accept_prob,
-                                               int* __restrict__ out_tokens,
-                                               int* __restrict__ n_accepted) {
-    const int c = blockIdx.x, l = lane_id(), gamma = rows.gamma, V = rows.V;
-    const int per = 2 * gamma + 1;
-    // non-finite rows (NaN, +inf, all -inf) go to the exact single-block path
-    int bad = 0;
-    for (int r = l; r < per; r += 64) {
-        const int rr = c * per + r;
-        bad |= !(w.row_m[rr] > -__builtin_inff()) || !(w.row_S[rr] <= FLT_MAX);
-        for (int s = 0; s < w.nseg; s++) bad |= w.seg_bad[segi(w, rr, s)];
-    }
-    bad = __any(bad);
-    const float* uu = u + (size_t)c * (gamma + 1);
-    bool reject = false;
-    if (l < gamma) {
-        const int x = tokens[(size_t)c * gamma + l];
-        float a = 0.0f;   // a draft token outside [0, V) is rejected
-        if (x >= 0 && x < V) {
-            const int rt = c * per + l, rd = c * per + gamma + 1 + l;
-            const float at = __fdiv_rn(__fsub_rn(rows.row(rt)[x], w.row_m[rt]), T);
-            const float ad = __fdiv_rn(__fsub_rn(rows.row(rd)[x], w.row_m[rd]), T);
-            const float px = __fdiv_rn(exp_glibc(at), w.row_S[rt]);
-            const float qx = __fdiv_rn(exp_glibc(ad), w.row_S[rd]);
-            a = qx < 1e-10f ? 1.0f : fminf(1.0f, __fdiv_rn(px, qx));
-        }
-        if (!bad) accept_prob[(size_t)c * gamma + l] = a;
-        reject = !(uu[l] < a);
-    }
-    const unsigned long long rb = __ballot(reject);
-    const int j = rb ? __builtin_ctzll(rb) : gamma;
-    if (bad) {
-        if (l == 0) {
-            w.flags[c] = 1;
-            w.task[c].kind = -1;
-        }
-        return;
-    }
-    int* out = out_tokens + (size_t)c * (gamma + 1);
-    for (int i = l; i <= gamma; i += 64) {
-        if (i < j) out[i] = tokens[(size_t)c * gamma + i];
-        else if (i > j) out[i] = -1;
-    }
-    if (l == 0) {
-        n_accepted[c] = j;
-        w.flags[c] = 0;
-        Task tk;
-        tk.kind = j < gamma ? kKindRes : kKindProb;
-        tk.ra = c * per + j;
-        tk.rb = c * per + gamma + 1 + (j < gamma ? j : 0);
-        tk.j = j;
-        tk.u = uu[j < gamma ? j + 1 : gamma];
-        tk.pad[0] = tk.pad[1] = tk.pad[2] = 0;
-        w.task[c] = tk;
-    }
-}
 
 // --------------------------------------------------------------- the find
 
@@ -1156,13 +1181,23 @@ __device__ int find_row(const Eval<KIND>& ev, const Work& w, int row, float thr,
     return sh.item < 0 ? dflt : sh.item;
 }
 
-__global__ __launch_bounds__(kT) void k_find(Rows rows, float T, Work w,
-                                             int* __restrict__ out_tokens) {
-    __shared__ FindShared sh;
+// Pass 2 of a chain: wave 0 walks the task row (exact starts, the sum R),
+// then the block finds the draw in it -- one launch for both.
+__global__ __launch_bounds__(kT) void k_walk2(Rows rows, float T, Work w,
+                                              int* __restrict__ out_tokens) {
+    __shared__ union {
+        WalkShared walk;
+        FindShared find;
+    } sh;
     const int c = blockIdx.x;
     const Task tk = w.task[c];
     if (tk.kind < 0) return;
     const int row = w.R1 + c;
+    if (wave_id() == 0) {
+        if (tk.kind == kKindProb) walk_row(task_eval<kKindProb>(rows, w, tk, T), w, row, sh.walk);
+        else walk_row(task_eval<kKindRes>(rows, w, tk, T), w, row, sh.walk);
+    }
+    __syncthreads();          // the walk's starts and sum, for every wave
     const float R = w.row_S[row];
     int tok;
     if (tk.kind == kKindRes) {
@@ -1171,9 +1206,10 @@ __global__ __launch_bounds__(kT) void k_find(Rows rows, float T, Work w,
             if (threadIdx.x == 0) w.flags[c] = 2;
             return;
         }
-        tok = find_row(task_eval<kKindRes>(rows, w, tk, T), w, row, __fmul_rn(tk.u, R), 0, sh);
+        tok = find_row(task_eval<kKindRes>(rows, w, tk, T), w, row, __fmul_rn(tk.u, R), 0,
+                       sh.find);
     } else {
-        tok = find_row(task_eval<kKindProb>(rows, w, tk, T), w, row, tk.u, rows.V - 1, sh);
+        tok = find_row(task_eval<kKindProb>(rows, w, tk, T), w, row, tk.u, rows.V - 1, sh.find);
     }
     if (threadIdx.x == 0) out_tokens[(size_t)c * (rows.gamma + 1) + tk.j] = tok;
 }
@@ -1347,17 +1383,13 @@ static int verify_pipe(const float* target, size_t ldt, const float* draft, cons
     if (launch_check("k_seg_fold1")) return -1;
     hipLaunchKernelGGL(k_walk1, dim3(R1), dim3(64), 0, st, rows, T, w);
     if (launch_check("k_walk1")) return -1;
-    hipLaunchKernelGGL(k_decide, dim3(batch), dim3(64), 0, st, rows, tokens, u, T, w, ap,
-                       out_tokens, n_accepted);
-    if (launch_check("k_decide")) return -1;
-    hipLaunchKernelGGL(k_res_stats, dim3(nseg, batch), dim3(kT), 0, st, rows, T, w);
+    hipLaunchKernelGGL(k_res_stats, dim3(nseg, batch), dim3(kT), 0, st, rows, tokens, u, T, w,
+                       ap, out_tokens, n_accepted);
     if (launch_check("k_res_stats")) return -1;
     hipLaunchKernelGGL(k_seg_fold2, dim3(nseg, batch), dim3(kT), 0, st, rows, T, w);
     if (launch_check("k_seg_fold2")) return -1;
-    hipLaunchKernelGGL(k_walk2, dim3(batch), dim3(64), 0, st, rows, T, w);
+    hipLaunchKernelGGL(k_walk2, dim3(batch), dim3(kT), 0, st, rows, T, w, out_tokens);
     if (launch_check("k_walk2")) return -1;
-    hipLaunchKernelGGL(k_find, dim3(batch), dim3(kT), 0, st, rows, T, w, out_tokens);
-    if (launch_check("k_find")) return -1;
     hipLaunchKernelGGL(k_verify_fallback, dim3(batch), dim3(kThreads), 0, st, rows, tokens, u,
                        T, w, ap, out_tokens, n_accepted);
     return launch_check("k_verify_fallback");
