@@ -223,10 +223,14 @@ def _draft_tokens_from(logits: np.ndarray, u: np.ndarray) -> np.ndarray:
     return np.asarray(toks, np.int32).reshape(u.shape)
 
 
-def bench_accept(lib, V, B, gamma, T, steps, warmup, sets=1, seed=5, top_k=0, top_p=1.0):
+def bench_accept(lib, V, B, gamma, T, steps, warmup, sets=1, seed=5, top_k=0, top_p=1.0,
+                 ratios=False):
     """cgx_verify_chain_batch_dev on B independent chains: target logits
     [B][gamma+1][V], draft [B][gamma][V] ~ N(0, 2^2), draft ids drawn from
-    the draft softmax, pre-drawn uniforms.  `sets` rotating input sets."""
+    the draft softmax, pre-drawn uniforms.  `sets` rotating input sets.
+    ratios=False asks for the emitted tokens and counts only, as the
+    speculative loops do (certified decisions); True also for every exact
+    acceptance ratio."""
     from cogito_amd.capi import DeviceArray, last_error
 
     rng = np.random.default_rng(seed)
@@ -244,12 +248,13 @@ def bench_accept(lib, V, B, gamma, T, steps, warmup, sets=1, seed=5, top_k=0, to
                      DeviceArray.from_numpy(lib, uv)))
     dout = DeviceArray(lib, B * (gamma + 1) * 4)
     dn = DeviceArray(lib, B * 4)
-    dap = DeviceArray(lib, B * gamma * 4)
+    dap = DeviceArray(lib, B * gamma * 4) if ratios else None
 
     def call(i):
         dt, dd, dtok, du = bufs[i % sets]
         return lib.cgx_verify_chain_batch_dev(dt.ptr, dd.ptr, dtok.ptr, du.ptr, B, gamma, V,
-                                              T, top_k, top_p, dout.ptr, dn.ptr, dap.ptr)
+                                              T, top_k, top_p, dout.ptr, dn.ptr,
+                                              dap.ptr if dap else None)
     for i in range(warmup):
         if call(i):
             raise RuntimeError(last_error(lib))
@@ -268,13 +273,14 @@ def bench_accept(lib, V, B, gamma, T, steps, warmup, sets=1, seed=5, top_k=0, to
     for b in bufs:
         for d in b:
             d.free()
-    for d in (dout, dn, dap):
+    for d in (dout, dn) + ((dap,) if dap else ()):
         d.free()
-    log(f"[bench] accept V={V} B={B} gamma={gamma} T={T} top_k={top_k} top_p={top_p}: "
+    log(f"[bench] accept V={V} B={B} gamma={gamma} T={T} top_k={top_k} top_p={top_p} "
+        f"ratios={ratios}: "
         f"{us:.2f} us/call, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}), "
         f"mean accepted {nacc.mean():.2f}")
     return {"V": V, "batch": B, "gamma": gamma, "temperature": T, "top_k": top_k,
-            "top_p": top_p, "us_per_call": round(us, 3), "bytes": nbytes,
+            "top_p": top_p, "ratios": ratios, "us_per_call": round(us, 3), "bytes": nbytes,
             "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
             "rotating_sets": sets, "mean_accepted_last_call": float(nacc.mean())}
 
@@ -858,6 +864,8 @@ def main() -> int:
     if "accept" in legs:
         extra["accept_c1"] = bench_accept(lib, 32000, 1, 4, 1.0, args.steps, args.warmup)
         extra["accept_roofline"] = bench_accept(lib, 128256, 64, 4, 1.0, 50, 5, sets=2)
+        extra["accept_roofline_ratios"] = bench_accept(lib, 128256, 64, 4, 1.0, 50, 5, sets=2,
+                                                       ratios=True)
         if cpu_on:
             extra["accept_c1"]["cpu_baseline"] = cpu_baseline_accept()
             log(f"[bench] CPU C1 verify: {extra['accept_c1']['cpu_baseline']['us_per_call']} "

@@ -364,8 +364,10 @@ int cgx_verify_chain(const float* target_logits, const float* draft_logits,
     int* dtok = (int*)o;
     float* dap = (float*)(o + (size_t)(gamma + 1) * 4);
     int* dn = (int*)(o + (size_t)(gamma + 1) * 4 + (size_t)gamma * 4);
+    /* the ratios only when asked for: without them the pipeline settles most
+     * accept tests from its segment statistics (same tokens) */
     if (cgx_verify_chain_batch_dev(t, d, x, uu, 1, gamma, V, temperature, top_k, top_p,
-                                   dtok, dn, dap))
+                                   dtok, dn, accept_prob ? dap : NULL))
         return -1;
     int n = -1;
     if (cgx_memcpy_d2h(out_tokens, dtok, (size_t)(gamma + 1) * 4) ||

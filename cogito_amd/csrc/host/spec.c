@@ -30,7 +30,6 @@ struct cgx_spec {
     float* d_u;           /* [2 gamma + 1]: draft draws, then verify draws */
     float* d_z;           /* [V] scaled draft row for the filtered samplers */
     int* d_out;           /* [gamma + 1] emitted tokens, then n accepted */
-    float* d_ap;
     int last;
     int have_last;
     int pend_extra;       /* the draft cache lacks d_gamma of the last step */
@@ -47,7 +46,6 @@ void cgx_spec_free(cgx_spec* s) {
     cgx_free(s->d_u);
     cgx_free(s->d_z);
     cgx_free(s->d_out);
-    cgx_free(s->d_ap);
     free(s);
 }
 
@@ -81,9 +79,8 @@ cgx_spec* cgx_spec_new(cgx_model* draft, cgx_model* target, int gamma, float tem
     s->d_u = (float*)cgx_malloc((size_t)(2 * gamma + 1) * 4);
     s->d_z = (float*)cgx_malloc(V * 4);
     s->d_out = (int*)cgx_malloc((size_t)(gamma + 2) * 4);
-    s->d_ap = (float*)cgx_malloc((size_t)gamma * 4);
     if (!s->d_tokens || !s->d_pending || !s->d_draft_logits || !s->d_target_logits ||
-        !s->d_u || !s->d_z || !s->d_out || !s->d_ap) {
+        !s->d_u || !s->d_z || !s->d_out) {
         cgx_spec_free(s);
         return NULL;
     }
@@ -191,7 +188,7 @@ int cgx_spec_step(cgx_spec* s, const float* u_draft, const float* u_verify, int*
     if (cgx_model_forward(s->target, s->d_tokens, g + 1, g + 1, s->d_target_logits) ||
         cgx_verify_chain_batch_dev(s->d_target_logits, s->d_draft_logits, s->d_tokens + 1,
                                    s->d_u + g, 1, g, s->V, s->T, s->top_k, s->top_p, s->d_out,
-                                   s->d_out + g + 1, s->d_ap))
+                                   s->d_out + g + 1, NULL))
         return -1;
     int hout[64 + 2];
     int* ho = (g + 2) <= 66 ? hout : (int*)malloc((size_t)(g + 2) * sizeof(int));
@@ -249,7 +246,6 @@ struct cgx_spec_batch {
     float* d_target_logits; /* [B][gamma + 1][V] */
     float* d_u;             /* draft draws [gamma][B], then verify draws [B][gamma + 1] */
     int* d_out;             /* [B][gamma + 1] tokens, then [B] accepted counts */
-    float* d_ap;            /* [B][gamma] */
     int prev[16], last[16];
     int have_last;
     long long steps, drafted, accepted;
@@ -265,7 +261,6 @@ void cgx_spec_batch_free(cgx_spec_batch* s) {
     cgx_free(s->d_target_logits);
     cgx_free(s->d_u);
     cgx_free(s->d_out);
-    cgx_free(s->d_ap);
     free(s);
 }
 
@@ -306,9 +301,8 @@ cgx_spec_batch* cgx_spec_batch_new(cgx_model* draft, cgx_model* target, int gamm
     s->d_target_logits = (float*)cgx_malloc(b * (g + 1) * V * 4);
     s->d_u = (float*)cgx_malloc(b * (2 * g + 1) * 4);
     s->d_out = (int*)cgx_malloc(b * (g + 2) * 4);
-    s->d_ap = (float*)cgx_malloc(b * g * 4);
     if (!s->d_feed || !s->d_dtok || !s->d_ttok || !s->d_vtok || !s->d_draft_logits ||
-        !s->d_target_logits || !s->d_u || !s->d_out || !s->d_ap) {
+        !s->d_target_logits || !s->d_u || !s->d_out) {
         cgx_spec_batch_free(s);
         return NULL;
     }
@@ -393,7 +387,7 @@ int cgx_spec_batch_step(cgx_spec_batch* s, const float* u_draft, const float* u_
     if (cgk_spec_tokens(s->d_feed, s->d_dtok, B, g, s->d_ttok, s->d_vtok) ||
         cgx_model_forward_batch(s->target, s->d_ttok, g + 1, g + 1, s->d_target_logits) ||
         cgk_verify_pipe(s->d_target_logits, s->d_draft_logits, s->d_vtok, uv, B, g, s->V, s->T,
-                        s->d_ap, s->d_out, dn))
+                        NULL, s->d_out, dn))
         return -1;
     int* ho = (int*)malloc((size_t)B * (g + 2) * sizeof(int));
     if (!ho) return -1;

@@ -187,6 +187,9 @@ struct Work {
     MI* chunk_mi;        // [chains][nseg][kT] pass-2 chunk summaries (identity if staged)
     Task* task;          // [chains]
     int* flags;          // [chains] 1: non-finite row, 2: residual mass < 1e-10
+    // certified decisions (null: every pass-1 row is summed exactly)
+    int* need;           // [chains][R1 / chains + 1]: count, then the rows to sum exactly
+    int* pre;            // [chains][gamma] accept test: 1 accept, 0 reject, -1 open
 };
 
 __device__ __forceinline__ size_t segi(const Work& w, int row, int seg) {
@@ -457,6 +460,149 @@ __device__ __forceinline__ int block_first256(bool pred, int* s_w) {
     return r;
 }
 
+// One segment's term of a row guide: c G with c = exp(-(m - ms) / T), and
+// its error bound (see exp_prefix).
+__device__ __forceinline__ void guide_term(double G, double H, float ms, bool mine, float m,
+                                           float T, double* cg, double* eb) {
+    *cg = *eb = 0.0;
+    if (mine && G > 0.0) {
+        const double D = ((double)m - (double)ms) / (double)T;
+        const bool ok = D <= 87.0;
+        const double c = ok ? (double)exp_fast(-(float)D) : 0.0;
+        *cg = c * G;
+        const double cu = ok ? c * (1.0 + 0x1p-19 + 0x1p-23 * D) : 0x1p-125;
+        *eb = cu * (0x1p-22 * 1.01 * H + (0x1p-23 * 1.01 * D + 0x1p-18) * G) +
+              (cu - c) * G + 0x1p-136;
+    }
+}
+
+// ------------------------------------------------- certified decisions
+
+// The fp32 values a positive binary64 bound admits: the least fp32 value
+// >= x, the greatest <= x (x a normal fp32 magnitude).
+__device__ __forceinline__ float f32_at_least(double x) {
+    const float f = (float)x;
+    return (double)f < x ? __uint_as_float(__float_as_uint(f) + 1u) : f;
+}
+__device__ __forceinline__ float f32_at_most(double x) {
+    const float f = (float)x;
+    return (double)f > x ? __uint_as_float(__float_as_uint(f) - 1u) : f;
+}
+
+struct PreShared {
+    float m[2 * kMaxGamma + 1];
+    float lo[2 * kMaxGamma + 1], hi[2 * kMaxGamma + 1];
+};
+
+// Chain c's certified decisions, from its segment stats alone (one block
+// per chain after k_seg_stats; its waves share the rows).
+// Each row's maximum m (exact) and an interval [lo, hi] of fp32 values
+// holding its sum S, the reference's sequential fp32 sum of
+// e_i = expf((x_i - m) / T): the guide c G within E (as in exp_prefix), and
+// at most V - 1 roundings of a sum of non-negative values, which stay within
+// (1 -/+ V 2^-24) of the real sum; S >= 1 (the maximum's element is
+// expf(0) = 1) and S <= V.  An accept test u < a, a = min(1, p(x) / q(x)),
+// p(x) = e_t(x) / S_t and q(x) = e_d(x) / S_d in fp32 (a = 1 if
+// q(x) < 1e-10), is settled when u lies outside the interval of a those
+// bounds allow: rounded division and min are monotone.  Listed for the exact
+// sums are the rows the chain's outcome can still depend on: both rows of
+// every open test before the first settled reject k, then both rows of
+// test k, or the bonus row gamma when no test is a settled reject.  A chain
+// with a non-finite row lists none (the fallback takes it).
+__device__ void pre_decide_chain(const Rows& rows, const int* __restrict__ tokens,
+                                 const float* __restrict__ u, float T, const Work& w, int c,
+                                 PreShared& sh) {
+    const int l = lane_id(), gamma = rows.gamma, V = rows.V;
+    const int per = 2 * gamma + 1;
+    const double ku = (double)V * 0x1p-24;
+    int bad = 0;
+    for (int i = wave_id(); i < per; i += (int)(blockDim.x / 64)) {
+        const int r = c * per + i;
+        float ms = -__builtin_inff();
+        double G = 0.0, H = 0.0;
+        if (l < w.nseg) {
+            const size_t si = segi(w, r, l);
+            ms = w.seg_m[si];
+            G = w.seg_gh[2 * si];
+            H = w.seg_gh[2 * si + 1];
+            bad |= w.seg_bad[si];
+        }
+        float m = ms;
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        double cg, eb;
+        guide_term(G, H, ms, l < w.nseg, m, T, &cg, &eb);
+        for (int o = 32; o > 0; o >>= 1) {
+            cg += __shfl_xor(cg, o);
+            eb += __shfl_xor(eb, o);
+        }
+        bad |= !(m > -__builtin_inff());
+        const double E = eb * (1.0 + 0x1p-40);
+        const double lo = fmax((cg - E) * (1.0 - ku), 1.0);
+        const double hi = fmin((cg + E) * (1.0 + ku / (1.0 - ku)) + 0x1p-140, (double)V);
+        if (l == 0) {
+            w.row_m[r] = m;
+            sh.m[i] = m;
+            sh.lo[i] = f32_at_least(lo);
+            sh.hi[i] = f32_at_most(hi);
+        }
+    }
+    bad = __syncthreads_or(bad);
+    if (wave_id() != 0) return;
+    int st = -1;
+    if (l < gamma) {
+        const int x = tokens[(size_t)c * gamma + l];
+        st = 0;   // a draft token outside [0, V): a = 0, rejected
+        if (x >= 0 && x < V && !bad) {
+            const int it = l, id = gamma + 1 + l;
+            const float at = __fdiv_rn(__fsub_rn(rows.row(c * per + it)[x], sh.m[it]), T);
+            const float ad = __fdiv_rn(__fsub_rn(rows.row(c * per + id)[x], sh.m[id]), T);
+            const float et = exp_glibc(at), ed = exp_glibc(ad);
+            const float plo = __fdiv_rn(et, sh.hi[it]), phi = __fdiv_rn(et, sh.lo[it]);
+            const float qlo = __fdiv_rn(ed, sh.hi[id]), qhi = __fdiv_rn(ed, sh.lo[id]);
+            float alo = 1.0f, ahi = 1.0f;
+            if (!(qhi < 1e-10f)) {
+                alo = fminf(1.0f, __fdiv_rn(plo, qhi));
+                if (!(qlo < 1e-10f)) ahi = fminf(1.0f, __fdiv_rn(phi, qlo));
+            }
+            const float uu = u[(size_t)c * (gamma + 1) + l];
+            st = uu < alo ? 1 : (!(uu < ahi) ? 0 : -1);
+        }
+        w.pre[(size_t)c * gamma + l] = st;
+    }
+    const unsigned long long rej = __ballot(l < gamma && st == 0);
+    const unsigned long long open = __ballot(l < gamma && st < 0);
+    const int k = rej ? __builtin_ctzll(rej) : gamma;
+    if (l == 0) {
+        int* nd = w.need + (size_t)c * (per + 1);
+        int n = 0;
+        if (!bad) {
+            if (k < gamma) {
+                nd[1 + n++] = c * per + k;
+                nd[1 + n++] = c * per + gamma + 1 + k;
+            } else {
+                nd[1 + n++] = c * per + gamma;
+            }
+            const unsigned long long below = k >= 64 ? ~0ull : (1ull << k) - 1ull;
+            for (unsigned long long o = open & below; o; o &= o - 1) {
+                const int i = __builtin_ctzll(o);
+                nd[1 + n++] = c * per + i;
+                nd[1 + n++] = c * per + gamma + 1 + i;
+            }
+        }
+        nd[0] = n;
+    }
+}
+
+constexpr int kPreThreads = 1024;        // k_pre_decide: up to 16 rows at a time
+
+__global__ __launch_bounds__(kPreThreads) void k_pre_decide(Rows rows,
+                                                            const int* __restrict__ tokens,
+                                                            const float* __restrict__ u, float T,
+                                                            Work w) {
+    __shared__ PreShared sh;
+    pre_decide_chain(rows, tokens, u, T, w, blockIdx.x, sh);
+}
+
 // ------------------------------------------------------- stats (pass 1)
 
 // Per segment of a pass-1 row: its maximum m_s and, against m_s, the
@@ -549,16 +695,8 @@ __global__ __launch_bounds__(kT) void k_seg_stats(Rows rows, float T, Work w) {
 __device__ __forceinline__ void exp_prefix(double G, double H, float ms, bool mine, float m,
                                            float T, double* s_d, double* P, double* E) {
     if (wave_id() == 0) {
-        double cg = 0.0, eb = 0.0;
-        if (mine && G > 0.0) {
-            const double D = ((double)m - (double)ms) / (double)T;
-            const bool ok = D <= 87.0;
-            const double c = ok ? (double)exp_fast(-(float)D) : 0.0;
-            cg = c * G;
-            const double cu = ok ? c * (1.0 + 0x1p-19 + 0x1p-23 * D) : 0x1p-125;
-            eb = cu * (0x1p-22 * 1.01 * H + (0x1p-23 * 1.01 * D + 0x1p-18) * G) +
-                 (cu - c) * G + 0x1p-136;
-        }
+        double cg, eb;
+        guide_term(G, H, ms, mine, m, T, &cg, &eb);
         for (int o = 32; o > 0; o >>= 1) {
             cg += __shfl_xor(cg, o);
             eb += __shfl_xor(eb, o);
@@ -737,9 +875,19 @@ __device__ __forceinline__ Eval<KIND> task_eval(const Rows& rows, const Work& w,
 
 // Every global load of the block is issued first (the chunk and the row's
 // segment stats), so their latencies overlap.
-__global__ __launch_bounds__(kT) void k_seg_fold1(Rows rows, float T, Work w) {
-    __shared__ FoldShared sh;
-    const int seg = blockIdx.x, r = blockIdx.y;
+// The k-th pass-1 row of chain c to sum exactly, and how many there are:
+// every row of the chain, or the list the certified decisions left.
+__device__ __forceinline__ int need_count(const Rows& rows, const Work& w, int c) {
+    const int per = 2 * rows.gamma + 1;
+    return w.need ? w.need[(size_t)c * (per + 1)] : per;
+}
+__device__ __forceinline__ int need_row(const Rows& rows, const Work& w, int c, int k) {
+    const int per = 2 * rows.gamma + 1;
+    return w.need ? w.need[(size_t)c * (per + 1) + 1 + k] : c * per + k;
+}
+
+__device__ __forceinline__ void fold1_row(const Rows& rows, float T, const Work& w, int r,
+                                          int seg, FoldShared& sh) {
     float X[kC], Y[kC];
     load_raw(rows.row(r), seg * kSeg + threadIdx.x * kC, rows.V, X);
     const SegStats st = seg_stats_of(w, r);
@@ -748,6 +896,16 @@ __global__ __launch_bounds__(kT) void k_seg_fold1(Rows rows, float T, Work w) {
     double P0, E0;
     exp_prefix(st.G, st.H, st.m, (int)threadIdx.x < seg, m, T, sh.d, &P0, &E0);
     fold_segment(pass1_eval(rows, r, m, T), w, r, seg, X, Y, P0, E0, sh);
+}
+
+// Block (seg, k * chains + c) folds segment seg of chain c's k-th listed row
+// (every pass-1 row, or those the certified decisions left; blocks past the
+// list end at once, and come last in dispatch order).
+__global__ __launch_bounds__(kT) void k_seg_fold1(Rows rows, float T, Work w) {
+    __shared__ FoldShared sh;
+    const int c = blockIdx.y % w.chains, k = blockIdx.y / w.chains;
+    if (k >= need_count(rows, w, c)) return;
+    fold1_row(rows, T, w, need_row(rows, w, c, k), blockIdx.x, sh);
 }
 
 // The decisions of chain c, by one wave: non-finite rows (NaN, +inf, all
@@ -764,19 +922,25 @@ __device__ Task decide_chain(const Rows& rows, const int* __restrict__ tokens,
     const int l = lane_id(), gamma = rows.gamma, V = rows.V;
     const int per = 2 * gamma + 1;
     // only the storing caller checks for non-finite rows: a chain that has
-    // them is finished by the fallback whatever the others compute for it
+    // them is finished by the fallback whatever the others compute for it.
+    // (A finite row's sum cannot overflow: every element is at most 1.)
     int bad = 0;
     if (write) {
         for (int r = l; r < per; r += 64) {
             const int rr = c * per + r;
-            bad |= !(w.row_m[rr] > -__builtin_inff()) || !(w.row_S[rr] <= FLT_MAX);
+            bad |= !(w.row_m[rr] > -__builtin_inff());
             for (int s = 0; s < w.nseg; s++) bad |= w.seg_bad[segi(w, rr, s)];
         }
         bad = __any(bad);
     }
     const float* uu = u + (size_t)c * (gamma + 1);
     bool reject = false;
-    if (l < gamma) {
+    // a test the certified decisions settled stands; an open one is taken
+    // exactly (its rows were summed exactly)
+    const int pre = w.pre && l < gamma ? w.pre[(size_t)c * gamma + l] : -1;
+    if (pre >= 0) {
+        reject = pre == 0;
+    } else if (l < gamma) {
         const int x = tokens[(size_t)c * gamma + l];
         float a = 0.0f;   // a draft token outside [0, V) is rejected
         if (x >= 0 && x < V) {
@@ -787,7 +951,7 @@ __device__ Task decide_chain(const Rows& rows, const int* __restrict__ tokens,
             const float qx = __fdiv_rn(exp_glibc(ad), w.row_S[rd]);
             a = qx < 1e-10f ? 1.0f : fminf(1.0f, __fdiv_rn(px, qx));
         }
-        if (write && !bad) accept_prob[(size_t)c * gamma + l] = a;
+        if (write && !bad && accept_prob) accept_prob[(size_t)c * gamma + l] = a;
         reject = !(uu[l] < a);
     }
     const unsigned long long rb = __ballot(reject);
@@ -1062,14 +1226,16 @@ __device__ void walk_row(const Eval<KIND>& ev, const Work& w, int row, WalkShare
     }
 }
 
+// Block k * chains + c walks chain c's k-th listed row.
 __global__ __launch_bounds__(64) void k_walk1(Rows rows, float T, Work w) {
     __shared__ WalkShared sh;
-    const int r = blockIdx.x;
+    const int c = blockIdx.x % w.chains, k = blockIdx.x / w.chains;
+    if (k >= need_count(rows, w, c)) return;
+    const int r = need_row(rows, w, c, k);
     walk_row(pass1_eval(rows, r, w.row_m[r], T), w, r, sh);
 }
 
 
-// ----------------------------------------------------------- decisions
 
 
 // --------------------------------------------------------------- the find
@@ -1277,6 +1443,16 @@ __global__ __launch_bounds__(kThreads) void k_verify_fallback(
 
 // ------------------------------------------------------------- launcher
 
+// pass-1 workgroups (segments x rows) from which calls without accept_prob
+// take the certified decisions
+static int g_lean_min_blocks = 2048;
+
+extern "C" int cgx_verify_lean_min_blocks(int blocks) {
+    const int old = g_lean_min_blocks;
+    if (blocks >= 0) g_lean_min_blocks = blocks;
+    return old;
+}
+
 extern "C" int cgk_verify_pipe_supported(int batch, int gamma, int V, float T) {
     return batch >= 1 && batch <= 65535 && gamma >= 0 && gamma <= vp::kMaxGamma && V >= 1 &&
            V <= kRound * kMaxRounds && T > 0.0f && T <= FLT_MAX;
@@ -1347,6 +1523,8 @@ static int verify_pipe(const float* target, size_t ldt, const float* draft, cons
     const size_t o_flags = take((size_t)batch * 4);
     const size_t o_ap = take((size_t)batch * gamma * 4);
     const size_t o_n = take((size_t)batch * 4);
+    const size_t o_need = take((size_t)batch * (2 * gamma + 2) * 4);
+    const size_t o_pre = take((size_t)batch * gamma * 4 + 4);
     if (ws_fixed && off > ws_cap) {
         cgx_set_error("verify: batch %d, gamma %d, V %d needs %zu bytes of workspace, above "
                       "the static maximum of %zu", batch, gamma, V, off, ws_cap);
@@ -1373,18 +1551,32 @@ static int verify_pipe(const float* target, size_t ldt, const float* draft, cons
     w.task_ge = (double*)(ws + o_tge);
     w.task = (Task*)(ws + o_task);
     w.flags = (int*)(ws + o_flags);
+    // Without accept_prob only the emitted tokens are asked for: the accept
+    // tests the segment stats settle need no exact sums (certified decisions),
+    // and the exact fold and walk run only over the rows still needed.
+    // (Only where the pass-1 grid is large: on a small one every kernel runs
+    // at its latency, and the extra launch costs more than the work saved.)
+    const bool lean = accept_prob == nullptr && gamma > 0 &&
+                      (long long)nseg * R1 >= g_lean_min_blocks;
+    w.need = lean ? (int*)(ws + o_need) : nullptr;
+    w.pre = lean ? (int*)(ws + o_pre) : nullptr;
     float* ap = accept_prob ? accept_prob : (float*)(ws + o_ap);
     if (!n_accepted) n_accepted = (int*)(ws + o_n);
     Rows rows{target, draft, gamma, V, ldt};
     hipStream_t st = stream();
     hipLaunchKernelGGL(k_seg_stats, dim3(nseg, R1), dim3(kT), 0, st, rows, T, w);
     if (launch_check("k_seg_stats")) return -1;
+    if (lean) {
+        const int nt = min(kPreThreads, 64 * (2 * gamma + 1));
+        hipLaunchKernelGGL(k_pre_decide, dim3(batch), dim3(nt), 0, st, rows, tokens, u, T, w);
+        if (launch_check("k_pre_decide")) return -1;
+    }
     hipLaunchKernelGGL(k_seg_fold1, dim3(nseg, R1), dim3(kT), 0, st, rows, T, w);
     if (launch_check("k_seg_fold1")) return -1;
     hipLaunchKernelGGL(k_walk1, dim3(R1), dim3(64), 0, st, rows, T, w);
     if (launch_check("k_walk1")) return -1;
     hipLaunchKernelGGL(k_res_stats, dim3(nseg, batch), dim3(kT), 0, st, rows, tokens, u, T, w,
-                       ap, out_tokens, n_accepted);
+                       lean ? nullptr : ap, out_tokens, n_accepted);
     if (launch_check("k_res_stats")) return -1;
     hipLaunchKernelGGL(k_seg_fold2, dim3(nseg, batch), dim3(kT), 0, st, rows, T, w);
     if (launch_check("k_seg_fold2")) return -1;

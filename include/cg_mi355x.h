@@ -113,6 +113,15 @@ int cgx_verify_chain_batch_dev(const float* target_logits,
                                int top_k, float top_p, int* out_tokens,
                                int* n_accepted, float* accept_prob);
 
+/* Without accept_prob (NULL) only the emitted tokens and counts are asked
+ * for, and a large call (at least `blocks` pass-1 workgroups: 4096-value
+ * segments times the 2 gamma + 1 rows of every chain; 2048 at load) settles
+ * most accept tests from certified bounds of the row sums, summing exactly
+ * only the rows its outcome still depends on.  The results are the same
+ * either way.  Sets the threshold (blocks >= 0) and returns the previous one;
+ * no counterpart in the reference (a tuning and test hook). */
+int cgx_verify_lean_min_blocks(int blocks);
+
 /* Allocation-free form of cgx_verify_chain_batch_dev.  No counterpart in
  * the reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid

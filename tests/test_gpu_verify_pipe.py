@@ -16,6 +16,15 @@ from oracle_lib import ptr
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True)
+def _certified_at_every_size(gpu):
+    """Calls without accept_prob take the certified decisions at every size
+    (by default only large calls do)."""
+    old = gpu.cgx_verify_lean_min_blocks(0)
+    yield
+    gpu.cgx_verify_lean_min_blocks(old)
+
+
 def _bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
@@ -41,6 +50,12 @@ def _run(gpu, oracle, target, draft, toks, u, gamma, V, T):
     np.testing.assert_array_equal(_bits(ap_g), _bits(ap_o))
     assert n_g == n_o, (n_g, n_o)
     np.testing.assert_array_equal(out_g[:n_g + 1], out_o[:n_o + 1])
+    # without the ratios: certified decisions, the same tokens
+    out_l = np.zeros(gamma + 1, np.int32)
+    n_l = gpu.cgx_verify_chain(target.ctypes.data, draft.ctypes.data, toks.ctypes.data,
+                               u.ctypes.data, gamma, V, T, 0, 1.0, out_l.ctypes.data, None)
+    assert n_l == n_o, (n_l, n_o)
+    np.testing.assert_array_equal(out_l[:n_l + 1], out_o[:n_o + 1])
     return n_g, out_g
 
 
@@ -196,3 +211,59 @@ def test_batch_matches_single_chains(gpu, oracle):
         np.testing.assert_array_equal(out[c, :n_o + 1], out_o[:n_o + 1])
         assert (out[c, n_o + 1:] == -1).all()
         np.testing.assert_array_equal(_bits(ap[c]), _bits(ap_o))
+
+
+def _batch(gpu, tg, df, tk, uu, T, with_ap):
+    B, g1, V = tg.shape
+    gamma = g1 - 1
+    args = [DeviceArray.from_numpy(gpu, a) for a in (tg, df, tk, uu)]
+    dout = DeviceArray(gpu, B * (gamma + 1) * 4)
+    dn = DeviceArray(gpu, B * 4)
+    dap = DeviceArray(gpu, B * gamma * 4) if with_ap else None
+    assert gpu.cgx_verify_chain_batch_dev(*(a.ptr for a in args), B, gamma, V, T, 0, 1.0,
+                                          dout.ptr, dn.ptr, dap.ptr if dap else None) == 0, \
+        last_error(gpu)
+    assert gpu.cgx_synchronize() == 0, last_error(gpu)
+    res = (dout.numpy(np.int32, (B, gamma + 1)), dn.numpy(np.int32, (B,)),
+           dap.numpy(np.float32, (B, gamma)) if dap else None)
+    for a in args + [dout, dn] + ([dap] if dap else []):
+        a.free()
+    return res
+
+
+@pytest.mark.parametrize("V", [4097, 32000, 128256])
+def test_certified_decisions_on_ratio_boundaries(gpu, oracle, V):
+    """Without accept_prob the pipeline settles accept tests from bounds of
+    the row sums and sums exactly only the rows the outcome still needs.
+    Draws on, one ulp either side of, and at small relative offsets from
+    each chain's exact ratio at one position (earlier positions accepted)
+    leave that test open; the tokens and counts must equal those taken with
+    every ratio exact, and the oracle's."""
+    rng = np.random.default_rng(V + 1)
+    B, gamma, T = 12, 4, 1.0
+    tg = rng.normal(0, 2, (B, gamma + 1, V)).astype(np.float32)
+    df = (tg[:, :gamma] + rng.normal(0, 0.3, (B, gamma, V))).astype(np.float32)
+    tk = rng.integers(0, V, (B, gamma)).astype(np.int32)
+    uu = rng.uniform(0, 1, (B, gamma + 1)).astype(np.float32)
+    _, _, ap = _batch(gpu, tg, df, tk, uu, T, True)
+    f32 = np.float32
+    offsets = [lambda a: a, lambda a: np.nextafter(a, f32(0)), lambda a: np.nextafter(a, f32(2)),
+               lambda a: f32(a * f32(1 - 1e-4)), lambda a: f32(a * f32(1 + 1e-4)),
+               lambda a: f32(a * f32(1 - 3e-3)), lambda a: f32(a * f32(1 + 3e-3))]
+    for rep in range(3):
+        u = rng.uniform(0, 1, (B, gamma + 1)).astype(np.float32)
+        for c in range(B):
+            pos = (c + rep) % gamma
+            u[c, :pos] = 0.0
+            u[c, pos] = min(offsets[(c + 5 * rep) % len(offsets)](ap[c, pos]), f32(1.0))
+        out_e, n_e, _ = _batch(gpu, tg, df, tk, u, T, True)
+        out_l, n_l, _ = _batch(gpu, tg, df, tk, u, T, False)
+        np.testing.assert_array_equal(n_l, n_e)
+        np.testing.assert_array_equal(out_l, out_e)
+        for c in range(B):
+            out_o = np.zeros(gamma + 1, np.int32)
+            ap_o = np.zeros(gamma, np.float32)
+            n_o = oracle.orc_verify_chain(ptr(tg[c]), ptr(df[c]), ptr(tk[c]), ptr(u[c]), gamma,
+                                          V, T, 0, 1.0, ptr(out_o), ptr(ap_o))
+            assert n_l[c] == n_o, (rep, c, n_l[c], n_o)
+            np.testing.assert_array_equal(out_l[c, :n_o + 1], out_o[:n_o + 1])

@@ -25,19 +25,23 @@ def _inputs(gpu, rng, batch, gamma, V):
     return [DeviceArray.from_numpy(gpu, a) for a in (t, d, x, u)]
 
 
-def _run(gpu, fn, args, batch, gamma, T):
+def _run(gpu, fn, args, batch, gamma, T, with_ap=True):
+    """(tokens, counts, ratios or None); without ratios the pipeline takes
+    the certified decisions."""
     out = DeviceArray(gpu, batch * (gamma + 1) * 4)
     n = DeviceArray(gpu, batch * 4)
-    ap = DeviceArray(gpu, batch * gamma * 4)
+    ap = DeviceArray(gpu, batch * gamma * 4) if with_ap else None
     t, d, x, u = args
     V = t.nbytes // 4 // (batch * (gamma + 1))
-    rc = fn(t.ptr, d.ptr, x.ptr, u.ptr, batch, gamma, V, T, 0, 1.0, out.ptr, n.ptr, ap.ptr)
+    rc = fn(t.ptr, d.ptr, x.ptr, u.ptr, batch, gamma, V, T, 0, 1.0, out.ptr, n.ptr,
+            ap.ptr if ap else None)
     assert rc == 0, last_error(gpu)
     assert gpu.cgx_synchronize() == 0, last_error(gpu)
     res = (out.numpy(np.int32, (batch, gamma + 1)), n.numpy(np.int32, (batch,)),
-           ap.numpy(np.float32, (batch, gamma)))
+           ap.numpy(np.float32, (batch, gamma)) if ap else None)
     for a in (out, n, ap):
-        a.free()
+        if a:
+            a.free()
     return res
 
 
@@ -51,6 +55,11 @@ def test_noalloc_matches_allocating_entry(gpu, T):
         np.testing.assert_array_equal(got[0], exp[0])
         np.testing.assert_array_equal(got[1], exp[1])
         np.testing.assert_array_equal(got[2].view(np.uint32), exp[2].view(np.uint32))
+        old = gpu.cgx_verify_lean_min_blocks(0)     # certified decisions at this size
+        lean = _run(gpu, gpu.cgx_verify_chain_batch_dev_noalloc, args, batch, gamma, T, False)
+        gpu.cgx_verify_lean_min_blocks(old)
+        np.testing.assert_array_equal(lean[0], exp[0])
+        np.testing.assert_array_equal(lean[1], exp[1])
         assert 0 < got[1].sum() < batch * gamma or batch == 3
         for a in args:
             a.free()
