@@ -45,7 +45,9 @@ __constant__ uint64_t kExp2Tab[32] = {
 // Branch-free: the main path runs on the argument clamped into the range
 // where it applies and the out-of-range results are selected afterwards, so
 // several evaluations can be in flight in one thread.
-__device__ __forceinline__ float exp_glibc(float x) {
+// tab: kExp2Tab, or a copy of it (a workgroup's copy in LDS reads faster
+// than the constant table at a lane-dependent index)
+__device__ __forceinline__ float exp_glibc_t(float x, const uint64_t* tab) {
     const bool over = !(x <= 0x1.62e42ep6f);       // NaN included
     const bool under = x < -0x1.9fe368p6f;
     const float special = x != x ? x + x : (over ? __builtin_inff() : 0.0f);
@@ -60,7 +62,7 @@ __device__ __forceinline__ float exp_glibc(float x) {
     uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd -= shift;
     double r = fma(inv_ln2_n, xd, -kd);
-    uint64_t t = kExp2Tab[ki & 31] + (ki << 47);
+    uint64_t t = tab[ki & 31] + (ki << 47);
     double s = __longlong_as_double((long long)t);
     double z = fma(c0, r, c1);
     double r2 = r * r;
@@ -69,6 +71,8 @@ __device__ __forceinline__ float exp_glibc(float x) {
     y = y * s;
     return over || under ? special : (float)y;
 }
+
+__device__ __forceinline__ float exp_glibc(float x) { return exp_glibc_t(x, kExp2Tab); }
 
 // ------------------------------------------------- fast, certified expf
 // exp(x) for x in [kExpFastMin, 0]: x log2(e) = n + f by a two-part

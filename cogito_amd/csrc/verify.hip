@@ -79,7 +79,8 @@ struct Item {
     int q0, q1;     // run increments in ulps for input parity 0 / 1
     int c;          // output parities: bit 0 for input parity 0, bit 1 for 1
     int slot;       // staging slot of the first staged chunk
-    int pad0, pad1;
+    int end;        // one past the run's last chunk
+    int pad;
 };
 
 // Monoid of a run of additions inside one binade, integer form (a run never
@@ -204,6 +205,7 @@ struct Eval {
     const float* b;
     float ma, mb, Sa, Sb, ia, ib, T;
     int V;
+    const uint64_t* tab;     // exp_glibc's table (kExp2Tab or a copy in LDS)
 
     __device__ __forceinline__ float arg(float x, float m) const {
         return T == 1.0f ? __fsub_rn(x, m) : __fdiv_rn(__fsub_rn(x, m), T);
@@ -211,11 +213,12 @@ struct Eval {
     // exact value from arguments
     __device__ __forceinline__ float exact(float A, float B) const {
         if constexpr (KIND == kKindExp) {
-            return exp_glibc(A);
+            return exp_glibc_t(A, tab);
         } else if constexpr (KIND == kKindProb) {
-            return __fdiv_rn(exp_glibc(A), Sa);
+            return __fdiv_rn(exp_glibc_t(A, tab), Sa);
         } else {
-            return fmaxf(0.0f, __fsub_rn(__fdiv_rn(exp_glibc(A), Sa), __fdiv_rn(exp_glibc(B), Sb)));
+            return fmaxf(0.0f, __fsub_rn(__fdiv_rn(exp_glibc_t(A, tab), Sa),
+                                         __fdiv_rn(exp_glibc_t(B, tab), Sb)));
         }
     }
     // approximation and its bound: exp_fast on [-87, 0]; below, expf is
@@ -732,6 +735,7 @@ __device__ __forceinline__ SegStats seg_stats_of(const Work& w, int r) {
 // ------------------------------------------------------------ the fold
 
 struct FoldShared {
+    uint64_t tab[32];        // exp_glibc's table
     float f[kW];
     float f2[2 * kW];
     double d[kW];
@@ -784,7 +788,8 @@ __device__ void fold_segment(const Eval<KIND>& ev, const Work& w, int row, int s
     sh.bin[t] = clean ? b : kDirty;
     __syncthreads();
     const bool head = t == 0 || sh.bin[t - 1] != sh.bin[t];
-    const bool last = clean && (t == kT - 1 || sh.bin[t + 1] != b);
+    const bool tail = t == kT - 1 || sh.bin[t + 1] != sh.bin[t];
+    const bool last = clean && tail;
 
     // item index (heads in order) and staging slot (dirty chunks in order)
     const unsigned long long hb = __ballot(head), db = __ballot(!clean);
@@ -818,6 +823,7 @@ __device__ void fold_segment(const Eval<KIND>& ev, const Work& w, int row, int s
             it[item].binade = clean ? b : kDirty;
             it[item].slot = clean ? -1 : slot;
         }
+        if (tail) it[item].end = t + 1;
         if (last) {
             it[item].q0 = sv.m.q0;
             it[item].q1 = sv.m.q1;
@@ -853,6 +859,7 @@ __device__ __forceinline__ Eval<kKindExp> pass1_eval(const Rows& rows, int r, fl
     ev.ia = ev.ib = 1.0f;
     ev.T = T;
     ev.V = rows.V;
+    ev.tab = kExp2Tab;
     return ev;
 }
 
@@ -870,6 +877,7 @@ __device__ __forceinline__ Eval<KIND> task_eval(const Rows& rows, const Work& w,
     ev.ib = 1.0f / ev.Sb;
     ev.T = T;
     ev.V = rows.V;
+    ev.tab = kExp2Tab;
     return ev;
 }
 
@@ -895,7 +903,9 @@ __device__ __forceinline__ void fold1_row(const Rows& rows, float T, const Work&
     if (seg == 0 && threadIdx.x == 0) w.row_m[r] = m;
     double P0, E0;
     exp_prefix(st.G, st.H, st.m, (int)threadIdx.x < seg, m, T, sh.d, &P0, &E0);
-    fold_segment(pass1_eval(rows, r, m, T), w, r, seg, X, Y, P0, E0, sh);
+    Eval<kKindExp> ev = pass1_eval(rows, r, m, T);
+    ev.tab = sh.tab;
+    fold_segment(ev, w, r, seg, X, Y, P0, E0, sh);
 }
 
 // Block (seg, k * chains + c) folds segment seg of chain c's k-th listed row
@@ -905,6 +915,7 @@ __global__ __launch_bounds__(kT) void k_seg_fold1(Rows rows, float T, Work w) {
     __shared__ FoldShared sh;
     const int c = blockIdx.y % w.chains, k = blockIdx.y / w.chains;
     if (k >= need_count(rows, w, c)) return;
+    if (threadIdx.x < 32) sh.tab[threadIdx.x] = kExp2Tab[threadIdx.x];   // read after a barrier
     fold1_row(rows, T, w, need_row(rows, w, c, k), blockIdx.x, sh);
 }
 
@@ -1029,11 +1040,13 @@ __global__ __launch_bounds__(kT) void k_seg_fold2(Rows rows, float T, Work w) {
     const int seg = blockIdx.x, c = blockIdx.y;
     const Task tk = w.task[c];
     if (tk.kind < 0) return;
+    if (threadIdx.x < 32) sh.tab[threadIdx.x] = kExp2Tab[threadIdx.x];   // read after a barrier
     const int base = seg * kSeg + threadIdx.x * kC;
     float X[kC], Y[kC];
     if (tk.kind == kKindProb) {
         // p_i = e_i / S: the pass-1 guide of row ra, divided by S
-        const Eval<kKindProb> ev = task_eval<kKindProb>(rows, w, tk, T);
+        Eval<kKindProb> ev = task_eval<kKindProb>(rows, w, tk, T);
+        ev.tab = sh.tab;
         ev.raw(base, X, Y);
         const SegStats st = seg_stats_of(w, tk.ra);
         double P, E;
@@ -1042,7 +1055,8 @@ __global__ __launch_bounds__(kT) void k_seg_fold2(Rows rows, float T, Work w) {
         const double E0 = E / (double)ev.Sa + P0 * 0x1p-22;
         fold_segment(ev, w, w.R1 + c, seg, X, Y, P0, E0, sh);
     } else {
-        const Eval<kKindRes> ev = task_eval<kKindRes>(rows, w, tk, T);
+        Eval<kKindRes> ev = task_eval<kKindRes>(rows, w, tk, T);
+        ev.tab = sh.tab;
         ev.raw(base, X, Y);
         double g = 0.0, e = 0.0;
         if ((int)threadIdx.x < seg) {
@@ -1090,34 +1104,9 @@ __device__ __forceinline__ void load_lds16(const void* src, void* dst) {
 }
 
 struct WalkShared {
-    alignas(16) Item items[kWalkItems];
-    alignas(16) float staged[kWalkStaged];
-    int ioff[kMaxSegs + 1];    // prefix counts over the row's segments: runs
-    int soff[kMaxSegs + 1];    // staged values
-    int over[kMaxSegs];
+    alignas(16) Item items[kWalkItems + 2];   // + 2: reads ahead past the last
+    alignas(16) float staged[kWalkStaged + 2 * kC];
 };
-
-// Replay n staged chunks (exact values at sv, in LDS) from s: fp32 additions
-// in order.  Every lane reads the whole chunk (one address: a broadcast) and
-// runs the same additions in its own registers, so the serial chain has no
-// cross-lane moves; the next chunk's read is in flight meanwhile.  The exact
-// value at each chunk start goes to out[chunk].
-__device__ __forceinline__ float replay_lds(const float* sv, int n, float s,
-                                            float* __restrict__ out) {
-    const vf4* p = (const vf4*)sv;
-    vf4 a = p[0], b = p[1], c = p[2], d = p[3];
-    for (int k = 0; k < n; k++) {
-        const int kn = k + 1 < n ? k + 1 : k;
-        const vf4 an = p[4 * kn], bn = p[4 * kn + 1], cn = p[4 * kn + 2], dn = p[4 * kn + 3];
-        if (lane_id() == 0) out[k] = s;
-        s = add4(add4(add4(add4(s, a), b), c), d);
-        a = an;
-        b = bn;
-        c = cn;
-        d = dn;
-    }
-    return s;
-}
 
 // One wave per row: exact value at every segment and item start, row sum.
 // Segments are walked in batches; a batch's runs and staged values are
@@ -1132,10 +1121,14 @@ __device__ __forceinline__ void walk_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int KIND>
+// With STARTS, the exact value at every segment, run and staged-chunk start
+// is stored for the find (each kept in lane k of a register and stored 64 at
+// a time); without, only the row sum.
+template <bool STARTS, int KIND>
 __device__ void walk_row(const Eval<KIND>& ev, const Work& w, int row, WalkShared& sh) {
     const int l = lane_id();
-    // every segment's counts (nseg <= 64), and their prefix sums
+    // every segment's counts (nseg <= 64; lane l: segment l), and their
+    // prefix sums; a segment whose runs overflowed (-1) is replayed exactly
     int c = 0, dc = 0;
     if (l < w.nseg) {
         c = w.cnt[2 * segi(w, row, l)];
@@ -1149,16 +1142,10 @@ __device__ void walk_row(const Eval<KIND>& ev, const Work& w, int row, WalkShare
             so += b;
         }
     }
-    if (l < w.nseg) {
-        sh.ioff[l + 1] = io;
-        sh.soff[l + 1] = so;
-        sh.over[l] = c < 0;
-    }
-    if (l == 0) sh.ioff[0] = sh.soff[0] = 0;
-    walk_sync();
     const float* rdirty = w.dirty + segi(w, row, 0) * kDirtyCap * kC;
     const Item* ritems = w.items + segi(w, row, 0) * kItemCap;
     float s = 0.0f;
+    float seg_st = 0.0f;      // lane g: start of segment g
     int g0 = 0;
     while (g0 < w.nseg) {
         // batch [g0, g1): as many segments as fit (lane l holds the prefix
@@ -1168,60 +1155,112 @@ __device__ void walk_row(const Eval<KIND>& ev, const Work& w, int row, WalkShare
         const unsigned long long fit = __ballot(l >= g0 && l < w.nseg && io - ib <= kWalkItems &&
                                                 so - sb <= kWalkStaged);
         const int g1 = max(g0 + 1, 64 - __clzll(fit));
-        const int i0 = ib, s0 = sb;
         // gather the batch's runs and staged values into LDS, every load in
         // flight together (counts from the lanes' prefix sums: no LDS read
-        // between the loads)
+        // between the loads).  Runs and staged values of consecutive segments
+        // land back to back, in walk order.
         for (int seg = g0; seg < g1; seg++) {
             const int sa = seg > 0 ? __builtin_amdgcn_readlane(so, seg - 1) : 0;
             const int sz = __builtin_amdgcn_readlane(so, seg) - sa;         // floats
             const float* ssrc = rdirty + (size_t)seg * kDirtyCap * kC;
-            float* sdst = sh.staged + (sa - s0);
+            float* sdst = sh.staged + (sa - sb);
             for (int f = 0; f < sz; f += 256)
                 if (f + 4 * l < sz) load_lds16(ssrc + f + 4 * l, sdst + f);
             const int ia = seg > 0 ? __builtin_amdgcn_readlane(io, seg - 1) : 0;
             const int iz = (__builtin_amdgcn_readlane(io, seg) - ia) * (int)(sizeof(Item) / 4);
             const int* isrc = (const int*)(ritems + (size_t)seg * kItemCap);
-            int* idst = (int*)(sh.items + (ia - i0));
+            int* idst = (int*)(sh.items + (ia - ib));
             for (int f = 0; f < iz; f += 256)
                 if (f + 4 * l < iz) load_lds16(isrc + f + 4 * l, idst + f);
         }
         __builtin_amdgcn_s_waitcnt(0);
         walk_sync();
+        // One stream over the batch.  A segment's runs are read into lanes
+        // (lane i: run i) one segment ahead, and inside a dirty run the next
+        // two staged chunks are read ahead, all independent of the running
+        // value, so the serial chain holds only the additions and register
+        // reads.  Staged chunks are consumed in order: a dirty run's chunks
+        // are the next ones in the stream.  (Read-ahead buffers live inside
+        // one loop only: a buffer carried across loop levels is copied at
+        // each entry, and a copy waits for its reads.)
+        Item nxt = Item{};
+        {
+            const int n0 = __builtin_amdgcn_readlane(c, g0);
+            if (l < n0) nxt = sh.items[l];
+        }
+        const vf4* sp = (const vf4*)sh.staged;
+        int q = 0;                // staged chunks consumed
         for (int seg = g0; seg < g1; seg++) {
             const size_t si = segi(w, row, seg);
-            if (l == 0) w.seg_start[(size_t)row * (w.nseg + 1) + seg] = s;
             const int segbase = seg * kSeg;
-            if (sh.over[seg]) {
+            if (STARTS) seg_st = l == seg ? s : seg_st;
+            const int n = __builtin_amdgcn_readlane(c, seg);
+            const Item mine = nxt;
+            if (seg + 1 < g1) {
+                const int n1 = __builtin_amdgcn_readlane(c, seg + 1);
+                if (l < n1) nxt = sh.items[__builtin_amdgcn_readlane(io, seg) - ib + l];
+            }
+            if (n < 0) {
                 s = replay_exact(ev, segbase, min(segbase + kSeg, ev.V), s);
                 continue;
             }
-            const int n = sh.ioff[seg + 1] - sh.ioff[seg];
-            const Item* its = sh.items + (sh.ioff[seg] - i0);
-            const float* sv = sh.staged + (sh.soff[seg] - s0);
-            Item nx = n > 0 ? its[0] : Item{};
+            float item_st = 0.0f;     // lane i: start of run i (n <= kItemCap = 64)
             for (int i = 0; i < n; i++) {
-                const Item it = nx;
-                if (i + 1 < n) nx = its[i + 1];
-                const int cend = i + 1 < n ? nx.chunk : kT;
-                if (l == 0) w.item_start[si * kItemCap + i] = s;
+                Item it;
+                it.chunk = __builtin_amdgcn_readlane(mine.chunk, i);
+                it.binade = __builtin_amdgcn_readlane(mine.binade, i);
+                it.end = __builtin_amdgcn_readlane(mine.end, i);
+                if (STARTS) item_st = l == i ? s : item_st;
                 if (it.binade == kDirty) {
-                    s = replay_lds(sv + it.slot * kC, cend - it.chunk, s,
-                                   w.dirty_start + si * kDirtyCap + it.slot);
+                    it.slot = __builtin_amdgcn_readlane(mine.slot, i);
+                    float* out = w.dirty_start + si * kDirtyCap + it.slot;
+                    const int nd = it.end - it.chunk;
+                    float dst = 0.0f;    // lane k % 64: start of staged chunk k
+                    // chunk k of the run in X (k even) or Y (k odd); each
+                    // buffer is reloaded with chunk k + 2 right after its
+                    // additions, so neither is copied while its read is in
+                    // flight
+                    const vf4* rp = sp + 4 * q;
+                    vf4 x0 = rp[0], x1 = rp[1], x2 = rp[2], x3 = rp[3];
+                    vf4 y0 = rp[4], y1 = rp[5], y2 = rp[6], y3 = rp[7];
+                    auto step = [&](vf4& v0, vf4& v1, vf4& v2, vf4& v3, int k) {
+                        if (STARTS) dst = l == (k & 63) ? s : dst;
+                        s = add4(add4(add4(add4(s, v0), v1), v2), v3);
+                        const vf4* np = rp + 4 * (k + 2);
+                        v0 = np[0];
+                        v1 = np[1];
+                        v2 = np[2];
+                        v3 = np[3];
+                        __builtin_amdgcn_sched_barrier(0);   // reads issued here
+                        if (STARTS && ((k & 63) == 63 || k == nd - 1) && l <= (k & 63))
+                            out[(k & ~63) + l] = dst;
+                    };
+                    int k = 0;
+                    for (; k + 1 < nd; k += 2) {
+                        step(x0, x1, x2, x3, k);
+                        step(y0, y1, y2, y3, k + 1);
+                    }
+                    if (k < nd) step(x0, x1, x2, x3, k);
+                    q += nd;
                 } else if (binade_bits(s) != it.binade) {
                     // the run's start is not in the binade its chunks assumed
                     // (excluded by the bounds; replayed exactly anyway)
-                    s = replay_exact(ev, segbase + it.chunk * kC, min(segbase + cend * kC, ev.V), s);
+                    s = replay_exact(ev, segbase + it.chunk * kC,
+                                     min(segbase + it.end * kC, ev.V), s);
                 } else {
-                    s = mi_apply(s, MI{it.q0, it.q1, it.c});
+                    s = mi_apply(s, MI{__builtin_amdgcn_readlane(mine.q0, i),
+                                       __builtin_amdgcn_readlane(mine.q1, i),
+                                       __builtin_amdgcn_readlane(mine.c, i)});
                 }
             }
+            if (STARTS && l < n) w.item_start[si * kItemCap + l] = item_st;
         }
         walk_sync();
         g0 = g1;
     }
+    if (STARTS && l < w.nseg) w.seg_start[(size_t)row * (w.nseg + 1) + l] = seg_st;
     if (l == 0) {
-        w.seg_start[(size_t)row * (w.nseg + 1) + w.nseg] = s;
+        if (STARTS) w.seg_start[(size_t)row * (w.nseg + 1) + w.nseg] = s;
         w.row_S[row] = s;
     }
 }
@@ -1232,7 +1271,7 @@ __global__ __launch_bounds__(64) void k_walk1(Rows rows, float T, Work w) {
     const int c = blockIdx.x % w.chains, k = blockIdx.x / w.chains;
     if (k >= need_count(rows, w, c)) return;
     const int r = need_row(rows, w, c, k);
-    walk_row(pass1_eval(rows, r, w.row_m[r], T), w, r, sh);
+    walk_row<false>(pass1_eval(rows, r, w.row_m[r], T), w, r, sh);
 }
 
 
@@ -1360,8 +1399,10 @@ __global__ __launch_bounds__(kT) void k_walk2(Rows rows, float T, Work w,
     if (tk.kind < 0) return;
     const int row = w.R1 + c;
     if (wave_id() == 0) {
-        if (tk.kind == kKindProb) walk_row(task_eval<kKindProb>(rows, w, tk, T), w, row, sh.walk);
-        else walk_row(task_eval<kKindRes>(rows, w, tk, T), w, row, sh.walk);
+        if (tk.kind == kKindProb)
+            walk_row<true>(task_eval<kKindProb>(rows, w, tk, T), w, row, sh.walk);
+        else
+            walk_row<true>(task_eval<kKindRes>(rows, w, tk, T), w, row, sh.walk);
     }
     __syncthreads();          // the walk's starts and sum, for every wave
     const float R = w.row_S[row];
