@@ -54,8 +54,8 @@ constexpr int kItemCap = 64;             // runs per segment (more: exact replay
 constexpr int kDirtyCap = kT;            // staged chunks per segment (all of them)
 constexpr int kWalkItems = 512;          // walk: runs held in LDS per batch
 constexpr int kMaxGamma = 64;
+constexpr int kCompactMaxBlocks = 256;   // pass-2 folds with wave-shared exact evaluations
 constexpr int kMaxSegs = 64;             // segments per row (V <= 262144)
-constexpr int kExactBatch = 4;           // exact element evaluations in flight per thread
 
 enum { kKindExp = 0, kKindProb = 1, kKindRes = 2 };
 
@@ -309,47 +309,93 @@ __device__ __forceinline__ void Eval<KIND>::args(int base, float (&A)[kC], float
 
 // Summary of one chunk in binade b from its approximations (v, bound er) and
 // exact arguments: exact, re-evaluating the elements the bound cannot decide.
+// LDS ordering inside one wave (the wave's own LDS writes, then its reads):
+// wavefront-scope fences around a wave barrier.
+__device__ __forceinline__ void walk_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// One wave's list of elements to evaluate exactly (64 per round).
+struct WaveList {
+    float a[64], b[64], r[64];
+};
+
+// Exact values of the elements flagged in `need` (bit k: element k of this
+// lane's chunk), replacing v[k].  The wave evaluates them 64 at a time: the
+// flagged elements are listed in LDS in lane order, each lane evaluates one,
+// and the owners read their results back -- one exact evaluation per lane
+// and round instead of every flagged position of every lane in turn.  A
+// wave-uniform call.
 template <int KIND>
-__device__ __forceinline__ MI fold_chunk16(const Eval<KIND>& ev, const float (&A)[kC],
-                                           const float (&B)[kC], float (&v)[kC],
-                                           const float (&er)[kC], int b) {
-    // y = v / ulp and its bound by a power-of-two scale (exact; ldexp, as the
-    // scale itself can exceed the fp32 range for tiny binades)
-    const int e = b == -127 ? 149 : 23 - b;
-    bool amb = false;
-    float Q = 0.0f;                           // < 2^24: exact
+__device__ __forceinline__ void exact_compact(const Eval<KIND>& ev, const float (&A)[kC],
+                                              const float (&B)[kC], unsigned need,
+                                              float (&v)[kC], WaveList& wl) {
+    const int l = lane_id();
+    const int cnt = __popc(need);
+    int off = cnt;                            // inclusive prefix over the wave
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(off, o);
+        if (l >= o) off += t;
+    }
+    const int total = __shfl(off, 63);
+    off -= cnt;
+    for (int r0 = 0; r0 < total; r0 += 64) {
+        int idx = off - r0;
+#pragma unroll
+        for (int k = 0; k < kC; k++) {
+            if ((need >> k) & 1u) {
+                if (idx >= 0 && idx < 64) {
+                    wl.a[idx] = A[k];
+                    if constexpr (KIND == kKindRes) wl.b[idx] = B[k];
+                }
+                idx++;
+            }
+        }
+        walk_sync();
+        if (l < total - r0) wl.r[l] = ev.exact(wl.a[l], KIND == kKindRes ? wl.b[l] : 0.0f);
+        walk_sync();
+        idx = off - r0;
+#pragma unroll
+        for (int k = 0; k < kC; k++) {
+            if ((need >> k) & 1u) {
+                if (idx >= 0 && idx < 64) v[k] = wl.r[idx];
+                idx++;
+            }
+        }
+        walk_sync();
+    }
+}
+
+// The certified fold of a clean chunk in binade b, in two halves around the
+// wave's exact evaluations.  chunk_need: y = v / ulp and its bound, by a
+// power-of-two scale (exact; ldexp, as the scale itself can exceed the fp32
+// range for tiny binades); an element whose bound holds a half-integer (ties
+// included) is flagged for its exact value.
+__device__ __forceinline__ int chunk_scale(int b) { return b == -127 ? 149 : 23 - b; }
+
+__device__ __forceinline__ unsigned chunk_need(const float (&v)[kC], const float (&er)[kC],
+                                               int b) {
+    const int e = chunk_scale(b);
+    unsigned need = 0;
 #pragma unroll
     for (int k = 0; k < kC; k++) {
         const float y = ldexpf(v[k], e);
-        const float rr = rintf(y);
-        // a half-integer within the bound of y (ties included)
-        amb |= fabsf(y - rr) + ldexpf(er[k], e) >= 0.5f;
-        Q += rr;
+        if (fabsf(y - rintf(y)) + ldexpf(er[k], e) >= 0.5f) need |= 1u << k;
     }
-    if (!amb) {
-        const int q = (int)Q;
+    return need;
+}
+
+// chunk_fold: with every flagged element exact, each element's rounding to
+// the binade's ulp is decided (ties by the running parity).
+__device__ __forceinline__ MI chunk_fold(const float (&v)[kC], int b, bool any) {
+    const int e = chunk_scale(b);
+    if (!any) {                               // no element near a half-integer
+        int q = 0;
+#pragma unroll
+        for (int k = 0; k < kC; k++) q += (int)rintf(ldexpf(v[k], e));
         return MI{q, q, (q & 1) | (((q & 1) ^ 1) << 1)};
-    }
-    // exact values four at a time: four independent evaluation chains in
-    // flight instead of one long dependent chain per element
-#pragma unroll
-    for (int k0 = 0; k0 < kC; k0 += kExactBatch) {
-        bool need[kExactBatch];
-        bool any = false;
-#pragma unroll
-        for (int j = 0; j < kExactBatch; j++) {
-            const float y = ldexpf(v[k0 + j], e);
-            need[j] = fabsf(y - rintf(y)) + ldexpf(er[k0 + j], e) >= 0.5f;
-            any |= need[j];
-        }
-        if (any) {
-            float ex[kExactBatch];
-#pragma unroll
-            for (int j = 0; j < kExactBatch; j++) ex[j] = ev.exact(A[k0 + j], B[k0 + j]);
-#pragma unroll
-            for (int j = 0; j < kExactBatch; j++) v[k0 + j] = need[j] ? ex[j] : v[k0 + j];
-        }
-        __builtin_amdgcn_sched_barrier(0);
     }
     int q0 = 0, q1 = 0, c0 = 0, c1 = 1;
 #pragma unroll
@@ -374,6 +420,32 @@ __device__ __forceinline__ MI fold_chunk16(const Eval<KIND>& ev, const float (&A
         }
     }
     return MI{q0, q1, c0 | (c1 << 1)};
+}
+
+constexpr int kExactBatch = 4;           // exact evaluations in flight per lane
+
+// The certified fold of a clean chunk with each lane evaluating its own
+// flagged elements, four at a time (four independent evaluation chains in
+// flight instead of one long dependent chain per element).
+template <int KIND>
+__device__ __forceinline__ MI fold_chunk16(const Eval<KIND>& ev, const float (&A)[kC],
+                                           const float (&B)[kC], float (&v)[kC],
+                                           const float (&er)[kC], int b) {
+    const unsigned need = chunk_need(v, er, b);
+    if (!need) return chunk_fold(v, b, false);
+#pragma unroll
+    for (int k0 = 0; k0 < kC; k0 += kExactBatch) {
+        if ((need >> k0) & ((1u << kExactBatch) - 1u)) {
+            float ex[kExactBatch];
+#pragma unroll
+            for (int j = 0; j < kExactBatch; j++) ex[j] = ev.exact(A[k0 + j], B[k0 + j]);
+#pragma unroll
+            for (int j = 0; j < kExactBatch; j++)
+                v[k0 + j] = (need >> (k0 + j)) & 1u ? ex[j] : v[k0 + j];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    return chunk_fold(v, b, true);
 }
 
 // ------------------------------------------------------ block reductions
@@ -736,6 +808,7 @@ __device__ __forceinline__ SegStats seg_stats_of(const Work& w, int r) {
 
 struct FoldShared {
     uint64_t tab[32];        // exp_glibc's table
+    WaveList wl[kW];
     float f[kW];
     float f2[2 * kW];
     double d[kW];
@@ -746,9 +819,12 @@ struct FoldShared {
 };
 
 // One segment of a row through the certified fold: items and staged chunks
-// for the walk.  X/Y: this thread's chunk as loaded (raw); P0/E0: guide of
+// for the walk.  COMPACT: exact evaluations listed and shared across the
+// wave (fewer per lane: the shorter latency when the grid is small); else
+// each lane evaluates its own (fewer instructions: the higher throughput on
+// a large grid).  X/Y: this thread's chunk as loaded (raw); P0/E0: guide of
 // the row before this segment and its bound.
-template <int KIND>
+template <bool COMPACT, int KIND>
 __device__ void fold_segment(const Eval<KIND>& ev, const Work& w, int row, int seg,
                              const float (&X)[kC], const float (&Y)[kC], double P0, double E0,
                              FoldShared& sh) {
@@ -782,7 +858,14 @@ __device__ void fold_segment(const Eval<KIND>& ev, const Work& w, int row, int s
     const double hi = (Pend + Eend) * (1.0 + ke / (1.0 - ke)) + 0x1p-140;
     const int b = binade_of(lo);
     const bool clean = binade_of(hi) == b;
-    const MI own = clean ? fold_chunk16(ev, A, B, v, er, b) : mi_id();
+    MI own;
+    if constexpr (COMPACT) {
+        const unsigned need = clean ? chunk_need(v, er, b) : 0u;
+        exact_compact(ev, A, B, need, v, sh.wl[wave_id()]);
+        own = clean ? chunk_fold(v, b, need != 0u) : mi_id();
+    } else {
+        own = clean ? fold_chunk16(ev, A, B, v, er, b) : mi_id();
+    }
     if constexpr (KIND != kKindExp)   // pass 2: the find resolves a clean run from these
         w.chunk_mi[((size_t)(row - w.R1) * w.nseg + seg) * kT + t] = own;
     sh.bin[t] = clean ? b : kDirty;
@@ -829,15 +912,22 @@ __device__ void fold_segment(const Eval<KIND>& ev, const Work& w, int row, int s
             it[item].q1 = sv.m.q1;
             it[item].c = sv.m.c;
         }
-        if (!clean) {
+        // staged chunks: every element exact (0 past V: argument -inf)
+        if constexpr (COMPACT) {
+            exact_compact(ev, A, B, clean ? 0u : (1u << kC) - 1u, v, sh.wl[wave_id()]);
+            if (!clean) {
+                float* dv = w.dirty + (si * kDirtyCap + slot) * kC;
+#pragma unroll
+                for (int k0 = 0; k0 < kC; k0 += 4)
+                    *(float4*)(dv + k0) = make_float4(v[k0], v[k0 + 1], v[k0 + 2], v[k0 + 3]);
+            }
+        } else if (!clean) {
             float* dv = w.dirty + (si * kDirtyCap + slot) * kC;
-            // four exact elements live at a time
 #pragma unroll
             for (int k0 = 0; k0 < kC; k0 += kExactBatch) {
                 float ex[kExactBatch];
 #pragma unroll
-                for (int j = 0; j < kExactBatch; j++)   // 0 past V (argument -inf)
-                    ex[j] = ev.exact(A[k0 + j], B[k0 + j]);
+                for (int j = 0; j < kExactBatch; j++) ex[j] = ev.exact(A[k0 + j], B[k0 + j]);
                 *(float4*)(dv + k0) = make_float4(ex[0], ex[1], ex[2], ex[3]);
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -905,7 +995,7 @@ __device__ __forceinline__ void fold1_row(const Rows& rows, float T, const Work&
     exp_prefix(st.G, st.H, st.m, (int)threadIdx.x < seg, m, T, sh.d, &P0, &E0);
     Eval<kKindExp> ev = pass1_eval(rows, r, m, T);
     ev.tab = sh.tab;
-    fold_segment(ev, w, r, seg, X, Y, P0, E0, sh);
+    fold_segment<false>(ev, w, r, seg, X, Y, P0, E0, sh);
 }
 
 // Block (seg, k * chains + c) folds segment seg of chain c's k-th listed row
@@ -1035,6 +1125,7 @@ __global__ __launch_bounds__(kT) void k_res_stats(Rows rows, const int* __restri
     }
 }
 
+template <bool COMPACT>
 __global__ __launch_bounds__(kT) void k_seg_fold2(Rows rows, float T, Work w) {
     __shared__ FoldShared sh;
     const int seg = blockIdx.x, c = blockIdx.y;
@@ -1053,7 +1144,7 @@ __global__ __launch_bounds__(kT) void k_seg_fold2(Rows rows, float T, Work w) {
         exp_prefix(st.G, st.H, st.m, (int)threadIdx.x < seg, ev.ma, T, sh.d, &P, &E);
         const double P0 = P / (double)ev.Sa;
         const double E0 = E / (double)ev.Sa + P0 * 0x1p-22;
-        fold_segment(ev, w, w.R1 + c, seg, X, Y, P0, E0, sh);
+        fold_segment<COMPACT>(ev, w, w.R1 + c, seg, X, Y, P0, E0, sh);
     } else {
         Eval<kKindRes> ev = task_eval<kKindRes>(rows, w, tk, T);
         ev.tab = sh.tab;
@@ -1066,7 +1157,7 @@ __global__ __launch_bounds__(kT) void k_seg_fold2(Rows rows, float T, Work w) {
         }
         const double P0 = block_sum256_d(g, sh.d);
         const double E0 = block_sum256_d(e, sh.d);
-        fold_segment(ev, w, w.R1 + c, seg, X, Y, P0, E0, sh);
+        fold_segment<COMPACT>(ev, w, w.R1 + c, seg, X, Y, P0, E0, sh);
     }
 }
 
@@ -1115,11 +1206,6 @@ struct WalkShared {
 // The walk runs in one wave: its LDS traffic (and the LDS-bound loads,
 // waited for with s_waitcnt) needs ordering inside the wave only, so the walk
 // also runs as one wave of a larger block.
-__device__ __forceinline__ void walk_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // With STARTS, the exact value at every segment, run and staged-chunk start
 // is stored for the find (each kept in lane k of a register and stored 64 at
@@ -1619,7 +1705,12 @@ static int verify_pipe(const float* target, size_t ldt, const float* draft, cons
     hipLaunchKernelGGL(k_res_stats, dim3(nseg, batch), dim3(kT), 0, st, rows, tokens, u, T, w,
                        lean ? nullptr : ap, out_tokens, n_accepted);
     if (launch_check("k_res_stats")) return -1;
-    hipLaunchKernelGGL(k_seg_fold2, dim3(nseg, batch), dim3(kT), 0, st, rows, T, w);
+    // a grid of at most one block per CU runs at its blocks' latency: the
+    // wave-shared exact evaluations then; the per-lane ones on a larger grid
+    if ((long long)nseg * batch <= kCompactMaxBlocks)
+        hipLaunchKernelGGL(k_seg_fold2<true>, dim3(nseg, batch), dim3(kT), 0, st, rows, T, w);
+    else
+        hipLaunchKernelGGL(k_seg_fold2<false>, dim3(nseg, batch), dim3(kT), 0, st, rows, T, w);
     if (launch_check("k_seg_fold2")) return -1;
     hipLaunchKernelGGL(k_walk2, dim3(batch), dim3(kT), 0, st, rows, T, w, out_tokens);
     if (launch_check("k_walk2")) return -1;
