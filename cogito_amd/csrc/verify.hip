@@ -1580,8 +1580,10 @@ extern "C" int cgx_verify_lean_min_blocks(int blocks) {
     return old;
 }
 
+// (the pass-1 grids take one row per y index: at most 65535 rows)
 extern "C" int cgk_verify_pipe_supported(int batch, int gamma, int V, float T) {
-    return batch >= 1 && batch <= 65535 && gamma >= 0 && gamma <= vp::kMaxGamma && V >= 1 &&
+    return batch >= 1 && gamma >= 0 && gamma <= vp::kMaxGamma &&
+           (long long)batch * (2 * gamma + 1) <= 65535 && V >= 1 &&
            V <= kRound * kMaxRounds && T > 0.0f && T <= FLT_MAX;
 }
 
