@@ -52,7 +52,7 @@ constexpr int kC = 16;                   // elements per chunk (per thread)
 constexpr int kSeg = kT * kC;            // 4096 elements per segment
 constexpr int kItemCap = 64;             // runs per segment (more: exact replay)
 constexpr int kDirtyCap = kT;            // staged chunks per segment (all of them)
-constexpr int kWalkItems = 512;          // walk: runs held in LDS per batch
+constexpr int kWalkItems = 256;          // walk: runs held in LDS per batch
 constexpr int kMaxGamma = 64;
 constexpr int kCompactMaxBlocks = 256;   // pass-2 folds with wave-shared exact evaluations
 constexpr int kMaxSegs = 64;             // segments per row (V <= 262144)
@@ -1194,9 +1194,33 @@ __device__ __forceinline__ void load_lds16(const void* src, void* dst) {
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
 }
 
+// One step of a walk: a stretch of consecutive clean runs (their summaries
+// composed: adding q ulps adds q to the bit pattern, across binades too), a
+// dirty run (its staged chunks replayed), or a segment replayed exactly.
+struct WalkOp {
+    int kind;            // kOpClean, kOpDirty, kOpExact
+    int j0, j1;          // element range (for an exact replay)
+    int q0, q1, c;       // clean: the stretch's composed summary
+    int bin0, bin1;      // clean: binade of its first and last run
+    int nd;              // dirty: staged chunks
+    int sidx;            // dirty: index of its first chunk in dirty_start
+    int r0, r1;          // its runs (batch indices), first and last
+};
+enum { kOpClean = 0, kOpDirty = 1, kOpExact = 2 };
+constexpr int kWalkOps = kWalkItems + kMaxSegs;
+
 struct WalkShared {
-    alignas(16) Item items[kWalkItems + 2];   // + 2: reads ahead past the last
-    alignas(16) float staged[kWalkStaged + 2 * kC];
+    alignas(16) Item items[kWalkItems];
+    alignas(16) float staged[kWalkStaged + 2 * kC];   // + 2 chunks: reads ahead past the last
+    alignas(16) WalkOp ops[kWalkOps];
+    int segof[kWalkItems];       // segment of each run
+    int item_op[kWalkItems];     // op of each run
+    int heads[kWalkItems];       // ops begun by runs 0..j (inclusive)
+    MI item_pre[kWalkItems];     // composed summaries of the stretch's runs before it
+    float op_start[kWalkOps];    // exact value at each op's start
+    int op_slow[kWalkOps];       // 1: replayed exactly run by run (starts stored then)
+    int seg_first[kMaxSegs];     // first run of each segment of the batch
+    int seg_ovb[kMaxSegs];       // overflowed segments of the batch before it
 };
 
 // One wave per row: exact value at every segment and item start, row sum.
@@ -1207,11 +1231,10 @@ struct WalkShared {
 // waited for with s_waitcnt) needs ordering inside the wave only, so the walk
 // also runs as one wave of a larger block.
 
-// With STARTS, the exact value at every segment, run and staged-chunk start
-// is stored for the find (each kept in lane k of a register and stored 64 at
-// a time); without, only the row sum.
+// The walk of a short row (few segments): one step per run and segment, the
+// starts (with STARTS) kept in lanes and stored 64 at a time.
 template <bool STARTS, int KIND>
-__device__ void walk_row(const Eval<KIND>& ev, const Work& w, int row, WalkShared& sh) {
+__device__ void walk_row_runs(const Eval<KIND>& ev, const Work& w, int row, WalkShared& sh) {
     const int l = lane_id();
     // every segment's counts (nseg <= 64; lane l: segment l), and their
     // prefix sums; a segment whose runs overflowed (-1) is replayed exactly
@@ -1349,6 +1372,298 @@ __device__ void walk_row(const Eval<KIND>& ev, const Work& w, int row, WalkShare
         if (STARTS) w.seg_start[(size_t)row * (w.nseg + 1) + w.nseg] = s;
         w.row_S[row] = s;
     }
+}
+
+// The walk of a long row.  Per batch of segments: the runs and staged values are gathered into LDS
+// (all loads in flight together); then, in parallel, the runs become a list
+// of ops -- consecutive clean runs composed into one stretch, a dirty run,
+// or a segment whose runs overflowed -- so that the serial chain takes one
+// step per op instead of one per run and segment.  Ops are read 64 at a time
+// into lanes; the staged chunks of a dirty run are consumed in stream order
+// (two read ahead).  With STARTS the starts of the runs inside a stretch
+// follow afterwards, in parallel, from the stretch's start and the composed
+// summaries of the runs before them.
+template <bool STARTS, int KIND>
+__device__ void walk_row_ops(const Eval<KIND>& ev, const Work& w, int row, WalkShared& sh) {
+    const int l = lane_id();
+    // every segment's counts (nseg <= 64; lane l: segment l), and their
+    // prefix sums; a segment whose runs overflowed (-1) is replayed exactly
+    int c = 0, dc = 0;
+    if (l < w.nseg) {
+        c = w.cnt[2 * segi(w, row, l)];
+        dc = w.cnt[2 * segi(w, row, l) + 1];
+    }
+    const bool lane_over = l < w.nseg && c < 0;
+    int io = c > 0 ? c : 0, so = c >= 0 && dc > 0 ? dc * kC : 0;
+    int ov = lane_over ? 1 : 0;               // overflowed segments through l
+    for (int o = 1; o < 64; o <<= 1) {
+        const int a = __shfl_up(io, o), b = __shfl_up(so, o), d = __shfl_up(ov, o);
+        if (l >= o) {
+            io += a;
+            so += b;
+            ov += d;
+        }
+    }
+    const float* rdirty = w.dirty + segi(w, row, 0) * kDirtyCap * kC;
+    const Item* ritems = w.items + segi(w, row, 0) * kItemCap;
+    float s = 0.0f;
+    int g0 = 0;
+    while (g0 < w.nseg) {
+        // batch [g0, g1): as many segments as fit (lane l holds the prefix
+        // counts through segment l, so the fitting segments form a ballot)
+        const int ib = g0 > 0 ? __builtin_amdgcn_readlane(io, g0 - 1) : 0;
+        const int sb = g0 > 0 ? __builtin_amdgcn_readlane(so, g0 - 1) : 0;
+        const int ob = g0 > 0 ? __builtin_amdgcn_readlane(ov, g0 - 1) : 0;
+        const unsigned long long fit = __ballot(l >= g0 && l < w.nseg && io - ib <= kWalkItems &&
+                                                so - sb <= kWalkStaged);
+        const int g1 = max(g0 + 1, 64 - __clzll(fit));
+        const int nit = __builtin_amdgcn_readlane(io, g1 - 1) - ib;
+        for (int seg = g0; seg < g1; seg++) {
+            const int sa = seg > 0 ? __builtin_amdgcn_readlane(so, seg - 1) : 0;
+            const int sz = __builtin_amdgcn_readlane(so, seg) - sa;         // floats
+            const float* ssrc = rdirty + (size_t)seg * kDirtyCap * kC;
+            float* sdst = sh.staged + (sa - sb);
+            for (int f = 0; f < sz; f += 256)
+                if (f + 4 * l < sz) load_lds16(ssrc + f + 4 * l, sdst + f);
+            const int ia = seg > 0 ? __builtin_amdgcn_readlane(io, seg - 1) : 0;
+            const int iz = (__builtin_amdgcn_readlane(io, seg) - ia) * (int)(sizeof(Item) / 4);
+            const int* isrc = (const int*)(ritems + (size_t)seg * kItemCap);
+            int* idst = (int*)(sh.items + (ia - ib));
+            for (int f = 0; f < iz; f += 256)
+                if (f + 4 * l < iz) load_lds16(isrc + f + 4 * l, idst + f);
+        }
+        // per segment of the batch (lane l: segment l): its runs' segment,
+        // first run and the overflowed segments before it
+        if (l >= g0 && l < g1) {
+            const int e0 = io - (c > 0 ? c : 0) - ib;
+            for (int i = 0; i < c; i++) sh.segof[e0 + i] = l;
+            sh.seg_first[l] = e0;
+            sh.seg_ovb[l] = ov - (lane_over ? 1 : 0) - ob;
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        walk_sync();
+
+        // ---- the ops, in parallel: lane l takes runs kIPL l .. kIPL l + kIPL - 1.
+        // A run begins an op unless it is clean and follows a clean run of
+        // the same or the next segment (every segment that is not replayed
+        // exactly has a run, so a larger step passes such a segment).
+        constexpr int kIPL = kWalkItems / 64;
+        Item it[kIPL];
+        int sg[kIPL];
+        bool head[kIPL];
+        SMI loc[kIPL];                            // inclusive summaries in the lane
+        int nhead = 0;
+        SMI acc{mi_id(), 0};
+#pragma unroll
+        for (int i = 0; i < kIPL; i++) {
+            const int j = kIPL * l + i;
+            const bool live = j < nit;
+            it[i] = live ? sh.items[j] : Item{};
+            sg[i] = live ? sh.segof[j] : 0;
+            const bool dirty = it[i].binade == kDirty;
+            bool h = true;
+            if (live && j > 0) {
+                const bool pdirty = (i > 0 ? it[i - 1].binade : sh.items[j - 1].binade) == kDirty;
+                const int ps = i > 0 ? sg[i - 1] : sh.segof[j - 1];
+                h = dirty || pdirty || sg[i] - ps > 1;
+            }
+            head[i] = live && h;
+            nhead += head[i] ? 1 : 0;
+            const MI m = (live && !dirty) ? MI{it[i].q0, it[i].q1, it[i].c} : mi_id();
+            acc = smi_then(acc, SMI{m, head[i] ? 1 : 0});
+            loc[i] = acc;
+        }
+        int hx = nhead;                           // heads through this lane
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(hx, o);
+            if (l >= o) hx += t;
+        }
+        const int nheads = __shfl(hx, 63);
+        hx -= nhead;
+        const SMI lin = wave_incl_smi(acc);       // lanes' aggregates, scanned
+        SMI before;                               // through the lanes below
+        before.m.q0 = __shfl_up(lin.m.q0, 1);
+        before.m.q1 = __shfl_up(lin.m.q1, 1);
+        before.m.c = __shfl_up(lin.m.c, 1);
+        before.flag = __shfl_up(lin.flag, 1);
+        if (l == 0) before = SMI{mi_id(), 0};
+        const int next_head = __shfl_down(head[0] ? 1 : 0, 1);   // next lane's first run
+#pragma unroll
+        for (int i = 0; i < kIPL; i++) {
+            const int j = kIPL * l + i;
+            if (j < nit) {
+                if (head[i]) hx++;
+                const int seg = sg[i];
+                const int op = hx - 1 + sh.seg_ovb[seg];
+                sh.heads[j] = hx;
+                sh.item_op[j] = op;
+                sh.item_pre[j] = head[i] ? mi_id()
+                                         : (i > 0 ? smi_then(before, loc[i - 1]) : before).m;
+                const bool last = j + 1 >= nit || (i + 1 < kIPL ? head[i + 1] : next_head != 0);
+                WalkOp& o = sh.ops[op];
+                const int segbase = seg * kSeg;
+                if (head[i]) {
+                    o.kind = it[i].binade == kDirty ? kOpDirty : kOpClean;
+                    o.j0 = segbase + it[i].chunk * kC;
+                    o.bin0 = it[i].binade;
+                    o.nd = it[i].end - it[i].chunk;
+                    o.sidx = (int)(segi(w, row, seg) * kDirtyCap) + it[i].slot;
+                    o.r0 = j;
+                }
+                if (last) {
+                    const SMI incl = smi_then(before, loc[i]);
+                    o.q0 = incl.m.q0;
+                    o.q1 = incl.m.q1;
+                    o.c = incl.m.c;
+                    o.bin1 = it[i].binade;
+                    o.j1 = min(segbase + it[i].end * kC, ev.V);
+                    o.r1 = j;
+                }
+            }
+        }
+        walk_sync();
+        // overflowed segments: one exact op each, after the heads of the
+        // runs before it (lane l: segment l)
+        if (l >= g0 && l < g1 && lane_over) {
+            const int e = sh.seg_first[l];
+            const int op = (e > 0 ? sh.heads[e - 1] : 0) + sh.seg_ovb[l];
+            WalkOp& o = sh.ops[op];
+            o.kind = kOpExact;
+            o.j0 = l * kSeg;
+            o.j1 = min(l * kSeg + kSeg, ev.V);
+            o.r0 = 0;
+            o.r1 = -1;
+        }
+        const int nops = nheads + (__builtin_amdgcn_readlane(ov, g1 - 1) - ob);
+        walk_sync();
+
+        // ---- the serial chain: 64 ops at a time in lanes
+        const vf4* sp = (const vf4*)sh.staged;
+        int q = 0;                                // staged chunks consumed
+        for (int p0 = 0; p0 < nops; p0 += 64) {
+            const WalkOp mo = p0 + l < nops ? sh.ops[p0 + l] : WalkOp{};
+            float ost = 0.0f;                     // lane k: start of op p0 + k
+            int slow = 0;                         // lane k: op p0 + k replayed run by run
+            const int pn = min(64, nops - p0);
+            for (int k = 0; k < pn; k++) {
+                if (STARTS) ost = l == k ? s : ost;
+                const int kind = __builtin_amdgcn_readlane(mo.kind, k);
+                if (kind == kOpDirty) {
+                    const int nd = __builtin_amdgcn_readlane(mo.nd, k);
+                    float* out = w.dirty_start + __builtin_amdgcn_readlane(mo.sidx, k);
+                    float dst = 0.0f;    // lane kk % 64: start of staged chunk kk
+                    // chunk kk of the run in X (kk even) or Y (kk odd); each
+                    // buffer is reloaded with chunk kk + 2 right after its
+                    // additions, so neither is copied while its read is in
+                    // flight
+                    const vf4* rp = sp + 4 * q;
+                    vf4 x0 = rp[0], x1 = rp[1], x2 = rp[2], x3 = rp[3];
+                    vf4 y0 = rp[4], y1 = rp[5], y2 = rp[6], y3 = rp[7];
+                    auto step = [&](vf4& v0, vf4& v1, vf4& v2, vf4& v3, int kk) {
+                        if (STARTS) dst = l == (kk & 63) ? s : dst;
+                        s = add4(add4(add4(add4(s, v0), v1), v2), v3);
+                        const vf4* np = rp + 4 * (kk + 2);
+                        v0 = np[0];
+                        v1 = np[1];
+                        v2 = np[2];
+                        v3 = np[3];
+                        __builtin_amdgcn_sched_barrier(0);   // reads issued here
+                        if (STARTS && ((kk & 63) == 63 || kk == nd - 1) && l <= (kk & 63))
+                            out[(kk & ~63) + l] = dst;
+                    };
+                    int kk = 0;
+                    for (; kk + 1 < nd; kk += 2) {
+                        step(x0, x1, x2, x3, kk);
+                        step(y0, y1, y2, y3, kk + 1);
+                    }
+                    if (kk < nd) step(x0, x1, x2, x3, kk);
+                    q += nd;
+                    continue;
+                }
+                bool fast = false;
+                if (kind == kOpClean &&
+                    binade_bits(s) == __builtin_amdgcn_readlane(mo.bin0, k)) {
+                    const float sn = mi_apply(s, MI{__builtin_amdgcn_readlane(mo.q0, k),
+                                                    __builtin_amdgcn_readlane(mo.q1, k),
+                                                    __builtin_amdgcn_readlane(mo.c, k)});
+                    // the stretch ends in its last run's binade (the bounds
+                    // exclude anything else)
+                    if (binade_bits(sn) == __builtin_amdgcn_readlane(mo.bin1, k)) {
+                        s = sn;
+                        fast = true;
+                    }
+                }
+                if (!fast) {
+                    // an overflowed segment, or a stretch that left the
+                    // binades its runs assumed (excluded by the bounds):
+                    // exact replay, run by run so that every start is exact
+                    const int r0 = __builtin_amdgcn_readlane(mo.r0, k);
+                    const int r1 = __builtin_amdgcn_readlane(mo.r1, k);
+                    if (r1 < r0) {
+                        s = replay_exact(ev, __builtin_amdgcn_readlane(mo.j0, k),
+                                         __builtin_amdgcn_readlane(mo.j1, k), s);
+                    } else {
+                        slow = l == k ? 1 : slow;
+                        for (int r = r0; r <= r1; r++) {
+                            const int seg = sh.segof[r];
+                            const Item ir = sh.items[r];
+                            if (STARTS && l == 0) {
+                                w.item_start[segi(w, row, seg) * kItemCap +
+                                             (r - sh.seg_first[seg])] = s;
+                                if (r == sh.seg_first[seg])
+                                    w.seg_start[(size_t)row * (w.nseg + 1) + seg] = s;
+                            }
+                            s = replay_exact(ev, seg * kSeg + ir.chunk * kC,
+                                             min(seg * kSeg + ir.end * kC, ev.V), s);
+                        }
+                    }
+                }
+            }
+            if (STARTS && p0 + l < nops) {
+                sh.op_start[p0 + l] = ost;
+                sh.op_slow[p0 + l] = slow;
+            }
+        }
+        if (STARTS) {
+            walk_sync();
+            // run starts: the stretch's start advanced by the runs before it;
+            // segment starts: the segment's first run, or its exact op
+            for (int j = l; j < nit; j += 64) {
+                const int op = sh.item_op[j];
+                if (sh.op_slow[op]) continue;
+                const int seg = sh.segof[j];
+                const int first = sh.seg_first[seg];
+                const float st = mi_apply(sh.op_start[op], sh.item_pre[j]);
+                w.item_start[segi(w, row, seg) * kItemCap + (j - first)] = st;
+                if (j == first) w.seg_start[(size_t)row * (w.nseg + 1) + seg] = st;
+            }
+            if (l >= g0 && l < g1 && lane_over) {
+                const int e = sh.seg_first[l];
+                const int op = (e > 0 ? sh.heads[e - 1] : 0) + sh.seg_ovb[l];
+                w.seg_start[(size_t)row * (w.nseg + 1) + l] = sh.op_start[op];
+            }
+        }
+        walk_sync();
+        g0 = g1;
+    }
+    if (l == 0) {
+        if (STARTS) w.seg_start[(size_t)row * (w.nseg + 1) + w.nseg] = s;
+        w.row_S[row] = s;
+    }
+}
+
+// One wave walks a row: the exact value at every segment, run and
+// staged-chunk start is stored for the find with STARTS; without, only the
+// row sum.  A row of many segments takes the op list (its parallel set-up
+// pays once the clean runs it merges across segment boundaries are many);
+// a short row steps through its runs directly.
+constexpr int kOpWalkMinSegs = 16;
+
+template <bool STARTS, int KIND>
+__device__ __forceinline__ void walk_row(const Eval<KIND>& ev, const Work& w, int row,
+                                         WalkShared& sh) {
+    if (w.nseg >= kOpWalkMinSegs) walk_row_ops<STARTS>(ev, w, row, sh);
+    else walk_row_runs<STARTS>(ev, w, row, sh);
 }
 
 // Block k * chains + c walks chain c's k-th listed row.
