@@ -285,6 +285,50 @@ def bench_accept(lib, V, B, gamma, T, steps, warmup, sets=1, seed=5, top_k=0, to
             "rotating_sets": sets, "mean_accepted_last_call": float(nacc.mean())}
 
 
+def bench_accept_graph(lib, V, B, gamma, T, steps, warmup, seed=5):
+    """The same verify as bench_accept (tokens only), through the
+    allocation-free entry point captured once into a HIP graph and replayed:
+    the launch cost a serving loop pays per call without the host's seven
+    launches."""
+    from cogito_amd.capi import DeviceArray, last_error
+
+    rng = np.random.default_rng(seed)
+    nt, nd = B * (gamma + 1) * V, B * gamma * V
+    dt, dd = DeviceArray(lib, nt * 4), DeviceArray(lib, nd * 4)
+    if (lib.cgx_fill_normal_dev(dt.ptr, nt, seed, 100, 2.0) or
+            lib.cgx_fill_normal_dev(dd.ptr, nd, seed, 101, 2.0)):
+        raise RuntimeError(last_error(lib))
+    ud = rng.random((B, gamma), dtype=np.float32)
+    toks = _draft_tokens_from(dd.numpy(np.float32, (B, gamma, V)) / T, ud)
+    uv = rng.random((B, gamma + 1), dtype=np.float32)
+    dtok, du = DeviceArray.from_numpy(lib, toks), DeviceArray.from_numpy(lib, uv)
+    dout, dn = DeviceArray(lib, B * (gamma + 1) * 4), DeviceArray(lib, B * 4)
+    if lib.cgx_graph_begin():
+        raise RuntimeError(last_error(lib))
+    rc = lib.cgx_verify_chain_batch_dev_noalloc(dt.ptr, dd.ptr, dtok.ptr, du.ptr, B, gamma, V, T,
+                                                0, 1.0, dout.ptr, dn.ptr, None)
+    g = lib.cgx_graph_end()
+    if rc or not g:
+        raise RuntimeError(last_error(lib))
+    for _ in range(warmup):
+        lib.cgx_graph_launch(g)
+    if lib.cgx_synchronize():
+        raise RuntimeError(last_error(lib))
+    lib.cgx_event_record(0)
+    for _ in range(steps):
+        lib.cgx_graph_launch(g)
+    lib.cgx_event_record(1)
+    if lib.cgx_synchronize():
+        raise RuntimeError(last_error(lib))
+    us = lib.cgx_event_elapsed_ms(0, 1) / steps * 1e3
+    lib.cgx_graph_free(g)
+    for d in (dt, dd, dtok, du, dout, dn):
+        d.free()
+    log(f"[bench] accept (HIP graph replay) V={V} B={B} gamma={gamma} T={T}: {us:.2f} us/call")
+    return {"V": V, "batch": B, "gamma": gamma, "temperature": T, "ratios": False,
+            "us_per_call": round(us, 3), "graph": True}
+
+
 def bench_attention(lib, ctx, Nq, H, Hk, D, kv_gs, steps, warmup, seed=9):
     """INT4-KV verify attention (chain mask) of one layer per launch at the
     7B shape; launches rotate over enough layers to stream past the MALL."""
@@ -863,6 +907,8 @@ def main() -> int:
     cpu_on = not args.no_cpu
     if "accept" in legs:
         extra["accept_c1"] = bench_accept(lib, 32000, 1, 4, 1.0, args.steps, args.warmup)
+        extra["accept_c1_graph"] = bench_accept_graph(lib, 32000, 1, 4, 1.0, args.steps,
+                                                       args.warmup)
         extra["accept_roofline"] = bench_accept(lib, 128256, 64, 4, 1.0, 50, 5, sets=2)
         extra["accept_roofline_ratios"] = bench_accept(lib, 128256, 64, 4, 1.0, 50, 5, sets=2,
                                                        ratios=True)

@@ -247,6 +247,10 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_verify_chain_batch_dev": (I, [VP, VP, VP, VP, I, I, I, F, I, F, VP, VP, VP]),
     "cgx_verify_chain_batch_dev_noalloc": (I, [VP, VP, VP, VP, I, I, I, F, I, F, VP, VP, VP]),
     "cgx_verify_lean_min_blocks": (I, [I]),
+    "cgx_graph_begin": (I, []),
+    "cgx_graph_end": (VP, []),
+    "cgx_graph_launch": (I, [VP]),
+    "cgx_graph_free": (I, [VP]),
     "cgx_sample_temperature_u": (I, [VP, I, F, F]),
     "cgx_sample_top_k_u": (I, [VP, I, I, F]),
     "cgx_sample_top_p_u": (I, [VP, I, F, F]),

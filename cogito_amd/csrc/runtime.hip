@@ -244,6 +244,50 @@ extern "C" float cgx_event_elapsed_ms(int a, int b) {
     return ms;
 }
 
+// ------------------------------------------------------------ graphs
+// Capture of the library stream into a HIP graph (thread-local mode: other
+// threads' HIP calls are not affected) and its replays on the same stream.
+extern "C" int cgx_graph_begin(void) {
+    if (cgx_ensure_init()) return -1;
+    CGX_TRY(hipStreamBeginCapture(g_rt.stream, hipStreamCaptureModeThreadLocal));
+    return 0;
+}
+
+extern "C" void* cgx_graph_end(void) {
+    if (cgx_ensure_init()) return nullptr;
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(g_rt.stream, &g);
+    if (e != hipSuccess || !g) {
+        cgx_set_error("graph capture failed: %s", hipGetErrorString(e));
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) {
+        cgx_set_error("graph instantiation failed: %s", hipGetErrorString(e));
+        return nullptr;
+    }
+    return (void*)x;
+}
+
+extern "C" int cgx_graph_launch(void* graph) {
+    if (cgx_ensure_init()) return -1;
+    if (!graph) {
+        cgx_set_error("cgx_graph_launch: no graph");
+        return -1;
+    }
+    CGX_TRY(hipGraphLaunch((hipGraphExec_t)graph, g_rt.stream));
+    return 0;
+}
+
+extern "C" int cgx_graph_free(void* graph) {
+    if (!graph) return 0;
+    CGX_TRY(hipGraphExecDestroy((hipGraphExec_t)graph));
+    return 0;
+}
+
 extern "C" void* cgx_scratch(int slot, size_t bytes) {
     if (cgx_ensure_init()) return nullptr;
     if (slot < 0 || slot >= CGX_NUM_SLOTS) {

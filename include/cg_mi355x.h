@@ -44,6 +44,19 @@ int cgx_memcpy_d2d(void* dst, const void* src, size_t bytes);
 int cgx_memset(void* dst, int byte_value, size_t bytes);
 int cgx_is_device_ptr(const void* p);  /* 1 device, 0 host */
 
+/* HIP graphs of the library stream (no counterpart in the reference; for
+ * callers that replay a fixed-shape call, such as a serving loop's verify,
+ * without its launch cost).  Calls issued between cgx_graph_begin and
+ * cgx_graph_end are captured, not run; cgx_graph_end returns the executable
+ * graph (NULL on error) and cgx_graph_launch replays it on the library
+ * stream, reading and writing the same device addresses each time.  Only
+ * calls that allocate and set no memory may be captured: the verify through
+ * cgx_verify_chain_batch_dev_noalloc is the one this build tests. */
+int cgx_graph_begin(void);
+void* cgx_graph_end(void);
+int cgx_graph_launch(void* graph);
+int cgx_graph_free(void* graph);
+
 /* Timing with HIP events on the library stream (milliseconds). */
 int cgx_event_record(int slot);      /* slot 0..7 */
 float cgx_event_elapsed_ms(int slot_begin, int slot_end);
