@@ -324,25 +324,30 @@ __global__ __launch_bounds__(64 * W, (NG == 2 && T == 2 && MP <= 5) ? 4 : 1) voi
         // are issued at once, so the wave waits for memory once (up to 5
         // rows: with 8 the second round's activations cost the registers of
         // a second block per CU, measured slower)
+        // (each round's activations before its weights: loads complete in
+        // issue order, so the A-prep waits for the activations only)
         ARaw a0, a1;
         __builtin_amdgcn_sched_barrier(0);
-        load_w(wave, wcur);
         load_a(wave, a0);
+        load_w(wave, wcur);
         __builtin_amdgcn_sched_barrier(0);
-        load_w(wave + W, wnxt);
         load_a(wave + W, a1);
+        load_w(wave + W, wnxt);
         __builtin_amdgcn_sched_barrier(0);
         round_body(a0, wcur);
         __builtin_amdgcn_sched_barrier(0);
         round_body(a1, wnxt);
     } else {
         ARaw acur;
-        if (my_rounds > 0) load_w(wave, wcur);
+        // activations before weights: the A-prep waits for them, and loads
+        // complete in issue order, so the weights stay in flight meanwhile
+        if (my_rounds > 0) {
+            load_a(wave, acur);
+            load_w(wave, wcur);
+        }
         for (int i = 0; i < my_rounds; i++) {
             const int r = wave + i * W;
-            // activations first: the A-prep waits for them, and loads complete
-            // in issue order, so the next round's weights stay in flight
-            load_a(r, acur);
+            if (i > 0) load_a(r, acur);
             if (i + 1 < my_rounds) load_w(r + W, wnxt);
             round_body(acur, wcur);
             if (i + 1 < my_rounds) {
