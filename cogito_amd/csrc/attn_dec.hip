@@ -255,14 +255,19 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_dec(DecArgs a) {
                 t.kw[kh][0] = *(const uint32_t*)p;
             }
         }
+        // the scores need K and its scales, the O update V and its scales:
+        // loads complete in issue order, so the K scales come before V
         const int kl = kt + 4 * g;
 #pragma unroll
         for (int p = 0; p < 8; p++) {
             const uint32_t key = (uint32_t)min(kl + (p < 4 ? p : 12 + p), klast);
+            t.sk[p] = ksb[key * (uint32_t)Hk];
+        }
+#pragma unroll
+        for (int p = 0; p < 8; p++) {
+            const uint32_t key = (uint32_t)min(kl + (p < 4 ? p : 12 + p), klast);
             t.vw[p] = *(const uint32_t*)(vbase + (key * krow32 + (uint32_t)(4 * nb)));
-            const uint32_t so = key * (uint32_t)Hk;
-            t.sk[p] = ksb[so];
-            t.sv[p] = vsb[so];
+            t.sv[p] = vsb[key * (uint32_t)Hk];
         }
     };
 
@@ -284,15 +289,11 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_dec(DecArgs a) {
         lim_row[rt] = a.mask_kind == kMaskCausal ? Nk - a.Nq + rq[rt]
                     : a.mask_kind == kMaskTree ? Nk - a.tw - 1 : Nk;
     }
-    // the first tile is issued first (HBM), then the Q rows (the previous
-    // kernel just wrote them: they come from cache); the operand preparation
-    // below waits for Q only and overlaps the tile's latency.  The tile load
-    // is unconditional, like the prefetch below: a wave without a tile reads
-    // the split's last key (k_end >= 1 whenever the block runs).  Rows past R
-    // read row 0 (valid memory) and are zeroed, so the Q loads are
-    // unconditional too.
-    TileData td;
-    load_tile(k_begin + wave * kTile, td);
+    // the Q rows are loaded first (the previous kernel just wrote them, they
+    // come from cache), then the first tile: loads complete in issue order,
+    // so the operand preparation below waits for Q only and overlaps the
+    // tile's HBM latency.  Rows past R read row 0 (valid memory) and are
+    // zeroed, so the loads are unconditional.
     float qv[RT][DPL];
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
@@ -305,6 +306,10 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_dec(DecArgs a) {
             qv[rt][i] = t.x; qv[rt][i + 1] = t.y; qv[rt][i + 2] = t.z; qv[rt][i + 3] = t.w;
         }
     }
+    // unconditional, like the prefetch below: a wave without a tile reads the
+    // split's last key (k_end >= 1 whenever the block runs)
+    TileData td;
+    load_tile(k_begin + wave * kTile, td);
     {
         // rows are per lane (n); every wave computes the row exponent of its
         // lanes' rows for all RT (cheap), the fp16 splits are divided: wave w
