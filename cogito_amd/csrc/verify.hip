@@ -986,9 +986,11 @@ __device__ __forceinline__ int need_row(const Rows& rows, const Work& w, int c, 
 
 __device__ __forceinline__ void fold1_row(const Rows& rows, float T, const Work& w, int r,
                                           int seg, FoldShared& sh) {
+    // the segment stats first: loads complete in issue order, so the row
+    // maximum and the guide wait for them only while the chunk arrives
+    const SegStats st = seg_stats_of(w, r);
     float X[kC], Y[kC];
     load_raw(rows.row(r), seg * kSeg + threadIdx.x * kC, rows.V, X);
-    const SegStats st = seg_stats_of(w, r);
     const float m = block_max256(st.m, sh.f);        // the row maximum
     if (seg == 0 && threadIdx.x == 0) w.row_m[r] = m;
     double P0, E0;
@@ -1138,8 +1140,8 @@ __global__ __launch_bounds__(kT) void k_seg_fold2(Rows rows, float T, Work w) {
         // p_i = e_i / S: the pass-1 guide of row ra, divided by S
         Eval<kKindProb> ev = task_eval<kKindProb>(rows, w, tk, T);
         ev.tab = sh.tab;
+        const SegStats st = seg_stats_of(w, tk.ra);   // before the chunk (issue order)
         ev.raw(base, X, Y);
-        const SegStats st = seg_stats_of(w, tk.ra);
         double P, E;
         exp_prefix(st.G, st.H, st.m, (int)threadIdx.x < seg, ev.ma, T, sh.d, &P, &E);
         const double P0 = P / (double)ev.Sa;
@@ -1148,13 +1150,13 @@ __global__ __launch_bounds__(kT) void k_seg_fold2(Rows rows, float T, Work w) {
     } else {
         Eval<kKindRes> ev = task_eval<kKindRes>(rows, w, tk, T);
         ev.tab = sh.tab;
-        ev.raw(base, X, Y);
-        double g = 0.0, e = 0.0;
+        double g = 0.0, e = 0.0;                       // before the chunk (issue order)
         if ((int)threadIdx.x < seg) {
             const size_t i = (size_t)c * w.nseg + threadIdx.x;
             g = w.task_ge[2 * i];
             e = w.task_ge[2 * i + 1];
         }
+        ev.raw(base, X, Y);
         const double P0 = block_sum256_d(g, sh.d);
         const double E0 = block_sum256_d(e, sh.d);
         fold_segment<COMPACT>(ev, w, w.R1 + c, seg, X, Y, P0, E0, sh);
