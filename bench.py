@@ -42,7 +42,7 @@ MALL_BYTES = 256 * 1024 * 1024
 # HBM bytes per GEMV launch measured with rocprofv3 FETCH_SIZE + WRITE_SIZE,
 # scaled by a copy kernel of known size (profiles/int4_gemv_4096x4096.md).
 # Measured for k_gemv_mfma (layout 3); re-measure when the kernel changes.
-GEMV_TRAFFIC_BYTES = {1: 9140224, 2: 9291776, 3: 9432064, 4: 9579520, 5: 9740288}
+GEMV_TRAFFIC_BYTES = {1: 9149663, 2: 9287892, 3: 9431241, 4: 9578685, 5: 9735345}
 
 
 def log(msg: str) -> None:
