@@ -80,25 +80,28 @@ __global__ void k_rope_append(const float* __restrict__ qkv, int ld, int H, int 
     ks += (size_t)sq * rb.seq_groups;
     vs += (size_t)sq * rb.seq_groups;
     const float* row = qkv + (size_t)m * ld;
+    // the head's values first, so that their latency overlaps the rotary
+    // angle's evaluation (a query head: its two halves; a KV head: K's
+    // halves and V's)
+    const bool is_q = head < H;
+    const int hk = head - H;
+    const float* k = is_q ? row + head * D : row + H * D + hk * D;
+    const float* v = is_q ? k : row + (H + Hk) * D + hk * D;
+    const float k0 = k[i], k1 = k[i + half];
+    const float v0 = v[i], v1 = v[i + half];
     float freq = __fdiv_rn(1.0f, powf(theta, __fdiv_rn((float)(2 * i), (float)D)));
     float angle = __fmul_rn((float)rpos, freq);
     float c = cosf(angle), s = sinf(angle);
-    if (head < H) {
-        const float* q = row + head * D;
-        float x0 = q[i], x1 = q[i + half];
+    if (is_q) {
         float* o = q_out + ((size_t)m * H + head) * D;
-        o[i] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
-        o[i + half] = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
+        o[i] = __fsub_rn(__fmul_rn(k0, c), __fmul_rn(k1, s));
+        o[i + half] = __fadd_rn(__fmul_rn(k0, s), __fmul_rn(k1, c));
         return;
     }
-    const int hk = head - H;
-    const float* k = row + H * D + hk * D;
-    const float* v = row + (H + Hk) * D + hk * D;
-    float k0 = k[i], k1 = k[i + half];
     sk[i] = __fsub_rn(__fmul_rn(k0, c), __fmul_rn(k1, s));
     sk[i + half] = __fadd_rn(__fmul_rn(k0, s), __fmul_rn(k1, c));
-    sv[i] = v[i];
-    sv[i + half] = v[i + half];
+    sv[i] = v0;
+    sv[i + half] = v1;
     __syncthreads();
     // quantise: thread i packs dims 2i, 2i+1 (same group: gs is even).  The
     // group absmax (order-free) is a shuffle reduction over the gs/2 threads
