@@ -117,7 +117,8 @@ struct ExpGen {                 // expf((src - m) / T), speculative.c:61
     S src;
     float m, T;
     __device__ float operator()(int j) const {
-        return exp_glibc(__fdiv_rn(__fsub_rn(src(j), m), T));
+        const float d = __fsub_rn(src(j), m);
+        return exp_glibc(T == 1.0f ? d : __fdiv_rn(d, T));   // d / 1 == d exactly
     }
 };
 
@@ -195,17 +196,20 @@ __device__ __forceinline__ int binade_of(double v) {
     return ilogb(v);
 }
 
-__device__ __forceinline__ double ulp_scale(int b) {   // 1 / ulp
-    return b == -127 ? 0x1p149 : ldexp(1.0, 23 - b);
+// The same for a binary32 value, from its bits: the exponent field minus the
+// bias (zero and subnormals: -127); +inf, NaN and negative values lie in no
+// binade.
+__device__ __forceinline__ int binade_bits(float s) {
+    const int e = (int)(__float_as_uint(s) >> 23);
+    return e >= 255 ? 0x7fffffff : e - 127;
 }
 
-__device__ __forceinline__ double ulp_of(int b) {
-    return b == -127 ? 0x1p-149 : ldexp(1.0, b - 23);
-}
-
-__device__ __forceinline__ int parity_of(float s, int b) {
-    double n = (double)s * ulp_scale(b);
-    return (int)((long long)n & 1);
+// Inside binade b the bits of a non-negative binary32 value are its count of
+// ulps u_b plus a constant, so for s in b: the parity of s / u_b is the low
+// bit, and s + q u_b (while it stays in b) is the bit pattern plus q.
+__device__ __forceinline__ unsigned parity_bits(float s) { return __float_as_uint(s) & 1u; }
+__device__ __forceinline__ float add_ulps(float s, int q) {
+    return __uint_as_float(__float_as_uint(s) + (unsigned)q);
 }
 
 struct EosShared {
@@ -476,7 +480,7 @@ __device__ __forceinline__ float eos_tail(const Mono& own, bool clean, int b, co
                     s = replay_chunk_staged(g, __builtin_amdgcn_readlane(my_slot, k),
                                             rd * kRound + c * kCh, n, s, sh);
                     if (lane_id() == 0) sh.cend[rd][c] = s;
-                } else if (binade_of((double)s) != bc) {
+                } else if (binade_bits(s) != bc) {
                     // a clean run whose start is not in the binade its chunks
                     // assumed (excluded by the error bound, handled exactly
                     // anyway): replay it chunk by chunk from the generator
@@ -490,10 +494,9 @@ __device__ __forceinline__ float eos_tail(const Mono& own, bool clean, int b, co
                     }
                 } else {
                     if (lane_id() == 0) sh.cstart[rd][c] = s;
-                    const double q0 = __builtin_amdgcn_readlane(my_q0, k),
-                                 q1 = __builtin_amdgcn_readlane(my_q1, k);
-                    const double q = parity_of(s, bc) ? q1 : q0;
-                    s = (float)((double)s + q * ulp_of(bc));
+                    const int q0 = __builtin_amdgcn_readlane(my_q0, k),
+                              q1 = __builtin_amdgcn_readlane(my_q1, k);
+                    s = add_ulps(s, parity_bits(s) ? q1 : q0);
                 }
             }
         }
@@ -506,7 +509,7 @@ __device__ __forceinline__ float eos_tail(const Mono& own, bool clean, int b, co
     if (bt != kDirty) {
         const int h = sh.head[t];
         const float sh0 = sh.cstart[rd][h];
-        const int par = parity_of(sh0, bt);
+        const unsigned par = parity_bits(sh0);
         Mono ex = mono_id();
         if (t != h) {
             ex.q0 = sh.incl[t - 1].q0;
@@ -514,12 +517,12 @@ __device__ __forceinline__ float eos_tail(const Mono& own, bool clean, int b, co
             ex.c0 = sh.incl[t - 1].c0;
             ex.c1 = sh.incl[t - 1].c1;
         }
-        const double u = ulp_of(bt);
-        const double s0 = (double)sh0 + (par ? ex.q1 : ex.q0) * u;
+        // the run stays in binade bt, so every boundary is s + q ulps
+        const float s0 = add_ulps(sh0, par ? ex.q1 : ex.q0);
         const int par2 = par ? ex.c1 : ex.c0;
-        const double s1 = s0 + (par2 ? own.q1 : own.q0) * u;
-        if (t != h) sh.cstart[rd][t] = (float)s0;
-        sh.cend[rd][t] = (float)s1;
+        const float s1 = add_ulps(s0, par2 ? own.q1 : own.q0);
+        if (t != h) sh.cstart[rd][t] = s0;
+        sh.cend[rd][t] = s1;
     }
     const float total = sh.total;
     __syncthreads();
@@ -774,6 +777,12 @@ __device__ __forceinline__ float vals_max(const float (&x)[kCh], EosShared& sh) 
 __device__ __forceinline__ void vals_exp(const float (&x)[kCh], float m, float T, int n,
                                          float (&e)[kCh]) {
     const int base = threadIdx.x * kCh;
+    if (T == 1.0f) {   // d / 1 == d exactly: the division is skipped
+#pragma unroll
+        for (int k = 0; k < kCh; k++)
+            e[k] = base + k < n ? exp_glibc(__fsub_rn(x[k], m)) : 0.0f;
+        return;
+    }
 #pragma unroll
     for (int k = 0; k < kCh; k++)
         e[k] = base + k < n ? exp_glibc(__fdiv_rn(__fsub_rn(x[k], m), T)) : 0.0f;
