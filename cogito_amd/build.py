@@ -31,8 +31,11 @@ HIP_FLAGS = [
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
 # Files whose arithmetic must round exactly where written (no implicit
-# contraction of a*b+c into fma).
-EXACT_FP = {"accept.hip", "int4.hip", "filter.hip", "tree.hip"}
+# contraction of a*b+c into fma).  decoder.hip is among them so that RoPE's
+# x0 c - x1 s rounds twice, as the reference's CPU code does, whatever the
+# surrounding code looks like (with contraction the backend fuses such pairs,
+# in the inlined sin / cos / pow too, depending on the code's layout).
+EXACT_FP = {"accept.hip", "int4.hip", "filter.hip", "tree.hip", "decoder.hip"}
 C_FLAGS = ["-O2", "-fPIC", "-std=c11", "-Wall", "-Wextra", "-Wno-unused-parameter",
            # a call to an undeclared function (e.g. POSIX strdup under C11)
            # would truncate a returned pointer to int
