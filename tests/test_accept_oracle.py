@@ -274,3 +274,51 @@ def test_top_p_tie_rule_matches_selection_sort(oracle, rng, V, levels):
         pi = np.zeros(V, np.float32)
         pi[idx] = probs
         assert _tie_rule_order(pi) == idx.tolist()
+
+
+def test_ulp_count_identities_of_the_exact_sum_walk():
+    """The exact ordered sum's walk works on binary32 bit patterns (eos.hpp:
+    binade_bits, parity_bits, add_ulps): inside binade b (ulp u_b) the bits
+    of a non-negative value are its ulp count plus a constant, so s + q u_b
+    is the bit pattern plus q, the count's parity is the low bit, and the
+    binade is the exponent field minus 127 (-127: zero and subnormals).
+    Checked here against real fp32 additions (numpy) over every binade:
+    running sums of values that keep s inside one binade, each addition's
+    ulp increment rounded as the hardware does (ties to even), land exactly
+    on bits(s0) + sum of increments."""
+    rng = np.random.default_rng(5)
+    for b in range(-127, 128):
+        ub = 2.0 ** (b - 23) if b > -127 else 2.0 ** -149
+        lo = 2.0 ** b if b > -127 else 0.0
+        hi = 2.0 ** (b + 1) if b > -127 else 2.0 ** -126
+        for _ in range(20):
+            start = int(rng.integers(0, 1 << 22))
+            bits0 = ((b + 127) << 23 | start) if b > -127 else start
+            s = np.array([bits0], np.uint32).view(np.float32)[0]
+            assert lo <= float(s) < hi
+            # binade from the exponent field; parity = low bit of the count
+            assert (int(bits0) >> 23) - 127 == b
+            n0 = float(s) / ub
+            assert n0 == int(n0) and int(n0) & 1 == bits0 & 1
+            # a run of additions that stays in the binade: values on the
+            # half-ulp grid (ties included) below 4 ulps each; binary32 has no
+            # half ulp below 2^-149, so binades -127 and -126 take whole ulps
+            cnt = bits0
+            cur = s
+            halves = rng.integers(0, 8, 40)
+            if b <= -126:
+                halves &= ~1
+            for h in halves:
+                x = np.float32(h * ub / 2)
+                nxt = np.float32(cur + x)
+                if float(nxt) >= hi:
+                    break
+                f, half = divmod(int(h), 2)
+                n = int(float(cur) / ub)
+                inc = f + ((n + f) & 1) if half else f
+                cnt += inc
+                cur = nxt
+                assert np.array([cnt], np.uint32).view(np.float32)[0] == cur
+                assert float(cur) == float(s) + (cnt - bits0) * ub
+    # +inf and NaN lie in no binade (exponent field 255)
+    assert (int(np.array([np.inf], np.float32).view(np.uint32)[0]) >> 23) == 255
