@@ -23,6 +23,9 @@ struct cgx_spec {
     float T;
     int top_k;
     float top_p;
+    /* one allocation, so that a step's inputs go over in one copy:
+     * d_u, then d_pending, then d_tokens */
+    uint32_t* d_in;
     int* d_tokens;        /* [gamma + 1]: last, d_1 .. d_gamma */
     int* d_pending;       /* [2]: draft inputs not yet in the draft cache */
     float* d_draft_logits;
@@ -39,11 +42,9 @@ struct cgx_spec {
 
 void cgx_spec_free(cgx_spec* s) {
     if (!s) return;
-    cgx_free(s->d_tokens);
-    cgx_free(s->d_pending);
+    cgx_free(s->d_in);
     cgx_free(s->d_draft_logits);
     cgx_free(s->d_target_logits);
-    cgx_free(s->d_u);
     cgx_free(s->d_z);
     cgx_free(s->d_out);
     free(s);
@@ -72,15 +73,17 @@ cgx_spec* cgx_spec_new(cgx_model* draft, cgx_model* target, int gamma, float tem
     s->top_k = top_k;
     s->top_p = top_p;
     size_t V = (size_t)s->V;
-    s->d_tokens = (int*)cgx_malloc((size_t)(gamma + 1) * 4);
-    s->d_pending = (int*)cgx_malloc(2 * 4);
+    s->d_in = (uint32_t*)cgx_malloc((size_t)(2 * gamma + 1 + 2 + gamma + 1) * 4);
+    if (s->d_in) {
+        s->d_u = (float*)s->d_in;
+        s->d_pending = (int*)(s->d_in + 2 * gamma + 1);
+        s->d_tokens = s->d_pending + 2;
+    }
     s->d_draft_logits = (float*)cgx_malloc((size_t)gamma * V * 4);
     s->d_target_logits = (float*)cgx_malloc((size_t)(gamma + 1) * V * 4);
-    s->d_u = (float*)cgx_malloc((size_t)(2 * gamma + 1) * 4);
     s->d_z = (float*)cgx_malloc(V * 4);
     s->d_out = (int*)cgx_malloc((size_t)(gamma + 2) * 4);
-    if (!s->d_tokens || !s->d_pending || !s->d_draft_logits || !s->d_target_logits ||
-        !s->d_u || !s->d_z || !s->d_out) {
+    if (!s->d_in || !s->d_draft_logits || !s->d_target_logits || !s->d_z || !s->d_out) {
         cgx_spec_free(s);
         return NULL;
     }
@@ -158,24 +161,23 @@ int cgx_spec_step(cgx_spec* s, const float* u_draft, const float* u_verify, int*
         cgx_set_error("cgx_spec_step: KV cache full (%d + %d)", L, g + 1);
         return -1;
     }
-    /* inputs of the step: draws, the last token, the draft's pending tokens */
-    float hu[2 * 64 + 1];
-    float* hbuf = (2 * g + 1) <= (int)(sizeof(hu) / sizeof(hu[0]))
-                      ? hu
-                      : (float*)malloc((size_t)(2 * g + 1) * sizeof(float));
+    /* inputs of the step in one copy: the draws, the draft's pending tokens
+     * (pend_tok, last; the draft reads the last np of them), the last token */
+    uint32_t hu[2 * 64 + 1 + 3];
+    const size_t nin = (size_t)(2 * g + 1) + 3;
+    uint32_t* hbuf = nin <= sizeof(hu) / sizeof(hu[0]) ? hu : (uint32_t*)malloc(nin * 4);
     if (!hbuf) return -1;
+    const int pend[3] = {s->pend_tok, s->last, s->last};
     memcpy(hbuf, u_draft, (size_t)g * sizeof(float));
     memcpy(hbuf + g, u_verify, (size_t)(g + 1) * sizeof(float));
-    int pend[2] = {s->pend_tok, s->last};
-    int np = s->pend_extra ? 2 : 1;
-    int rc = cgx_memcpy_h2d(s->d_u, hbuf, (size_t)(2 * g + 1) * sizeof(float)) ||
-             cgx_memcpy_h2d(s->d_tokens, &s->last, sizeof(int)) ||
-             cgx_memcpy_h2d(s->d_pending, pend + (2 - np), (size_t)np * sizeof(int));
+    memcpy(hbuf + 2 * g + 1, pend, sizeof(pend));
+    const int np = s->pend_extra ? 2 : 1;
+    const int rc = cgx_memcpy_h2d(s->d_in, hbuf, nin * 4);
     if (hbuf != hu) free(hbuf);
     if (rc) return -1;
 
     /* draft: gamma tokens */
-    if (cgx_model_forward(s->draft, s->d_pending, np, 1, s->d_draft_logits) ||
+    if (cgx_model_forward(s->draft, s->d_pending + (2 - np), np, 1, s->d_draft_logits) ||
         draft_sample(s, 0, u_draft[0]))
         return -1;
     for (int i = 1; i < g; i++) {
