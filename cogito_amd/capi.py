@@ -288,6 +288,8 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_model_kv": (PKV, [VP]),
     "cgx_model_fill_context": (I, [VP, I, C.c_uint64]),
     "cgx_model_export": (I, [VP, I, I, VP, VP]),
+    "cgx_model_load": (VP, [C.POINTER(CgxModelConfig), C.c_char_p, VP]),
+    "cgx_model_save": (I, [VP, C.c_char_p, I]),
     "cgx_fill_normal_dev": (I, [VP, SZ, C.c_uint64, C.c_uint32, F]),
     "cgx_spec_new": (VP, [VP, VP, I, F, I, F]),
     "cgx_spec_free": (None, [VP]),

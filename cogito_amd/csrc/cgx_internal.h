@@ -70,6 +70,10 @@ int cgk_int4_repack_mfma(const uint8_t* flat, const float* scales, int K, int N,
                          int paired, uint8_t* w, float* scales_t);
 int cgk_int4_dequantize_mfma(const uint8_t* w, const float* scales_t, int K, int N, int gs,
                              int paired, float* out);
+/* The inverse of cgk_int4_repack_mfma: layout 3 back to the reference's
+ * flat nibbles (K*N/2 bytes) and flat scales [K][N/gs]. */
+int cgk_int4_unpack_mfma(const uint8_t* w, const float* scales_t, int K, int N, int gs,
+                         int paired, uint8_t* flat, float* scales);
 /* INT4 GEMM for M >= 32 rows over layout 3 (gemv.hip): same arguments and
  * epilogues as cgk_gemv_mfma plus smax >= every |scale| of the weight.
  * stats_in ([M][nstat_in][2] partial max|x*nw| and sum x^2, from the
@@ -210,6 +214,27 @@ cgx_model* cgx_model_from_handle(const void* p);
 uint64_t cgx_model_epoch(const cgx_model* m);
 /* The driver (host/driver.c) drops what it knows about a freed model. */
 void cgx_driver_forget_model(const cgx_model* m);
+
+/* A COG1 file opened for a decoder's weights (host/model_file.c).  Entry
+ * indices come from cgx_wfile_find (-1: absent).  A matrix [K, N] is nb
+ * column blocks (entries idx[b] of widths[b]); cgx_wfile_matrix_kind checks
+ * their directory entries and returns 0 (fp32) or 2 (INT4 of group gs), or
+ * -1 with the error set; the readers then fill host buffers: fp32 [K][N], or
+ * flat nibbles [K][N/2] and scales [K][N/gs].  cgx_wfile_vector returns the
+ * index of an fp32 vector of n values, -1 when absent, -2 (error set) when
+ * malformed. */
+typedef struct cgx_wfile cgx_wfile;
+cgx_wfile* cgx_wfile_open(const char* path, const char* who);
+void cgx_wfile_close(cgx_wfile* w);
+int cgx_wfile_find(const cgx_wfile* w, const char* name);
+int cgx_wfile_vector(const cgx_wfile* w, const char* name, int n, const char* who);
+int cgx_wfile_matrix_kind(const cgx_wfile* w, const int* idx, const int* widths, int nb, int K,
+                          int gs, const char* who);
+int cgx_wfile_read_vector(const cgx_wfile* w, int i, float* out, int n);
+int cgx_wfile_read_f32(const cgx_wfile* w, const int* idx, const int* widths, int nb, int K,
+                       float* out);
+int cgx_wfile_read_int4(const cgx_wfile* w, const int* idx, const int* widths, int nb, int K,
+                        int gs, uint8_t* data, float* scales);
 
 /* Static draft tree (tree.hip, host/tree.c): node 0 is the verified root;
  * nodes are in breadth-first order; kids[i][0..nkids[i]) the children of

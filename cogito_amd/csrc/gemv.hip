@@ -471,6 +471,30 @@ __global__ void k_dequant_mfma(const uint32_t* __restrict__ w, const float* __re
     }
 }
 
+// Layout 3 -> cogito's row-major nibbles (two's complement, flat): the
+// inverse of k_repack_mfma.  One thread per flat byte (two columns of one
+// row, which sit in neighbouring lanes of the same layout word index).
+__global__ void k_unpack_mfma(const uint32_t* __restrict__ w, int K, int N, int paired,
+                              uint8_t* __restrict__ flat) {
+    size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= (size_t)K * N / 2) return;
+    const int nchunks = K / kChunkK, ff_tiles = N / 32;
+    unsigned out = 0;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const size_t idx = 2 * b + h;
+        const int k = (int)(idx / N), col = (int)(idx % N);
+        const int lt = col >> 4;
+        const int L = paired ? (lt < ff_tiles ? 2 * lt : 2 * (lt - ff_tiles) + 1) : lt;
+        const int c = k / kChunkK, kk = k % kChunkK;
+        const int j = kk >> 5, l = ((kk & 31) >> 3) * 16 + (col & 15), p = kk & 7;
+        const uint32_t word = w[(((size_t)L * nchunks + c) * 64 + l) * 4 + j];
+        const unsigned nib = (word >> (4 * ((p >> 1) + 4 * (p & 1)))) & 0xFu;
+        out |= (nib ^ 0x8u) << (4 * h);                 // offset binary -> two's complement
+    }
+    flat[b] = (uint8_t)out;
+}
+
 template <int MP, int T, int NG, int PRO, int EPI, int W = kWaves>
 int launch_t(const MfmaArgs& a, int nblocks) {
     hipLaunchKernelGGL((k_gemv_mfma<MP, T, NG, PRO, EPI, W>), dim3(nblocks), dim3(64 * W), 0,
@@ -942,6 +966,20 @@ extern "C" int cgk_int4_repack_mfma(const uint8_t* flat, const float* scales, in
                        stream(), flat, K, N, paired, (uint32_t*)w);
     if (launch_check("k_repack_mfma")) return -1;
     return cgk_int4_transpose_scales(scales, K, N / gs, scales_t);
+}
+
+extern "C" int cgk_int4_unpack_mfma(const uint8_t* w, const float* scales_t, int K, int N,
+                                    int gs, int paired, uint8_t* flat, float* scales) {
+    if (K % kRoundK || N % 16 || gs % 16 || N % gs || (paired && (N % 32))) {
+        cgx_set_error("unpack_mfma: unsupported shape K=%d N=%d gs=%d", K, N, gs);
+        return -1;
+    }
+    size_t bytes = (size_t)K * N / 2;
+    hipLaunchKernelGGL(k_unpack_mfma, dim3((unsigned)((bytes + 255) / 256)), dim3(256), 0,
+                       stream(), (const uint32_t*)w, K, N, paired, flat);
+    if (launch_check("k_unpack_mfma")) return -1;
+    // scales_t [N/gs][K] -> flat [K][N/gs]
+    return cgk_int4_transpose_scales(scales_t, N / gs, K, scales);
 }
 
 extern "C" int cgk_int4_dequantize_mfma(const uint8_t* w, const float* scales_t, int K, int N,

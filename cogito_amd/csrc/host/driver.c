@@ -587,12 +587,15 @@ cg_tensor* cg_forward_tree_attention(void* model, cg_tensor* input, cg_tensor* t
     const size_t V = (size_t)c.vocab;
     int P = 0;
     cgx_tree_rows tr;
-    if (!tree_mask || !tree_mask->data || tree_mask->size != S * S) {
-        cgx_set_error("%s: tree_mask must hold [S][S] = %d x %d values", who, S, S);
-        goto done;
-    }
+    /* the length first, then the mask size (formed in size_t: S * S can
+     * exceed the int range) */
     if (S > c.max_seq) {
         cgx_set_error("%s: %d tokens exceed the KV cache (%d)", who, S, c.max_seq);
+        goto done;
+    }
+    if (!tree_mask || !tree_mask->data || tree_mask->size < 0 ||
+        (size_t)tree_mask->size != (size_t)S * (size_t)S) {
+        cgx_set_error("%s: tree_mask must hold [S][S] = %d x %d values", who, S, S);
         goto done;
     }
     mk = (float*)malloc((size_t)S * S * sizeof(float));

@@ -14,6 +14,7 @@
 #include <string.h>
 
 #include "cg_mi355x.h"
+#include "cg_serialization.h"
 #include "cgx_internal.h"
 
 int cgk_embed(const float* table, const int* tokens, int M, int d, int V, float* x);
@@ -50,7 +51,10 @@ struct cgx_model {
     float* embed;
     lin_t lm;
     int shared;              /* embed / lm_head borrowed from another model */
-    float* ones;             /* RMSNorm weights */
+    int from_file;           /* weights read from a file (no seed behind them) */
+    float* ones;             /* d_ff ones: the RMSNorm weights of a seeded model */
+    float* nw;               /* [2 n_layers + 1][d]: each layer's attention and MLP
+                              * RMSNorm weights, then the final one; NULL: all 1 */
     layer_t* layers;
     cg_kv_cache_int4* kv;
     int* tok;
@@ -75,6 +79,12 @@ static uint32_t lin_sid(int layer, int which) {
     return which == W_LM ? 2u : (uint32_t)(16 * layer + 3 + which);
 }
 
+/* RMSNorm weights: i = 2 l (before attention of layer l), 2 l + 1 (before
+ * its MLP), 2 n_layers (before the lm_head). */
+static const float* norm_w(const cgx_model* m, int i) {
+    return m->nw ? m->nw + (size_t)i * m->c.d_model : m->ones;
+}
+
 /* Seeded fp32 values -> reference-layout INT4 (flat) in tmp buffers. */
 static int gen_flat(const cgx_model* m, uint32_t sid, int K, int N, float* tf, uint8_t* tq,
                     float* ts) {
@@ -83,15 +93,147 @@ static int gen_flat(const cgx_model* m, uint32_t sid, int K, int N, float* tf, u
     return cgk_int4_quantize(tf, (int)n, m->c.group_size, tq, ts);
 }
 
+/* ---------------------------------------------------------- model files */
+/* Entry names (the fields of the reference's transformer block,
+ * include/cg_transformer.h:41-50):
+ *   embed [V, d] fp32;  norm [d] (final RMSNorm);  lm_head [d, V]
+ *   layers.<l>.norm1, layers.<l>.norm2 [d]            RMSNorm weights
+ *   layers.<l>.attn_qkv_proj [d, (H + 2 Hk) hd]      or attn_q_proj,
+ *                                                    attn_k_proj, attn_v_proj
+ *   layers.<l>.attn_o_proj [H hd, d]
+ *   layers.<l>.mlp_gate_up [d, 2 ff]                 or mlp_gate, mlp_up
+ *   layers.<l>.mlp_down [ff, d]
+ * Matrices are fp32 (quantized at load with cg_quantize_int4's rule) or INT4
+ * entries (host/model_file.c).  Missing norms are 1. */
+static const char* const kQkvParts[3] = {"attn_q_proj", "attn_k_proj", "attn_v_proj"};
+static const char* const kGuParts[2] = {"mlp_gate", "mlp_up"};
+
+static void lin_name(int which, int layer, char* out) {
+    static const char* const whole[4] = {"attn_qkv_proj", "attn_o_proj", "mlp_gate_up",
+                                         "mlp_down"};
+    if (which == W_LM)
+        snprintf(out, 64, "lm_head");
+    else
+        snprintf(out, 64, "layers.%d.%s", layer, whole[which]);
+}
+
+/* The entries of matrix `which` of `layer`: the whole matrix, else its column
+ * blocks.  Returns the block count (idx, widths filled; *kind 0 fp32 / 2
+ * INT4), or -1 with the error set. */
+static int lin_entries(const cgx_wfile* f, const cgx_model_config* c, int which, int layer,
+                       int idx[3], int widths[3], int* kind, const char* who) {
+    int K, N, nb = 1;
+    lin_shape(c, which, &K, &N);
+    char whole[64], parts[3][64];
+    int np = 0, pw[3] = {0, 0, 0};
+    lin_name(which, layer, whole);
+    if (which == W_QKV) {
+        np = 3;
+        pw[0] = c->n_heads * c->head_dim;
+        pw[1] = pw[2] = c->n_kv_heads * c->head_dim;
+        for (int b = 0; b < 3; b++) snprintf(parts[b], 64, "layers.%d.%s", layer, kQkvParts[b]);
+    } else if (which == W_GU) {
+        np = 2;
+        pw[0] = pw[1] = c->d_ff;
+        for (int b = 0; b < 2; b++) snprintf(parts[b], 64, "layers.%d.%s", layer, kGuParts[b]);
+    }
+    idx[0] = cgx_wfile_find(f, whole);
+    widths[0] = N;
+    if (idx[0] < 0) {
+        nb = np;
+        for (int b = 0; b < np; b++) {
+            idx[b] = cgx_wfile_find(f, parts[b]);
+            widths[b] = pw[b];
+            if (idx[b] < 0) nb = 0;
+        }
+        if (!nb) {
+            if (np)
+                cgx_set_error("%s: no entry %s, nor all of its blocks (%s, %s%s%s)", who, whole,
+                              parts[0], parts[1], np > 2 ? ", " : "", np > 2 ? parts[2] : "");
+            else
+                cgx_set_error("%s: no entry %s", who, whole);
+            return -1;
+        }
+    }
+    *kind = cgx_wfile_matrix_kind(f, idx, widths, nb, K, c->group_size, who);
+    return *kind < 0 ? -1 : nb;
+}
+
+/* Matrix `which` of `layer` from the file into the flat INT4 buffers tq, ts
+ * (device): INT4 entries are copied, fp32 entries quantized on the device. */
+static int file_flat(const cgx_wfile* f, const cgx_model_config* c, int which, int layer,
+                     float* tf, uint8_t* tq, float* ts) {
+    int idx[3], widths[3], kind, K, N;
+    const int nb = lin_entries(f, c, which, layer, idx, widths, &kind, "cgx_model_load");
+    if (nb < 0) return -1;
+    lin_shape(c, which, &K, &N);
+    const size_t n = (size_t)K * N, gs = (size_t)c->group_size;
+    int rc;
+    if (kind == 0) {
+        float* h = (float*)malloc(n * 4);
+        rc = !h || cgx_wfile_read_f32(f, idx, widths, nb, K, h) || cgx_memcpy_h2d(tf, h, n * 4) ||
+             cgk_int4_quantize(tf, (int)n, c->group_size, tq, ts);
+        free(h);
+    } else {
+        uint8_t* hd = (uint8_t*)malloc(n / 2);
+        float* hs = (float*)malloc(n / gs * 4);
+        rc = !hd || !hs || cgx_wfile_read_int4(f, idx, widths, nb, K, c->group_size, hd, hs) ||
+             cgx_memcpy_h2d(tq, hd, n / 2) || cgx_memcpy_h2d(ts, hs, n / gs * 4);
+        free(hd);
+        free(hs);
+    }
+    if (rc && !cgx_last_error()[0]) cgx_set_error("cgx_model_load: out of memory");
+    return rc ? -1 : 0;
+}
+
+static void norm_name(int i, int n_layers, char* out) {
+    if (i == 2 * n_layers)
+        snprintf(out, 64, "norm");
+    else
+        snprintf(out, 64, "layers.%d.norm%d", i / 2, 1 + (i & 1));
+}
+
+/* Every entry the model needs is present and well formed (directory only). */
+static int check_file(const cgx_wfile* f, const cgx_model_config* c, int shared) {
+    const char* who = "cgx_model_load";
+    int idx[3], widths[3], kind;
+    if (!shared) {
+        const int ei = cgx_wfile_find(f, "embed");
+        int ew = c->d_model;
+        if (ei < 0) {
+            cgx_set_error("%s: no entry embed", who);
+            return -1;
+        }
+        const int kind_e = cgx_wfile_matrix_kind(f, &ei, &ew, 1, c->vocab, c->group_size, who);
+        if (kind_e < 0) return -1;
+        if (kind_e != 0) {
+            cgx_set_error("%s: entry embed must be fp32 [%d, %d]", who, c->vocab, c->d_model);
+            return -1;
+        }
+        if (lin_entries(f, c, W_LM, 0, idx, widths, &kind, who) < 0) return -1;
+    }
+    for (int l = 0; l < c->n_layers; l++)
+        for (int w = 0; w < 4; w++)
+            if (lin_entries(f, c, w, l, idx, widths, &kind, who) < 0) return -1;
+    for (int i = 0; i <= 2 * c->n_layers; i++) {
+        char nm[64];
+        norm_name(i, c->n_layers, nm);
+        if (cgx_wfile_vector(f, nm, c->d_model, who) == -2) return -1;
+    }
+    return 0;
+}
+
 static int make_lin(cgx_model* m, lin_t* L, int which, int layer, float* tf, uint8_t* tq,
-                    float* ts) {
+                    float* ts, const cgx_wfile* f) {
     lin_shape(&m->c, which, &L->K, &L->N);
     L->sid = lin_sid(layer, which);
     size_t n = (size_t)L->K * L->N;
     L->tiled = (uint8_t*)cgx_malloc(n / 2);
     L->scales_t = (float*)cgx_malloc(n / m->c.group_size * 4);
     if (!L->tiled || !L->scales_t) return -1;
-    if (gen_flat(m, L->sid, L->K, L->N, tf, tq, ts)) return -1;
+    if (f ? file_flat(f, &m->c, which, layer, tf, tq, ts)
+          : gen_flat(m, L->sid, L->K, L->N, tf, tq, ts))
+        return -1;
     if (cgk_int4_repack_mfma(tq, ts, L->K, L->N, m->c.group_size, which == W_GU, L->tiled,
                              L->scales_t))
         return -1;
@@ -176,6 +318,7 @@ void cgx_model_free(cgx_model* m) {
         free_lin(&m->lm);
     }
     cgx_free(m->ones);
+    cgx_free(m->nw);
     cg_kv_cache_int4_free(m->kv);
     cgx_free(m->tok);
     cgx_free(m->x);
@@ -189,20 +332,16 @@ void cgx_model_free(cgx_model* m) {
     free(m);
 }
 
-cgx_model* cgx_model_new(const cgx_model_config* cfg, uint64_t seed, cgx_model* share_from) {
-    if (!cfg || check_config(cfg)) return NULL;
-    if (share_from && (share_from->c.d_model != cfg->d_model ||
-                       share_from->c.vocab != cfg->vocab ||
-                       share_from->c.group_size != cfg->group_size)) {
-        cgx_set_error("cgx_model_new: share_from has another d_model / vocab / group size");
-        return NULL;
-    }
+/* The model with seeded weights (f NULL) or the weights of file f. */
+static cgx_model* build(const cgx_model_config* cfg, uint64_t seed, cgx_model* share_from,
+                        const cgx_wfile* f) {
     if (cgx_ensure_init()) return NULL;
     cgx_model* m = (cgx_model*)calloc(1, sizeof(*m));
     if (!m) return NULL;
     m->c = *cfg;
     m->nb = cfg->max_batch > 0 ? cfg->max_batch : 1;
     m->seed = seed;
+    m->from_file = f != NULL;
     const cgx_model_config* c = &m->c;
     int d = c->d_model, V = c->vocab, Mx = c->max_tokens * m->nb;   /* rows per forward */
     size_t maxn = 0;
@@ -223,19 +362,47 @@ cgx_model* cgx_model_new(const cgx_model_config* cfg, uint64_t seed, cgx_model* 
         m->lm = share_from->lm;
     } else if (ok) {
         m->embed = (float*)cgx_malloc((size_t)V * d * 4);
-        ok = m->embed && !cgk_fill_normal(m->embed, (size_t)V * d, seed, 1u, c->init_std) &&
-             !make_lin(m, &m->lm, W_LM, 0, tf, tq, ts);
+        ok = m->embed != NULL;
+        if (ok && f) {
+            const int ei = cgx_wfile_find(f, "embed");
+            int ew = d;
+            float* h = (float*)malloc((size_t)V * d * 4);
+            ok = h && !cgx_wfile_read_f32(f, &ei, &ew, 1, V, h) &&
+                 !cgx_memcpy_h2d(m->embed, h, (size_t)V * d * 4);
+            free(h);
+        } else if (ok) {
+            ok = !cgk_fill_normal(m->embed, (size_t)V * d, seed, 1u, c->init_std);
+        }
+        ok = ok && !make_lin(m, &m->lm, W_LM, 0, tf, tq, ts, f);
     }
     for (int l = 0; ok && l < c->n_layers; l++)
-        for (int w = 0; ok && w < 4; w++) ok = !make_lin(m, &m->layers[l].w[w], w, l, tf, tq, ts);
+        for (int w = 0; ok && w < 4; w++)
+            ok = !make_lin(m, &m->layers[l].w[w], w, l, tf, tq, ts, f);
     if (ok) {
         int maxd = d > c->d_ff ? d : c->d_ff;
+        const int nn = 2 * c->n_layers + 1;
+        int any_norm = 0;
+        for (int i = 0; f && i < nn; i++) {
+            char nm[64];
+            norm_name(i, c->n_layers, nm);
+            any_norm |= cgx_wfile_find(f, nm) >= 0;
+        }
         m->ones = (float*)cgx_malloc((size_t)maxd * 4);
-        float* h = (float*)malloc((size_t)maxd * 4);
+        const size_t hn = any_norm ? (size_t)nn * d : (size_t)maxd;
+        float* h = (float*)malloc(hn * 4);
         ok = m->ones && h;
-        if (ok) {
-            for (int i = 0; i < maxd; i++) h[i] = 1.0f;
-            ok = !cgx_memcpy_h2d(m->ones, h, (size_t)maxd * 4);
+        for (size_t i = 0; ok && i < hn; i++) h[i] = 1.0f;
+        ok = ok && !cgx_memcpy_h2d(m->ones, h, (size_t)maxd * 4);
+        if (ok && any_norm) {
+            /* the file's norms; those it lacks stay 1 */
+            for (int i = 0; ok && i < nn; i++) {
+                char nm[64];
+                norm_name(i, c->n_layers, nm);
+                const int vi = cgx_wfile_find(f, nm);
+                ok = vi < 0 || !cgx_wfile_read_vector(f, vi, h + (size_t)i * d, d);
+            }
+            m->nw = ok ? (float*)cgx_malloc(hn * 4) : NULL;
+            ok = m->nw && !cgx_memcpy_h2d(m->nw, h, hn * 4);
         }
         free(h);
     }
@@ -268,6 +435,162 @@ cgx_model* cgx_model_new(const cgx_model_config* cfg, uint64_t seed, cgx_model* 
         return NULL;
     }
     return m;
+}
+
+static int check_share(const cgx_model_config* cfg, const cgx_model* share_from,
+                       const char* who) {
+    if (share_from && (share_from->c.d_model != cfg->d_model ||
+                       share_from->c.vocab != cfg->vocab ||
+                       share_from->c.group_size != cfg->group_size)) {
+        cgx_set_error("%s: share_from has another d_model / vocab / group size", who);
+        return -1;
+    }
+    return 0;
+}
+
+cgx_model* cgx_model_new(const cgx_model_config* cfg, uint64_t seed, cgx_model* share_from) {
+    if (!cfg || check_config(cfg) || check_share(cfg, share_from, "cgx_model_new")) return NULL;
+    return build(cfg, seed, share_from, NULL);
+}
+
+cgx_model* cgx_model_load(const cgx_model_config* cfg, const char* path, cgx_model* share_from) {
+    if (!cfg || !path) {
+        cgx_set_error("cgx_model_load: NULL argument");
+        return NULL;
+    }
+    if (check_config(cfg) || check_share(cfg, share_from, "cgx_model_load")) return NULL;
+    cgx_wfile* f = cgx_wfile_open(path, "cgx_model_load");
+    if (!f) return NULL;
+    cgx_model* m = NULL;
+    cgx_clear_error();
+    if (!check_file(f, cfg, share_from != NULL)) m = build(cfg, 0, share_from, f);
+    cgx_wfile_close(f);
+    return m;
+}
+
+/* Directory entry of a model file being written. */
+static void put_entry(cg_tensor_entry* e, int* k, uint64_t* off, const char* name, int ndim,
+                      int s0, int s1, int dtype, int gs, uint64_t bytes) {
+    cg_tensor_entry* x = &e[(*k)++];
+    memset(x, 0, sizeof(*x));
+    snprintf(x->name, sizeof(x->name), "%s", name);
+    x->ndim = ndim;
+    x->shape[0] = s0;
+    x->shape[1] = ndim > 1 ? s1 : 0;
+    x->shape[7] = gs;
+    x->dtype = dtype;
+    x->offset = *off;
+    x->size_bytes = bytes;
+    *off += bytes;
+}
+
+/* Matrix `which` (of `layer`) of the model in the reference's flat form:
+ * fp32 (the seeded values before quantization; tf) or nibbles and scales. */
+static int lin_host(cgx_model* m, const lin_t* L, int which, int fp32, float* tf, uint8_t* tq,
+                    float* ts, void* hdata, float* hscales) {
+    const size_t n = (size_t)L->K * L->N, gs = (size_t)m->c.group_size;
+    if (fp32)
+        return cgk_fill_normal(tf, n, m->seed, L->sid, m->c.init_std) ||
+               cgx_memcpy_d2h(hdata, tf, n * 4) ? -1 : 0;
+    return cgk_int4_unpack_mfma(L->tiled, L->scales_t, L->K, L->N, m->c.group_size,
+                                which == W_GU, tq, ts) ||
+           cgx_memcpy_d2h(hdata, tq, n / 2) || cgx_memcpy_d2h(hscales, ts, n / gs * 4) ? -1 : 0;
+}
+
+int cgx_model_save(cgx_model* m, const char* path, int fp32) {
+    if (!m || !path) {
+        cgx_set_error("cgx_model_save: NULL argument");
+        return -1;
+    }
+    if (fp32 && m->from_file) {
+        cgx_set_error("cgx_model_save: fp32 weights exist only for seeded models (this one was "
+                      "loaded from a file; save it as INT4)");
+        return -1;
+    }
+    const cgx_model_config* c = &m->c;
+    const int L = c->n_layers, d = c->d_model, V = c->vocab, gs = c->group_size;
+    const int nmat = 4 * L + (m->shared ? 0 : 1);
+    const int nent = (m->shared ? 0 : 1) + 2 * L + 1 + nmat * (fp32 ? 1 : 2);
+    cg_tensor_entry* e = (cg_tensor_entry*)calloc((size_t)nent, sizeof(*e));
+    if (!e) {
+        cgx_set_error("cgx_model_save: out of memory");
+        return -1;
+    }
+    int k = 0;
+    uint64_t off = sizeof(cg_model_header) + (uint64_t)nent * sizeof(cg_tensor_entry);
+    size_t maxn = 0;
+    if (!m->shared) put_entry(e, &k, &off, "embed", 2, V, d, 0, 0, (uint64_t)V * d * 4);
+    for (int i = 0; i <= 2 * L; i++) {
+        char nm[64];
+        norm_name(i, L, nm);
+        put_entry(e, &k, &off, nm, 1, d, 0, 0, 0, (uint64_t)d * 4);
+    }
+    for (int j = 0; j < nmat; j++) {
+        const int which = j < 4 * L ? j % 4 : W_LM, layer = j / 4;
+        int K, N;
+        char nm[64], sn[80];
+        lin_shape(c, which, &K, &N);
+        lin_name(which, layer, nm);
+        const uint64_t n = (uint64_t)K * N;
+        if (n > maxn) maxn = (size_t)n;
+        if (fp32) {
+            put_entry(e, &k, &off, nm, 2, K, N, 0, 0, n * 4);
+        } else {
+            put_entry(e, &k, &off, nm, 2, K, N, 2, gs, n / 2);
+            snprintf(sn, sizeof(sn), "%s.scales", nm);
+            put_entry(e, &k, &off, sn, 1, (int)(n / gs), 0, 0, 0, n / gs * 4);
+        }
+    }
+    FILE* f = fopen(path, "wb");
+    if (!f) {
+        free(e);
+        cgx_set_error("cgx_model_save: cannot open %s", path);
+        return -1;
+    }
+    cg_model_header h;
+    memset(&h, 0, sizeof(h));
+    h.magic = CG_MODEL_MAGIC;
+    h.version = 1;
+    h.num_tensors = (uint32_t)nent;
+    h.total_size = off;
+    int rc = fwrite(&h, sizeof(h), 1, f) == 1 &&
+                     fwrite(e, sizeof(*e), (size_t)nent, f) == (size_t)nent ? 0 : -1;
+    free(e);
+    /* data in directory order */
+    const size_t hbytes = maxn * (fp32 ? 4 : 1) > (size_t)V * d * 4 ? maxn * (fp32 ? 4 : 1)
+                                                                    : (size_t)V * d * 4;
+    void* hd = malloc(hbytes);
+    float* hs = (float*)malloc(maxn / (size_t)gs * 4 + 4);
+    float* tf = fp32 ? (float*)cgx_malloc(maxn * 4) : NULL;
+    uint8_t* tq = fp32 ? NULL : (uint8_t*)cgx_malloc(maxn / 2);
+    float* ts = fp32 ? NULL : (float*)cgx_malloc(maxn / (size_t)gs * 4);
+    if (!rc && (!hd || !hs || (fp32 ? !tf : (!tq || !ts)))) rc = -1;
+    if (!rc && !m->shared)
+        rc = cgx_memcpy_d2h(hd, m->embed, (size_t)V * d * 4) ||
+             fwrite(hd, 4, (size_t)V * d, f) != (size_t)V * d ? -1 : 0;
+    for (int i = 0; !rc && i <= 2 * L; i++)
+        rc = cgx_memcpy_d2h(hd, norm_w(m, i), (size_t)d * 4) ||
+             fwrite(hd, 4, (size_t)d, f) != (size_t)d ? -1 : 0;
+    for (int j = 0; !rc && j < nmat; j++) {
+        const int which = j < 4 * L ? j % 4 : W_LM;
+        const lin_t* Lw = which == W_LM ? &m->lm : &m->layers[j / 4].w[which];
+        const size_t n = (size_t)Lw->K * Lw->N;
+        rc = lin_host(m, Lw, which, fp32, tf, tq, ts, hd, hs);
+        if (!rc && fp32) rc = fwrite(hd, 4, n, f) == n ? 0 : -1;
+        if (!rc && !fp32)
+            rc = fwrite(hd, 1, n / 2, f) == n / 2 &&
+                         fwrite(hs, 4, n / (size_t)gs, f) == n / (size_t)gs ? 0 : -1;
+    }
+    free(hd);
+    free(hs);
+    cgx_free(tf);
+    cgx_free(tq);
+    cgx_free(ts);
+    if (fclose(f) || rc) {
+        if (!cgx_last_error()[0] || !rc) cgx_set_error("cgx_model_save: write to %s failed", path);
+        return -1;
+    }
+    return 0;
 }
 
 float* cgx_model_logits(cgx_model* m) { return m ? m->logits : NULL; }
@@ -414,8 +737,8 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
         float* ks = kv->k_scales + lg * slot;
         float* vs = kv->v_scales + lg * slot;
         stats_t sq = {xs_ok ? m->stats_x : NULL, d / 256, NULL, NULL, 0};
-        if (linear(&w[W_QKV], m->x, d, R, m->qkv, nq, PRO_RMSNORM, m->ones, eps, EPI_STORE,
-                   gs, &sq) ||
+        if (linear(&w[W_QKV], m->x, d, R, m->qkv, nq, PRO_RMSNORM, norm_w(m, 2 * l), eps,
+                   EPI_STORE, gs, &sq) ||
             cgk_rope_append_batch(m->qkv, nq, B, M, H, Hk, hd, kv->group_size, pos0,
                                   tr ? tr->rel : NULL, c->rope_theta, m->q, kc, vc, ks, vs, lb,
                                   lg))
@@ -434,15 +757,17 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
         }
         /* o -> (x) -> gate|up -> (g) -> down -> (x) -> next qkv / lm_head: each
          * reduction leaves the row statistics its consumer needs */
-        stats_t so = {NULL, 0, m->stats_x, m->ones, 0};
+        stats_t so = {NULL, 0, m->stats_x, norm_w(m, 2 * l + 1), 0};
         if (linear(&w[W_O], m->attn, hq, R, m->x, d, PRO_NONE, NULL, 0.0f, EPI_ACCUMULATE,
                    gs, &so))
             return -1;
         stats_t sg = {so.produced ? m->stats_x : NULL, d / 256, m->stats_g, NULL, 0};
-        if (linear(&w[W_GU], m->x, d, R, m->gu, ff, PRO_RMSNORM, m->ones, eps, EPI_SWIGLU, gs,
-                   &sg))
+        if (linear(&w[W_GU], m->x, d, R, m->gu, ff, PRO_RMSNORM, norm_w(m, 2 * l + 1), eps,
+                   EPI_SWIGLU, gs, &sg))
             return -1;
-        stats_t sd = {sg.produced ? m->stats_g : NULL, ff / 256, m->stats_x, m->ones, 0};
+        /* the next consumer of x: layer l + 1's attention norm, or the final one */
+        stats_t sd = {sg.produced ? m->stats_g : NULL, ff / 256, m->stats_x,
+                      norm_w(m, 2 * l + 2), 0};
         if (linear(&w[W_DOWN], m->gu, ff, R, m->x, d, PRO_NONE, NULL, 0.0f, EPI_ACCUMULATE, gs,
                    &sd))
             return -1;
@@ -453,20 +778,21 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
     if (n_logits == M && ldl == (size_t)M * c->vocab) {
         /* every row, sequences in order */
         stats_t sl = {xs_ok ? m->stats_x : NULL, d / 256, NULL, NULL, 0};
-        if (linear(&m->lm, m->x, d, R, out, c->vocab, PRO_RMSNORM, m->ones, eps, EPI_STORE, gs,
-                   &sl))
+        if (linear(&m->lm, m->x, d, R, out, c->vocab, PRO_RMSNORM, norm_w(m, 2 * c->n_layers),
+                   eps, EPI_STORE, gs, &sl))
             return -1;
     } else if (n_logits == 1) {
         /* the last row of each sequence: rows M-1, 2M-1, ... */
         if (cgk_gemv_mfma(m->x + (size_t)(M - 1) * d, M * d, B, d, c->vocab, gs, m->lm.tiled,
-                          m->lm.scales_t, out, (int)ldl, PRO_RMSNORM, m->ones, eps, EPI_STORE))
+                          m->lm.scales_t, out, (int)ldl, PRO_RMSNORM,
+                          norm_w(m, 2 * c->n_layers), eps, EPI_STORE))
             return -1;
     } else if (n_logits > 0) {
         for (int b = 0; b < B; b++)
             if (cgk_gemv_mfma(m->x + ((size_t)b * M + M - n_logits) * d, d, n_logits, d,
                               c->vocab, gs, m->lm.tiled, m->lm.scales_t,
                               out + (size_t)b * ldl, c->vocab, PRO_RMSNORM,
-                              m->ones, eps, EPI_STORE))
+                              norm_w(m, 2 * c->n_layers), eps, EPI_STORE))
                 return -1;
     }
     for (int b = 0; b < B; b++) m->len[b] = pos0[b] + M;
@@ -598,23 +924,12 @@ int cgx_model_export(cgx_model* m, int layer, int which, uint8_t* data, float* s
         cgx_set_error("cgx_model_export: invalid argument");
         return -1;
     }
-    int K, N;
-    lin_shape(&m->c, which, &K, &N);
-    size_t n = (size_t)K * N;
-    float* tf = (float*)cgx_malloc(n * 4);
+    const lin_t* L = which == W_LM ? &m->lm : &m->layers[layer].w[which];
+    const size_t n = (size_t)L->K * L->N;
     uint8_t* tq = (uint8_t*)cgx_malloc(n / 2 + 16);
     float* ts = (float*)cgx_malloc(n / m->c.group_size * 4 + 16);
-    int rc = (tf && tq && ts) ? 0 : -1;
-    uint32_t sid = which == W_LM ? m->lm.sid : m->layers[layer].w[which].sid;
-    /* a shared lm_head was generated with the owner's seed */
-    if (which == W_LM && m->shared) {
-        cgx_set_error("cgx_model_export: lm_head of a sharing model: export it from the owner");
-        rc = -1;
-    }
-    if (!rc) rc = gen_flat(m, sid, K, N, tf, tq, ts);
-    if (!rc) rc = cgx_memcpy_d2h(data, tq, n / 2);
-    if (!rc) rc = cgx_memcpy_d2h(scales, ts, n / m->c.group_size * 4);
-    cgx_free(tf);
+    int rc = (tq && ts) ? 0 : -1;
+    if (!rc) rc = lin_host(m, L, which, 0, NULL, tq, ts, data, scales);
     cgx_free(tq);
     cgx_free(ts);
     return rc ? -1 : 0;

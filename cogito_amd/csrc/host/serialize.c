@@ -118,24 +118,39 @@ void cg_load_model(const char* filename, cg_tensor*** out_tensors, char*** out_n
         fclose(f);
         return;
     }
-    const int count = (int)h.num_tensors;
+    /* Only fp32 entries (dtype 0) become tensors.  Entries of other dtypes
+     * (this library's INT4 entries, dtype 2) are skipped and counted in the
+     * last-error string; cgx_load_quantized reads them.  An fp32 entry must
+     * hold exactly the elements its shape names. */
+    int count = 0, skipped = 0;
+    for (uint32_t i = 0; i < h.num_tensors; i++) {
+        if (e[i].dtype == 0)
+            count++;
+        else
+            skipped++;
+    }
     cg_tensor** ts = (cg_tensor**)calloc((size_t)(count ? count : 1), sizeof(cg_tensor*));
     char** ns = (char**)calloc((size_t)(count ? count : 1), sizeof(char*));
-    int ok = ts && ns;
-    for (int i = 0; ok && i < count; i++) {
+    int ok = ts && ns, k = 0;
+    for (uint32_t i = 0; ok && i < h.num_tensors; i++) {
+        if (e[i].dtype != 0) continue;
         e[i].name[63] = 0;
-        ns[i] = copy_name(e[i].name);
-        ts[i] = (e[i].ndim >= 1 && e[i].ndim <= 8) ? cg_tensor_new(e[i].shape, e[i].ndim, false)
-                                                    : NULL;
-        const uint64_t cap = ts[i] ? (uint64_t)ts[i]->size * sizeof(float) : 0;
-        ok = ns[i] && ts[i] && e[i].size_bytes <= cap &&
-             fseek(f, (long)e[i].offset, SEEK_SET) == 0 &&
-             fread(ts[i]->data, 1, (size_t)e[i].size_bytes, f) == e[i].size_bytes;
+        uint64_t n = 1;
+        for (int d = 0; ok && e[i].ndim >= 1 && e[i].ndim <= 8 && d < e[i].ndim; d++) {
+            n *= e[i].shape[d] > 0 ? (uint64_t)e[i].shape[d] : 0;
+            ok = n < (1ull << 31);
+        }
+        ok = ok && e[i].ndim >= 1 && e[i].ndim <= 8 && n > 0 && e[i].size_bytes == n * 4;
+        ns[k] = ok ? copy_name(e[i].name) : NULL;
+        ts[k] = ok ? cg_tensor_new(e[i].shape, e[i].ndim, false) : NULL;
+        k++;
+        ok = ok && ns[k - 1] && ts[k - 1] && fseek(f, (long)e[i].offset, SEEK_SET) == 0 &&
+             fread(ts[k - 1]->data, 1, (size_t)e[i].size_bytes, f) == e[i].size_bytes;
     }
     free(e);
     fclose(f);
     if (!ok) {
-        for (int i = 0; ts && ns && i < count; i++) {
+        for (int i = 0; ts && ns && i < k; i++) {
             cg_tensor_free(ts[i]);
             free(ns[i]);
         }
@@ -144,6 +159,9 @@ void cg_load_model(const char* filename, cg_tensor*** out_tensors, char*** out_n
         cgx_set_error("cg_load_model: malformed entry in %s", filename);
         return;
     }
+    if (skipped)
+        cgx_set_error("cg_load_model: skipped %d entries of dtype other than fp32 in %s "
+                      "(INT4 entries: cgx_load_quantized)", skipped, filename);
     *out_tensors = ts;
     *out_names = ns;
     *out_count = count;
@@ -257,9 +275,13 @@ int cgx_load_quantized(const char* filename, cg_tensor_quant*** out_tensors, cha
             if (e[j].dtype == 0 && strncmp(e[j].name, want, 64) == 0) si = (int)j;
         const int nd = e[i].ndim, gs = e[i].shape[7];
         size_t n = 1;
-        for (int d = 0; nd >= 1 && nd <= 7 && d < nd; d++) n *= (size_t)(e[i].shape[d] > 0 ? e[i].shape[d] : 0);
+        int fits = 1;   /* the product stays below 2^31 at every step */
+        for (int d = 0; fits && nd >= 1 && nd <= 7 && d < nd; d++) {
+            n *= (size_t)(e[i].shape[d] > 0 ? e[i].shape[d] : 0);
+            fits = n < (1u << 31);
+        }
         const size_t ng = gs > 0 ? (n + (size_t)gs - 1) / (size_t)gs : 0;
-        ok = si >= 0 && nd >= 1 && nd <= 7 && gs > 0 && n > 0 && n < (1u << 31) &&
+        ok = fits && si >= 0 && nd >= 1 && nd <= 7 && gs > 0 && n > 0 && n < (1u << 31) &&
              e[i].size_bytes == (n + 1) / 2 && e[si].size_bytes == ng * sizeof(float);
         cg_tensor_quant* q = ok ? (cg_tensor_quant*)calloc(1, sizeof(*q)) : NULL;
         ok = ok && q;

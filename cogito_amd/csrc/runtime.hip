@@ -166,9 +166,24 @@ extern "C" int cgx_memcpy_d2d(void* dst, const void* src, size_t bytes) {
     return 0;
 }
 
+// True while the library stream is being captured into a graph.  Calls that
+// would record a memset node or allocate, free or synchronise then refuse:
+// memset nodes have given wrong results on replays after the first, and an
+// allocation or a synchronisation ends the capture with an error.
+static bool capturing(const char* who) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(g_rt.stream, &st) != hipSuccess || st == hipStreamCaptureStatusNone)
+        return false;
+    cgx_set_error("%s: the library stream is being captured into a graph (cgx_graph_begin); "
+                  "only calls that allocate, clear and synchronise nothing may be captured",
+                  who);
+    return true;
+}
+
 extern "C" int cgx_memset(void* dst, int value, size_t bytes) {
     if (cgx_ensure_init()) return -1;
     if (!bytes) return 0;
+    if (capturing("cgx_memset")) return -1;
     CGX_TRY(hipMemsetAsync(dst, value, bytes, g_rt.stream));
     return 0;
 }
@@ -295,6 +310,7 @@ extern "C" void* cgx_scratch(int slot, size_t bytes) {
         return nullptr;
     }
     if (bytes > g_rt.scratch_bytes[slot]) {
+        if (capturing("cgx_scratch (growth)")) return nullptr;
         size_t want = bytes < 4096 ? 4096 : bytes + bytes / 4;
         if (g_rt.scratch[slot]) {
             if (hipStreamSynchronize(g_rt.stream) != hipSuccess ||
@@ -321,6 +337,7 @@ extern "C" void* cgx_scratch(int slot, size_t bytes) {
 extern "C" unsigned int* cgx_counters(size_t count) {
     if (cgx_ensure_init()) return nullptr;
     if (count > g_rt.counter_count) {
+        if (capturing("cgx_counters (growth)")) return nullptr;
         size_t want = count < 4096 ? 4096 : count;
         if (g_rt.counters) {
             if (hipStreamSynchronize(g_rt.stream) != hipSuccess ||

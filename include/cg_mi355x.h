@@ -317,6 +317,31 @@ int cgx_model_fill_context(cgx_model* m, int len, uint64_t seed);
  * 4 lm_head.  data: K*N/2 bytes, scales: K*N/group_size floats (host). */
 int cgx_model_export(cgx_model* m, int layer, int which, uint8_t* data,
                      float* scales);
+/* Model files ("COG1", reference src/core/serialization.c:9-77; INT4
+ * entries as cgx_save_quantized writes them).  Entry names are the fields of
+ * the reference's transformer block (include/cg_transformer.h:41-50):
+ *   embed [V, d] (fp32), norm [d] (final RMSNorm), lm_head [d, V];
+ *   layers.<l>.norm1, layers.<l>.norm2 [d];
+ *   layers.<l>.attn_qkv_proj [d, (H + 2 Hk) hd] (columns q | k | v), or
+ *     its blocks attn_q_proj [d, H hd], attn_k_proj, attn_v_proj [d, Hk hd];
+ *   layers.<l>.attn_o_proj [H hd, d];
+ *   layers.<l>.mlp_gate_up [d, 2 ff] (columns gate | up), or its blocks
+ *     mlp_gate, mlp_up [d, ff];
+ *   layers.<l>.mlp_down [ff, d].
+ * Matrices are fp32 entries, quantized at load by cg_quantize_int4's rule
+ * (groups of cfg->group_size along the flat index of the whole matrix), or
+ * INT4 entries of that group size, copied (split blocks must then hold whole
+ * groups of their rows).  Missing norms are 1.  cgx_model_load builds the
+ * decoder of `cfg` from such a file (every entry is checked before anything
+ * is allocated; a missing or malformed one is named in cgx_last_error); with
+ * `share_from`, embed and lm_head come from that model and the file's are not
+ * read.  cgx_model_save writes every entry the model holds (embed and lm_head
+ * unless shared): INT4 entries (fp32 = 0), or, for a seeded model, the fp32
+ * values before quantization (fp32 = 1), which load back to the same INT4
+ * weights. */
+cgx_model* cgx_model_load(const cgx_model_config* cfg, const char* path,
+                          cgx_model* share_from);
+int cgx_model_save(cgx_model* m, const char* path, int fp32);
 /* The fill rule of the seeded weights, into device memory. */
 int cgx_fill_normal_dev(float* out, size_t n, uint64_t seed, uint32_t stream_id,
                         float stddev);

@@ -63,11 +63,24 @@ def fill(orc, n, seed, stream_id, std):
 
 
 class OracleModel:
-    def __init__(self, orc, cfg: Cfg, seed: int, share_from: "OracleModel | None" = None):
+    """weights: None (the library's seeded weights) or a dict of fp32 arrays
+    {"embed": [V, d], (layer, which): [K, N], W_LM: [d, V]} quantized here by
+    orc_quantize_int4; norms: None (all 1) or 2 n_layers + 1 vectors (each
+    layer's attention and MLP RMSNorm weights, then the final one)."""
+
+    def __init__(self, orc, cfg: Cfg, seed: int, share_from: "OracleModel | None" = None,
+                 weights=None, norms=None):
         self.orc, self.c, self.seed = orc, cfg, seed
+        self.weights = weights
+        d = cfg.d_model
+        self.norms = ([np.ones(d, np.float32)] * (2 * cfg.n_layers + 1) if norms is None
+                      else [np.ascontiguousarray(w, np.float32) for w in norms])
         if share_from is None:
-            self.embed = fill(orc, cfg.vocab * cfg.d_model, seed, 1, cfg.init_std).reshape(
-                cfg.vocab, cfg.d_model)
+            if weights is None:
+                self.embed = fill(orc, cfg.vocab * cfg.d_model, seed, 1, cfg.init_std).reshape(
+                    cfg.vocab, cfg.d_model)
+            else:
+                self.embed = np.ascontiguousarray(weights["embed"], np.float32)
             self.lm = self._lin(0, W_LM)
         else:
             self.embed, self.lm = share_from.embed, share_from.lm
@@ -82,7 +95,12 @@ class OracleModel:
 
     def _lin(self, layer, which):
         K, N = self.c.shape(which)
-        w = fill(self.orc, K * N, self.seed, sid(layer, which), self.c.init_std)
+        if self.weights is None:
+            w = fill(self.orc, K * N, self.seed, sid(layer, which), self.c.init_std)
+        else:
+            key = W_LM if which == W_LM else (layer, which)
+            w = np.ascontiguousarray(self.weights[key], np.float32).ravel()
+            assert w.size == K * N
         data = np.zeros(K * N // 2, np.uint8)
         scales = np.zeros(K * N // self.c.group_size, np.float32)
         self.orc.orc_quantize_int4(ptr(w), K * N, self.c.group_size, ptr(data), ptr(scales))
@@ -96,9 +114,11 @@ class OracleModel:
                                  self.c.group_size, ptr(y))
         return y
 
-    def rmsnorm(self, x):
+    def rmsnorm(self, x, i):
+        """RMSNorm with weights i: 2 l / 2 l + 1 (layer l's attention / MLP
+        norm), 2 n_layers (the final one)."""
         x = np.ascontiguousarray(x, np.float32)
-        w = np.ones(x.shape[1], np.float32)
+        w = self.norms[i]
         y = np.zeros_like(x)
         self.orc.orc_rmsnorm(ptr(x), ptr(w), ptr(y), x.shape[0], x.shape[1], self.c.norm_eps)
         return y
@@ -118,7 +138,7 @@ class OracleModel:
         scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
         for l in range(c.n_layers):
             wq, wo, wgu, wd = self.layers[l]
-            qkv = self.matmul(self.rmsnorm(x), wq)
+            qkv = self.matmul(self.rmsnorm(x, 2 * l), wq)
             q = np.ascontiguousarray(qkv[:, :H * hd]).reshape(M, H, hd)
             k = np.ascontiguousarray(qkv[:, H * hd:(H + Hk) * hd]).reshape(M, Hk, hd)
             v = np.ascontiguousarray(qkv[:, (H + Hk) * hd:]).reshape(M, Hk, hd)
@@ -155,7 +175,7 @@ class OracleModel:
                 orc.orc_flash_fwd(ptr(q), ptr(K), ptr(V), ptr(O), None, 1, M, n, H, Hk, hd,
                                   scale, 3, 0, ptr(mask))
             x = x + self.matmul(O.reshape(M, H * hd), wo)
-            gu = self.matmul(self.rmsnorm(x), wgu)
+            gu = self.matmul(self.rmsnorm(x, 2 * l + 1), wgu)
             g = np.ascontiguousarray(gu[:, :ff])
             u = np.ascontiguousarray(gu[:, ff:])
             a = np.zeros_like(g)
@@ -165,7 +185,7 @@ class OracleModel:
         n_logits = M if n_logits is None else n_logits
         if n_logits == 0:
             return None
-        return self.matmul(self.rmsnorm(x[M - n_logits:]), self.lm)
+        return self.matmul(self.rmsnorm(x[M - n_logits:], 2 * c.n_layers), self.lm)
 
     def truncate(self, n):
         assert 0 <= n <= self.len

@@ -77,3 +77,22 @@ def test_graph_replays_match_eager_verify(gpu, ratios):
         gpu.cgx_verify_lean_min_blocks(old)
         for a in dev + outs + refs:
             a.free()
+
+
+def test_capture_refuses_memset_and_allocation(gpu):
+    """During a capture, calls that would record a memset node or grow the
+    library's device memory refuse with an error naming the capture; the
+    capture (which then holds no node) ends and is freed, never replayed."""
+    print("capture guard: cgx_memset inside a capture", flush=True)
+    buf = DeviceArray(gpu, 4096)
+    assert gpu.cgx_graph_begin() == 0, last_error(gpu)
+    rc = gpu.cgx_memset(buf.ptr, 0, 4096)
+    err = last_error(gpu)
+    g = gpu.cgx_graph_end()
+    if g:
+        assert gpu.cgx_graph_free(g) == 0
+    assert rc == -1 and "captured" in err, err
+    gpu.cgx_clear_error()
+    # outside a capture the same call works
+    assert gpu.cgx_memset(buf.ptr, 0, 4096) == 0 and gpu.cgx_synchronize() == 0
+    buf.free()
