@@ -126,10 +126,20 @@ __device__ __forceinline__ float wave_max_nonneg(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Sum over the wave with the same DPP pattern (no LDS round trips: a chain of
+// ds_bpermute exchanges at the end of every wave cost ~1.5 us on the 7B
+// gate|up launch); fixed order, so the result is deterministic.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+#define CGX_DPP_ADD(CTRL, RMASK)                                                           \
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, RMASK, 0xF, true))
+    CGX_DPP_ADD(0x111, 0xF);      // row_shr:1
+    CGX_DPP_ADD(0x112, 0xF);      // row_shr:2
+    CGX_DPP_ADD(0x114, 0xF);      // row_shr:4
+    CGX_DPP_ADD(0x118, 0xF);      // row_shr:8   -> lane 15 of each row: row sum
+    CGX_DPP_ADD(0x142, 0xA);      // row_bcast:15 into rows 1 and 3
+    CGX_DPP_ADD(0x143, 0xC);      // row_bcast:31 into rows 2 and 3
+#undef CGX_DPP_ADD
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // MP: rows padded (1, 2, 4, 5, 8 or 16); T: column tiles per block; NG: scale groups
@@ -234,16 +244,24 @@ __global__ __launch_bounds__(64 * W, (NG == 2 && T == 2 && MP <= 5) ? 4 : 1) voi
                 ssq[m] = fmaf(t.y, t.y, ssq[m]);
                 ssq[m] = fmaf(t.z, t.z, ssq[m]);
                 ssq[m] = fmaf(t.w, t.w, ssq[m]);
-                t.x *= acur.nw.x; t.y *= acur.nw.y; t.z *= acur.nw.z; t.w *= acur.nw.w;
             }
             xv[m] = t;
             amax = fmaxf(amax, fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
         }
+        // the RMSNorm weight multiplies the scale of each k (x * nw * s =
+        // x * (nw * s)): 4 products per group and round instead of one per
+        // row and k, and no second copy of the rows (the 7B gate|up instance
+        // spilled with one: 20.6 -> 17.4 us)
         float smax = 0.0f;
 #pragma unroll
-        for (int q = 0; q < NG; q++)
+        for (int q = 0; q < NG; q++) {
+            if (PRO == kProRmsNorm) {
+                acur.s[q].x *= acur.nw.x; acur.s[q].y *= acur.nw.y;
+                acur.s[q].z *= acur.nw.z; acur.s[q].w *= acur.nw.w;
+            }
             smax = fmaxf(smax, fmaxf(fmaxf(fabsf(acur.s[q].x), fabsf(acur.s[q].y)),
                                      fmaxf(fabsf(acur.s[q].z), fabsf(acur.s[q].w))));
+        }
         // |x * s| <= amax * smax over the round; scale so that it is < 2^15
         float bound = wave_max_nonneg(amax) * wave_max_nonneg(smax);
         int E = 0;
