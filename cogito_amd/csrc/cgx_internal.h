@@ -133,9 +133,18 @@ int cgk_verify_chain_dist(const float* p, const float* q, const int* tokens, con
                           int batch, int gamma, int V, const int* bonus, float* accept_prob,
                           int* correction, int* out_tokens, int* n_accepted);
 /* One token from a device logits row with the verify filters (host/sampling.c):
- * draw at du (device), the same value uh on the host; z: V-float workspace. */
+ * draw at du (device), the same value uh on the host; z: V-float workspace.
+ * With top-k / top-p, dist (device, V floats, or NULL) also receives the
+ * row's filtered distribution from the same launches. */
 int cgx_sample_row_dev(const float* row, int V, float T, int top_k, float top_p,
-                       const float* du, float uh, float* z, int* out);
+                       const float* du, float uh, float* z, int* out, float* dist);
+/* cgx_verify_chain_batch_dev with the draft's filtered distributions
+ * already computed (qdist [batch][gamma][V], device, as cgx_sample_row_dev
+ * writes them; NULL: computed from draft_logits). */
+int cgx_verify_chain_dev_q(const float* target_logits, const float* draft_logits,
+                           const float* qdist, const int* draft_tokens, const float* u,
+                           int batch, int gamma, int V, float temperature, int top_k,
+                           float top_p, int* out_tokens, int* n_accepted, float* accept_prob);
 /* The global LCG of the drop-in samplers (host/speculative.c). */
 float cgx_lcg_draw(void);
 /* Typical sampling (decision D16) over rows of logits at T = 1: tokens drawn
@@ -157,6 +166,11 @@ int cgk_scale(const float* x, float* z, size_t n, float T);
  * (dist != NULL).  Uses scratch slot WS0. */
 int cgk_filter_rows(const float* z, int rows, int V, int top_k, float top_p, const float* u,
                     int* tokens, float* dist);
+/* The same with both outputs from one pass: distributions of every row
+ * (dist != NULL) and tokens of the rows r with (r + 1) % tok_every == 0
+ * (tokens[r / tok_every], drawn with u[(r / tok_every) * u_stride]). */
+int cgk_filter_rows_ex(const float* z, int rows, int V, int top_k, float top_p,
+                       const float* u, int u_stride, int* tokens, int tok_every, float* dist);
 
 /* ---------------------------------------- KV cache, attention, RoPE */
 /* attention mask kinds of cgk_attention */

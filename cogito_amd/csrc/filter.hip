@@ -220,13 +220,15 @@ __device__ int certified_prefix(const float* s, int V, float thr, EosShared& sh)
     return first >= kThreads ? V : min(V, (first + 1) * kCh);
 }
 
-// Cutoff, draw and (optionally) the filtered distribution of top-p over
-// one row: `probs` (index order) and `sorted` (descending).  ws holds 2V
-// ints per row.
+// Cutoff, draw and the filtered distribution of top-p over one row: `probs`
+// (index order) and `sorted` (descending).  Rows r with (r + 1) % tok_every
+// == 0 draw a token (tokens[r / tok_every], draw u[(r / tok_every) *
+// u_stride]; tok_every 0: none); every row writes its distribution when
+// dist is given.  ws holds 2V ints per row.
 __global__ __launch_bounds__(kThreads) void k_top_p_finish(
     const float* __restrict__ probs, const float* __restrict__ sorted, int V, float top_p,
-    const float* __restrict__ u, int* __restrict__ tokens, float* __restrict__ dist,
-    int* __restrict__ ws) {
+    const float* __restrict__ u, int u_stride, int* __restrict__ tokens, int tok_every,
+    float* __restrict__ dist, int* __restrict__ ws) {
     __shared__ EosShared sh;
     __shared__ int lds[kWaves];
     __shared__ int s_tok;
@@ -252,9 +254,10 @@ __global__ __launch_bounds__(kThreads) void k_top_p_finish(
     const int ci = gen_find_val(s, n, thr, -1, total, &C, sh);
     const int cutoff = ci < 0 ? V : ci + 1;
 
-    if (tokens) {
+    if (tokens && tok_every > 0 && (row + 1) % tok_every == 0) {
         // speculative.c:109-115: r = u * cumsum; first i < cutoff with r < cumsum
-        float r = __fmul_rn(u[row], C);
+        const int ti = row / tok_every;
+        float r = __fmul_rn(u[(size_t)ti * u_stride], C);
         int pos = gen_find(s, n, r, 0, sh);
         if (pos >= cutoff) pos = 0;
         float v = sr[pos];
@@ -263,29 +266,28 @@ __global__ __launch_bounds__(kThreads) void k_top_p_finish(
         if ((pos == 0 || sr[pos - 1] != v) && (pos == V - 1 || sr[pos + 1] != v)) {
             for (int j = threadIdx.x; j < V; j += kThreads)
                 if (pr[j] == v) s_tok = j;
-            __syncthreads();
-            if (threadIdx.x == 0) tokens[row] = s_tok;
-            return;
-        }
-        int rank = pos - count_above_sorted(sr, V, v);
-        int gtt;
-        int m = tie_members(pr, V, v, wi, wc, &gtt, lds);
-        if (threadIdx.x == 0) {
-            // walk the rotations backwards from the final slot `rank`
-            int p = rank, tok = wi[0];
-            for (int t = m; t >= 1; t--) {
-                p = (int)(((long long)p + tie_gap(wc, m, gtt, t)) % t);
-                if (p == t - 1) {
-                    tok = wi[t - 1];
-                    break;
+        } else {
+            int rank = pos - count_above_sorted(sr, V, v);
+            int gtt;
+            int m = tie_members(pr, V, v, wi, wc, &gtt, lds);
+            if (threadIdx.x == 0) {
+                // walk the rotations backwards from the final slot `rank`
+                int p = rank, tok = wi[0];
+                for (int t = m; t >= 1; t--) {
+                    p = (int)(((long long)p + tie_gap(wc, m, gtt, t)) % t);
+                    if (p == t - 1) {
+                        tok = wi[t - 1];
+                        break;
+                    }
                 }
+                s_tok = tok;
             }
-            s_tok = tok;
         }
         __syncthreads();
-        if (threadIdx.x == 0) tokens[row] = s_tok;
-        return;
+        if (threadIdx.x == 0) tokens[ti] = s_tok;
+        __syncthreads();
     }
+    if (!dist) return;
 
     // filtered distribution: kept elements are the first `cutoff` of the
     // sorted order, divided by the kept mass C
@@ -325,8 +327,8 @@ __device__ __forceinline__ unsigned long long topk_entry(uint32_t key, int j) {
 // filtered distribution (dense row).
 __global__ __launch_bounds__(kThreads) void k_top_k(const float* __restrict__ z, int V, int k,
                                                     int kpow2, float top_p,
-                                                    const float* __restrict__ u,
-                                                    int* __restrict__ tokens,
+                                                    const float* __restrict__ u, int u_stride,
+                                                    int* __restrict__ tokens, int tok_every,
                                                     float* __restrict__ dist,
                                                     int* __restrict__ lidx,
                                                     float* __restrict__ lp,
@@ -505,10 +507,16 @@ __global__ __launch_bounds__(kThreads) void k_top_k(const float* __restrict__ z,
 
     const bool use_p = top_p < 1.0f;
     RowSrc vs{vals};
-    if (tokens && !use_p) {
-        int j = sample_temperature_gen(vs, k, 1.0f, u[row], sh);
-        if (t == 0) tokens[row] = idx[j];
-        return;
+    // this row's token (rows r with (r + 1) % tok_every == 0): tokens[ti]
+    // with the draw u[ti * u_stride]
+    const bool want_tok = tokens && tok_every > 0 && (row + 1) % tok_every == 0;
+    const int ti = want_tok ? row / tok_every : 0;
+    const bool more = dist || lidx;      // a distribution or list after the token
+    if (want_tok && !use_p) {
+        int j = sample_temperature_gen(vs, k, 1.0f, u[(size_t)ti * u_stride], sh);
+        if (t == 0) tokens[ti] = idx[j];
+        if (!more) return;
+        __syncthreads();
     }
     // list probabilities: cg_sample_temperature's softmax at T = 1
     float m = gen_max(vs, k, sh);
@@ -522,11 +530,12 @@ __global__ __launch_bounds__(kThreads) void k_top_k(const float* __restrict__ z,
         int ci = gen_find_val(pr, k, float_below(top_p), -1, tot, &mass, sh);
         keep = ci < 0 ? k : ci + 1;
     }
-    if (tokens) {
-        int j = gen_find(pr, k, __fmul_rn(u[row], mass), 0, sh);
+    if (want_tok && use_p) {
+        int j = gen_find(pr, k, __fmul_rn(u[(size_t)ti * u_stride], mass), 0, sh);
         if (j >= keep) j = 0;
-        if (t == 0) tokens[row] = idx[j];
-        return;
+        if (t == 0) tokens[ti] = idx[j];
+        if (!more) return;
+        __syncthreads();
     }
     if (lidx) {
         // the list itself: entry j of the row is (idx[j], probability); past
@@ -539,6 +548,7 @@ __global__ __launch_bounds__(kThreads) void k_top_k(const float* __restrict__ z,
         }
         return;
     }
+    if (!dist) return;
     float* dr = dist + (size_t)row * V;
     for (int j = t; j < V; j += kThreads) dr[j] = 0.0f;
     __syncthreads();
@@ -661,7 +671,7 @@ __global__ __launch_bounds__(kTKThreads) void k_topk_collect(const float* __rest
 
 // Launch of k_top_k, through the multi-workgroup candidate pass for long rows.
 int launch_top_k(const float* z, int rows, int V, int k, int kpow2, float top_p, const float* u,
-                 int* tokens, float* dist, int* lidx, float* lp) {
+                 int u_stride, int* tokens, int tok_every, float* dist, int* lidx, float* lp) {
     const unsigned long long* gcand = nullptr;
     const int* gstate = nullptr;
     if (V >= 4 * kTK) {
@@ -683,7 +693,7 @@ int launch_top_k(const float* z, int rows, int V, int k, int kpow2, float top_p,
         gstate = state;
     }
     hipLaunchKernelGGL(k_top_k, dim3(rows), dim3(kThreads), 0, stream(), z, V, k, kpow2, top_p,
-                       u, tokens, dist, lidx, lp, gcand, gstate);
+                       u, u_stride, tokens, tok_every, dist, lidx, lp, gcand, gstate);
     return launch_check("k_top_k");
 }
 
@@ -853,7 +863,8 @@ extern "C" int cgk_topk_lists(const float* z, int rows, int V, int top_k, float 
     }
     int kpow2 = 64;
     while (kpow2 < top_k) kpow2 <<= 1;
-    return launch_top_k(z, rows, V, top_k, kpow2, top_p, nullptr, nullptr, nullptr, lidx, lp);
+    return launch_top_k(z, rows, V, top_k, kpow2, top_p, nullptr, 0, nullptr, 0, nullptr, lidx,
+                        lp);
 }
 
 extern "C" int cgk_scale(const float* x, float* z, size_t n, float T) {
@@ -863,11 +874,16 @@ extern "C" int cgk_scale(const float* x, float* z, size_t n, float T) {
     return launch_check("k_scale");
 }
 
-// Top-k / top-p over `rows` rows of z [rows][V]: tokens[row] drawn with
-// u[row] (tokens != NULL), or dense filtered distributions (dist != NULL).
-extern "C" int cgk_filter_rows(const float* z, int rows, int V, int top_k, float top_p,
-                               const float* u, int* tokens, float* dist) {
-    if (rows <= 0 || V <= 0 || rows > 65535 || (!tokens == !dist)) {
+// Top-k / top-p over `rows` rows of z [rows][V]: dense filtered
+// distributions of every row (dist != NULL) and tokens of the rows r with
+// (r + 1) % tok_every == 0 (tokens[r / tok_every], drawn with
+// u[(r / tok_every) * u_stride]), in the same launches.
+extern "C" int cgk_filter_rows_ex(const float* z, int rows, int V, int top_k, float top_p,
+                                  const float* u, int u_stride, int* tokens, int tok_every,
+                                  float* dist) {
+    if (!tokens) tok_every = 0;
+    if (rows <= 0 || V <= 0 || rows > 65535 || (!tok_every && !dist) || tok_every < 0 ||
+        (tok_every && !u)) {
         cgx_set_error("filter: invalid arguments");
         return -1;
     }
@@ -882,7 +898,8 @@ extern "C" int cgk_filter_rows(const float* z, int rows, int V, int top_k, float
         }
         int kpow2 = 64;
         while (kpow2 < top_k) kpow2 <<= 1;
-        return launch_top_k(z, rows, V, top_k, kpow2, top_p, u, tokens, dist, nullptr, nullptr);
+        return launch_top_k(z, rows, V, top_k, kpow2, top_p, u, u_stride, tokens, tok_every,
+                            dist, nullptr, nullptr);
     }
     // the descending sort of each row's probabilities (rowsort.hip, on the
     // values' bit patterns, monotone for non-negative floats) shares its
@@ -902,6 +919,17 @@ extern "C" int cgk_filter_rows(const float* z, int rows, int V, int top_k, float
                      wsb))
         return -1;
     hipLaunchKernelGGL(k_top_p_finish, dim3(rows), dim3(kThreads), 0, stream(), probs, sorted,
-                       V, top_p, u, tokens, dist, ws);
+                       V, top_p, u, u_stride, tokens, tok_every, dist, ws);
     return launch_check("k_top_p_finish");
+}
+
+// One token per row drawn with u[row] (tokens != NULL), or dense filtered
+// distributions (dist != NULL).
+extern "C" int cgk_filter_rows(const float* z, int rows, int V, int top_k, float top_p,
+                               const float* u, int* tokens, float* dist) {
+    if (!tokens == !dist) {
+        cgx_set_error("filter: invalid arguments");
+        return -1;
+    }
+    return cgk_filter_rows_ex(z, rows, V, top_k, top_p, u, 1, tokens, tokens ? 1 : 0, dist);
 }

@@ -217,7 +217,7 @@ static int draft_chain(const cg_speculative_decoder* dec, cgx_model* dm, const i
         float* row = dlog + (size_t)i * V;
         rc = cgx_model_forward(dm, dtok + i, 1, 1, row) ||
              cgx_sample_row_dev(row, V, dec->temperature, dec->top_k, dec->top_p, du + i,
-                                hu[i], dz, dtok + i + 1);
+                                hu[i], dz, dtok + i + 1, NULL);
     }
     free(hu);
     rc = rc || cgx_memcpy_d2h(tok_out, dtok + 1, (size_t)g * sizeof(int));

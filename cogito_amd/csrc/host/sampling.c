@@ -40,7 +40,7 @@ static int read_token(const int* dev) {
  * the same value on the host, for the single-block sampler.  z is a V-float
  * device workspace; out a device int. */
 int cgx_sample_row_dev(const float* row, int V, float T, int top_k, float top_p,
-                       const float* du, float uh, float* z, int* out) {
+                       const float* du, float uh, float* z, int* out, float* dist) {
     if (!uses_filters(V, top_k, top_p)) {
         /* one row of up to 32768 values: the single-workgroup exact sampler
          * (one launch, the row in registers) beats the chunk-parallel
@@ -51,7 +51,7 @@ int cgx_sample_row_dev(const float* row, int V, float T, int top_k, float top_p,
         return cgk_sample_temperature(row, V, T, uh, out);
     }
     if (cgk_scale(row, z, (size_t)V, T)) return -1;
-    return cgk_filter_rows(z, 1, V, top_k, top_p, du, out, NULL);
+    return cgk_filter_rows_ex(z, 1, V, top_k, top_p, du, 1, out, 1, dist);
 }
 
 /* ------------------------------------------------ explicit-uniform forms */
@@ -260,12 +260,14 @@ int cg_sample_top_p(float* logits, int vocab_size, float top_p) {
 
 /* D5 verify: filtered distributions of every row, then the same accept /
  * correction composition over them; the bonus token is the filtered
- * sampler's draw from target row gamma. */
-static int verify_filtered(const float* target, const float* draft, const int* tokens,
-                           const float* u, int batch, int gamma, int V, float T, int top_k,
-                           float top_p, float* ap, int* corr, int* bonus, int* out_tokens,
-                           int* n_accepted) {
-    size_t rt = (size_t)batch * (gamma + 1), rd = (size_t)batch * gamma;
+ * sampler's draw from target row gamma, taken in the same launches as the
+ * target rows' distributions.  qdist: the draft rows' distributions when the
+ * caller has them (the loop's draft draws write them), else NULL. */
+static int verify_filtered(const float* target, const float* draft, const float* qdist,
+                           const int* tokens, const float* u, int batch, int gamma, int V,
+                           float T, int top_k, float top_p, float* ap, int* corr, int* bonus,
+                           int* out_tokens, int* n_accepted) {
+    size_t rt = (size_t)batch * (gamma + 1), rd = qdist ? 0 : (size_t)batch * gamma;
     float* z = (float*)cgx_scratch(CGX_SLOT_WS3, (rt + rd) * V * 4);
     float* dist = (float*)cgx_scratch(CGX_SLOT_WS2, (rt + rd) * V * 4);
     if (!z || !dist) return -1;
@@ -273,18 +275,15 @@ static int verify_filtered(const float* target, const float* draft, const int* t
     float* zd = z + rt * V;
     float* p = dist;
     float* q = dist + rt * V;
-    if (cgk_scale(target, zt, rt * V, T) || cgk_scale(draft, zd, rd * V, T) ||
-        cgk_filter_rows(zt, (int)rt, V, top_k, top_p, NULL, NULL, p) ||
-        cgk_filter_rows(zd, (int)rd, V, top_k, top_p, NULL, NULL, q))
+    if (cgk_scale(target, zt, rt * V, T) ||
+        cgk_filter_rows_ex(zt, (int)rt, V, top_k, top_p, u + gamma, gamma + 1, bonus, gamma + 1,
+                           p))
         return -1;
-    for (int c = 0; c < batch; c++) {
-        const float* zb = zt + ((size_t)c * (gamma + 1) + gamma) * V;
-        if (cgk_filter_rows(zb, 1, V, top_k, top_p, u + (size_t)c * (gamma + 1) + gamma,
-                            bonus + c, NULL))
-            return -1;
-    }
-    return cgk_verify_chain_dist(p, q, tokens, u, batch, gamma, V, bonus, ap, corr, out_tokens,
-                                 n_accepted);
+    if (!qdist && (cgk_scale(draft, zd, rd * V, T) ||
+                   cgk_filter_rows(zd, (int)rd, V, top_k, top_p, NULL, NULL, q)))
+        return -1;
+    return cgk_verify_chain_dist(p, qdist ? qdist : q, tokens, u, batch, gamma, V, bonus, ap,
+                                 corr, out_tokens, n_accepted);
 }
 
 
@@ -293,6 +292,15 @@ int cgx_verify_chain_batch_dev(const float* target_logits, const float* draft_lo
                                int gamma, int V, float temperature, int top_k,
                                float top_p, int* out_tokens, int* n_accepted,
                                float* accept_prob) {
+    return cgx_verify_chain_dev_q(target_logits, draft_logits, NULL, draft_tokens, u, batch,
+                                  gamma, V, temperature, top_k, top_p, out_tokens, n_accepted,
+                                  accept_prob);
+}
+
+int cgx_verify_chain_dev_q(const float* target_logits, const float* draft_logits,
+                           const float* qdist, const int* draft_tokens, const float* u,
+                           int batch, int gamma, int V, float temperature, int top_k,
+                           float top_p, int* out_tokens, int* n_accepted, float* accept_prob) {
     if (!target_logits || !draft_logits || !draft_tokens || !u || !out_tokens ||
         !n_accepted || batch <= 0 || gamma <= 0 || V <= 0) {
         cgx_set_error("cgx_verify_chain_batch_dev: invalid argument");
@@ -306,9 +314,9 @@ int cgx_verify_chain_batch_dev(const float* target_logits, const float* draft_lo
     int* corr = (int*)(ws + na * 4);
     int* bonus = (int*)(ws + na * 8);
     if (uses_filters(V, top_k, top_p))
-        return verify_filtered(target_logits, draft_logits, draft_tokens, u, batch, gamma, V,
-                               temperature, top_k, top_p, ap, corr, bonus, out_tokens,
-                               n_accepted);
+        return verify_filtered(target_logits, draft_logits, qdist, draft_tokens, u, batch,
+                               gamma, V, temperature, top_k, top_p, ap, corr, bonus,
+                               out_tokens, n_accepted);
     if (cgk_verify_pipe_supported(batch, gamma, V, temperature))
         return cgk_verify_pipe(target_logits, draft_logits, draft_tokens, u, batch, gamma, V,
                                temperature, accept_prob, out_tokens, n_accepted);

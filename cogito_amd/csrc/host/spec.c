@@ -32,6 +32,7 @@ struct cgx_spec {
     float* d_target_logits;
     float* d_u;           /* [2 gamma + 1]: draft draws, then verify draws */
     float* d_z;           /* [V] scaled draft row for the filtered samplers */
+    float* d_draft_dist;  /* [gamma][V] filtered draft distributions (with filters) */
     int* d_out;           /* [gamma + 1] emitted tokens, then n accepted */
     int last;
     int have_last;
@@ -46,6 +47,7 @@ void cgx_spec_free(cgx_spec* s) {
     cgx_free(s->d_draft_logits);
     cgx_free(s->d_target_logits);
     cgx_free(s->d_z);
+    cgx_free(s->d_draft_dist);
     cgx_free(s->d_out);
     free(s);
 }
@@ -83,7 +85,12 @@ cgx_spec* cgx_spec_new(cgx_model* draft, cgx_model* target, int gamma, float tem
     s->d_target_logits = (float*)cgx_malloc((size_t)(gamma + 1) * V * 4);
     s->d_z = (float*)cgx_malloc(V * 4);
     s->d_out = (int*)cgx_malloc((size_t)(gamma + 2) * 4);
-    if (!s->d_in || !s->d_draft_logits || !s->d_target_logits || !s->d_z || !s->d_out) {
+    /* with filters, the draft draws keep their filtered distributions for
+     * the verify (the same launches compute both) */
+    const int filtered = (top_k > 0 && top_k < s->V) || top_p < 1.0f;
+    s->d_draft_dist = filtered ? (float*)cgx_malloc((size_t)gamma * V * 4) : NULL;
+    if (!s->d_in || !s->d_draft_logits || !s->d_target_logits || !s->d_z || !s->d_out ||
+        (filtered && !s->d_draft_dist)) {
         cgx_spec_free(s);
         return NULL;
     }
@@ -140,7 +147,8 @@ int cgx_spec_prefill(cgx_spec* s, const int* prompt, int n) {
 /* Draft token i + 1 from the draft logits row i, written to d_tokens[i + 1]. */
 static int draft_sample(cgx_spec* s, int i, float u_host) {
     return cgx_sample_row_dev(s->d_draft_logits + (size_t)i * s->V, s->V, s->T, s->top_k,
-                              s->top_p, s->d_u + i, u_host, s->d_z, s->d_tokens + i + 1);
+                              s->top_p, s->d_u + i, u_host, s->d_z, s->d_tokens + i + 1,
+                              s->d_draft_dist ? s->d_draft_dist + (size_t)i * s->V : NULL);
 }
 
 int cgx_spec_step(cgx_spec* s, const float* u_draft, const float* u_verify, int* out_tokens) {
@@ -188,9 +196,9 @@ int cgx_spec_step(cgx_spec* s, const float* u_draft, const float* u_verify, int*
     }
     /* target: gamma + 1 rows in one forward, then the verify kernels */
     if (cgx_model_forward(s->target, s->d_tokens, g + 1, g + 1, s->d_target_logits) ||
-        cgx_verify_chain_batch_dev(s->d_target_logits, s->d_draft_logits, s->d_tokens + 1,
-                                   s->d_u + g, 1, g, s->V, s->T, s->top_k, s->top_p, s->d_out,
-                                   s->d_out + g + 1, NULL))
+        cgx_verify_chain_dev_q(s->d_target_logits, s->d_draft_logits, s->d_draft_dist,
+                               s->d_tokens + 1, s->d_u + g, 1, g, s->V, s->T, s->top_k,
+                               s->top_p, s->d_out, s->d_out + g + 1, NULL))
         return -1;
     int hout[64 + 2];
     int* ho = (g + 2) <= 66 ? hout : (int*)malloc((size_t)(g + 2) * sizeof(int));

@@ -340,3 +340,51 @@ def test_eagle_compute_branching(gpu, oracle, rng):
     gpu.cg_tensor_free(t)
     gpu.cg_eagle_draft_free(e)
     gpu.cgx_model_free(dm)
+
+
+@pytest.mark.parametrize("T,top_k,top_p", [(0.8, 0, 0.9), (0.7, 50, 0.9)])
+def test_spec_loop_equals_driver_steps(gpu, oracle, rng, T, top_k, top_p):
+    """The device loop (cgx_spec_step: each filtered draft draw also writes
+    the draft row's filtered distribution, which the verify then uses) and
+    the driver (cg_speculative_step: the verify filters the draft logits
+    again) on identical model pairs with the same draws emit the same tokens
+    at every step.  The driver takes its draws from the global LCG (gamma
+    for the drafts, then the verify's, of which it keeps n + 2 on a reject at
+    n and gamma + 1 when all are accepted); the loop gets the mirror's."""
+    g, seed, steps = 4, 123, 8
+    loop_t, loop_d = new_model(gpu, TARGET, 51), new_model(gpu, DRAFT, 52)
+    drv_t, drv_d = new_model(gpu, TARGET, 51), new_model(gpu, DRAFT, 52)
+    prompt = [int(x) for x in rng.integers(0, TARGET.vocab, 6)]
+    s = gpu.cgx_spec_new(loop_d, loop_t, g, T, top_k, top_p)
+    assert s, last_error(gpu)
+    pr = np.asarray(prompt, np.int32)
+    assert gpu.cgx_spec_prefill(s, pr.ctypes.data, len(pr)) == 0, last_error(gpu)
+    dec = gpu.cg_speculative_decoder_new(drv_d, drv_t, g)
+    dec.contents.temperature, dec.contents.top_k, dec.contents.top_p = T, top_k, top_p
+    tree = gpu.cg_token_tree_new(g)
+    gpu.cgx_lcg_seed(seed)
+    lcg = LCG(seed)
+    seq = list(prompt)
+    for step in range(steps):
+        ids = ids_tensor(gpu, seq)
+        n = gpu.cg_speculative_step(dec, ids, tree)
+        gpu.cg_tensor_free(ids)
+        assert n >= 0, last_error(gpu)
+        drv = [tree.contents.tokens[i] for i in range(n)] + [gpu.cgx_last_verify_token()]
+        ud = np.array([lcg.draw(oracle) for _ in range(g)], np.float32)
+        state_v = lcg.state.value
+        uv = np.array([lcg.draw(oracle) for _ in range(g + 1)], np.float32)
+        out = np.zeros(g + 1, np.int32)
+        m = gpu.cgx_spec_step(s, ud.ctypes.data, uv.ctypes.data, out.ctypes.data)
+        assert m == n and out[:n + 1].tolist() == drv, (step, m, out.tolist(), n, drv)
+        # the draws the sequential reference consumed
+        lcg = LCG(state_v)
+        for _ in range(n + 2 if n < g else g + 1):
+            lcg.draw(oracle)
+        assert gpu.cgx_lcg_state() == lcg.state.value
+        seq += drv
+    gpu.cg_token_tree_free(tree)
+    gpu.cg_speculative_decoder_free(dec)
+    gpu.cgx_spec_free(s)
+    for m_ in (loop_t, loop_d, drv_t, drv_d):
+        gpu.cgx_model_free(m_)
