@@ -378,6 +378,66 @@ def bench_attention(lib, ctx, Nq, H, Hk, D, kv_gs, steps, warmup, seed=9):
             "frac": round(gbs / HBM_PEAK_GBS, 4), "layers_rotated": layers}
 
 
+def bench_attention_step(lib, ctx, Nq, H, Hk, D, steps, warmup, seed=9, theta=10000.0):
+    """The decoder's attention step of one layer per launch at the 7B shape:
+    RoPE of the new q / k rows, their INT4 append at positions ctx .. ctx+Nq-1,
+    attention over the whole cache and the split combine
+    (cgx_attention_rope_append_dev); launches rotate over layers as above."""
+    from cogito_amd.capi import DeviceArray, last_error
+
+    Nk = ctx + Nq
+    per_layer = Nk * Hk * D // 2 * 2 + Nk * Hk * 4 * 2
+    layers = _rotations(per_layer)
+    cache = lib.cg_kv_cache_int4_new(layers, Nk, Hk, D, D)
+    if not cache:
+        raise RuntimeError(last_error(lib))
+    n = ctx * Hk * D
+    dk, dv = DeviceArray(lib, n * 4), DeviceArray(lib, n * 4)
+    if (lib.cgx_fill_normal_dev(dk.ptr, n, seed, 1, 1.0) or
+            lib.cgx_fill_normal_dev(dv.ptr, n, seed, 2, 1.0)):
+        raise RuntimeError(last_error(lib))
+    for l in range(layers):
+        if lib.cgx_kv_cache_int4_write(cache, l, 0, dk.ptr, dv.ptr, ctx):
+            raise RuntimeError(last_error(lib))
+    dk.free()
+    dv.free()
+    ldq = (H + 2 * Hk) * D
+    dqkv = DeviceArray(lib, Nq * ldq * 4)
+    lib.cgx_fill_normal_dev(dqkv.ptr, Nq * ldq, seed, 3, 1.0)
+    dcs = DeviceArray(lib, Nq * D * 4)
+    do = DeviceArray(lib, Nq * H * D * 4)
+    if lib.cgx_rope_table_dev(Nq, D, ctx, theta, dcs.ptr):
+        raise RuntimeError(last_error(lib))
+
+    def call(i):
+        return lib.cgx_attention_rope_append_dev(dqkv.ptr, ldq, dcs.ptr, Nq, H, cache,
+                                                 i % layers, ctx, do.ptr)
+    for i in range(warmup):
+        if call(i):
+            raise RuntimeError(last_error(lib))
+    if lib.cgx_synchronize():
+        raise RuntimeError(last_error(lib))
+    lib.cgx_event_record(0)
+    for i in range(steps):
+        call(i)
+    lib.cgx_event_record(1)
+    if lib.cgx_synchronize():
+        raise RuntimeError(last_error(lib))
+    us = lib.cgx_event_elapsed_ms(0, 1) / steps * 1e3
+    # cache read, new rows and Q in, O out, new K/V rows written
+    nbytes = per_layer + Nq * ldq * 4 + Nq * H * D * 4
+    gbs = nbytes / (us * 1e-6) / 1e9
+    lib.cg_kv_cache_int4_free(cache)
+    for a in (dqkv, dcs, do):
+        a.free()
+    log(f"[bench] attention step (RoPE + append + attention) ctx={ctx} Nq={Nq}: {us:.2f} "
+        f"us/layer, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%})")
+    return {"ctx": ctx, "Nq": Nq, "H": H, "Hk": Hk, "D": D, "kv_group": D,
+            "us_per_layer": round(us, 3), "bytes": nbytes, "GB/s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "layers_rotated": layers,
+            "fused": "RoPE + INT4 append + attention + split combine"}
+
+
 def _model_cfg(n_layers, d, H, Hk, hd, ff, V, max_seq, max_tokens, kv_gs):
     from cogito_amd.capi import CgxModelConfig
     return CgxModelConfig(n_layers=n_layers, d_model=d, n_heads=H, n_kv_heads=Hk,
@@ -919,6 +979,8 @@ def main() -> int:
     if "attn" in legs:
         extra["attention_7b"] = bench_attention(lib, 4096, 5, 32, 8, 128, 128, args.steps,
                                                 args.warmup)
+        extra["attention_7b_step"] = bench_attention_step(lib, 4096, 5, 32, 8, 128, args.steps,
+                                                          args.warmup)
     if "e2e" in legs or "c3" in legs:
         c3t, c3d = (12, 768, 12, 12, 64, 3072, 32000), (2, 768, 12, 12, 64, 3072, 32000)
         extra["e2e_tiny_c3"] = bench_e2e(lib, "C3 tiny", c3t, c3d, False, 1024, 4, 0.8, 0,

@@ -37,6 +37,7 @@
 #include <cfloat>
 #include <cmath>
 #include <cstdint>
+#include <cstring>
 
 #include "cgx_internal.h"
 
@@ -77,7 +78,7 @@ struct DecArgs {
     const uint8_t* vc;
     const float* ks;             // [pos][Hk] (one group per head row)
     const float* vs;
-    int Nq, Nk, H, Hk;
+    int Nq, Nk, H, Hk, D_;
     float scale;
     int mask_kind;
     int splits, keys_per_split;
@@ -93,6 +94,19 @@ struct DecArgs {
     int B, chunks;
     size_t seq_kbytes, seq_groups;
     int nk[kMaxBatch];
+    // fused RoPE and cache append (k_attn_dec<..., true>): the Q rows come
+    // from the raw projections and are rotated here; the Nq new keys of each
+    // sequence (positions nk - Nq .. nk - 1) are rotated, quantised and
+    // written to the cache by split nsplit_old, which attends over them from
+    // LDS; splits below it cover the cached keys [0, nk - Nq)
+    const float* qkv;            // [B][Nq][ldq]: q heads, k heads, v heads
+    int ldq;
+    const float2* rope;          // [B][Nq][D/2] (cos, sin) of each row's rotary position
+    uint8_t* kcw;                // the caches (kc, vc, ks, vs), written
+    uint8_t* vcw;
+    float* ksw;
+    float* vsw;
+    int nsplit_old;
 };
 
 __device__ __forceinline__ int head_begin(int hk, int H, int Hk) { return (hk * H + Hk - 1) / Hk; }
@@ -165,7 +179,26 @@ __device__ __forceinline__ void lds_barrier() {
 // lane of group g holds)
 __device__ __forceinline__ int key_of_pos(int g, int p) { return p < 4 ? 4 * g + p : 16 + 4 * g + p - 4; }
 
-template <int D, int RT>
+// Rotate-half RoPE with k_rope_append's operations (decoder.hip): value d of
+// a head row from its own value and its partner's (d +- D/2), (c, s) of i =
+// d mod D/2.  Each product rounds on its own, as in the reference's CPU code:
+// contraction is off here (this file is otherwise built with it, and the
+// _rn intrinsics lower to plain operations the backend would fuse).
+__device__ __forceinline__ float rope_val(float own, float partner, float2 cs, bool second) {
+#pragma clang fp contract(off)
+    const float a = second ? partner * cs.y : own * cs.x;
+    const float b = second ? own * cs.x : partner * cs.y;
+    return second ? a + b : a - b;
+}
+
+// own c + partner s', each product rounded on its own (s' = -s gives the
+// first half's own c - partner s, s' = s the second half's partner s + own c)
+__device__ __forceinline__ float rope_sum(float own, float partner, float c, float s) {
+#pragma clang fp contract(off)
+    return own * c + partner * s;
+}
+
+template <int D, int RT, bool FUSED>
 __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_dec(DecArgs a) {
     constexpr int NC = D / 32;          // QK MFMAs per 16 keys (32 head-dim values each)
     constexpr int DPL = D / 4;          // head-dim values per lane group
@@ -179,6 +212,22 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_dec(DecArgs a) {
     float (*s_o)[ROWS][D + 4] = (float (*)[ROWS][D + 4])s_raw;
     __shared__ float s_m[kWaves][ROWS], s_l[kWaves][ROWS];
     __shared__ float s_w[kWaves][ROWS], s_M[ROWS], s_L[ROWS];
+    // fused launches keep two more things in s_raw, past the Q operands
+    // (s_o overwrites all of it only after the last tile): the rotary table
+    // of the block's rows (read while the Q operands are built) and the new
+    // keys in the cache's layout (up to 64 keys, read by the tiles)
+    constexpr int kTblBytes = ROWS * (D / 2) * (int)sizeof(float2);
+    constexpr int kNewKeys = 64;
+    static_assert(!FUSED || kQBytes + kTblBytes + kNewKeys * (D + 8) <= (int)sizeof(s_raw),
+                  "fused staging fits the block's LDS");
+    // the table transposed: tbl[j][2 t + h] = (cos, sin) of frequency
+    // DPL h + j of table row t, so that the lanes reading one j (every query
+    // row, both halves) read neighbouring words, with no bank conflict
+    float2 (*tbl)[2 * ROWS] = (float2 (*)[2 * ROWS])(s_raw + kQBytes);
+    uint8_t (*st_k)[D / 2] = (uint8_t (*)[D / 2])(s_raw + kQBytes + kTblBytes);
+    uint8_t (*st_v)[D / 2] = st_k + kNewKeys;
+    float* st_ks = (float*)(st_v + kNewKeys);
+    float* st_vs = st_ks + kNewKeys;
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const NibConst nk = nib_consts();
@@ -199,8 +248,11 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_dec(DecArgs a) {
     const int Hk = a.Hk;
     const size_t krow = (size_t)Hk * (D / 2);       // bytes between positions
 
-    const int k_begin = split * a.keys_per_split;
-    const int k_end = min(Nk, k_begin + a.keys_per_split);
+    // fused: split nsplit_old is the new keys, the others the cached ones
+    const bool new_split = FUSED && split == a.nsplit_old;
+    const int nk_old = FUSED ? Nk - a.Nq : Nk;
+    const int k_begin = new_split ? nk_old : split * a.keys_per_split;
+    const int k_end = new_split ? Nk : min(nk_old, k_begin + a.keys_per_split);
     const int ntiles = (k_end - k_begin + kTile - 1) / kTile;
     // first key under the mask's bits: the new positions (chain), or the
     // tree window (the tree's nodes, of this call and of earlier calls)
@@ -239,7 +291,9 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_dec(DecArgs a) {
     const float* __restrict__ ksb = kscale + hk;
     const float* __restrict__ vsb = vscale + hk;
     const uint32_t krow32 = (uint32_t)krow;
-    const int klast = k_end - 1;
+    // (a split past a short sequence's cached keys reads position 0: valid
+    // memory, never used)
+    const int klast = max(k_end - 1, 0);
     auto load_tile = [&](int kt, TileData& t) {
 #pragma unroll
         for (int kh = 0; kh < 2; kh++) {
@@ -268,6 +322,26 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_dec(DecArgs a) {
             const uint32_t key = (uint32_t)min(kl + (p < 4 ? p : 12 + p), klast);
             t.vw[p] = *(const uint32_t*)(vbase + (key * krow32 + (uint32_t)(4 * nb)));
             t.sv[p] = vsb[key * (uint32_t)Hk];
+        }
+    };
+    // the same tile from the LDS staging of the new keys (key kt + j is row
+    // kt + j - k_begin; rows past the last are clamped and masked)
+    auto load_tile_lds = [&](int kt, TileData& t) {
+        const int rlast = k_end - 1 - k_begin;
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++) {
+            const int r = min(kt - k_begin + 16 * kh + n, rlast);
+            const uint8_t* p = &st_k[r][(D / 8) * g];
+#pragma unroll
+            for (int c = 0; c < NC; c++) t.kw[kh][c] = *(const uint32_t*)(p + 4 * c);
+        }
+        const int kl = kt - k_begin + 4 * g;
+#pragma unroll
+        for (int p = 0; p < 8; p++) {
+            const int r = min(kl + (p < 4 ? p : 12 + p), rlast);
+            t.sk[p] = st_ks[r];
+            t.vw[p] = *(const uint32_t*)&st_v[r][4 * nb];
+            t.sv[p] = st_vs[r];
         }
     };
 
@@ -299,17 +373,162 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_dec(DecArgs a) {
     for (int rt = 0; rt < RT; rt++) {
         const int r = row0 + 16 * rt + n;
         const int h = h0 + (rok[rt] ? r / a.Nq : 0), q = rq[rt];
-        const float* qp = Qs + ((size_t)q * a.H + h) * D + DPL * g;
+        if (FUSED) {
+            // the raw q row (rotated below, once the rotary table is in LDS)
+            const float* qp = a.qkv + ((size_t)sq * a.Nq + q) * a.ldq + (size_t)h * D + DPL * g;
 #pragma unroll
-        for (int i = 0; i < DPL; i += 4) {
-            const float4 t = *(const float4*)(qp + i);
-            qv[rt][i] = t.x; qv[rt][i + 1] = t.y; qv[rt][i + 2] = t.z; qv[rt][i + 3] = t.w;
+            for (int i = 0; i < DPL; i += 4) {
+                const float4 t = *(const float4*)(qp + i);
+                qv[rt][i] = t.x; qv[rt][i + 1] = t.y; qv[rt][i + 2] = t.z; qv[rt][i + 3] = t.w;
+            }
+        } else {
+            const float* qp = Qs + ((size_t)q * a.H + h) * D + DPL * g;
+#pragma unroll
+            for (int i = 0; i < DPL; i += 4) {
+                const float4 t = *(const float4*)(qp + i);
+                qv[rt][i] = t.x; qv[rt][i + 1] = t.y; qv[rt][i + 2] = t.z; qv[rt][i + 3] = t.w;
+            }
         }
     }
     // unconditional, like the prefetch below: a wave without a tile reads the
     // split's last key (k_end >= 1 whenever the block runs)
     TileData td;
-    load_tile(k_begin + wave * kTile, td);
+    // fused: the rotary table rows of the block's queries, loaded before the
+    // first tile (loads complete in issue order, so the rotation below waits
+    // for Q and the table only).  With Nq <= ROWS the table holds the Nq rows
+    // of the sequence (indexed by q), else the block's rows (by r - row0).
+    constexpr int kTblQuads = D / 4;                    // float4 = two (cos, sin)
+    constexpr int kTblLoads = (ROWS * kTblQuads + 64 * kWaves - 1) / (64 * kWaves);
+    const bool tbl_by_q = a.Nq <= ROWS;
+    const int tbl_rows = tbl_by_q ? a.Nq : ROWS;
+    float4 tv[FUSED ? kTblLoads : 1];
+    if (FUSED) {
+#pragma unroll
+        for (int j = 0; j < kTblLoads; j++) {
+            const int e = min((int)threadIdx.x + j * 64 * kWaves, tbl_rows * kTblQuads - 1);
+            const int i = e / kTblQuads, c = e % kTblQuads;
+            const int q = tbl_by_q ? i : (row0 + i < R ? (row0 + i) % a.Nq : 0);
+            tv[j] = *(const float4*)(a.rope + ((size_t)sq * a.Nq + q) * (D / 2) + 2 * c);
+        }
+    }
+    // the new-key split: the raw K / V values of its rows (a batch of up to
+    // kStage rows a wave, all loads in flight before the first is used)
+    constexpr int kStage = 4;
+    const int half = D / 2;
+    const int sl = lane < half ? lane : half - 1;       // lane -> dims 2 sl, 2 sl + 1
+    const int e0 = 2 * sl;
+    const bool k_second = e0 >= half;
+    const int e_par = k_second ? e0 - half : e0 + half, i_rot = k_second ? e0 - half : e0;
+    float sv0[kStage], sv1[kStage], su0[kStage], su1[kStage];
+    float2 sc0[kStage], sc1[kStage];
+    auto stage_load = [&](int rbase) {
+#pragma unroll
+        for (int b = 0; b < kStage; b++) {
+            const int rr = min(rbase + b * kWaves, 2 * a.Nq - 1);
+            const int pnew = rr >> 1;
+            const bool isv = rr & 1;
+            const size_t qrow = (size_t)sq * a.Nq + pnew;
+            const float* src = a.qkv + qrow * a.ldq + (size_t)(a.H + (isv ? Hk : 0) + hk) * D;
+            sv0[b] = src[e0];
+            sv1[b] = src[e0 + 1];
+            su0[b] = src[e_par];
+            su1[b] = src[e_par + 1];
+            sc0[b] = a.rope[qrow * half + i_rot];
+            sc1[b] = a.rope[qrow * half + i_rot + 1];
+        }
+    };
+    // the staged rows: K rotated, K and V quantised as k_rope_append does
+    // (absmax / 7 per head row, floor 1e-8, roundf, clamp to [-8, 7]) into
+    // LDS, and, by the block of row chunk 0, into the cache
+    auto stage_store = [&](int rbase) {
+        const bool writer = (int)blockIdx.z % a.chunks == 0;
+#pragma unroll
+        for (int b = 0; b < kStage; b++) {
+            const int rr = rbase + b * kWaves;
+            if (rr >= 2 * a.Nq) break;                 // wave-uniform
+            const int pnew = rr >> 1;
+            const bool isv = rr & 1;
+            float v0 = sv0[b], v1 = sv1[b];
+            if (!isv) {
+                v0 = rope_val(v0, su0[b], sc0[b], k_second);
+                v1 = rope_val(v1, su1[b], sc1[b], k_second);
+            }
+            float mx = lane < half ? fmaxf(fabsf(v0), fabsf(v1)) : 0.0f;
+            mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mx), 0x111, 0xF, 0xF, true)));
+            mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mx), 0x112, 0xF, 0xF, true)));
+            mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mx), 0x114, 0xF, 0xF, true)));
+            mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mx), 0x118, 0xF, 0xF, true)));
+            mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mx), 0x142, 0xA, 0xF, true)));
+            mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mx), 0x143, 0xC, 0xF, true)));
+            mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 63));
+            float sc = __fdiv_rn(mx, 7.0f);
+            if (sc < 1e-8f) sc = 1.0f;
+            int q0 = (int)roundf(__fdiv_rn(v0, sc)), q1 = (int)roundf(__fdiv_rn(v1, sc));
+            q0 = q0 > 7 ? 7 : (q0 < -8 ? -8 : q0);
+            q1 = q1 > 7 ? 7 : (q1 < -8 ? -8 : q1);
+            const uint8_t byte = (uint8_t)((q0 & 0xF) | ((q1 & 0xF) << 4));
+            const size_t th = (size_t)(nk_old + pnew) * Hk + hk;   // (position, head)
+            if (lane < half) {
+                (isv ? st_v : st_k)[pnew][lane] = byte;
+                if (writer) {
+                    uint8_t* cw = (isv ? a.vcw : a.kcw) + (size_t)sq * a.seq_kbytes;
+                    cw[th * half + lane] = byte;
+                }
+            }
+            if (lane == 0) {
+                (isv ? st_vs : st_ks)[pnew] = sc;
+                if (writer) ((isv ? a.vsw : a.ksw) + (size_t)sq * a.seq_groups)[th] = sc;
+            }
+        }
+    };
+    if (new_split) stage_load(wave);
+    if (!new_split) load_tile(k_begin + wave * kTile, td);
+    if (FUSED) {
+#pragma unroll
+        for (int j = 0; j < kTblLoads; j++) {
+            const int e = (int)threadIdx.x + j * 64 * kWaves;
+            if (e < tbl_rows * kTblQuads) {
+                // entries i, i + 1 of row t (i even: the same half)
+                const int t = e / kTblQuads, i = 2 * (e % kTblQuads);
+                const int h = i / DPL, jj = i % DPL;
+                tbl[jj][2 * t + h] = make_float2(tv[j].x, tv[j].y);
+                tbl[jj + 1][2 * t + h] = make_float2(tv[j].z, tv[j].w);
+            }
+        }
+    }
+    if (new_split) {
+        // wave w takes rows w, w + 4, ... of the 2 Nq (key, value) rows
+        for (int rb = wave;;) {
+            stage_store(rb);
+            rb += kWaves * kStage;
+            if (rb >= 2 * a.Nq) break;
+            stage_load(rb);
+        }
+    }
+    if (FUSED) {
+        // rotate the Q rows: lane (n, g) holds dims DPL g .. DPL g + DPL - 1,
+        // its partners (d +- D/2) are in lane group g ^ 2, i.e. the lane 32
+        // apart; v_permlane32_swap exchanges the two halves of the wave
+        lds_barrier();                               // the rotary table is in LDS
+        // value d: own c - partner s (first half) or partner s + own c
+        // (second half), i.e. own c + partner s' with s' = -s / s: negation
+        // and the order of an addition's operands are exact
+        const uint32_t sflip = g >= 2 ? 0u : 0x80000000u;
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            const int col = 2 * (tbl_by_q ? rq[rt] : 16 * rt + n) + (g & 1);
+#pragma unroll
+            for (int i = 0; i < DPL; i++) {
+                const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(qv[rt][i]),
+                                                                 __float_as_uint(qv[rt][i]),
+                                                                 false, false);
+                const float partner = __uint_as_float(g >= 2 ? sw[0] : sw[1]);
+                const float2 cs = tbl[i][col];
+                const float sn = __uint_as_float(__float_as_uint(cs.y) ^ sflip);
+                qv[rt][i] = rope_sum(qv[rt][i], partner, cs.x, sn);
+            }
+        }
+    }
     {
         // rows are per lane (n); every wave computes the row exponent of its
         // lanes' rows for all RT (cheap), the fp16 splits are divided: wave w
@@ -480,14 +699,22 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_dec(DecArgs a) {
             }
         }
     };
-    TileData tn;
-    int tile = wave;
-    for (; tile + kWaves < ntiles; tile += kWaves) {
-        load_tile(k_begin + (tile + kWaves) * kTile, tn);
-        process(td, tile);
-        td = tn;
+    if (new_split) {
+        // at most 64 new keys: one tile each for waves 0 and 1
+        if (wave < ntiles) {
+            load_tile_lds(k_begin + wave * kTile, td);
+            process(td, wave);
+        }
+    } else {
+        TileData tn;
+        int tile = wave;
+        for (; tile + kWaves < ntiles; tile += kWaves) {
+            load_tile(k_begin + (tile + kWaves) * kTile, tn);
+            process(td, tile);
+            td = tn;
+        }
+        if (tile < ntiles) process(td, tile);
     }
-    if (tile < ntiles) process(td, tile);
 
     // ---- per wave: true-unit O, row max and sum -> LDS (s_o reuses the
     // bytes of s_q: every wave is past its last read of the Q operands)
@@ -604,9 +831,9 @@ __global__ void k_attn_dec_combine(const float* __restrict__ part_o,
     O[(size_t)row * D + d] = L > 0.0f ? acc / L : 0.0f;
 }
 
-template <int D, int RT>
+template <int D, int RT, bool FUSED = false>
 int launch(const DecArgs& a, dim3 grid) {
-    hipLaunchKernelGGL((k_attn_dec<D, RT>), grid, dim3(64 * kWaves), 0, stream(), a);
+    hipLaunchKernelGGL((k_attn_dec<D, RT, FUSED>), grid, dim3(64 * kWaves), 0, stream(), a);
     return launch_check("k_attn_dec");
 }
 
@@ -619,41 +846,11 @@ extern "C" int cgk_attn_dec_supported(int D, int gs, int B, int mask_kind) {
            (mask_kind == kMaskNone || mask_kind == kMaskCausal || mask_kind == kMaskTree);
 }
 
-// Batched form: B sequences, each Nq query rows against its own cache
-// (sequence b at kc + b * seq_kbytes, scales + b * seq_groups) of nk[b] keys.
-extern "C" int cgk_attn_dec_batch(const float* Q, const uint8_t* kc, const uint8_t* vc,
-                                  const float* ks, const float* vs, int B, const int* nk,
-                                  size_t seq_kbytes, size_t seq_groups, int Nq, int H, int Hk,
-                                  int D, float scale, int mask_kind,
-                                  const unsigned long long* anc, int tw, float* O) {
-    int nkmax = 0, nkmin = 1 << 30;
-    for (int b = 0; b < B; b++) {
-        nkmax = nk[b] > nkmax ? nk[b] : nkmax;
-        nkmin = nk[b] < nkmin ? nk[b] : nkmin;
-    }
-    if (mask_kind == kMaskTree && tw <= 0) tw = Nq;
-    if (B < 1 || B > kMaxBatch || Nq <= 0 || nkmin < Nq || Hk <= 0 || H % Hk ||
-        (mask_kind == kMaskTree && (Nq > 64 || !anc || tw < Nq || tw > 64 || nkmin < tw)) ||
-        (D != 32 && D != 64 && D != 128)) {
-        cgx_set_error("attn_dec: unsupported shape B=%d Nq=%d Nk=%d..%d H=%d Hk=%d D=%d", B, Nq,
-                      nkmin, nkmax, H, Hk, D);
-        return -1;
-    }
-    if (((uintptr_t)Q & 15) || ((uintptr_t)O & 15) || ((uintptr_t)kc & 15) || (seq_kbytes & 15)) {
-        cgx_set_error("attn_dec: Q, O and the K cache must be 16-byte aligned");
-        return -1;
-    }
-    DecArgs a;
-    a.Q = Q; a.kc = kc; a.vc = vc; a.ks = ks; a.vs = vs;
-    a.Nq = Nq; a.Nk = nkmax; a.H = H; a.Hk = Hk;
-    a.scale = scale;
-    a.mask_kind = mask_kind;
-    a.tw = mask_kind == kMaskTree ? tw : Nq;
-    for (int i = 0; i < 64; i++) a.anc[i] = (mask_kind == kMaskTree && i < Nq) ? anc[i] : 0ull;
-    a.B = B;
-    a.seq_kbytes = seq_kbytes;
-    a.seq_groups = seq_groups;
-    for (int b = 0; b < kMaxBatch; b++) a.nk[b] = b < B ? nk[b] : 0;
+// Launch shape and launch of one call: rows per block (RT), key splits over
+// the keys the splits stream (the cached keys when fused; the new keys are
+// one more split), the split combine.  `a` holds the shape and pointers.
+static int launch_dec(DecArgs& a, int nk_split_max, bool fused, float* O) {
+    const int B = a.B, Nq = a.Nq, H = a.H, Hk = a.Hk, D = a.D_;
     const int R = (H / Hk) * Nq;
     // rows per block: 32 (RT = 2) dequantises each K/V tile once for both
     // 16-row halves, 16 (RT = 1) gives twice the blocks.  RT = 2 when RT = 1
@@ -662,7 +859,7 @@ extern "C" int cgk_attn_dec_batch(const float* Q, const uint8_t* kc, const uint8
     // chain at batch 1 (528 rounds) 14.1 us at RT = 1 against 16.6 at RT = 2;
     // batch 8 (4224) 33.6 against 39.8; the 64-node tree at batch 4 (8704)
     // 47.4 against 51.4.  The block targets were measured the same way.
-    const int total_rounds = (nkmax + kSplitKeys - 1) / kSplitKeys;
+    const int total_rounds = (a.Nk + kSplitKeys - 1) / kSplitKeys;
     const long rounds1 = (long)total_rounds * Hk * B * ((R + 15) / 16);
     const int RT = (R > 16 && rounds1 > 1024) ? 2 : 1;
     const int target_blocks = RT == 2 ? kTargetBlocks2 : kTargetBlocks1;
@@ -673,13 +870,16 @@ extern "C" int cgk_attn_dec_batch(const float* Q, const uint8_t* kc, const uint8
     // context just past a multiple of the split size adds a split rather than
     // doubling every split); the splits follow the longest sequence, shorter
     // ones leave their last splits empty
+    const int split_rounds = (nk_split_max + kSplitKeys - 1) / kSplitKeys;
     const int nrb = Hk * B * chunks;    // blocks of one split
     int maxsp = target_blocks / nrb;
     maxsp = maxsp < 1 ? 1 : (maxsp > kMaxSplits ? kMaxSplits : maxsp);
-    const int rps = total_rounds / maxsp > 1 ? total_rounds / maxsp : 1;
+    const int rps = split_rounds / maxsp > 1 ? split_rounds / maxsp : 1;
     int kps = kSplitKeys * rps;
-    while ((nkmax + kps - 1) / kps > 128) kps += kSplitKeys;
-    const int splits = (nkmax + kps - 1) / kps;
+    while ((nk_split_max + kps - 1) / kps > 127) kps += kSplitKeys;
+    const int nsplit = (nk_split_max + kps - 1) / kps;
+    const int splits = fused ? nsplit + 1 : nsplit;
+    a.nsplit_old = nsplit;
     a.splits = splits;
     a.keys_per_split = kps;
     a.O = O;
@@ -693,7 +893,17 @@ extern "C" int cgk_attn_dec_batch(const float* Q, const uint8_t* kc, const uint8
     }
     dim3 grid(splits, Hk, chunks * B);
     int rc;
-    if (RT == 2) {
+    if (fused) {
+        if (RT == 2) {
+            if (D == 128) rc = launch<128, 2, true>(a, grid);
+            else if (D == 64) rc = launch<64, 2, true>(a, grid);
+            else rc = launch<32, 2, true>(a, grid);
+        } else {
+            if (D == 128) rc = launch<128, 1, true>(a, grid);
+            else if (D == 64) rc = launch<64, 1, true>(a, grid);
+            else rc = launch<32, 1, true>(a, grid);
+        }
+    } else if (RT == 2) {
         if (D == 128) rc = launch<128, 2>(a, grid);
         else if (D == 64) rc = launch<64, 2>(a, grid);
         else rc = launch<32, 2>(a, grid);
@@ -704,15 +914,97 @@ extern "C" int cgk_attn_dec_batch(const float* Q, const uint8_t* kc, const uint8
     }
     if (rc) return rc;
     if (splits > 1) {
-        if (splits > 128) {
-            cgx_set_error("attn_dec: too many splits");
-            return -1;
-        }
         hipLaunchKernelGGL(k_attn_dec_combine, dim3(nrow), dim3(D), 0, stream(), a.part_o,
                            a.part_ml, splits, nrow, D, O);
         if (launch_check("k_attn_dec_combine")) return -1;
     }
     return 0;
+}
+
+static int fill_args(DecArgs& a, const uint8_t* kc, const uint8_t* vc, const float* ks,
+                     const float* vs, int B, const int* nk, size_t seq_kbytes,
+                     size_t seq_groups, int Nq, int H, int Hk, int D, float scale,
+                     int mask_kind, const unsigned long long* anc, int tw, int* nkmax_out) {
+    int nkmax = 0, nkmin = 1 << 30;
+    for (int b = 0; b < B && b < kMaxBatch; b++) {
+        nkmax = nk[b] > nkmax ? nk[b] : nkmax;
+        nkmin = nk[b] < nkmin ? nk[b] : nkmin;
+    }
+    if (mask_kind == kMaskTree && tw <= 0) tw = Nq;
+    if (B < 1 || B > kMaxBatch || Nq <= 0 || nkmin < Nq || Hk <= 0 || H % Hk ||
+        (mask_kind == kMaskTree && (Nq > 64 || !anc || tw < Nq || tw > 64 || nkmin < tw)) ||
+        (D != 32 && D != 64 && D != 128)) {
+        cgx_set_error("attn_dec: unsupported shape B=%d Nq=%d Nk=%d..%d H=%d Hk=%d D=%d", B, Nq,
+                      nkmin, nkmax, H, Hk, D);
+        return -1;
+    }
+    if (((uintptr_t)kc & 15) || (seq_kbytes & 15)) {
+        cgx_set_error("attn_dec: the K cache must be 16-byte aligned");
+        return -1;
+    }
+    memset(&a, 0, sizeof(a));
+    a.kc = kc; a.vc = vc; a.ks = ks; a.vs = vs;
+    a.Nq = Nq; a.Nk = nkmax; a.H = H; a.Hk = Hk; a.D_ = D;
+    a.scale = scale;
+    a.mask_kind = mask_kind;
+    a.tw = mask_kind == kMaskTree ? tw : Nq;
+    for (int i = 0; i < 64; i++) a.anc[i] = (mask_kind == kMaskTree && i < Nq) ? anc[i] : 0ull;
+    a.B = B;
+    a.seq_kbytes = seq_kbytes;
+    a.seq_groups = seq_groups;
+    for (int b = 0; b < kMaxBatch; b++) a.nk[b] = b < B ? nk[b] : 0;
+    *nkmax_out = nkmax;
+    return 0;
+}
+
+// Batched form: B sequences, each Nq query rows against its own cache
+// (sequence b at kc + b * seq_kbytes, scales + b * seq_groups) of nk[b] keys.
+extern "C" int cgk_attn_dec_batch(const float* Q, const uint8_t* kc, const uint8_t* vc,
+                                  const float* ks, const float* vs, int B, const int* nk,
+                                  size_t seq_kbytes, size_t seq_groups, int Nq, int H, int Hk,
+                                  int D, float scale, int mask_kind,
+                                  const unsigned long long* anc, int tw, float* O) {
+    DecArgs a;
+    int nkmax;
+    if (fill_args(a, kc, vc, ks, vs, B, nk, seq_kbytes, seq_groups, Nq, H, Hk, D, scale,
+                  mask_kind, anc, tw, &nkmax))
+        return -1;
+    if (((uintptr_t)Q & 15) || ((uintptr_t)O & 15)) {
+        cgx_set_error("attn_dec: Q, O and the K cache must be 16-byte aligned");
+        return -1;
+    }
+    a.Q = Q;
+    return launch_dec(a, nkmax, false, O);
+}
+
+// Fused RoPE, cache append and attention: qkv [B][Nq][ldq] are the raw
+// projections of the step's rows (q heads, k heads, v heads), rope [B][Nq][D/2]
+// the (cos, sin) of each row's rotary position (cgk_embed_rope); nk[b] counts
+// the new keys, which this call rotates, quantises and writes to positions
+// nk[b] - Nq .. nk[b] - 1 of the cache (one scale per head row).
+extern "C" int cgk_attn_dec_rope(const float* qkv, int ldq, const float* rope, uint8_t* kc,
+                                 uint8_t* vc, float* ks, float* vs, int B, const int* nk,
+                                 size_t seq_kbytes, size_t seq_groups, int Nq, int H, int Hk,
+                                 int D, float scale, int mask_kind,
+                                 const unsigned long long* anc, int tw, float* O) {
+    DecArgs a;
+    int nkmax;
+    if (fill_args(a, kc, vc, ks, vs, B, nk, seq_kbytes, seq_groups, Nq, H, Hk, D, scale,
+                  mask_kind, anc, tw, &nkmax))
+        return -1;
+    if (Nq > 64 || ((uintptr_t)qkv & 15) || (ldq & 3) || ((uintptr_t)rope & 15) ||
+        ((uintptr_t)O & 15) || ldq < (H + 2 * Hk) * D) {
+        cgx_set_error("attn_dec_rope: %d rows (at most 64), or qkv / rope / O not 16-byte "
+                      "aligned with ldq %% 4 == 0", Nq);
+        return -1;
+    }
+    a.qkv = qkv;
+    a.ldq = ldq;
+    a.rope = (const float2*)rope;
+    a.kcw = kc; a.vcw = vc; a.ksw = ks; a.vsw = vs;
+    int nk_old_max = 0;
+    for (int b = 0; b < B; b++) nk_old_max = nk[b] - Nq > nk_old_max ? nk[b] - Nq : nk_old_max;
+    return launch_dec(a, nk_old_max, true, O);
 }
 
 extern "C" int cgk_attn_dec(const float* Q, const uint8_t* kc, const uint8_t* vc, const float* ks,

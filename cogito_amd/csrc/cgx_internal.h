@@ -284,6 +284,14 @@ int cgx_tree_shape_default(cgx_tree_shape* t, int nodes, int depth);
  * rank of each node among its siblings (0 .. 3, distinct, in order). */
 int cgx_tree_shape_from_parents(cgx_tree_shape* t, const int* parent, int nodes);
 int cgk_rope(float* x, int S, int H, int D, int pos0, float theta);
+/* (cos, sin) of positions pos0 .. pos0 + rows - 1 times each RoPE frequency:
+ * cs [rows][D/2][2] (decoder.hip; the arithmetic of the cache append). */
+int cgk_rope_table(int rows, int D, int pos0, float theta, float* cs);
+/* Fused RoPE, INT4 cache append of the Nq new keys and attention (attn_dec.hip). */
+int cgk_attn_dec_rope(const float* qkv, int ldq, const float* rope, uint8_t* kc, uint8_t* vc,
+                      float* ks, float* vs, int B, const int* nk, size_t seq_kbytes,
+                      size_t seq_groups, int Nq, int H, int Hk, int D, float scale,
+                      int mask_kind, const unsigned long long* anc, int tw, float* O);
 int cgk_rope_freqs(float* cs, float* sn, int S, int D, float theta);
 int cgk_alibi_slopes(float* slopes, int H);
 int cgk_alibi_bias(float* bias, int Sq, int Sk, int H, const float* slopes);

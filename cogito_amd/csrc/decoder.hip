@@ -61,13 +61,52 @@ struct RopeBatch {
     int rel[kMaxTreeRows];
 };
 
+// Embedding rows of the step's tokens, and the rotary table of each row:
+// cs[r][i] = (cos, sin) of the row's rotary position times frequency i (i <
+// D/2), with k_rope_append's arithmetic, so that the fused attention
+// (attn_dec.hip) rotates Q and K to the same bits.  Block (x, r); blocks with
+// x == 0 also fill row r's table.
+__global__ void k_embed_rope(const float* __restrict__ table, const int* __restrict__ tokens,
+                             int d, int V, float* __restrict__ x, RopeBatch rb, int D,
+                             float theta, float2* __restrict__ cs) {
+    const int m = blockIdx.y;
+    int tok = tokens[m];
+    tok = tok < 0 ? 0 : (tok >= V ? V - 1 : tok);
+    const float* row = table + (size_t)tok * d;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < d; i += gridDim.x * blockDim.x)
+        x[(size_t)m * d + i] = row[i];
+    if (blockIdx.x == 0) {
+        const int sq = m / rb.M;
+        const int rpos = rb.pos0[sq] + (rb.has_rel ? rb.rel[m % rb.M] : m % rb.M);
+        for (int i = threadIdx.x; i < D / 2; i += blockDim.x) {
+            float freq = __fdiv_rn(1.0f, powf(theta, __fdiv_rn((float)(2 * i), (float)D)));
+            float angle = __fmul_rn((float)rpos, freq);
+            cs[(size_t)m * (D / 2) + i] = make_float2(cosf(angle), sinf(angle));
+        }
+    }
+}
+
+// cs[r][i] = (cos, sin) of (pos0 + r) times frequency i, as k_embed_rope.
+__global__ void k_rope_table(int rows, int D, int pos0, float theta, float2* __restrict__ cs) {
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= rows * (D / 2)) return;
+    const int r = e / (D / 2), i = e % (D / 2);
+    float freq = __fdiv_rn(1.0f, powf(theta, __fdiv_rn((float)(2 * i), (float)D)));
+    float angle = __fmul_rn((float)(pos0 + r), freq);
+    cs[e] = make_float2(cosf(angle), sinf(angle));
+}
+
 // One workgroup of D/2 threads per (token row, head): heads [0, H) are query
 // heads (rotated into q_out), heads [H, H + Hk) are KV heads (K rotated, then
 // K and V quantised into the cache row of the token's position).
+// With cs (k_embed_rope's table of the same rows) the rotation takes its
+// (cos, sin) from there, as the fused attention does, so both write the same
+// cache bits.
 __global__ void k_rope_append(const float* __restrict__ qkv, int ld, int H, int Hk, int D,
-                              int gs, RopeBatch rb, float theta, float* __restrict__ q_out,
-                              uint8_t* __restrict__ kc, uint8_t* __restrict__ vc,
-                              float* __restrict__ ks, float* __restrict__ vs) {
+                              int gs, RopeBatch rb, float theta, const float2* __restrict__ cs,
+                              float* __restrict__ q_out, uint8_t* __restrict__ kc,
+                              uint8_t* __restrict__ vc, float* __restrict__ ks,
+                              float* __restrict__ vs) {
     __shared__ float sk[256], sv[256];
     const int m = blockIdx.x, head = blockIdx.y, i = threadIdx.x, half = D / 2;
     const int sq = m / rb.M;
@@ -89,9 +128,17 @@ __global__ void k_rope_append(const float* __restrict__ qkv, int ld, int H, int 
     const float* v = is_q ? k : row + (H + Hk) * D + hk * D;
     const float k0 = k[i], k1 = k[i + half];
     const float v0 = v[i], v1 = v[i + half];
-    float freq = __fdiv_rn(1.0f, powf(theta, __fdiv_rn((float)(2 * i), (float)D)));
-    float angle = __fmul_rn((float)rpos, freq);
-    float c = cosf(angle), s = sinf(angle);
+    float c, s;
+    if (cs) {
+        const float2 t = cs[(size_t)m * half + i];
+        c = t.x;
+        s = t.y;
+    } else {
+        float freq = __fdiv_rn(1.0f, powf(theta, __fdiv_rn((float)(2 * i), (float)D)));
+        float angle = __fmul_rn((float)rpos, freq);
+        c = cosf(angle);
+        s = sinf(angle);
+    }
     if (is_q) {
         float* o = q_out + ((size_t)m * H + head) * D;
         o[i] = __fsub_rn(__fmul_rn(k0, c), __fmul_rn(k1, s));
@@ -182,10 +229,38 @@ extern "C" int cgk_embed(const float* table, const int* tokens, int M, int d, in
     return launch_check("k_embed");
 }
 
+extern "C" int cgk_rope_table(int rows, int D, int pos0, float theta, float* cs) {
+    const int n = rows * (D / 2);
+    hipLaunchKernelGGL(k_rope_table, dim3((n + 255) / 256), dim3(256), 0, stream(), rows, D,
+                       pos0, theta, (float2*)cs);
+    return launch_check("k_rope_table");
+}
+
+extern "C" int cgk_embed_rope(const float* table, const int* tokens, int B, int M, int d, int V,
+                              float* x, const int* pos0, const int* rel, int D, float theta,
+                              float* cs) {
+    if (M <= 0) return 0;
+    if (B < 1 || B > kMaxBatch || (rel && M > kMaxTreeRows) || D < 2 || (D & 1)) {
+        cgx_set_error("embed_rope: batch %d, %d rows, head_dim %d", B, M, D);
+        return -1;
+    }
+    RopeBatch rb;
+    rb.has_rel = rel != nullptr;
+    for (int r = 0; r < kMaxTreeRows; r++) rb.rel[r] = rel && r < M ? rel[r] : 0;
+    rb.M = M;
+    for (int b = 0; b < kMaxBatch; b++) rb.pos0[b] = b < B ? pos0[b] : 0;
+    rb.seq_kbytes = rb.seq_groups = 0;
+    int bx = (d + 255) / 256;
+    hipLaunchKernelGGL(k_embed_rope, dim3(bx > 16 ? 16 : bx, B * M), dim3(256), 0, stream(),
+                       table, tokens, d, V, x, rb, D, theta, (float2*)cs);
+    return launch_check("k_embed_rope");
+}
+
 extern "C" int cgk_rope_append_batch(const float* qkv, int ld, int B, int M, int H, int Hk,
                                      int D, int gs, const int* pos0, const int* rel, float theta,
-                                     float* q_out, uint8_t* kc, uint8_t* vc, float* ks, float* vs,
-                                     size_t seq_kbytes, size_t seq_groups) {
+                                     const float* cs, float* q_out, uint8_t* kc, uint8_t* vc,
+                                     float* ks, float* vs, size_t seq_kbytes,
+                                     size_t seq_groups) {
     if (M <= 0) return 0;
     if (D < 2 || D > 256 || (D & 1) || gs <= 0 || (gs & 1) || D % gs) {
         cgx_set_error("rope_append: unsupported head_dim %d / group %d", D, gs);
@@ -207,15 +282,15 @@ extern "C" int cgk_rope_append_batch(const float* qkv, int ld, int B, int M, int
     rb.seq_kbytes = seq_kbytes;
     rb.seq_groups = seq_groups;
     hipLaunchKernelGGL(k_rope_append, dim3(B * M, H + Hk), dim3(D / 2), 0, stream(), qkv, ld, H,
-                       Hk, D, gs, rb, theta, q_out, kc, vc, ks, vs);
+                       Hk, D, gs, rb, theta, (const float2*)cs, q_out, kc, vc, ks, vs);
     return launch_check("k_rope_append");
 }
 
 extern "C" int cgk_rope_append(const float* qkv, int ld, int M, int H, int Hk, int D, int gs,
                                int pos0, float theta, float* q_out, uint8_t* kc, uint8_t* vc,
                                float* ks, float* vs) {
-    return cgk_rope_append_batch(qkv, ld, 1, M, H, Hk, D, gs, &pos0, nullptr, theta, q_out, kc,
-                                 vc, ks, vs, 0, 0);
+    return cgk_rope_append_batch(qkv, ld, 1, M, H, Hk, D, gs, &pos0, nullptr, theta, nullptr,
+                                 q_out, kc, vc, ks, vs, 0, 0);
 }
 
 extern "C" int cgk_spec_tokens(const int* feed, const int* dtok, int B, int gamma, int* ttok,

@@ -195,6 +195,37 @@ int cgx_attention_int4_kv_batch_dev(const float* Q, int B, int Nq, int H, cg_kv_
                               O);
 }
 
+int cgx_rope_table_dev(int rows, int head_dim, int pos0, float theta, float* cs) {
+    if (!cs || rows <= 0 || head_dim < 2 || (head_dim & 1) || pos0 < 0) {
+        cgx_set_error("cgx_rope_table_dev: invalid argument");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    return cgk_rope_table(rows, head_dim, pos0, theta, cs);
+}
+
+int cgx_attention_rope_append_dev(const float* qkv, int ldq, const float* rope, int Nq, int H,
+                                  cg_kv_cache_int4* c, int layer, int pos, float* O) {
+    if (!qkv || !rope || !O || !c || Nq <= 0 || Nq > 64 || H <= 0 || layer < 0 ||
+        layer >= c->num_layers || pos < 0 || pos + Nq > c->max_seq_len) {
+        cgx_set_error("cgx_attention_rope_append_dev: invalid argument (%d rows at position "
+                      "%d, at most 64 rows)", Nq, pos);
+        return -1;
+    }
+    if (c->group_size != c->head_dim) {
+        cgx_set_error("cgx_attention_rope_append_dev: needs one scale per head row "
+                      "(group_size == head_dim)");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    const size_t lb = layer_bytes(c), lg = layer_groups(c);
+    const int nk = pos + Nq;
+    return cgk_attn_dec_rope(qkv, ldq, rope, c->k_cache + lb * layer, c->v_cache + lb * layer,
+                             c->k_scales + lg * layer, c->v_scales + lg * layer, 1, &nk, 0, 0,
+                             Nq, H, c->n_heads, c->head_dim, 1.0f / sqrtf((float)c->head_dim),
+                             CGK_MASK_CAUSAL_ALIGNED, NULL, Nq, O);
+}
+
 int cgx_attention_int4_kv_dev(const float* Q, int Nq, int H, cg_kv_cache_int4* c,
                               int layer, int mask_kind, const int* parents, float* O) {
     if (!Q || !O || !c || Nq <= 0 || H <= 0 || layer < 0 || layer >= c->num_layers) {

@@ -6,8 +6,9 @@
  * work fused around it (gemv.hip: RMSNorm folded into the activation side,
  * SwiGLU computed in the epilogue of the gate|up product, whose gate and up
  * column tiles are interleaved), attention reads the INT4 cache directly
- * (attn_dec.hip).  Per layer: 4 GEMVs, RoPE + KV append, attention (+ split
- * combine).
+ * (attn_dec.hip).  Per layer: 4 GEMVs and attention (+ split combine), with
+ * RoPE and the KV append inside the attention launch (or, for tree forwards
+ * of more than 16 rows, a launch of their own before it).
  */
 #include <math.h>
 #include <stdlib.h>
@@ -17,11 +18,16 @@
 #include "cg_serialization.h"
 #include "cgx_internal.h"
 
-int cgk_embed(const float* table, const int* tokens, int M, int d, int V, float* x);
+int cgk_embed_rope(const float* table, const int* tokens, int B, int M, int d, int V, float* x,
+                   const int* pos0, const int* rel, int D, float theta, float* cs);
+int cgk_attn_dec_rope(const float* qkv, int ldq, const float* rope, uint8_t* kc, uint8_t* vc,
+                      float* ks, float* vs, int B, const int* nk, size_t seq_kbytes,
+                      size_t seq_groups, int Nq, int H, int Hk, int D, float scale,
+                      int mask_kind, const unsigned long long* anc, int tw, float* O);
 int cgk_rope_append_batch(const float* qkv, int ld, int B, int M, int H, int Hk, int D, int gs,
-                          const int* pos0, const int* rel, float theta, float* q_out,
-                          uint8_t* kc, uint8_t* vc, float* ks, float* vs, size_t seq_kbytes,
-                          size_t seq_groups);
+                          const int* pos0, const int* rel, float theta, const float* cs,
+                          float* q_out, uint8_t* kc, uint8_t* vc, float* ks, float* vs,
+                          size_t seq_kbytes, size_t seq_groups);
 int cgk_fill_normal(float* out, size_t n, uint64_t seed, uint32_t stream_id, float stddev);
 
 enum { PRO_NONE = 0, PRO_RMSNORM = 1 };
@@ -59,6 +65,7 @@ struct cgx_model {
     cg_kv_cache_int4* kv;
     int* tok;
     float *x, *qkv, *q, *attn, *gu, *logits;
+    float* rope;             /* [rows][head_dim / 2] (cos, sin) of the step's positions */
     float *stats_x, *stats_g;  /* row statistics of x and of the SwiGLU output */
 };
 
@@ -327,6 +334,7 @@ void cgx_model_free(cgx_model* m) {
     cgx_free(m->attn);
     cgx_free(m->gu);
     cgx_free(m->logits);
+    cgx_free(m->rope);
     cgx_free(m->stats_x);
     cgx_free(m->stats_g);
     free(m);
@@ -417,10 +425,11 @@ static cgx_model* build(const cgx_model_config* cfg, uint64_t seed, cgx_model* s
         m->attn = (float*)cgx_malloc((size_t)Mx * c->n_heads * c->head_dim * 4);
         m->gu = (float*)cgx_malloc((size_t)Mx * c->d_ff * 4);      /* SwiGLU output */
         m->logits = (float*)cgx_malloc((size_t)Mx * V * 4);
+        m->rope = (float*)cgx_malloc((size_t)Mx * c->head_dim * 4);
         m->stats_x = (float*)cgx_malloc((size_t)Mx * (d / 256 + 1) * 2 * 4);
         m->stats_g = (float*)cgx_malloc((size_t)Mx * (c->d_ff / 256 + 1) * 2 * 4);
         ok = m->kv && m->tok && m->x && m->qkv && m->q && m->attn && m->gu && m->logits &&
-             m->stats_x && m->stats_g;
+             m->rope && m->stats_x && m->stats_g;
     }
     if (ok) ok = !cgx_synchronize();
     cgx_free(tf);
@@ -648,6 +657,16 @@ static size_t kv_layer_groups(const cg_kv_cache_int4* c) {
     return (size_t)c->max_seq_len * c->n_heads * (c->head_dim / c->group_size);
 }
 
+/* RoPE and the cache append inside the attention launch (1), or as a launch
+ * of their own before it (0; a test hook: both must give the same cache). */
+static int g_fused_attention = 1;
+
+int cgx_decoder_fused_attention(int on) {
+    const int old = g_fused_attention;
+    if (on >= 0) g_fused_attention = on != 0;
+    return old;
+}
+
 /* Row statistics handed from one GEMM's reduction to the next GEMM (rows
  * >= 32): [rows][width / 256][2] partial (max|y * nw|, sum y^2). */
 typedef struct {
@@ -713,11 +732,20 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
     const int d = c->d_model, H = c->n_heads, Hk = c->n_kv_heads, hd = c->head_dim;
     const int hq = H * hd, gs = c->group_size, ff = c->d_ff, nq = nqkv(c);
     const float eps = c->norm_eps, scale = 1.0f / sqrtf((float)hd);
-    if (cgk_embed(m->embed, dtok, R, d, c->vocab, m->x)) return -1;
     const size_t lb = kv_layer_bytes(kv), lg = kv_layer_groups(kv);
     int xs_ok = 0;     /* m->stats_x holds the statistics of m->x */
     const int mask = tr ? CGK_MASK_TREE : CGK_MASK_CAUSAL_ALIGNED;
     const int batched = cgk_attn_dec_supported(hd, kv->group_size, 1, mask);
+    /* RoPE and the cache append run inside the attention launch for up to 16
+     * rows a sequence (chains, draft levels: the new keys are one more key
+     * split, staged by its blocks); the 64-row tree forward keeps a launch of
+     * its own, since there the extra split and its staging of 128 rows cost
+     * more than the launch (C5: 13.6 -> 14.6 ms a step).  The rotary table of
+     * the step's positions is filled with the embedding rows either way. */
+    const int fused = batched && M <= 16 && g_fused_attention;
+    if (cgk_embed_rope(m->embed, dtok, B, M, d, c->vocab, m->x, pos0, tr ? tr->rel : NULL, hd,
+                       c->rope_theta, m->rope))
+        return -1;
     if (tr && !batched) {
         cgx_set_error("cgx_model_forward_tree: head_dim %d / KV group %d not supported", hd,
                       kv->group_size);
@@ -738,12 +766,18 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
         float* vs = kv->v_scales + lg * slot;
         stats_t sq = {xs_ok ? m->stats_x : NULL, d / 256, NULL, NULL, 0};
         if (linear(&w[W_QKV], m->x, d, R, m->qkv, nq, PRO_RMSNORM, norm_w(m, 2 * l), eps,
-                   EPI_STORE, gs, &sq) ||
-            cgk_rope_append_batch(m->qkv, nq, B, M, H, Hk, hd, kv->group_size, pos0,
-                                  tr ? tr->rel : NULL, c->rope_theta, m->q, kc, vc, ks, vs, lb,
-                                  lg))
+                   EPI_STORE, gs, &sq))
             return -1;
-        if (batched) {
+        if (fused) {
+            if (cgk_attn_dec_rope(m->qkv, nq, m->rope, kc, vc, ks, vs, B, nk, lb, lg, M, H, Hk,
+                                  hd, scale, mask, tr ? tr->anc : NULL, tr ? tr->tw : M,
+                                  m->attn))
+                return -1;
+        } else if (cgk_rope_append_batch(m->qkv, nq, B, M, H, Hk, hd, kv->group_size, pos0,
+                                         tr ? tr->rel : NULL, c->rope_theta, m->rope, m->q, kc,
+                                         vc, ks, vs, lb, lg)) {
+            return -1;
+        } else if (batched) {
             if (cgk_attn_dec_batch(m->q, kc, vc, ks, vs, B, nk, lb, lg, M, H, Hk, hd, scale,
                                    mask, tr ? tr->anc : NULL, tr ? tr->tw : M, m->attn))
                 return -1;

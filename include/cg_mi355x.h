@@ -240,6 +240,24 @@ int cgx_attention_int4_kv_dev(const float* Q, int Nq, int H,
  * mask_kind 0: chain (query i sees keys < nk[b] - Nq + i + 1); 1: tree, the
  * last tw keys (Nq <= tw <= 64) visible to query i where bit j of anc[i]
  * (host array of Nq masks) is set.  Needs group_size == head_dim. */
+/* The decoder's attention step in one launch (no reference counterpart: it
+ * fuses cg_apply_rope, src/attention/flash_attn.c:335-360, the INT4 append of
+ * src/quantize/int4.c:155-231 and cg_attention_int4_kv): qkv [Nq][ldq] are
+ * the raw projections of Nq rows (q heads, then k heads, then v heads) at
+ * positions pos .. pos + Nq - 1; their K is rotated and quantised with V into
+ * those positions of `layer` (one scale per head row), Q is rotated, and O
+ * [Nq][H][head_dim] receives attention over positions 0 .. pos + Nq - 1 under
+ * the chain mask.  rope [Nq][head_dim / 2][2]: (cos, sin) of the rows'
+ * positions, from cgx_rope_table_dev(Nq, head_dim, pos, theta, rope).  Nq <= 64;
+ * device pointers, 16-byte aligned, ldq % 4 == 0.  The cache's current_len is
+ * left to the caller. */
+int cgx_rope_table_dev(int rows, int head_dim, int pos0, float theta, float* cs);
+int cgx_attention_rope_append_dev(const float* qkv, int ldq, const float* rope, int Nq, int H,
+                                  cg_kv_cache_int4* c, int layer, int pos, float* O);
+/* Test hook, no reference counterpart: 1 (default) runs the decoder's RoPE and
+ * cache append inside the attention launch, 0 as launches of their own (the
+ * same cache contents); returns the previous setting (-1 only reads it). */
+int cgx_decoder_fused_attention(int on);
 int cgx_attention_int4_kv_batch_dev(const float* Q, int B, int Nq, int H,
                                     cg_kv_cache_int4* cache, int slot0, const int* nk,
                                     int mask_kind, const unsigned long long* anc, int tw,

@@ -486,3 +486,71 @@ def test_alibi(gpu, oracle, H):
     gpu.cg_alibi_bias(b.ctypes.data, Sq, Sk, H, es.ctypes.data)
     oracle.orc_alibi_bias(ptr(eb), Sq, Sk, H, ptr(es))
     np.testing.assert_array_equal(_bits(b), _bits(eb))
+
+
+FUSED_CASES = [
+    # H, Hk, D, ctx, Nq: RoPE + INT4 append + attention in one call
+    (32, 8, 128, 4096, 5),         # 7B-shape verify step
+    (12, 12, 64, 1024, 5),         # tiny-decoder verify step
+    (16, 2, 64, 300, 33),          # new keys over two tiles
+    (8, 2, 32, 77, 7),
+    (4, 1, 64, 0, 16),             # no context: the new keys only
+    (32, 8, 128, 255, 64),         # 64 new keys, fewer cached than a block round
+]
+
+
+@pytest.mark.parametrize("H,Hk,D,ctx,Nq", FUSED_CASES)
+def test_attention_rope_append_vs_oracle(gpu, oracle, rng, H, Hk, D, ctx, Nq):
+    """cgx_attention_rope_append_dev against the oracle: RoPE of the new q and
+    k rows (src/attention/flash_attn.c:335-360), their INT4 append
+    (src/quantize/int4.c:155-231) and attention over the whole cache under the
+    chain mask.  The new V rows are bit-exact; K goes through RoPE, whose
+    device powf / cos / sin are within tolerance of glibc's, so its scales
+    agree to 1e-3 and its values to one quantisation step.  (The decoder test
+    test_fused_attention_step_matches_separate_launches pins the fused
+    append bit for bit against the separate RoPE / append launches.)"""
+    print(f"fused rope+append+attention H={H} Hk={Hk} D={D} ctx={ctx} Nq={Nq}", flush=True)
+    theta, S, gs = 10000.0, ctx + Nq, D
+    ldq = (H + 2 * Hk) * D
+    kc_ = rng.normal(0, 1, (ctx, Hk, D)).astype(np.float32)
+    vc_ = rng.normal(0, 1, (ctx, Hk, D)).astype(np.float32)
+    qkv = rng.normal(0, 1, (Nq, ldq)).astype(np.float32)
+    c = gpu.cg_kv_cache_int4_new(1, S, Hk, D, gs)
+    assert c, last_error(gpu)
+    if ctx:
+        assert gpu.cgx_kv_cache_int4_write(c, 0, 0, kc_.ctypes.data, vc_.ctypes.data, ctx) == 0
+    # oracle: rotate, append everything, attend
+    q = np.ascontiguousarray(qkv[:, :H * D]).reshape(Nq, H, D)
+    k = np.ascontiguousarray(qkv[:, H * D:(H + Hk) * D]).reshape(Nq, Hk, D)
+    v = np.ascontiguousarray(qkv[:, (H + Hk) * D:]).reshape(Nq, Hk, D)
+    oracle.orc_apply_rope(ptr(q), Nq, H, D, ctx, theta)
+    oracle.orc_apply_rope(ptr(k), Nq, Hk, D, ctx, theta)
+    arrs = oracle_kv_fill(oracle, np.concatenate([kc_, k]), np.concatenate([vc_, v]), Hk, D, gs,
+                          S)
+    K, V = oracle_kv_get(oracle, *arrs, S, Hk, D, gs)
+    exp, _ = orc_attention(oracle, q[None], K[None], V[None], H, Hk,
+                           float(np.float32(1.0 / np.sqrt(D))), 4)
+    dqkv = DeviceArray.from_numpy(gpu, qkv)
+    dcs = DeviceArray(gpu, Nq * D * 4)
+    do = DeviceArray(gpu, Nq * H * D * 4)
+    assert gpu.cgx_rope_table_dev(Nq, D, ctx, theta, dcs.ptr) == 0, last_error(gpu)
+    assert gpu.cgx_attention_rope_append_dev(dqkv.ptr, ldq, dcs.ptr, Nq, H, c, 0, ctx,
+                                             do.ptr) == 0, last_error(gpu)
+    got = do.numpy(np.float32, (Nq, H, D))
+    assert rel_err_rows(got.reshape(-1, D), exp.reshape(-1, D)) <= TOL
+    kb, vb, ks, vs = cache_arrays(gpu, c, 0)
+    okc, ovc, oks, ovs = arrs
+    nb, ng = ctx * Hk * D // 2, ctx * Hk
+    np.testing.assert_array_equal(vb[nb:S * Hk * D // 2], ovc[nb:S * Hk * D // 2])
+    np.testing.assert_array_equal(_bits(vs[ng:S * Hk]), _bits(ovs[ng:S * Hk]))
+    # the rotary angle is position * frequency: an ulp of a frequency (device
+    # powf against glibc's) grows with the position, ~2e-4 of |k| near 4096
+    assert np.allclose(ks[ng:S * Hk], oks[ng:S * Hk], rtol=1e-3, atol=0)
+    gk = np.zeros((S, Hk, D), np.float32)
+    gv = np.zeros_like(gk)
+    oracle.orc_kv_get(ptr(kb), ptr(vb), ptr(ks), ptr(vs), S, Hk, D, gs, ptr(gk), ptr(gv))
+    step = np.repeat(oks[:S * Hk].reshape(S, Hk, 1), D, axis=2)
+    assert np.all(np.abs(gk[ctx:] - K[ctx:]) <= step[ctx:] * 1.01)
+    for a in (dqkv, dcs, do):
+        a.free()
+    gpu.cg_kv_cache_int4_free(c)

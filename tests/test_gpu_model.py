@@ -308,3 +308,76 @@ def test_spec_batch_rejects_mismatched_models(gpu):
     assert "batch" in last_error(gpu)
     gpu.cgx_model_free(a)
     gpu.cgx_model_free(b)
+
+
+def _cache_arrays(gpu, m, length):
+    """Host copies of the written part (positions < length) of each layer
+    slot of a model's KV cache: {(kind, slot): array}, kind k / v (nibble
+    bytes) or ks / vs (scales)."""
+    cc = gpu.cgx_model_kv(m).contents
+    row_b = cc.n_heads * cc.head_dim // 2
+    row_g = cc.n_heads * cc.head_dim // cc.group_size
+    out = {}
+    for kind, arr, per, dt in (("k", cc.k_cache, row_b, np.uint8), ("v", cc.v_cache, row_b, np.uint8),
+                               ("ks", cc.k_scales, row_g, np.float32),
+                               ("vs", cc.v_scales, row_g, np.float32)):
+        esz = np.dtype(dt).itemsize
+        for slot in range(cc.num_layers):
+            h = np.empty(length * per, dt)
+            base = C.cast(arr, C.c_void_p).value + slot * cc.max_seq_len * per * esz
+            assert gpu.cgx_memcpy_d2h(h.ctypes.data, base, h.nbytes) == 0, last_error(gpu)
+            out[(kind, slot)] = h
+    return out
+
+
+def _dequant(c, kind, slot, length, Hk, D):
+    nib = c[(kind, slot)].reshape(length, Hk, D // 2)
+    lo = (nib & 0xF).astype(np.int8)
+    hi = (nib >> 4).astype(np.int8)
+    vals = np.stack([np.where(lo > 7, lo - 16, lo), np.where(hi > 7, hi - 16, hi)], -1)
+    vals = vals.reshape(length, Hk, D).astype(np.float32)
+    return vals * c[(kind + "s", slot)].reshape(length, Hk, 1)
+
+
+@pytest.mark.parametrize("batch", [0, 3])
+def test_fused_attention_step_matches_separate_launches(gpu, rng, batch):
+    """RoPE and the INT4 cache append inside the attention launch (the
+    default) and as launches of their own (cgx_decoder_fused_attention(0)).
+    Layer 0's cache is a function of the tokens and weights alone: the same
+    bytes.  Later layers see attention outputs that differ at the last bits
+    (the fused launch attends over the new keys in a key split of their own),
+    so their caches agree within a quantisation step (a value next to a
+    rounding boundary may flip a nibble) and the logits within 1e-4 of
+    max|logits| per row."""
+    cfg = Cfg(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, d_ff=512,
+              vocab=1024, max_seq=96, max_tokens=8, init_std=0.05, max_batch=batch)
+    B, V = max(batch, 1), cfg.vocab
+    steps = [rng.integers(0, V, (B, M)).astype(np.int32) for M in (7, 5, 1, 5, 8)]
+    models = [new_model(gpu, cfg, 77), new_model(gpu, cfg, 77)]
+    outs = [[], []]
+    old = gpu.cgx_decoder_fused_attention(-1)
+    try:
+        for k, m in enumerate(models):
+            gpu.cgx_decoder_fused_attention(1 - k)
+            for t in steps:
+                M = t.shape[1]
+                fwd = gpu.cgx_model_forward_batch if batch else gpu.cgx_model_forward
+                assert fwd(m, t.ctypes.data, M, M, None) == 0, last_error(gpu)
+                outs[k].append(logits_np(gpu, m, B * M, V))
+    finally:
+        gpu.cgx_decoder_fused_attention(old)
+    for a, b in zip(*outs):
+        assert rel_err_rows(a, b) < 1e-4
+    n = sum(t.shape[1] for t in steps)
+    ca, cb = (_cache_arrays(gpu, m, n) for m in models)
+    for (kind, slot), a in ca.items():
+        if slot < B:                                  # layer 0 of every sequence
+            np.testing.assert_array_equal(a.view(np.uint8), cb[(kind, slot)].view(np.uint8),
+                                          err_msg=f"{kind} slot {slot}")
+        elif kind in ("k", "v"):
+            da = _dequant(ca, kind, slot, n, cfg.n_kv_heads, cfg.head_dim)
+            db = _dequant(cb, kind, slot, n, cfg.n_kv_heads, cfg.head_dim)
+            step = ca[(kind + "s", slot)].reshape(n, cfg.n_kv_heads, 1)
+            assert np.all(np.abs(da - db) <= 1.01 * step), f"{kind} slot {slot}"
+    for m in models:
+        gpu.cgx_model_free(m)
