@@ -171,6 +171,11 @@ int cgk_filter_rows(const float* z, int rows, int V, int top_k, float top_p, con
  * (tokens[r / tok_every], drawn with u[(r / tok_every) * u_stride]). */
 int cgk_filter_rows_ex(const float* z, int rows, int V, int top_k, float top_p,
                        const float* u, int u_stride, int* tokens, int tok_every, float* dist);
+/* The same over rows of x at temperature T (z = x / T, computed as read;
+ * zbuf [rows][V] holds z for the top-k path when T != 1). */
+int cgk_filter_rows_t(const float* x, float T, float* zbuf, int rows, int V, int top_k,
+                      float top_p, const float* u, int u_stride, int* tokens, int tok_every,
+                      float* dist);
 
 /* ---------------------------------------- KV cache, attention, RoPE */
 /* attention mask kinds of cgk_attention */

@@ -112,6 +112,12 @@ struct RowSrc {                 // raw fp32 row
     __device__ float operator()(int j) const { return p[j]; }
 };
 
+struct ScaledSrc {              // row / T (the filtered distribution's first step)
+    const float* p;
+    float T;
+    __device__ float operator()(int j) const { return T == 1.0f ? p[j] : __fdiv_rn(p[j], T); }
+};
+
 template <class S>
 struct ExpGen {                 // expf((src - m) / T), speculative.c:61
     S src;
@@ -764,6 +770,16 @@ __device__ __forceinline__ void load_vals(const RowSrc& src, int n, float pad, f
 #pragma unroll
         for (int k = 0; k < kCh; k++) x[k] = base + k < n ? src.p[base + k] : pad;
     }
+}
+
+// scaled rows: the raw row's 16-byte loads, then the division (x / 1 == x)
+__device__ __forceinline__ void load_vals(const ScaledSrc& src, int n, float pad,
+                                          float (&x)[kCh]) {
+    load_vals(RowSrc{src.p}, n, pad, x);
+    if (src.T == 1.0f) return;
+    const int base = threadIdx.x * kCh;
+#pragma unroll
+    for (int k = 0; k < kCh; k++) x[k] = base + k < n ? __fdiv_rn(x[k], src.T) : pad;
 }
 
 __device__ __forceinline__ float vals_max(const float (&x)[kCh], EosShared& sh) {

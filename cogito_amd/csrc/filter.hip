@@ -127,12 +127,13 @@ __global__ void k_scale(const float* __restrict__ x, float* __restrict__ z, size
     if (i < n) z[i] = __fdiv_rn(x[i], T);
 }
 
-// Softmax at T = 1 of each row (speculative.c:81-90): max, expf(z - max),
-// running fp32 sum, division.
-__global__ __launch_bounds__(kThreads) void k_probs_rows(const float* __restrict__ z, int V,
-                                                         float* __restrict__ probs) {
+// Softmax at T = 1 of each row of z = x / T (speculative.c:81-90): max,
+// expf(z - max), running fp32 sum, division.  The rows of x are divided by T
+// as they are read (k_scale's operation, so z is never stored).
+__global__ __launch_bounds__(kThreads) void k_probs_rows(const float* __restrict__ x, int V,
+                                                         float T, float* __restrict__ probs) {
     __shared__ EosShared sh;
-    RowSrc src{z + (size_t)blockIdx.x * V};
+    ScaledSrc src{x + (size_t)blockIdx.x * V, T};
     float* pr = probs + (size_t)blockIdx.x * V;
     if (V <= kRound) {
         // one round: the row and its exponentials stay in registers
@@ -140,7 +141,7 @@ __global__ __launch_bounds__(kThreads) void k_probs_rows(const float* __restrict
         load_vals(src, V, -__builtin_inff(), x);
         const float m = vals_max(x, sh);
         vals_exp(x, m, 1.0f, V, e);
-        const float S = eos_sum_vals(e, ExpGen<RowSrc>{src, m, 1.0f}, V, sh);
+        const float S = eos_sum_vals(e, ExpGen<ScaledSrc>{src, m, 1.0f}, V, sh);
         const int base = threadIdx.x * kCh;
 #pragma unroll
         for (int k = 0; k < kCh; k++)
@@ -148,7 +149,7 @@ __global__ __launch_bounds__(kThreads) void k_probs_rows(const float* __restrict
         return;
     }
     float m = gen_max(src, V, sh);
-    ExpGen<RowSrc> e{src, m, 1.0f};
+    ExpGen<ScaledSrc> e{src, m, 1.0f};
     // the exponentials are evaluated once, into the output row, and summed
     // from there
     for (int j = threadIdx.x; j < V; j += kThreads) pr[j] = e(j);
@@ -834,7 +835,8 @@ extern "C" int cgk_typical_rows(const float* logits, int rows, int V, float typi
     uint32_t* skeys = (uint32_t*)(w + 4 * a);
     uint32_t* perm = (uint32_t*)(w + 5 * a);
     void* sws = w + 6 * a;
-    hipLaunchKernelGGL(k_probs_rows, dim3(rows), dim3(kThreads), 0, stream(), logits, V, probs);
+    hipLaunchKernelGGL(k_probs_rows, dim3(rows), dim3(kThreads), 0, stream(), logits, V, 1.0f,
+                       probs);
     if (launch_check("k_probs_rows")) return -1;
     hipLaunchKernelGGL(k_typ_scores, dim3(rows), dim3(kThreads), 0, stream(), probs, V, nl, terms,
                        keys);
@@ -881,6 +883,15 @@ extern "C" int cgk_scale(const float* x, float* z, size_t n, float T) {
 extern "C" int cgk_filter_rows_ex(const float* z, int rows, int V, int top_k, float top_p,
                                   const float* u, int u_stride, int* tokens, int tok_every,
                                   float* dist) {
+    return cgk_filter_rows_t(z, 1.0f, nullptr, rows, V, top_k, top_p, u, u_stride, tokens,
+                             tok_every, dist);
+}
+
+// The same over rows of x at temperature T (z = x / T): the top-p path
+// divides as it reads; the top-k path first writes z into zbuf ([rows][V]).
+extern "C" int cgk_filter_rows_t(const float* x, float T, float* zbuf, int rows, int V,
+                                 int top_k, float top_p, const float* u, int u_stride,
+                                 int* tokens, int tok_every, float* dist) {
     if (!tokens) tok_every = 0;
     if (rows <= 0 || V <= 0 || rows > 65535 || (!tok_every && !dist) || tok_every < 0 ||
         (tok_every && !u)) {
@@ -898,6 +909,15 @@ extern "C" int cgk_filter_rows_ex(const float* z, int rows, int V, int top_k, fl
         }
         int kpow2 = 64;
         while (kpow2 < top_k) kpow2 <<= 1;
+        const float* z = x;
+        if (T != 1.0f) {
+            if (!zbuf) {
+                cgx_set_error("filter: top-k at T != 1 needs a workspace for x / T");
+                return -1;
+            }
+            if (cgk_scale(x, zbuf, (size_t)rows * V, T)) return -1;
+            z = zbuf;
+        }
         return launch_top_k(z, rows, V, top_k, kpow2, top_p, u, u_stride, tokens, tok_every,
                             dist, nullptr, nullptr);
     }
@@ -913,7 +933,7 @@ extern "C" int cgk_filter_rows_ex(const float* z, int rows, int V, int top_k, fl
     float* probs = (float*)w;
     float* sorted = probs + n;
     int* ws = (int*)(sorted + n);
-    hipLaunchKernelGGL(k_probs_rows, dim3(rows), dim3(kThreads), 0, stream(), z, V, probs);
+    hipLaunchKernelGGL(k_probs_rows, dim3(rows), dim3(kThreads), 0, stream(), x, V, T, probs);
     if (launch_check("k_probs_rows")) return -1;
     if (cgk_row_sort((const uint32_t*)probs, nullptr, rows, V, 1, (uint32_t*)sorted, nullptr, ws,
                      wsb))

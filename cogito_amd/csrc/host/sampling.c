@@ -50,8 +50,7 @@ int cgx_sample_row_dev(const float* row, int V, float T, int top_k, float top_p,
             return cgk_sample_temperature_pipe(row, 1, V, T, du, out, (size_t)V);
         return cgk_sample_temperature(row, V, T, uh, out);
     }
-    if (cgk_scale(row, z, (size_t)V, T)) return -1;
-    return cgk_filter_rows_ex(z, 1, V, top_k, top_p, du, 1, out, 1, dist);
+    return cgk_filter_rows_t(row, T, z, 1, V, top_k, top_p, du, 1, out, 1, dist);
 }
 
 /* ------------------------------------------------ explicit-uniform forms */
@@ -104,8 +103,7 @@ int cgx_filtered_dist(const float* logits, int V, float T, int top_k, float top_
     if (!d || !o) return -1;
     if (uses_filters(V, top_k, top_p)) {
         float* z = (float*)cgx_scratch(CGX_SLOT_WS3, (size_t)V * 4);
-        if (!z || cgk_scale(d, z, (size_t)V, T) ||
-            cgk_filter_rows(z, 1, V, top_k, top_p, NULL, NULL, o))
+        if (!z || cgk_filter_rows_t(d, T, z, 1, V, top_k, top_p, NULL, 0, NULL, 0, o))
             return -1;
     } else if (cgk_temperature_probs(d, V, T, o)) {
         return -1;
@@ -275,12 +273,10 @@ static int verify_filtered(const float* target, const float* draft, const float*
     float* zd = z + rt * V;
     float* p = dist;
     float* q = dist + rt * V;
-    if (cgk_scale(target, zt, rt * V, T) ||
-        cgk_filter_rows_ex(zt, (int)rt, V, top_k, top_p, u + gamma, gamma + 1, bonus, gamma + 1,
-                           p))
+    if (cgk_filter_rows_t(target, T, zt, (int)rt, V, top_k, top_p, u + gamma, gamma + 1, bonus,
+                          gamma + 1, p))
         return -1;
-    if (!qdist && (cgk_scale(draft, zd, rd * V, T) ||
-                   cgk_filter_rows(zd, (int)rd, V, top_k, top_p, NULL, NULL, q)))
+    if (!qdist && cgk_filter_rows_t(draft, T, zd, (int)rd, V, top_k, top_p, NULL, 0, NULL, 0, q))
         return -1;
     return cgk_verify_chain_dist(p, qdist ? qdist : q, tokens, u, batch, gamma, V, bonus, ap,
                                  corr, out_tokens, n_accepted);
