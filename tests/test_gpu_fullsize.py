@@ -1,4 +1,6 @@
-"""GPU: the verify loops at the full shapes of configs 4 and 5 (32 layers,
+"""GPU: the verify loops at the full shapes of configs 3, 4 and 5 (config 3:
+12 layers, d = 768, 12 heads of 64, FFN 3072, V = 32000, context 1024; configs
+4 and 5: 32 layers,
 d = 4096, 32 heads over 8 KV heads, FFN 11008, INT4 weights and KV cache),
 checked through properties that hold at any size, so no CPU oracle has to
 run the 7B-shape stack:
@@ -12,7 +14,10 @@ run the 7B-shape stack:
   tokens plus the emitted one after every step (rollback);
 * the tree loop of config 5 (V = 128256, batch 4, 64-node trees, context
   2048, top-k 50) emits 1 + n tokens per sequence, n <= depth, keeps the
-  caches at the same lengths and writes -1 past the emitted tokens.
+  caches at the same lengths and writes -1 past the emitted tokens;
+* config 3's tiny stack: 5 rows at once against one at a time, and a draft
+  with the target's weights accepting every token under T = 0.8 / top-p 0.9
+  (p == q exactly through the filtered distributions).
 """
 from __future__ import annotations
 
@@ -186,3 +191,58 @@ def test_c5_tree_loop_invariants(gpu):
     gpu.cgx_tree_spec_free(sp)
     gpu.cgx_model_free(md)
     gpu.cgx_model_free(mt)
+
+
+C3 = dict(n_layers=12, d_model=768, n_heads=12, n_kv_heads=12, head_dim=64, d_ff=3072,
+          group_size=128, kv_group_size=64, rope_theta=10000.0, norm_eps=1e-5, init_std=0.02)
+
+
+def c3_model(gpu, max_seq, max_tokens, seed, layers=12):
+    cfg = CgxModelConfig(**{**C3, "n_layers": layers}, vocab=32000, max_seq=max_seq,
+                         max_tokens=max_tokens, max_batch=0)
+    m = gpu.cgx_model_new(C.byref(cfg), seed, None)
+    assert m, last_error(gpu)
+    return m
+
+
+def test_c3_stack_rows_and_identical_draft(gpu):
+    """Config 3's stack after a 1024-token context: the logits of 5 tokens at
+    once equal those of the same tokens one at a time (fp32 accumulation
+    tolerance), and a draft with the target's weights accepts every drafted
+    token with T = 0.8 and top-p 0.9 (the 768 x 6144 fused gate|up and the
+    768 x 32000 head at their real shapes)."""
+    print("C3 stack: 5 rows vs one at a time; identical draft, top-p 0.9", flush=True)
+    V, ctx, g, steps = 32000, 1024, 4, 4
+    ms = ctx + (g + 1) * (steps + 2)
+    m = c3_model(gpu, ms, g + 1, 3)
+    assert gpu.cgx_model_fill_context(m, ctx, 5) == 0, last_error(gpu)
+    toks = np.array([7, 700, 7000, 17000, 31999], np.int32)
+    assert gpu.cgx_model_forward(m, toks.ctypes.data, 5, 5, None) == 0, last_error(gpu)
+    all5 = np.zeros((5, V), np.float32)
+    assert gpu.cgx_memcpy_d2h(all5.ctypes.data, gpu.cgx_model_logits(m), all5.nbytes) == 0
+    assert np.isfinite(all5).all() and all5.std(axis=1).min() > 1e-3
+    assert gpu.cgx_model_truncate(m, ctx) == 0
+    one = np.zeros((5, V), np.float32)
+    for i in range(5):
+        assert gpu.cgx_model_forward(m, toks[i:i + 1].ctypes.data, 1, 1, None) == 0, \
+            last_error(gpu)
+        assert gpu.cgx_memcpy_d2h(one[i].ctypes.data, gpu.cgx_model_logits(m), V * 4) == 0
+    scale = float(np.abs(all5).max())
+    assert float(np.abs(one - all5).max()) <= 2e-3 * scale
+    assert gpu.cgx_model_truncate(m, ctx) == 0
+    d = c3_model(gpu, ms, 2, 3)
+    assert gpu.cgx_model_fill_context(d, ctx, 5) == 0, last_error(gpu)
+    sp = gpu.cgx_spec_new(d, m, g, 0.8, 0, 0.9)
+    assert sp and gpu.cgx_spec_set_last(sp, 5) == 0, last_error(gpu)
+    rng = np.random.default_rng(3)
+    out = np.zeros(g + 1, np.int32)
+    for s in range(steps):
+        ud = rng.random(g, dtype=np.float32)
+        uv = rng.random(g + 1, dtype=np.float32)
+        n = gpu.cgx_spec_step(sp, ud.ctypes.data, uv.ctypes.data, out.ctypes.data)
+        assert n == g, (s, n, last_error(gpu))
+        assert ((out >= 0) & (out < V)).all()
+        assert gpu.cgx_model_len(m) == ctx + (s + 1) * (g + 1)
+    gpu.cgx_spec_free(sp)
+    gpu.cgx_model_free(d)
+    gpu.cgx_model_free(m)
