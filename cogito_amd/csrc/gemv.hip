@@ -46,6 +46,7 @@ constexpr int kChunkBytes = 1024;
 // A-operand rows in LDS: 256 halfs + 16 bytes of padding, so the 16 rows a
 // ds_read_b128 touches start in different bank quads
 constexpr int kRowH = kRoundK + 8;
+constexpr int kBufWord3 = 0x00020000;    // buffer resource word 3 (raw dword access)
 
 inline hipStream_t stream() { return (hipStream_t)cgx_stream(); }
 
@@ -435,6 +436,296 @@ __global__ __launch_bounds__(64 * W, (NG == 2 && T == 2 && MP <= 5) ? 4 : 1) voi
     }
 }
 
+// ------------------------------------------------------------ streaming GEMV
+//
+// Very wide outputs at K = 4096 (an lm_head over a 128k vocabulary) with up to
+// 5 rows: a persistent grid, one 8-wave block per CU.  Wave w owns the
+// 256-row slices w and w + 8 of K for the whole launch.  A block walks a
+// contiguous run of column units (two layout tiles, 32 columns) and keeps the
+// A operands of the current scale group in registers, in MFMA layout; they
+// are rebuilt only when a unit enters a new group (every gs / 32 units), so
+// the rows are prepared once per group rather than once per 32 columns.  The
+// next unit's scales and weights are in flight while a unit is multiplied;
+// the wave partials of a unit are summed in a fixed order behind one barrier
+// (double-buffered), so results do not depend on timing.
+//
+// Measured against the block-per-tile kernel (7B rows, weights rotated over
+// the MALL): 4096 x 128256 at 5 rows 61.5 -> 53.1 us, at 1 row 47.9 -> 46.3
+// us.  Runs of about 3 units per block (4096 x 22016) lose to it (17.0 vs
+// 20.7 us): a unit's decode, MFMAs and reduction on 2 waves per SIMD take
+// about as long as its 64 KiB take to arrive, and the first unit waits for
+// the rows' preparation.
+constexpr int kStreamWaves = 8;
+constexpr int kStreamT = 2;                           // layout tiles per unit
+constexpr int kStreamK = 2 * kStreamWaves * kRoundK;  // 4096
+constexpr int kXRow = kRoundK + 4;                    // padded fp32 row of a slice
+constexpr int kStreamIdle = 1 << 30;                  // byte offset past any matrix taken
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_s_waitcnt(0xc07f);    // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int MP, int PRO, int EPI>
+__global__ __launch_bounds__(64 * kStreamWaves, 1) void k_gemv_stream(MfmaArgs a, int nunits) {
+    constexpr int W = kStreamWaves, T = kStreamT;
+    constexpr int RW = 2;                        // slices per wave
+    constexpr int R = W * RW;                    // 256-row slices of K
+    static_assert(MP <= 5, "x slices of up to 5 rows in LDS");
+    static_assert(EPI != kEpiSwiGlu, "one scale group per unit");
+    __shared__ float s_x[R][MP][kXRow];          // x (times the RMSNorm weight), by slice
+    __shared__ _Float16 s_ab[W][2 * MP * kRowH]; // A staging of one slice per wave
+    __shared__ float s_red[2][W][T][MP][16];     // wave partials of a unit, double-buffered
+    __shared__ float s_ssq[W][MP];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const NibConst nk = nib_consts();
+    const int M = a.M;
+    constexpr int nchunks = kStreamK / kChunkK;
+    // XCD-aware: the blocks of one XCD take neighbouring runs of units, which
+    // share scale rows (block b runs on XCD b % 8)
+    const int nblk = gridDim.x;
+    const int per_xcd = nblk / 8;
+    const int sb = (int)blockIdx.x < per_xcd * 8
+                       ? (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8)
+                       : (int)blockIdx.x;
+    const int u0 = (int)((long long)sb * nunits / nblk);
+    const int u1 = (int)((long long)(sb + 1) * nunits / nblk);
+    const int g4 = lane >> 4;
+    const int hl8 = (lane >> 3) & 1;
+    const int mrow8 = (lane & 7) < M ? (lane & 7) : M - 1;
+    _Float16* abuf = s_ab[wave];
+
+    auto group_of = [&](int u) __attribute__((always_inline)) { return u * T * 16 / a.gs; };
+    // whether unit u (inside the run, after its first unit) enters a new group
+    auto enters = [&](int u) __attribute__((always_inline)) {
+        return u > u0 && u < u1 && group_of(u) != group_of(u - 1);
+    };
+    // the lane's 4 scales in each of the wave's slices, for the group of unit u
+    typedef float4 SRow[RW];
+    auto load_s = [&](int u, SRow& dst) __attribute__((always_inline)) {
+        const float* row = a.scales_t + (size_t)group_of(u) * kStreamK;
+#pragma unroll
+        for (int i = 0; i < RW; i++)
+            dst[i] = *(const float4*)(row + (wave + i * W) * kRoundK + 4 * lane);
+    };
+    // weights through a buffer resource: an idle unit (past the end of the
+    // run) reads out of range, which returns zeros without touching memory,
+    // so every unit issues the same loads and the compiler's waits count
+    // them exactly (conditional loads made it wait for all of them)
+    typedef u32x4 WBuf[RW][T][2];
+    WBuf wa, wb;
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.w, (short)0, (int)((size_t)a.N / 16 * nchunks * kChunkBytes), kBufWord3);
+    auto load_w = [&](int u, WBuf& dst) __attribute__((always_inline)) {
+        const int base = u < u1 ? u * T * nchunks * kChunkBytes : kStreamIdle;
+#pragma unroll
+        for (int i = 0; i < RW; i++)
+#pragma unroll
+            for (int j = 0; j < T; j++)
+#pragma unroll
+                for (int c = 0; c < 2; c++) {
+                    const int vo = (j * nchunks + 2 * (wave + i * W) + c) * kChunkBytes + 16 * lane;
+                    dst[i][j][c] = __builtin_bit_cast(
+                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, vo + base, 0, 2));
+                }
+    };
+    // a unit's loads: the scales of a group it enters (at most one pending:
+    // a group spans at least two units), then its weights
+    SRow sp;
+    auto issue = [&](int u, WBuf& dst) __attribute__((always_inline)) {
+        if (enters(u)) load_s(u, sp);
+        load_w(u, dst);
+    };
+
+    // ---- prologue: the wave's slices of x and the first group's scales,
+    // then the first two units' loads (loads complete in issue order, so the
+    // preparation waits for these only)
+    const bool work = u0 < u1;
+    float amax = 0.0f;
+    float ssq[MP];
+#pragma unroll
+    for (int m = 0; m < MP; m++) ssq[m] = 0.0f;
+    SRow s0;
+    {
+        float4 xv[RW][MP], nwv[RW];
+#pragma unroll
+        for (int i = 0; i < RW; i++) {
+            const int r = wave + i * W;
+#pragma unroll
+            for (int m = 0; m < MP; m++)
+                // rows past M read row M - 1 (zeroed where used): no
+                // branches between the loads
+                xv[i][m] = *(const float4*)(a.x + (size_t)(m < M ? m : M - 1) * a.ldx + r * kRoundK +
+                                            4 * lane);
+            nwv[i] = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+            if (PRO == kProRmsNorm) nwv[i] = *(const float4*)(a.nw + r * kRoundK + 4 * lane);
+        }
+        if (work) load_s(u0, s0);
+        // in unit order, as the loop issues them (its waits assume it)
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(u0, wa);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(u0 + 1, wb);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < RW; i++) {
+            const int r = wave + i * W;
+#pragma unroll
+            for (int m = 0; m < MP; m++) {
+                const float4 t = m < M ? xv[i][m] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (PRO == kProRmsNorm) {
+                    ssq[m] = fmaf(t.x, t.x, ssq[m]);
+                    ssq[m] = fmaf(t.y, t.y, ssq[m]);
+                    ssq[m] = fmaf(t.z, t.z, ssq[m]);
+                    ssq[m] = fmaf(t.w, t.w, ssq[m]);
+                }
+                // the RMSNorm weight multiplies x once here (1 / rms is
+                // applied to the sums at the end)
+                const float4 n = nwv[i];
+                const float4 v = make_float4(t.x * n.x, t.y * n.y, t.z * n.z, t.w * n.w);
+                *(float4*)&s_x[r][m][4 * lane] = v;
+                amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            }
+        }
+    }
+    if (PRO == kProRmsNorm) {
+#pragma unroll
+        for (int m = 0; m < MP; m++) {
+            const float v = wave_sum(ssq[m]);
+            if (lane == 0) s_ssq[wave][m] = v;
+        }
+    }
+    amax = wave_max_nonneg(amax);
+
+    // ---- A operands from a group's scales: a[m][k] = x[m][k] s[k] 2^E as
+    // hi + lo fp16 (hi rounded toward zero, lo the rounded remainder), each
+    // lane converting its 4 columns of every row into the wave's staging
+    // rows, read back in MFMA layout (A rows 0-7 the hi parts of rows 0-7,
+    // rows 8-15 the lo parts).  2^E makes |a| < 2^15 over the wave's slices.
+    f16x8 A[RW][8];
+    float down;
+    auto build = [&](const SRow& sr) __attribute__((always_inline)) {
+        float smax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < RW; i++)
+            smax = fmaxf(smax, fmaxf(fmaxf(fabsf(sr[i].x), fabsf(sr[i].y)),
+                                     fmaxf(fabsf(sr[i].z), fabsf(sr[i].w))));
+        const float bound = amax * wave_max_nonneg(smax);
+        int E = 0;
+        if (bound > 0.0f && bound < __builtin_inff()) E = 14 - ilogbf(bound);
+        E = E > 100 ? 100 : (E < -100 ? -100 : E);
+        const float up = ldexpf(1.0f, E);
+        down = ldexpf(1.0f, -E);
+#pragma unroll
+        for (int i = 0; i < RW; i++) {
+            const int r = wave + i * W;
+            const float s0 = sr[i].x * up, s1 = sr[i].y * up, s2 = sr[i].z * up, s3 = sr[i].w * up;
+#pragma unroll
+            for (int m = 0; m < MP; m++) {
+                if (m < M) {
+                    const float4 xv = *(const float4*)&s_x[r][m][4 * lane];
+                    const float v0 = xv.x * s0, v1 = xv.y * s1, v2 = xv.z * s2, v3 = xv.w * s3;
+                    const f16x2 h01 = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(v0, v1));
+                    const f16x2 h23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(v2, v3));
+                    const f16x2 l01 = __builtin_bit_cast(
+                        f16x2, __builtin_amdgcn_cvt_pkrtz(v0 - (float)h01[0], v1 - (float)h01[1]));
+                    const f16x2 l23 = __builtin_bit_cast(
+                        f16x2, __builtin_amdgcn_cvt_pkrtz(v2 - (float)h23[0], v3 - (float)h23[1]));
+                    *(uint2*)(abuf + (0 * MP + m) * kRowH + 4 * lane) =
+                        make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
+                    *(uint2*)(abuf + (1 * MP + m) * kRowH + 4 * lane) =
+                        make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
+                }
+            }
+            wave_lds_sync();
+#pragma unroll
+            for (int kb = 0; kb < 8; kb++)
+                A[i][kb] = *(const f16x8*)(abuf + (hl8 * MP + mrow8) * kRowH + 32 * kb + 8 * g4);
+            // the staging rows are read before the next slice overwrites them
+            wave_lds_sync();
+        }
+    };
+    wave_lds_sync();                 // s_x
+    if (work) build(s0);
+    __syncthreads();                 // s_ssq
+
+    // the output this thread finishes for each unit, spread over the waves
+    // so that no wave carries the whole epilogue; and its 1 / rms
+    constexpr int kOuts = T * MP * 16;
+    static_assert(kOuts <= 64 * W, "one output per thread");
+    const int oe = lane * W + wave;
+    const int oj = oe / (MP * 16), orow = (oe / 16) % MP, ocol = oe % 16;
+    const bool outer = oe < kOuts && orow < M;
+    float rs = 1.0f;
+    if (PRO == kProRmsNorm && outer) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; w++) ss += s_ssq[w][orow];
+        rs = 1.0f / sqrtf(ss / (float)kStreamK + a.eps);
+    }
+
+    auto unit = [&](int u, WBuf& w, int buf) __attribute__((always_inline)) {
+        // idle units (past the run) only keep the loads in step
+        const bool live = u < u1;
+        if (enters(u)) build(sp);
+        f32x4 acc[T];
+#pragma unroll
+        for (int j = 0; j < T; j++) acc[j] = (f32x4)(0.0f);
+        if (live) {
+#pragma unroll
+            for (int i = 0; i < RW; i++)
+#pragma unroll
+                for (int kb = 0; kb < 8; kb++) {
+#pragma unroll
+                    for (int j = 0; j < T; j++) {
+                        const u32x4 wv = w[i][j][kb >> 2];
+                        const uint32_t word = (kb & 3) == 0 ? wv.x : (kb & 3) == 1 ? wv.y
+                                            : (kb & 3) == 2 ? wv.z : wv.w;
+                        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i][kb], nib_to_f16(word, nk),
+                                                                        acc[j], 0, 0, 0);
+                    }
+                    // decode k block by k block (all at once would hold 16
+                    // registers per tile and block)
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+        }
+        // the loads of unit u + 2 into the registers just consumed
+        issue(u + 2, w);
+        if (!live) return;
+        // hi + lo halves (D rows r and r + 8, 32 lanes apart: lanes 0-31
+        // take lane l + 32's value through v_permlane32_swap), then 2^-E
+#pragma unroll
+        for (int j = 0; j < T; j++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const auto sw = __builtin_amdgcn_permlane32_swap(
+                    __float_as_uint(acc[j][v]), __float_as_uint(acc[j][v]), false, false);
+                const float t = acc[j][v] + __uint_as_float(sw[1]);
+                const int row = 4 * g4 + v;
+                if (g4 < 2 && row < MP) s_red[buf][wave][j][row][lane & 15] = t * down;
+            }
+        __syncthreads();
+        if (outer) {
+            float v = 0.0f;
+#pragma unroll
+            for (int wv = 0; wv < W; wv++) v += s_red[buf][wv][oj][orow][ocol];
+            v *= rs;
+            float* yp = a.y + (size_t)orow * a.ldy + (u * T + oj) * 16 + ocol;
+            *yp = EPI == kEpiAccumulate ? *yp + v : v;
+        }
+    };
+    // whole pairs of units, the last padded with an idle unit: a unit
+    // skipped inside the loop would make the compiler assume the next
+    // unit's loads were the last ones issued and wait for all of them
+    for (int u = u0; u < u1; u += 2) {
+        unit(u, wa, 0);
+        unit(u + 1, wb, 1);
+    }
+}
+
 // Repack cogito's row-major nibbles (two's complement, flat) into layout 3.
 // One thread per output u32 word.
 __global__ void k_repack_mfma(const uint8_t* __restrict__ flat, int K, int N, int paired,
@@ -520,6 +811,52 @@ int launch_t(const MfmaArgs& a, int nblocks) {
     return launch_check("k_gemv_mfma");
 }
 
+// CUs of the current device: the streaming GEMV's grid.
+int stream_blocks() {
+    static int cus = 0;
+    if (cus <= 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+            cus = n;
+        if (cus <= 0) cus = 256;
+    }
+    return cus;
+}
+
+// Units on the busiest CU from which the streaming GEMV takes a product
+// (0: never).
+int g_stream_min_units = 8;
+
+template <int MP, int PRO, int EPI>
+int launch_stream(const MfmaArgs& a) {
+    const int nunits = a.N / (16 * kStreamT);
+    const int nb = stream_blocks() < nunits ? stream_blocks() : nunits;
+    hipLaunchKernelGGL((k_gemv_stream<MP, PRO, EPI>), dim3(nb), dim3(64 * kStreamWaves), 0,
+                       stream(), a, nunits);
+    return launch_check("k_gemv_stream");
+}
+
+// Whether the streaming GEMV takes y = x @ W: K = 4096, up to 5 rows, one
+// scale group per unit and at least two units per group, the matrix within
+// the idle offset, and enough units on the busiest CU (ceil(units / CUs) >=
+// the setting) to outweigh its preparation.
+bool stream_takes(const MfmaArgs& a, int epi) {
+    if (g_stream_min_units <= 0 || epi == kEpiSwiGlu || a.K != kStreamK || a.M > 5 ||
+        a.gs % (32 * kStreamT) || (size_t)a.K * a.N / 2 >= (size_t)kStreamIdle ||
+        a.N % (16 * kStreamT))
+        return false;
+    return a.N / (16 * kStreamT) > (g_stream_min_units - 1) * stream_blocks();
+}
+
+template <int PRO, int EPI>
+int launch_stream_pe(const MfmaArgs& a) {
+    if (a.M == 1) return launch_stream<1, PRO, EPI>(a);
+    if (a.M == 2) return launch_stream<2, PRO, EPI>(a);
+    if (a.M <= 4) return launch_stream<4, PRO, EPI>(a);
+    return launch_stream<5, PRO, EPI>(a);
+}
+
 template <int MP, int PRO, int EPI>
 int launch_mp(const MfmaArgs& a, int T) {
     const int tiles = a.N / 16;
@@ -578,7 +915,6 @@ int launch_pe(const MfmaArgs& a, int T) {
 // gate|up pair).
 
 constexpr int kGemmWaves = 4;
-constexpr int kBufWord3 = 0x00020000;    // buffer resource word 3 (raw dword access)
 constexpr int kGemmTiles = 4;            // column tiles per wave
 constexpr int kGemmRowH = kChunkK + 8;   // LDS pitch (halfs) of an A row
 
@@ -1041,7 +1377,13 @@ extern "C" int cgk_gemv_mfma(const float* x, int ldx, int M, int K, int N, int g
         a.nw = nw; a.eps = eps;
         a.ff = N / 2;
         int rc;
-        if (pro == kProRmsNorm) {
+        if (stream_takes(a, epi)) {
+            rc = pro == kProRmsNorm
+                     ? (epi == kEpiAccumulate ? launch_stream_pe<kProRmsNorm, kEpiAccumulate>(a)
+                                              : launch_stream_pe<kProRmsNorm, kEpiStore>(a))
+                     : (epi == kEpiAccumulate ? launch_stream_pe<kProNone, kEpiAccumulate>(a)
+                                              : launch_stream_pe<kProNone, kEpiStore>(a));
+        } else if (pro == kProRmsNorm) {
             rc = epi == kEpiSwiGlu ? launch_pe<kProRmsNorm, kEpiSwiGlu>(a, T)
                : epi == kEpiAccumulate ? launch_pe<kProRmsNorm, kEpiAccumulate>(a, T)
                : launch_pe<kProRmsNorm, kEpiStore>(a, T);
@@ -1053,6 +1395,15 @@ extern "C" int cgk_gemv_mfma(const float* x, int ldx, int M, int K, int N, int g
         if (rc) return rc;
     }
     return 0;
+}
+
+// Test hook: the units on the busiest CU from which the streaming GEMV takes
+// a product (0 never, 1 every product it supports); returns the previous
+// value, and a negative argument only reads it.
+extern "C" int cgx_gemv_stream_min_units(int units) {
+    const int old = g_stream_min_units;
+    if (units >= 0) g_stream_min_units = units;
+    return old;
 }
 
 // 1 when cgk_gemm_int4 takes this product: 8 layout tiles per block within

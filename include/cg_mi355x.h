@@ -258,6 +258,12 @@ int cgx_attention_rope_append_dev(const float* qkv, int ldq, const float* rope, 
  * cache append inside the attention launch, 0 as launches of their own (the
  * same cache contents); returns the previous setting (-1 only reads it). */
 int cgx_decoder_fused_attention(int on);
+/* Test hook, no reference counterpart: the INT4 GEMV takes the persistent
+ * streaming kernel for K = 4096 and up to 5 rows once the busiest CU gets at
+ * least this many 32-column units (default 8: a 64k- or 128k-vocabulary
+ * lm_head; 0 never, 1 every product it supports); returns the previous value
+ * (-1 only reads it). */
+int cgx_gemv_stream_min_units(int units);
 int cgx_attention_int4_kv_batch_dev(const float* Q, int B, int Nq, int H,
                                     cg_kv_cache_int4* cache, int slot0, const int* nk,
                                     int mask_kind, const unsigned long long* anc, int tw,

@@ -106,6 +106,56 @@ def test_gemm_mfma_vs_oracle(gpu, oracle, rng, K, N, gs, M):
     _gemv_case(gpu, oracle, rng, K, N, gs, M, 3, 4)
 
 
+def _stream_case(gpu, oracle, rng, K, N, gs, M, min_units):
+    """The persistent streaming GEMV (taken at K = 4096, up to 5 rows, once
+    the output has min_units 32-column units per CU) against the oracle, and
+    against the block-per-tile kernel on the same inputs (both carry the rows
+    as hi + lo fp16: within 1e-5 of max|y| per row)."""
+    # nibble bytes and fp16-valued scales drawn directly (a normal draw of a
+    # 4096 x 128256 matrix would take 2 GiB)
+    data = rng.integers(0, 256, K * N // 2, dtype=np.uint8)
+    scales = rng.uniform(0.005, 0.02, K * N // gs).astype(np.float16).astype(np.float32)
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    y_ref = oracle_matmul(oracle, x, data, scales, K, N, gs)
+    hq, keep = host_quant_from_arrays(data, scales, K, N, gs)
+    dq = gpu.cgx_quant_to_device_layout(C.byref(hq), 3)
+    assert dq, last_error(gpu)
+    dx = DeviceArray.from_numpy(gpu, x)
+    dy = DeviceArray(gpu, M * N * 4)
+    old = gpu.cgx_gemv_stream_min_units(-1)
+    ys = []
+    try:
+        for units in (min_units, 0):
+            gpu.cgx_gemv_stream_min_units(units)
+            for rep in range(2):         # a second call on the same buffers
+                gpu.cgx_memset(dy.ptr, 0xFF, M * N * 4)
+                assert gpu.cgx_matmul_int4_dev_kernel(dx.ptr, M, dq, dy.ptr, 3) == 0, \
+                    last_error(gpu)
+                assert gpu.cgx_synchronize() == 0, last_error(gpu)
+                y = dy.numpy(np.float32, (M, N))
+                assert np.all(np.isfinite(y))
+                assert rel_err_rows(y, y_ref) <= TOL
+            ys.append(y)
+    finally:
+        gpu.cgx_gemv_stream_min_units(old)
+    assert rel_err_rows(ys[0], ys[1]) <= 1e-5
+    gpu.cg_tensor_quant_free(dq)
+
+
+@pytest.mark.parametrize("N,M", [(128256, 5), (65536, 1), (65536, 3)])
+def test_gemv_stream_wide_vocab(gpu, oracle, rng, N, M):
+    # the default dispatch: a 64k / 128k-column lm_head at 1-5 rows
+    _stream_case(gpu, oracle, rng, 4096, N, 128, M, 8)
+
+
+@pytest.mark.parametrize("N,gs,M", [(4096, 128, 5), (22016, 128, 2), (2048, 64, 4),
+                                    (6144, 256, 1), (4160, 64, 5)])
+def test_gemv_stream_forced(gpu, oracle, rng, N, gs, M):
+    # every supported product through the streaming kernel: runs of one to
+    # three units (odd runs end with an idle unit), groups of two units
+    _stream_case(gpu, oracle, rng, 4096, N, gs, M, 1)
+
+
 def test_gemv_mfma_wide_dynamic_range(gpu, oracle, rng):
     # activations spanning many binades, a zero row, huge and tiny scales:
     # the per-round power-of-two scaling keeps the fp16 terms in range

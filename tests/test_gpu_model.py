@@ -107,6 +107,27 @@ def test_model_forward_k_split_vs_oracle(gpu, oracle, rng):
     gpu.cgx_model_free(m)
 
 
+def test_model_forward_stream_gemv_vs_oracle(gpu, oracle, rng):
+    # d_model 4096 with the streaming GEMV taking every product it supports
+    # (cgx_gemv_stream_min_units(1)): wqkv and lm_head with the RMSNorm
+    # prologue, wo accumulating into the residual
+    cfg = Cfg(n_layers=1, d_model=4096, n_heads=32, n_kv_heads=8, head_dim=128, d_ff=1024,
+              vocab=4096, group_size=128, kv_group_size=128, max_seq=64, max_tokens=8,
+              init_std=0.02)
+    m = new_model(gpu, cfg, 13)
+    om = OracleModel(oracle, cfg, 13)
+    old = gpu.cgx_gemv_stream_min_units(1)
+    try:
+        for M in (5, 1, 3):
+            toks = rng.integers(0, cfg.vocab, M).astype(np.int32)
+            assert gpu.cgx_model_forward(m, toks.ctypes.data, M, M, None) == 0, last_error(gpu)
+            err = rel_err_rows(logits_np(gpu, m, M, cfg.vocab), om.forward(toks))
+            assert err <= TOL, (M, err)
+    finally:
+        gpu.cgx_gemv_stream_min_units(old)
+    gpu.cgx_model_free(m)
+
+
 @pytest.mark.parametrize("cfg", [TINY, Cfg(n_layers=1, d_model=512, n_heads=8, n_kv_heads=2,
                                             head_dim=128, d_ff=768, vocab=2048, group_size=128,
                                             kv_group_size=128, max_seq=300, max_tokens=5,
