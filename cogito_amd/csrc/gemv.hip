@@ -929,7 +929,8 @@ struct GemmArgs {
     const float* stats;       // [M][nstat][2] partial (max|x*nw|, sum x^2) of x
     int nstat;                //   per 256 columns, written by the producer's reduction
     float smax, eps;          // the row factors' scale bound and RMSNorm epsilon
-    float* part;              // [ksplit][M][N] partial sums, logical columns
+    float* part;              // [ksplit][M][N] partial sums, logical columns (y itself
+                              // for one split storing rows of N floats)
     int ksteps;               // 128-row chunks per split
     int ff;                   // SwiGLU pair: N / 2
 };
@@ -1442,8 +1443,12 @@ extern "C" int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int g
     ksplit = ksplit < 1 ? 1 : (ksplit > 16 ? 16 : ksplit);
     const int ksteps = (nchunks + ksplit - 1) / ksplit;
     ksplit = (nchunks + ksteps - 1) / ksteps;
+    // one split storing plain rows (the lm_head of a tree verify): the GEMM
+    // writes y itself, and no reduction pass copies it
+    const bool direct = ksplit == 1 && epi == kEpiStore && !stats_out && ldy == N;
     const size_t row_bytes = (((size_t)M * 8) + 255) & ~(size_t)255;
-    char* ws = (char*)cgx_scratch(CGX_SLOT_WS5, row_bytes + (size_t)ksplit * M * N * 4);
+    char* ws = (char*)cgx_scratch(CGX_SLOT_WS5,
+                                  row_bytes + (direct ? 0 : (size_t)ksplit * M * N * 4));
     if (!ws) return -1;
     GemmArgs a;
     a.x = x; a.ldx = ldx; a.M = M; a.K = K; a.N = N; a.gs = gs;
@@ -1455,7 +1460,7 @@ extern "C" int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int g
     a.nstat = nstat_in;
     a.smax = smax;
     a.eps = eps;
-    a.part = (float*)(ws + row_bytes);
+    a.part = direct ? y : (float*)(ws + row_bytes);
     a.ksteps = ksteps;
     a.ff = N / 2;
     if (!stats_in) {
@@ -1475,7 +1480,7 @@ extern "C" int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int g
         rc = RT == 1 ? launch_gemm<1, 1>(a, grid) : RT == 2 ? launch_gemm<2, 1>(a, grid)
            : RT == 3 ? launch_gemm<3, 1>(a, grid) : launch_gemm<4, 1>(a, grid);
     }
-    if (rc) return rc;
+    if (rc || direct) return rc;
     const int Nout = paired ? N / 2 : N;
     const size_t outs = (size_t)M * Nout;
     const int blocks = (int)((outs + 255) / 256);
