@@ -1905,9 +1905,9 @@ extern "C" int cgk_verify_pipe_supported(int batch, int gamma, int V, float T) {
 }
 
 // Workspace of the allocation-free entry point (cgk_verify_pipe_static): a
-// file-scope device array.  Every GPU the library runs on holds its own copy
-// at its own address until the process ends; host code reaches it only
-// through the address hipGetSymbolAddress returns for that device.
+// file-scope device array.  Each GPU it is used on holds its own copy at its
+// own address until the process ends; host code reaches it only through the
+// address hipGetSymbolAddress returns with that device current.
 constexpr size_t kStaticWsBytes = (size_t)32 << 20;
 static __device__ __align__(256) unsigned char scratch[kStaticWsBytes];
 constexpr int kMaxDevices = 64;
@@ -1919,8 +1919,22 @@ extern "C" int cgk_verify_static_init(int device) {
         return -1;
     }
     if (g_static_ws[device]) return 0;
+    // the symbol's address on `device`: that device current for the lookup,
+    // the caller's current device restored after it
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) {
+        (void)hipGetLastError();
+        cgx_set_error("verify workspace: no current device");
+        return -1;
+    }
+    if (cur != device && hipSetDevice(device) != hipSuccess) {
+        (void)hipGetLastError();
+        cgx_set_error("verify workspace: device %d cannot be made current", device);
+        return -1;
+    }
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != device) (void)hipSetDevice(cur);
     if (e != hipSuccess || !p) {
         (void)hipGetLastError();
         cgx_set_error("verify workspace: hipGetSymbolAddress failed on device %d: %s", device,
