@@ -87,6 +87,7 @@ def test_sample_top_p_bitexact(gpu, oracle, rng, V, p, kind):
 
 
 SORT_CASES = [(1, 1, "full"), (3, 100, "dups"), (2, 4096, "full"), (2, 4097, "dups"),
+              (5, 32000, "probs"), (2, 32768, "full"), (1, 32767, "dups"),
               (4, 40000, "probs"), (1, 128256, "probs"), (2, 70001, "dups")]
 
 
