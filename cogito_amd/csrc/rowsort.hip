@@ -4,7 +4,8 @@
 // The samplers that order a whole vocabulary row (top-p by probability,
 // typical sampling by score) sort with it, so no row size is bounded by LDS.
 // Least-significant-digit first, 8-bit digits, four passes.  Each pass is two
-// launches over tiles of 4096 keys (grid: tiles x rows):
+// launches over tiles of 2048 keys (rows of more than 65536 keys: 4096)
+// (grid: tiles x rows):
 //   k_rs_hist     the tile's digit counts -> hist[row][tile][256];
 //   k_rs_scatter  the tile's output offsets (counts of every tile before it,
 //                 and of the digits before its own in the sort order), the
@@ -25,10 +26,14 @@ namespace {
 
 constexpr int kT = 256;                 // threads per block (4 waves)
 constexpr int kWv = kT / 64;
-constexpr int kItems = 16;              // keys per thread
-constexpr int kTile = kT * kItems;      // keys per block
 constexpr int kBins = 256;
-constexpr int kMaxTiles = 1024;         // rows up to 4 M keys
+constexpr int kMaxTiles = 1024;         // rows up to 4 M keys (tiles of 4096)
+constexpr int kSmallRow = 65536;        // rows up to this many keys: 8 keys a thread
+constexpr int kHistBatch = 16;          // tile counts loaded per round trip
+
+// Keys per thread for a row of n keys: short rows take smaller tiles, so more
+// workgroups share a row and each walks fewer keys in sequence.
+inline int row_items(int n) { return n <= kSmallRow ? 8 : 16; }
 
 inline hipStream_t stream() { return (hipStream_t)cgx_stream(); }
 
@@ -54,10 +59,12 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, bool valid) {
 }
 
 // Position of item q of lane `lane` in wave w of tile `tile`.
+template <int kItems>
 __device__ __forceinline__ int tile_pos(int tile, int w, int q, int lane) {
-    return tile * kTile + w * (kItems * 64) + q * 64 + lane;
+    return tile * (kT * kItems) + w * (kItems * 64) + q * 64 + lane;
 }
 
+template <int kItems>
 __global__ __launch_bounds__(kT) void k_rs_hist(const uint32_t* __restrict__ keys, int n,
                                                 int shift, int ntiles,
                                                 uint32_t* __restrict__ hist) {
@@ -70,12 +77,12 @@ __global__ __launch_bounds__(kT) void k_rs_hist(const uint32_t* __restrict__ key
     uint32_t kk[kItems];
 #pragma unroll
     for (int q = 0; q < kItems; q++) {
-        const int p = tile_pos(tile, w, q, lane);
+        const int p = tile_pos<kItems>(tile, w, q, lane);
         kk[q] = p < n ? src[p] : 0u;
     }
 #pragma unroll
     for (int q = 0; q < kItems; q++) {
-        const bool valid = tile_pos(tile, w, q, lane) < n;
+        const bool valid = tile_pos<kItems>(tile, w, q, lane) < n;
         const uint32_t d = (kk[q] >> shift) & 255u;
         const uint64_t m = match_digit(d, valid);
         if (valid && lane == __ffsll((unsigned long long)m) - 1)
@@ -103,7 +110,7 @@ __device__ __forceinline__ uint32_t block_excl_256(uint32_t v, uint32_t* part) {
     return off + x - v;
 }
 
-template <bool kDesc, bool kPay>
+template <int kItems, bool kDesc, bool kPay>
 __global__ __launch_bounds__(kT) void k_rs_scatter(const uint32_t* __restrict__ kin,
                                                    const uint32_t* __restrict__ pin, int n,
                                                    int shift, int ntiles,
@@ -122,18 +129,26 @@ __global__ __launch_bounds__(kT) void k_rs_scatter(const uint32_t* __restrict__ 
     uint32_t kk[kItems], pp[kItems], rk[kItems];
 #pragma unroll
     for (int q = 0; q < kItems; q++) {
-        const int p = tile_pos(tile, w, q, lane);
+        const int p = tile_pos<kItems>(tile, w, q, lane);
         kk[q] = p < n ? kin[rb + p] : 0u;
         if (kPay) pp[q] = p < n ? (pin ? pin[rb + p] : (uint32_t)p) : 0u;
     }
 
-    // digit d = t: keys of d in earlier tiles, and in the whole row
+    // digit d = t: keys of d in earlier tiles, and in the whole row; the
+    // tiles' counts are loaded kHistBatch at a time, so a row of up to
+    // kHistBatch tiles costs one round trip
     const uint32_t* hr = hist + (size_t)row * ntiles * kBins;
     uint32_t pre = 0, tot = 0;
-    for (int b = 0; b < ntiles; b++) {
-        const uint32_t c = hr[(size_t)b * kBins + t];
-        tot += c;
-        pre += b < tile ? c : 0u;
+    for (int b0 = 0; b0 < ntiles; b0 += kHistBatch) {
+        uint32_t c[kHistBatch];
+#pragma unroll
+        for (int i = 0; i < kHistBatch; i++)
+            c[i] = b0 + i < ntiles ? hr[(size_t)(b0 + i) * kBins + t] : 0u;
+#pragma unroll
+        for (int i = 0; i < kHistBatch; i++) {
+            tot += c[i];
+            pre += b0 + i < tile ? c[i] : 0u;
+        }
     }
     // digits in sort order: position o(d) = d (ascending) or 255 - d
     ord[kDesc ? 255 - t : t] = tot;
@@ -148,7 +163,7 @@ __global__ __launch_bounds__(kT) void k_rs_scatter(const uint32_t* __restrict__ 
     const uint64_t lt = (1ull << lane) - 1ull;
 #pragma unroll
     for (int q = 0; q < kItems; q++) {
-        const bool valid = tile_pos(tile, w, q, lane) < n;
+        const bool valid = tile_pos<kItems>(tile, w, q, lane) < n;
         const uint32_t d = (kk[q] >> shift) & 255u;
         const uint64_t m = match_digit(d, valid);
         rk[q] = 0;
@@ -172,7 +187,7 @@ __global__ __launch_bounds__(kT) void k_rs_scatter(const uint32_t* __restrict__ 
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < kItems; q++) {
-        if (tile_pos(tile, w, q, lane) >= n) continue;
+        if (tile_pos<kItems>(tile, w, q, lane) >= n) continue;
         const uint32_t d = (kk[q] >> shift) & 255u;
         const uint32_t pos = goff[d] + wcnt[w][d] + rk[q];
         if (pos >= (uint32_t)n) continue;   // unreachable with consistent counts
@@ -183,10 +198,49 @@ __global__ __launch_bounds__(kT) void k_rs_scatter(const uint32_t* __restrict__ 
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
+template <int kItems>
+int row_sort_passes(const uint32_t* kin, const uint32_t* pin, int rows, int n, int desc,
+                    uint32_t* kout, uint32_t* pout, uint32_t* const kb[2], uint32_t* const pb[2],
+                    uint32_t* hist) {
+    const int ntiles = (n + kT * kItems - 1) / (kT * kItems);
+    const dim3 grid(ntiles, rows);
+    const uint32_t* ks = kin;
+    const uint32_t* ps = pin;
+    for (int pass = 0; pass < 4; pass++) {
+        const int shift = 8 * pass;
+        uint32_t* kd = pass == 3 ? kout : kb[pass & 1];
+        uint32_t* pd = pass == 3 ? pout : pb[pass & 1];
+        hipLaunchKernelGGL(k_rs_hist<kItems>, grid, dim3(kT), 0, stream(), ks, n, shift, ntiles,
+                           hist);
+        if (launch_check("k_rs_hist")) return -1;
+        if (desc && pout)
+            hipLaunchKernelGGL((k_rs_scatter<kItems, true, true>), grid, dim3(kT), 0, stream(),
+                               ks, ps, n, shift, ntiles, hist, kd, pd);
+        else if (desc)
+            hipLaunchKernelGGL((k_rs_scatter<kItems, true, false>), grid, dim3(kT), 0, stream(),
+                               ks, ps, n, shift, ntiles, hist, kd, pd);
+        else if (pout)
+            hipLaunchKernelGGL((k_rs_scatter<kItems, false, true>), grid, dim3(kT), 0, stream(),
+                               ks, ps, n, shift, ntiles, hist, kd, pd);
+        else
+            hipLaunchKernelGGL((k_rs_scatter<kItems, false, false>), grid, dim3(kT), 0, stream(),
+                               ks, ps, n, shift, ntiles, hist, kd, pd);
+        if (launch_check("k_rs_scatter")) return -1;
+        ks = kd;
+        ps = pd;
+    }
+    return 0;
+}
+
+size_t row_tiles(int n) {
+    const size_t tile = (size_t)kT * row_items(n);
+    return ((size_t)n + tile - 1) / tile;
+}
+
 }  // namespace
 
 extern "C" size_t cgk_row_sort_ws(int rows, int n, int with_payload) {
-    const size_t ntiles = ((size_t)n + kTile - 1) / kTile;
+    const size_t ntiles = row_tiles(n);
     const size_t buf = align256((size_t)rows * n * 4);
     return (with_payload ? 4 : 2) * buf + align256((size_t)rows * ntiles * kBins * 4);
 }
@@ -197,7 +251,7 @@ extern "C" int cgk_row_sort(const uint32_t* kin, const uint32_t* pin, int rows, 
         cgx_set_error("row sort: invalid arguments (rows %d, n %d)", rows, n);
         return -1;
     }
-    const int ntiles = (n + kTile - 1) / kTile;
+    const int ntiles = (int)row_tiles(n);
     const int pay = pout != nullptr;
     if (ntiles > kMaxTiles || ws_bytes < cgk_row_sort_ws(rows, n, pay)) {
         cgx_set_error("row sort: %d keys per row need %d tiles (at most %d) or the workspace "
@@ -206,34 +260,11 @@ extern "C" int cgk_row_sort(const uint32_t* kin, const uint32_t* pin, int rows, 
     }
     const size_t buf = align256((size_t)rows * n * 4);
     char* w = (char*)ws;
-    uint32_t* kb[2] = {(uint32_t*)w, (uint32_t*)(w + buf)};
-    uint32_t* pb[2] = {pay ? (uint32_t*)(w + 2 * buf) : nullptr,
-                       pay ? (uint32_t*)(w + 3 * buf) : nullptr};
+    uint32_t* const kb[2] = {(uint32_t*)w, (uint32_t*)(w + buf)};
+    uint32_t* const pb[2] = {pay ? (uint32_t*)(w + 2 * buf) : nullptr,
+                             pay ? (uint32_t*)(w + 3 * buf) : nullptr};
     uint32_t* hist = (uint32_t*)(w + (pay ? 4 : 2) * buf);
-    const dim3 grid(ntiles, rows);
-    const uint32_t* ks = kin;
-    const uint32_t* ps = pin;
-    for (int pass = 0; pass < 4; pass++) {
-        const int shift = 8 * pass;
-        uint32_t* kd = pass == 3 ? kout : kb[pass & 1];
-        uint32_t* pd = pass == 3 ? pout : pb[pass & 1];
-        hipLaunchKernelGGL(k_rs_hist, grid, dim3(kT), 0, stream(), ks, n, shift, ntiles, hist);
-        if (launch_check("k_rs_hist")) return -1;
-        if (desc && pay)
-            hipLaunchKernelGGL((k_rs_scatter<true, true>), grid, dim3(kT), 0, stream(), ks, ps, n,
-                               shift, ntiles, hist, kd, pd);
-        else if (desc)
-            hipLaunchKernelGGL((k_rs_scatter<true, false>), grid, dim3(kT), 0, stream(), ks, ps,
-                               n, shift, ntiles, hist, kd, pd);
-        else if (pay)
-            hipLaunchKernelGGL((k_rs_scatter<false, true>), grid, dim3(kT), 0, stream(), ks, ps,
-                               n, shift, ntiles, hist, kd, pd);
-        else
-            hipLaunchKernelGGL((k_rs_scatter<false, false>), grid, dim3(kT), 0, stream(), ks, ps,
-                               n, shift, ntiles, hist, kd, pd);
-        if (launch_check("k_rs_scatter")) return -1;
-        ks = kd;
-        ps = pd;
-    }
-    return 0;
+    return row_items(n) == 8
+        ? row_sort_passes<8>(kin, pin, rows, n, desc, kout, pout, kb, pb, hist)
+        : row_sort_passes<16>(kin, pin, rows, n, desc, kout, pout, kb, pb, hist);
 }
