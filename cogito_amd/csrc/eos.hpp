@@ -239,6 +239,41 @@ struct EosShared {
     float rval;
 };
 
+// Row staging for stores.  A thread's chunk is kCh consecutive elements, so
+// writing it straight to memory makes every store instruction write 64
+// partial cache lines (one per lane).  Instead a row of at most kRound values
+// moves from the chunks to lane-consecutive positions through LDS (each wave
+// its own 64 chunks, with a pitch of kCh + 1 floats so the lanes' writes
+// along their chunks and the wave's reads of 64 consecutive values fall in
+// distinct banks) and is stored 256 contiguous bytes per instruction.  The
+// staging area overlaps EosShared (EosLds): it is used only where no EOS
+// state is live, behind barriers on both sides.
+constexpr int kTrPitch = kCh + 1;
+constexpr int kTrWave = 64 * kTrPitch;
+
+union EosLds {
+    EosShared sh;
+    float tr[kWaves * kTrWave];
+};
+
+// p[t*kCh + k] = q[k] for the elements below n (n <= kRound).
+__device__ __forceinline__ void store_vals(float* p, int n, const float (&q)[kCh], float* tr) {
+    const int l = lane_id(), w = wave_id();
+    const int wb = w * 64 * kCh;
+    float* tw = tr + w * kTrWave;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kCh; k++) tw[l * kTrPitch + k] = q[k];
+    // a wave reads back only its own area, and one wave's LDS accesses
+    // complete in order
+#pragma unroll
+    for (int i = 0; i < kCh; i++) {
+        const int e = 64 * i + l;
+        if (wb + e < n) p[wb + e] = tw[(e / kCh) * kTrPitch + e % kCh];
+    }
+    __syncthreads();
+}
+
 __device__ __forceinline__ float block_max_f(float v, EosShared& sh) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
     __syncthreads();

@@ -97,26 +97,44 @@ __device__ __forceinline__ int block_sum_int(int v, int* lds) {
     return tot;
 }
 
-// Number of leading entries of a descending array that are > v.
-__device__ __forceinline__ int count_above_sorted(const float* s, int n, float v) {
-    int lo = 0, hi = n;
-    while (lo < hi) {
-        int mid = (lo + hi) >> 1;
-        if (s[mid] > v) lo = mid + 1;
-        else hi = mid;
+// f(j) for every element j < V of a row, lane-consecutive; rows of at most
+// kRound elements in one fully unrolled sweep, so all of a thread's loads are
+// in flight together.
+template <class F>
+__device__ __forceinline__ void row_pass(int V, F f) {
+    if (V <= kRound) {
+#pragma unroll
+        for (int i = 0; i < kCh; i++) {
+            const int j = (int)threadIdx.x + i * kThreads;
+            if (j < V) f(j);
+        }
+    } else {
+        for (int j = threadIdx.x; j < V; j += kThreads) f(j);
     }
-    return lo;
 }
 
-// Number of leading entries of a descending array that are >= v.
-__device__ __forceinline__ int count_atleast_sorted(const float* s, int n, float v) {
-    int lo = 0, hi = n;
-    while (lo < hi) {
-        int mid = (lo + hi) >> 1;
-        if (s[mid] >= v) lo = mid + 1;
-        else hi = mid;
+// Number of leading entries of the descending s[0..n) that are > v (strict)
+// or >= v.  The predicate holds on a prefix, found by one round of loads at
+// kThreads evenly spaced entries and one over the bracket they leave (a
+// binary search would wait on log2 n dependent loads).  Block-wide call.
+__device__ int lead_count(const float* s, int n, float v, bool strict, int* lds) {
+    const int t = threadIdx.x;
+    const int step = (n + kThreads - 1) / kThreads;
+    bool in = false;
+    if (t * step < n) {
+        const float a = s[t * step];
+        in = strict ? a > v : a >= v;
     }
-    return lo;
+    const int c = block_sum_int(in ? 1 : 0, lds);       // samples 0 .. c-1 hold
+    if (c == 0) return 0;
+    const int lo = (c - 1) * step + 1;                   // entries below lo hold
+    const int hi = min(n, c * step);                     // entry hi fails, or hi == n
+    bool in2 = false;
+    if (lo + t < hi) {
+        const float a = s[lo + t];
+        in2 = strict ? a > v : a >= v;
+    }
+    return lo + block_sum_int(in2 ? 1 : 0, lds);
 }
 
 // ---------------------------------------------------------------- top-p
@@ -132,20 +150,21 @@ __global__ void k_scale(const float* __restrict__ x, float* __restrict__ z, size
 // as they are read (k_scale's operation, so z is never stored).
 __global__ __launch_bounds__(kThreads) void k_probs_rows(const float* __restrict__ x, int V,
                                                          float T, float* __restrict__ probs) {
-    __shared__ EosShared sh;
+    __shared__ EosLds lds;
+    EosShared& sh = lds.sh;
     ScaledSrc src{x + (size_t)blockIdx.x * V, T};
     float* pr = probs + (size_t)blockIdx.x * V;
     if (V <= kRound) {
-        // one round: the row and its exponentials stay in registers
+        // one round: the row and its exponentials stay in registers; the
+        // probabilities are written through the staging area
         float x[kCh], e[kCh];
         load_vals(src, V, -__builtin_inff(), x);
         const float m = vals_max(x, sh);
         vals_exp(x, m, 1.0f, V, e);
         const float S = eos_sum_vals(e, ExpGen<ScaledSrc>{src, m, 1.0f}, V, sh);
-        const int base = threadIdx.x * kCh;
 #pragma unroll
-        for (int k = 0; k < kCh; k++)
-            if (base + k < V) pr[base + k] = __fdiv_rn(e[k], S);
+        for (int k = 0; k < kCh; k++) e[k] = __fdiv_rn(e[k], S);
+        store_vals(pr, V, e, lds.tr);
         return;
     }
     float m = gen_max(src, V, sh);
@@ -196,14 +215,14 @@ __device__ __forceinline__ int tie_gap(const int* wc, int m, int gtt, int t) {
 }
 
 // Length of the shortest prefix of the non-negative values s[0..V) (whole
-// chunks of kCh, V <= kRound) whose sequential fp32 sum certainly exceeds
-// thr, V when none: the fp64 sum P through chunk t bounds the fp32 running
-// sum from below by P (1 - delta_t), the bound of the exact sum's guide for
-// (t + 1) kCh additions of non-negative values.
-__device__ int certified_prefix(const float* s, int V, float thr, EosShared& sh) {
+// chunks of kCh, V <= kRound; this thread's chunk in x, zero past V) whose
+// sequential fp32 sum certainly exceeds thr, V when none: the fp64 sum P
+// through chunk t bounds the fp32 running sum from below by P (1 - delta_t),
+// the bound of the exact sum's guide for (t + 1) kCh additions of
+// non-negative values.
+__device__ __forceinline__ int certified_prefix(const float (&x)[kCh], int V, float thr,
+                                                EosShared& sh) {
     const int t = threadIdx.x;
-    float x[kCh];
-    load_vals(RowSrc{s}, V, 0.0f, x);
     double gs = 0.0;
 #pragma unroll
     for (int k = 0; k < kCh; k++) gs += (double)x[k];
@@ -245,8 +264,21 @@ __global__ __launch_bounds__(kThreads) void k_top_p_finish(
     // exact sum away from the binade boundary at 1 that the whole row's sum
     // approaches.  The whole row when no prefix is certified (or V > kRound).
     const float thr = float_below(top_p);       // cumsum >= top_p <=> thr < cumsum
-    int n = V <= kRound ? certified_prefix(sr, V, thr, sh) : V;
-    float total = eos_sum(s, n, sh);
+    int n = V;
+    float total;
+    if (V <= kRound) {
+        // the sorted row is read once for the certified prefix and its exact
+        // sum
+        float x[kCh];
+        load_vals(s, V, 0.0f, x);
+        n = certified_prefix(x, V, thr, sh);
+        const int base = threadIdx.x * kCh;
+#pragma unroll
+        for (int k = 0; k < kCh; k++) x[k] = base + k < n ? x[k] : 0.0f;
+        total = eos_sum_vals(x, s, n, sh);
+    } else {
+        total = eos_sum(s, n, sh);
+    }
     if (n < V && !(thr < total)) {              // excluded by the bound; kept as a guard
         n = V;
         total = eos_sum(s, n, sh);
@@ -265,10 +297,11 @@ __global__ __launch_bounds__(kThreads) void k_top_p_finish(
         // a value held by one element (its sorted neighbours differ): the
         // token is that element, found by one coalesced pass
         if ((pos == 0 || sr[pos - 1] != v) && (pos == V - 1 || sr[pos + 1] != v)) {
-            for (int j = threadIdx.x; j < V; j += kThreads)
+            row_pass(V, [&](int j) {
                 if (pr[j] == v) s_tok = j;
+            });
         } else {
-            int rank = pos - count_above_sorted(sr, V, v);
+            int rank = pos - lead_count(sr, V, v, true, lds);
             int gtt;
             int m = tie_members(pr, V, v, wi, wc, &gtt, lds);
             if (threadIdx.x == 0) {
@@ -294,14 +327,14 @@ __global__ __launch_bounds__(kThreads) void k_top_p_finish(
     // sorted order, divided by the kept mass C
     float* dr = dist + (size_t)row * V;
     const float vc = sr[cutoff - 1];
-    const int above = count_above_sorted(sr, V, vc);
-    const int eq_end = count_atleast_sorted(sr, V, vc);
+    const int above = lead_count(sr, V, vc, true, lds);
+    const int eq_end = lead_count(sr, V, vc, false, lds);
     const int kept_in_group = cutoff - above;
     const bool whole = kept_in_group >= eq_end - above;
-    for (int j = threadIdx.x; j < V; j += kThreads) {
-        float x = pr[j];
+    row_pass(V, [&](int j) {
+        const float x = pr[j];
         dr[j] = (x > vc || (whole && x == vc)) ? __fdiv_rn(x, C) : 0.0f;
-    }
+    });
     __syncthreads();
     if (whole) return;
     int gtt;
