@@ -97,44 +97,27 @@ __device__ __forceinline__ int block_sum_int(int v, int* lds) {
     return tot;
 }
 
-// f(j) for every element j < V of a row, lane-consecutive; rows of at most
-// kRound elements in one fully unrolled sweep, so all of a thread's loads are
-// in flight together.
-template <class F>
-__device__ __forceinline__ void row_pass(int V, F f) {
-    if (V <= kRound) {
-#pragma unroll
-        for (int i = 0; i < kCh; i++) {
-            const int j = (int)threadIdx.x + i * kThreads;
-            if (j < V) f(j);
-        }
-    } else {
-        for (int j = threadIdx.x; j < V; j += kThreads) f(j);
+// Sums of four ints over the block (`lds` holds kWaves int4).
+__device__ __forceinline__ int4 block_sum_int4(int4 v, int4* lds) {
+    for (int o = 32; o > 0; o >>= 1) {
+        v.x += __shfl_xor(v.x, o);
+        v.y += __shfl_xor(v.y, o);
+        v.z += __shfl_xor(v.z, o);
+        v.w += __shfl_xor(v.w, o);
     }
-}
-
-// Number of leading entries of the descending s[0..n) that are > v (strict)
-// or >= v.  The predicate holds on a prefix, found by one round of loads at
-// kThreads evenly spaced entries and one over the bracket they leave (a
-// binary search would wait on log2 n dependent loads).  Block-wide call.
-__device__ int lead_count(const float* s, int n, float v, bool strict, int* lds) {
-    const int t = threadIdx.x;
-    const int step = (n + kThreads - 1) / kThreads;
-    bool in = false;
-    if (t * step < n) {
-        const float a = s[t * step];
-        in = strict ? a > v : a >= v;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+    __syncthreads();
+    int4 r = make_int4(0, 0, 0, 0);
+    for (int w = 0; w < kWaves; w++) {
+        const int4 a = lds[w];
+        r.x += a.x;
+        r.y += a.y;
+        r.z += a.z;
+        r.w += a.w;
     }
-    const int c = block_sum_int(in ? 1 : 0, lds);       // samples 0 .. c-1 hold
-    if (c == 0) return 0;
-    const int lo = (c - 1) * step + 1;                   // entries below lo hold
-    const int hi = min(n, c * step);                     // entry hi fails, or hi == n
-    bool in2 = false;
-    if (lo + t < hi) {
-        const float a = s[lo + t];
-        in2 = strict ? a > v : a >= v;
-    }
-    return lo + block_sum_int(in2 ? 1 : 0, lds);
+    __syncthreads();
+    return r;
 }
 
 // ---------------------------------------------------------------- top-p
@@ -251,6 +234,7 @@ __global__ __launch_bounds__(kThreads) void k_top_p_finish(
     float* __restrict__ dist, int* __restrict__ ws) {
     __shared__ EosShared sh;
     __shared__ int lds[kWaves];
+    __shared__ int4 lds4[kWaves];
     __shared__ int s_tok;
     const int row = blockIdx.x;
     const float* pr = probs + (size_t)row * V;
@@ -287,21 +271,54 @@ __global__ __launch_bounds__(kThreads) void k_top_p_finish(
     const int ci = gen_find_val(s, n, thr, -1, total, &C, sh);
     const int cutoff = ci < 0 ? V : ci + 1;
 
-    if (tokens && tok_every > 0 && (row + 1) % tok_every == 0) {
-        // speculative.c:109-115: r = u * cumsum; first i < cutoff with r < cumsum
-        const int ti = row / tok_every;
-        float r = __fmul_rn(u[(size_t)ti * u_stride], C);
-        int pos = gen_find(s, n, r, 0, sh);
+    // The token (speculative.c:109-115: r = u * cumsum; first i < cutoff with
+    // r < cumsum) is the sorted entry at `pos`; the distribution keeps the
+    // first `cutoff` sorted entries, divided by the kept mass C.  One pass
+    // over the row in index order serves both: it writes the distribution
+    // (every element >= vc kept, right unless the tie group of vc is cut),
+    // finds the element holding the token's value and counts the elements
+    // above and equal to both values.
+    const bool want_tok = tokens && tok_every > 0 && (row + 1) % tok_every == 0;
+    const int ti = want_tok ? row / tok_every : 0;
+    int pos = 0;
+    if (want_tok) {
+        const float r = __fmul_rn(u[(size_t)ti * u_stride], C);
+        pos = gen_find(s, n, r, 0, sh);
         if (pos >= cutoff) pos = 0;
-        float v = sr[pos];
-        // a value held by one element (its sorted neighbours differ): the
-        // token is that element, found by one coalesced pass
-        if ((pos == 0 || sr[pos - 1] != v) && (pos == V - 1 || sr[pos + 1] != v)) {
-            row_pass(V, [&](int j) {
-                if (pr[j] == v) s_tok = j;
-            });
-        } else {
-            int rank = pos - lead_count(sr, V, v, true, lds);
+    }
+    const float v = want_tok ? sr[pos] : 0.0f;
+    const float vc = sr[cutoff - 1];
+    float* dr = dist ? dist + (size_t)row * V : nullptr;
+    // counts of the elements == v, > v, > vc, == vc; rows of at most kRound
+    // elements keep their values in registers for the writes below
+    int4 c = make_int4(0, 0, 0, 0);
+    float xv[kCh];
+    auto count = [&](int j, float x) {
+        if (want_tok && x == v) s_tok = j;
+        c.x += x == v;
+        c.y += x > v;
+        c.z += x > vc;
+        c.w += x == vc;
+    };
+    if (V <= kRound) {
+#pragma unroll
+        for (int i = 0; i < kCh; i++) {
+            const int j = (int)threadIdx.x + i * kThreads;
+            xv[i] = j < V ? pr[j] : -1.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < kCh; i++)
+            if ((int)threadIdx.x + i * kThreads < V) count((int)threadIdx.x + i * kThreads, xv[i]);
+    } else {
+        for (int j = threadIdx.x; j < V; j += kThreads) count(j, pr[j]);
+    }
+    const int4 cnt = block_sum_int4(c, lds4);
+
+    if (want_tok) {
+        // a value held by one element: that element (s_tok, written by it);
+        // otherwise the reference's emission order of the tie group
+        if (cnt.x > 1) {
+            const int rank = pos - cnt.y;
             int gtt;
             int m = tie_members(pr, V, v, wi, wc, &gtt, lds);
             if (threadIdx.x == 0) {
@@ -319,24 +336,27 @@ __global__ __launch_bounds__(kThreads) void k_top_p_finish(
         }
         __syncthreads();
         if (threadIdx.x == 0) tokens[ti] = s_tok;
-        __syncthreads();
     }
-    if (!dist) return;
+    if (!dr) return;
 
-    // filtered distribution: kept elements are the first `cutoff` of the
-    // sorted order, divided by the kept mass C
-    float* dr = dist + (size_t)row * V;
-    const float vc = sr[cutoff - 1];
-    const int above = lead_count(sr, V, vc, true, lds);
-    const int eq_end = lead_count(sr, V, vc, false, lds);
-    const int kept_in_group = cutoff - above;
-    const bool whole = kept_in_group >= eq_end - above;
-    row_pass(V, [&](int j) {
-        const float x = pr[j];
-        dr[j] = (x > vc || (whole && x == vc)) ? __fdiv_rn(x, C) : 0.0f;
-    });
+    // the kept elements are those > vc and, when the whole tie group of vc
+    // is kept, those == vc
+    const int kept_in_group = cutoff - cnt.z;
+    const bool whole = kept_in_group >= cnt.w;
+    auto keep = [&](float x) { return (x > vc || (whole && x == vc)) ? __fdiv_rn(x, C) : 0.0f; };
+    if (V <= kRound) {
+#pragma unroll
+        for (int i = 0; i < kCh; i++) {
+            const int j = (int)threadIdx.x + i * kThreads;
+            if (j < V) dr[j] = keep(xv[i]);
+        }
+    } else {
+        for (int j = threadIdx.x; j < V; j += kThreads) dr[j] = keep(pr[j]);
+    }
     __syncthreads();
     if (whole) return;
+    // the first kept_in_group members of the group in the sort's emission
+    // order are kept
     int gtt;
     int m = tie_members(pr, V, vc, wi, wc, &gtt, lds);
     const float val = __fdiv_rn(vc, C);
