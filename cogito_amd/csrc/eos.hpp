@@ -170,16 +170,29 @@ struct SegMono {
     int flag;                    // a segment starts inside this range
 };
 
+// Field-wise selects throughout: a conditional copy of the whole struct is
+// not split into registers by the compiler and goes through scratch memory.
 __device__ __forceinline__ SegMono seg_then(const SegMono& a, const SegMono& b) {
+    const Mono ab = mono_then(a.m, b.m);
+    const bool f = b.flag != 0;
     SegMono r;
+    r.m.q0 = f ? b.m.q0 : ab.q0;
+    r.m.q1 = f ? b.m.q1 : ab.q1;
+    r.m.c0 = f ? b.m.c0 : ab.c0;
+    r.m.c1 = f ? b.m.c1 : ab.c1;
+    r.head = f ? b.head : a.head;
     r.flag = a.flag | b.flag;
-    if (b.flag) {
-        r.m = b.m;
-        r.head = b.head;
-    } else {
-        r.m = mono_then(a.m, b.m);
-        r.head = a.head;
-    }
+    return r;
+}
+
+__device__ __forceinline__ SegMono seg_pick(bool c, const SegMono& a, const SegMono& b) {
+    SegMono r;
+    r.m.q0 = c ? a.m.q0 : b.m.q0;
+    r.m.q1 = c ? a.m.q1 : b.m.q1;
+    r.m.c0 = c ? a.m.c0 : b.m.c0;
+    r.m.c1 = c ? a.m.c1 : b.m.c1;
+    r.head = c ? a.head : b.head;
+    r.flag = c ? a.flag : b.flag;
     return r;
 }
 
@@ -367,12 +380,12 @@ __device__ __forceinline__ SegMono dpp_seg(const SegMono& v) {
 
 __device__ __forceinline__ SegMono wave_incl_seg(SegMono v) {
     SegMono o;
-    o = dpp_seg<0x111, 0xF>(v); if (dpp_step_valid(0)) v = seg_then(o, v);
-    o = dpp_seg<0x112, 0xF>(v); if (dpp_step_valid(1)) v = seg_then(o, v);
-    o = dpp_seg<0x114, 0xF>(v); if (dpp_step_valid(2)) v = seg_then(o, v);
-    o = dpp_seg<0x118, 0xF>(v); if (dpp_step_valid(3)) v = seg_then(o, v);
-    o = dpp_seg<0x142, 0xA>(v); if (dpp_step_valid(4)) v = seg_then(o, v);
-    o = dpp_seg<0x143, 0xC>(v); if (dpp_step_valid(5)) v = seg_then(o, v);
+    o = dpp_seg<0x111, 0xF>(v); v = seg_pick(dpp_step_valid(0), seg_then(o, v), v);
+    o = dpp_seg<0x112, 0xF>(v); v = seg_pick(dpp_step_valid(1), seg_then(o, v), v);
+    o = dpp_seg<0x114, 0xF>(v); v = seg_pick(dpp_step_valid(2), seg_then(o, v), v);
+    o = dpp_seg<0x118, 0xF>(v); v = seg_pick(dpp_step_valid(3), seg_then(o, v), v);
+    o = dpp_seg<0x142, 0xA>(v); v = seg_pick(dpp_step_valid(4), seg_then(o, v), v);
+    o = dpp_seg<0x143, 0xC>(v); v = seg_pick(dpp_step_valid(5), seg_then(o, v), v);
     return v;
 }
 
@@ -408,6 +421,25 @@ __device__ __forceinline__ float replay_chunk_staged(const G& g, int slot, int b
 template <class XF>
 __device__ __forceinline__ Mono fold_chunk(XF xk, int b) {
     const int e = b == -127 ? 149 : 23 - b;
+    // Without a tie (y exactly halfway between integers) every increment is
+    // rint(y), whatever the running value; the increments are integers whose
+    // running total stays below 2^24 (the run stays in one binade), so their
+    // fp32 sum is exact.
+    {
+        float qs = 0.0f;
+        bool tie = false;
+#pragma unroll
+        for (int k = 0; k < kCh; k++) {
+            const float y = ldexpf(xk(k), e);
+            const float r = rintf(y);
+            tie |= fabsf(y - r) == 0.5f;
+            qs += r;
+        }
+        if (!tie) {
+            const int q = (int)qs;
+            return Mono{q, q, q & 1, (q + 1) & 1};
+        }
+    }
     int c0 = 0, c1 = 1;
     int q0 = 0, q1 = 0;
 #pragma unroll
