@@ -186,7 +186,17 @@ __global__ __launch_bounds__(kThreads) void k_verify_rows_dist(
         a = qx < 1e-10f ? 1.0f : fminf(1.0f, __fdiv_rn(px, qx));
     }
     if (threadIdx.x == 0) accept_prob[r] = a;
-    int tok = sample_corrected_gen(pt, pd, V, u[(size_t)chain * (gamma + 1) + pos + 1], sh);
+    const float ud = u[(size_t)chain * (gamma + 1) + pos + 1];
+    int tok;
+    if (V <= kRound) {
+        // both rows in registers (16-byte loads), the residual formed there
+        float pv[kCh], qv[kCh];
+        load_vals(pt, V, 0.0f, pv);
+        load_vals(pd, V, 0.0f, qv);
+        tok = sample_corrected_vals(pv, qv, pt, pd, V, ud, sh);
+    } else {
+        tok = sample_corrected_gen(pt, pd, V, ud, sh);
+    }
     if (threadIdx.x == 0) correction[r] = tok;
 }
 

@@ -70,7 +70,11 @@ TOPP_CASES = [(1000, 0.9, "ties"), (1000, 0.5, "halves"), (3000, 0.9, "flat"),
               # the summed prefix of the sorted row: cut after a few tokens, deep in
               # the row, and top_p close to 1 (the running sum near the binade at 1)
               (8000, 0.9, "peaked"), (8000, 0.3, "peaked"), (8000, 0.9, "spread"),
-              (8000, 0.999, "normal"), (8000, 0.99999, "peaked")]
+              (8000, 0.999, "normal"), (8000, 0.99999, "peaked"),
+              # full-size rows: long runs of ties, the largest row the
+              # probabilities hold in registers (32768), a cut deep in a wide row
+              (32000, 0.9, "ties"), (32768, 0.5, "halves"), (32768, 0.9, "normal"),
+              (32000, 0.99, "spread")]
 
 
 @pytest.mark.parametrize("V,p,kind", TOPP_CASES)
