@@ -150,6 +150,7 @@ _REF_SIGS = {
     "cg_cuda_rmsnorm_forward": (None, [C.POINTER(RefTensor), C.POINTER(RefTensor),
                                        C.POINTER(RefTensor), F]),
     "cg_cuda_softmax_forward": (None, [C.POINTER(RefTensor), C.POINTER(RefTensor), I]),
+    "cg_swiglu_forward_split": (C.POINTER(RefTensor), [C.POINTER(RefTensor)]),
 }
 
 

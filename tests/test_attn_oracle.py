@@ -358,3 +358,48 @@ def test_swiglu_closed_form(oracle, rng):
     np.testing.assert_allclose(out, exp, rtol=1e-6, atol=1e-30)
     # g = 0 gives 0; g = -100 overflows exp(100) to inf and gives (signed) 0
     assert out[-6] == 0.0 and out[-2] == 0.0
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 6), (3, 4096), (5, 11008)])
+def test_swiglu_vs_reference(ref, oracle, rng, rows, dim):
+    # orc_swiglu restates transformer.c:122-127; the reference's split form
+    # (activations.c:34-54, gate | value halves of one row) is the same
+    # expression, so the compiled reference pins it bit for bit, including
+    # gates whose exp(-g) overflows or underflows
+    g = rng.normal(0, 3, (rows, dim)).astype(np.float32)
+    g[0, :6] = [0.0, -0.0, 30.0, -30.0, -100.0, 88.0]
+    u = rng.normal(0, 1, (rows, dim)).astype(np.float32)
+    out = np.zeros_like(g)
+    oracle.orc_swiglu(ptr(g), ptr(u), ptr(out), g.size)
+    t = oracle_lib.ref_tensor(ref, np.concatenate([g, u], axis=1))
+    r = ref.cg_swiglu_forward_split(t)
+    yr = oracle_lib.ref_tensor_np(r)
+    ref.cg_tensor_free(t)
+    ref.cg_tensor_free(r)
+    assert yr.shape == (rows, dim)
+    np.testing.assert_array_equal(out.view(np.uint32), yr.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,V", [(1, 1), (4, 1000), (2, 32000)])
+def test_softmax_rows_vs_reference(ref, oracle, rng, rows, V):
+    # orc_softmax_rows restates tensor_kernels.c:699-740 over axis 1 of a
+    # [rows][V] tensor: the compiled reference pins it bit for bit (ties at
+    # the maximum, a -inf logit), fp64 pins the formula
+    x = rng.normal(0, 3, (rows, V)).astype(np.float32)
+    if V >= 8:
+        x[0, :3] = x[0].max()
+        x[-1, 5] = -np.inf
+    y = np.zeros_like(x)
+    oracle.orc_softmax_rows(ptr(x), ptr(y), rows, V)
+    tx, ty = oracle_lib.ref_tensor(ref, x), oracle_lib.ref_tensor(ref, np.zeros_like(x))
+    ref.cg_cuda_softmax_forward(tx, ty, 1)
+    yr = oracle_lib.ref_tensor_np(ty)
+    ref.cg_tensor_free(tx)
+    ref.cg_tensor_free(ty)
+    np.testing.assert_array_equal(y.view(np.uint32), yr.view(np.uint32))
+    # the sequential fp32 sum of V terms is within V 2^-24 (1 + 2^-7) of the
+    # real sum; expf and the division add a few ulps
+    xd = x.astype(np.float64)
+    e = np.exp(xd - xd.max(axis=1, keepdims=True))
+    rtol = V * 2.0**-24 * (1 + 2.0**-7) + 4 * 2.0**-24
+    np.testing.assert_allclose(y, e / e.sum(axis=1, keepdims=True), rtol=rtol, atol=1e-30)
