@@ -945,7 +945,20 @@ __global__ __launch_bounds__(64 * kGemmWaves, 2) void k_gemm_int4(GemmArgs a) {
     const NibConst nk = nib_consts();
     const int paired = NG == 2;
     const int nchunks = a.K / kChunkK;
-    const int bx = blockIdx.x;
+    // XCD-aware order (block b runs on XCD b % 8): with several row blocks,
+    // each XCD takes a contiguous run of (column block, row block) pairs, row
+    // blocks fastest, so the row blocks of one column block run together on
+    // one XCD and share its L2 copy of the weights (tree verify, 256 rows:
+    // 14.25 -> 13.70 ms a step; with one row block the plain order measured
+    // faster).  The tail past a multiple of 8 keeps the plain order.
+    int bx = blockIdx.x, by = blockIdx.y;
+    if (gridDim.y > 1) {
+        const int gy = gridDim.y, lin = blockIdx.y * gridDim.x + blockIdx.x;
+        const int per = gridDim.x * gy / 8;
+        const int q = lin < 8 * per ? (lin % 8) * per + lin / 8 : lin;
+        bx = q / gy;
+        by = q % gy;
+    }
     // slots: logical 128-column groups and their scale-group rows
     int slot_ok[2], grp[2], lcol[2];
 #pragma unroll
@@ -959,7 +972,7 @@ __global__ __launch_bounds__(64 * kGemmWaves, 2) void k_gemm_int4(GemmArgs a) {
         }
         grp[s] = slot_ok[s] ? lcol[s] / a.gs : 0;
     }
-    const int row0 = blockIdx.y * BM;
+    const int row0 = by * BM;
     const int c0 = blockIdx.z * a.ksteps;
     const int c1 = min(nchunks, c0 + a.ksteps);
     // preparation: thread -> 4 k values at pk, rows pr + 8 i (a row's 32
