@@ -264,6 +264,11 @@ int cgx_decoder_fused_attention(int on);
  * lm_head; 0 never, 1 every product it supports); returns the previous value
  * (-1 only reads it). */
 int cgx_gemv_stream_min_units(int units);
+/* Test hook, no reference counterpart: the GEMM (32+ rows) sums its K splits
+ * with four outputs a thread once that launch has at least this many
+ * 256-thread blocks (default 512; 0 always, a large value never); returns
+ * the previous value (-1 only reads it). */
+int cgx_gemm_reduce4_min_blocks(int blocks);
 int cgx_attention_int4_kv_batch_dev(const float* Q, int B, int Nq, int H,
                                     cg_kv_cache_int4* cache, int slot0, const int* nk,
                                     int mask_kind, const unsigned long long* anc, int tw,

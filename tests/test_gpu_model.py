@@ -132,12 +132,22 @@ def test_model_forward_stream_gemv_vs_oracle(gpu, oracle, rng):
                                             head_dim=128, d_ff=768, vocab=2048, group_size=128,
                                             kv_group_size=128, max_seq=300, max_tokens=5,
                                             init_std=0.05)])
-@pytest.mark.parametrize("B", [3, 8])
-def test_model_forward_batch_vs_oracle(gpu, oracle, rng, cfg, B):
+@pytest.mark.parametrize("B,reduce4", [(3, 512), (8, 512), (8, 0)])
+def test_model_forward_batch_vs_oracle(gpu, oracle, rng, cfg, B, reduce4):
     # B sequences with their own caches in one forward: each matches its own
     # oracle stack, also after rollbacks to different lengths per sequence
-    # (B = 8: 40 rows per forward, the GEMM path of every linear layer)
+    # (B = 8: 40 rows per forward, the GEMM path of every linear layer; with
+    # reduce4 = 0 its K splits are summed four outputs a thread, with the
+    # accumulate and SwiGLU epilogues and the row statistics by DPP)
     from dataclasses import replace
+    old = gpu.cgx_gemm_reduce4_min_blocks(reduce4)
+    try:
+        _forward_batch_case(gpu, oracle, rng, cfg, B, replace)
+    finally:
+        gpu.cgx_gemm_reduce4_min_blocks(old)
+
+
+def _forward_batch_case(gpu, oracle, rng, cfg, B, replace):
     m = new_model(gpu, replace(cfg, max_batch=B), 5)
     assert gpu.cgx_model_batch(m) == B
     oms = [OracleModel(oracle, cfg, 5) for _ in range(B)]
