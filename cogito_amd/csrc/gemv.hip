@@ -1108,17 +1108,20 @@ __global__ __launch_bounds__(64 * kGemmWaves, 2) void k_gemm_int4(GemmArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();                       // the previous step's A reads are done
         const float4 n4 = pn;
-        // rows past M and steps past c1 prepare zeros (masked, not
-        // multiplied, so that no inf or NaN of a clamped load leaks in; bit
-        // masks keep the step free of branches)
+        // x times the row factor, once per step for both slots; rows past M
+        // and steps past c1 take the factor 0.  Their loads are clamped to
+        // live data (a row past M reads row M - 1, a step past c1 the
+        // split's last chunk), so a product is non-finite only where the
+        // same values already enter a live row's sum, and a row past M
+        // feeds only its own, unstored, outputs.
         float4 xv[RPT];
 #pragma unroll
         for (int i = 0; i < RPT; i++) {
-            const uint32_t m = plive & rowmask[i];
-            xv[i].x = __uint_as_float(__float_as_uint(px[i].x) & m);
-            xv[i].y = __uint_as_float(__float_as_uint(px[i].y) & m);
-            xv[i].z = __uint_as_float(__float_as_uint(px[i].z) & m);
-            xv[i].w = __uint_as_float(__float_as_uint(px[i].w) & m);
+            const float r = (plive & rowmask[i]) ? rsc[i] : 0.0f;
+            xv[i].x = px[i].x * r;
+            xv[i].y = px[i].y * r;
+            xv[i].z = px[i].z * r;
+            xv[i].w = px[i].w * r;
         }
         // a missing slot (odd slot count) prepares from valid memory and is
         // never stored
@@ -1128,15 +1131,19 @@ __global__ __launch_bounds__(64 * kGemmWaves, 2) void k_gemm_int4(GemmArgs a) {
             const float n2 = n4.z * ps[s_].z, n3 = n4.w * ps[s_].w;
 #pragma unroll
             for (int i = 0; i < RPT; i++) {
-                const float r = rsc[i];
-                const float v0 = xv[i].x * n0 * r, v1 = xv[i].y * n1 * r;
-                const float v2 = xv[i].z * n2 * r, v3 = xv[i].w * n3 * r;
+                const float v0 = xv[i].x * n0, v1 = xv[i].y * n1;
+                const float v2 = xv[i].z * n2, v3 = xv[i].w * n3;
                 const f16x2 h01 = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(v0, v1));
                 const f16x2 h23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(v2, v3));
-                const f16x2 l01 = __builtin_bit_cast(
-                    f16x2, __builtin_amdgcn_cvt_pkrtz(v0 - (float)h01[0], v1 - (float)h01[1]));
-                const f16x2 l23 = __builtin_bit_cast(
-                    f16x2, __builtin_amdgcn_cvt_pkrtz(v2 - (float)h23[0], v3 - (float)h23[1]));
+                // hi: v rounded toward zero; lo: the exact remainder rounded
+                // to fp16 (one v_fma_mixlo / v_fma_mixhi each: 600 -> 504
+                // VALU instructions per step pair, with x times the row
+                // factor once per step)
+                f16x2 l01, l23;
+                l01[0] = (_Float16)(v0 - (float)h01[0]);
+                l01[1] = (_Float16)(v1 - (float)h01[1]);
+                l23[0] = (_Float16)(v2 - (float)h23[0]);
+                l23[1] = (_Float16)(v3 - (float)h23[1]);
                 const int r_ = pr + 8 * i;
                 *(uint2*)&sa[s_][0][r_][pk] = make_uint2(__builtin_bit_cast(uint32_t, h01),
                                                          __builtin_bit_cast(uint32_t, h23));
