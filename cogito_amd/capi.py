@@ -294,6 +294,7 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_decoder_fused_attention": (I, [I]),
     "cgx_gemv_stream_min_units": (I, [I]),
     "cgx_gemm_reduce4_min_blocks": (I, [I]),
+    "cgx_gemm_swiglu_here": (I, [I]),
     "cgx_model_save": (I, [VP, C.c_char_p, I]),
     "cgx_fill_normal_dev": (I, [VP, SZ, C.c_uint64, C.c_uint32, F]),
     "cgx_spec_new": (VP, [VP, VP, I, F, I, F]),

@@ -78,7 +78,7 @@ int cgk_int4_unpack_mfma(const uint8_t* w, const float* scales_t, int K, int N, 
  * epilogues as cgk_gemv_mfma plus smax >= every |scale| of the weight.
  * stats_in ([M][nstat_in][2] partial max|x*nw| and sum x^2, from the
  * producer's stats_out) replaces the row-statistics pass over x; stats_out
- * ([M][Nout/256][2], Nout % 256 == 0) receives those of the output, with
+ * ([M][Nout/128][2]) receives those of the output, per 128 columns, with
  * nw_next the consumer's RMSNorm weights (NULL: 1). */
 int cgk_gemm_int4_supported(int M, int K, int N, int gs, int paired);
 int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int gs, const uint8_t* w,

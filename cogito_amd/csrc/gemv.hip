@@ -143,6 +143,33 @@ __device__ __forceinline__ float wave_sum(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Inclusive scans over the 16 lanes of each DPP row (row_shr 1, 2, 4, 8):
+// lane 15 of a row holds the row's sum / maximum (non-negative values).
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xF, 0xF, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x112, 0xF, 0xF, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x114, 0xF, 0xF, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x118, 0xF, 0xF, true));
+    return v;
+}
+__device__ __forceinline__ float row16_max_nonneg(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xF, 0xF, true)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x112, 0xF, 0xF, true)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x114, 0xF, 0xF, true)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x118, 0xF, 0xF, true)));
+    return v;
+}
+// The same over each 32-lane half (row_bcast:15 adds row 0's total into row
+// 1 and row 2's into row 3): lanes 31 and 63 hold the halves' results.
+__device__ __forceinline__ float half_sum(float v) {
+    v = row16_sum(v);
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, true));
+}
+__device__ __forceinline__ float half_max_nonneg(float v) {
+    v = row16_max_nonneg(v);
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, true)));
+}
+
 // MP: rows padded (1, 2, 4, 5, 8 or 16); T: column tiles per block; NG: scale groups
 // per block (1, or 2 for a gate|up pair).
 // W: waves per block (8; 16 for deep K, each wave then has fewer rounds).
@@ -927,12 +954,17 @@ struct GemmArgs {
     const float* rowscale;    // [M] rstd * 2^E (k_gemm_rows), or
     const float* unscale;     // [M] 2^-E       ... nullptr with stats:
     const float* stats;       // [M][nstat][2] partial (max|x*nw|, sum x^2) of x
-    int nstat;                //   per 256 columns, written by the producer's reduction
+    int nstat;                //   per 128 columns, written by the producer's epilogue
     float smax, eps;          // the row factors' scale bound and RMSNorm epsilon
     float* part;              // [ksplit][M][N] partial sums, logical columns (y itself
                               // for one split storing rows of N floats)
     int ksteps;               // 128-row chunks per split
     int ff;                   // SwiGLU pair: N / 2
+    // one split of a gate|up pair: SwiGLU in the epilogue, straight into y
+    float* y;                 // [M][ldy] (nullptr: partial sums into part)
+    int ldy;
+    float* stats_out;         // [M][ff / 128][2] of y, or nullptr
+    const float* nw_next;     // the next linear's RMSNorm weights, or nullptr
 };
 
 template <int RT, int NG, int PRO>
@@ -1185,6 +1217,98 @@ __global__ __launch_bounds__(64 * kGemmWaves, 2) void k_gemm_int4(GemmArgs a) {
         step(c + 1, wb1);
     }
 
+    if (NG == 2 && a.y) {
+        // one K split of a gate|up pair: the up waves (slot 1) hand their
+        // sums to the gate waves through LDS (the A buffers are free once
+        // every wave is past its last step), which apply SwiGLU with the
+        // split reduction's arithmetic (0 + sum * 2^-E, then g / (1 +
+        // exp(-g)) * u) and store y and the row statistics of its 128
+        // columns
+        float (*s_up)[128] = (float (*)[128])&sa[0][0][0][0];
+        float (*s_st)[2] = (float (*)[2])&sa[0][0][0][0] + BM * 64;
+        static_assert(BM * 128 * 4 + BM * 2 * 4 <= (int)sizeof(sa), "epilogue fits the A buffers");
+        __syncthreads();
+        if (ws == 1) {
+#pragma unroll
+            for (int j = 0; j < kGemmTiles; j++)
+#pragma unroll
+                for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        const int r_ = rt * 16 + 4 * (lane >> 4) + v;
+                        s_up[r_][64 * (wave & 1) + 16 * j + (lane & 15)] =
+                            0.0f + acc[j][rt][v] * s_unscale[r_];
+                    }
+        }
+        __syncthreads();
+        float am[RT][4], ss[RT][4];
+        if (ws == 0) {
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    am[rt][v] = 0.0f;
+                    ss[rt][v] = 0.0f;
+                }
+#pragma unroll
+            for (int j = 0; j < kGemmTiles; j++) {
+                const int c = 64 * (wave & 1) + 16 * j + (lane & 15);
+                const int col = 128 * bx + c;
+                const float nwc = a.nw_next ? a.nw_next[col] : 1.0f;
+#pragma unroll
+                for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        const int r_ = rt * 16 + 4 * (lane >> 4) + v;
+                        const int row = row0 + r_;
+                        const float g = 0.0f + acc[j][rt][v] * s_unscale[r_];
+                        const float o = g / (1.0f + __expf(-g)) * s_up[r_][c];
+                        if (row < a.M) a.y[(size_t)row * a.ldy + col] = o;
+                        am[rt][v] = fmaxf(am[rt][v], fabsf(o * nwc));
+                        ss[rt][v] = fmaf(o, o, ss[rt][v]);
+                    }
+            }
+        }
+        if (!a.stats_out) return;
+        // per row: the 4 tiles in a lane, then the 16 lanes of its DPP row
+        // (lane 15 of each row), then the two gate waves (wave 1 through LDS)
+        if (ws == 0) {
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    am[rt][v] = row16_max_nonneg(am[rt][v]);
+                    ss[rt][v] = row16_sum(ss[rt][v]);
+                }
+        }
+        __syncthreads();                 // the gate waves' reads of s_up are done
+        if (wave == 1 && (lane & 15) == 15) {
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int r_ = rt * 16 + 4 * (lane >> 4) + v;
+                    s_st[r_][0] = am[rt][v];
+                    s_st[r_][1] = ss[rt][v];
+                }
+        }
+        __syncthreads();
+        if (wave == 0 && (lane & 15) == 15) {
+            const int nst = a.ff / 128;
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int r_ = rt * 16 + 4 * (lane >> 4) + v;
+                    const int row = row0 + r_;
+                    if (row < a.M) {
+                        a.stats_out[((size_t)row * nst + bx) * 2] = fmaxf(am[rt][v], s_st[r_][0]);
+                        a.stats_out[((size_t)row * nst + bx) * 2 + 1] = ss[rt][v] + s_st[r_][1];
+                    }
+                }
+        }
+        return;
+    }
     if (!wave_ok) return;
     float* pp = a.part + (size_t)blockIdx.z * a.M * a.N;
 #pragma unroll
@@ -1256,10 +1380,10 @@ __global__ __launch_bounds__(256) void k_gemm_rows(const float* __restrict__ x, 
     }
 }
 
-// Sum of the K splits in order, and the epilogue.  With stats_out (output
-// width a multiple of 256: a block is 256 outputs of one row), also the
-// block's (max|y * nw_next|, sum y^2) of the stored outputs y: the next
-// GEMM's row statistics without a pass over y.
+// Sum of the K splits in order, and the epilogue.  With stats_out, also the
+// (max|y * nw_next|, sum y^2) of every 128 stored outputs of a row (two
+// waves; the output width is a multiple of 128): the next GEMM's row
+// statistics without a pass over y.
 template <int EPI>
 __global__ __launch_bounds__(256) void k_gemm_reduce(const float* __restrict__ part, int ksplit,
                                                      int M, int N, float* __restrict__ y,
@@ -1298,21 +1422,23 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float* __restrict__ p
         s_s[threadIdx.x >> 6] = ss;
     }
     __syncthreads();
-    if (threadIdx.x == 0 && live) {
-        const int nblk = Nout / 256, blk = col / 256;
-        stats_out[((size_t)row * nblk + blk) * 2] =
-            fmaxf(fmaxf(s_a[0], s_a[1]), fmaxf(s_a[2], s_a[3]));
-        stats_out[((size_t)row * nblk + blk) * 2 + 1] = ((s_s[0] + s_s[1]) + s_s[2]) + s_s[3];
+    // threads 0 and 128 (each the first of its 128 outputs) store the pair
+    // of waves they lead
+    if ((threadIdx.x & 127) == 0 && live) {
+        const int h = threadIdx.x >> 6;
+        const int nblk = Nout / 128, blk = col / 128;
+        stats_out[((size_t)row * nblk + blk) * 2] = fmaxf(s_a[h], s_a[h + 1]);
+        stats_out[((size_t)row * nblk + blk) * 2 + 1] = s_s[h] + s_s[h + 1];
     }
 }
 
 // The same with four neighbouring outputs per thread: 16-byte loads of the
 // splits and 16-byte stores of y (y 16-byte aligned, ldy % 4 == 0, N % 8 ==
 // 0).  Each output is the same sum, in the same order, and the same epilogue
-// as in k_gemm_reduce.  A wave's 256 outputs lie in one row's 256-column
-// statistics block (output width a multiple of 256), so the wave reduces
-// its (max, sum of squares) by DPP and lane 0 stores them: no LDS, no
-// barrier, where the scalar kernel used a chain of shuffles.
+// as in k_gemm_reduce.  A half wave's 128 outputs are one row's 128-column
+// statistics block (the output width is a multiple of 128), so each half
+// reduces its (max, sum of squares) by DPP and its last lane stores them:
+// no LDS, no barrier, where the scalar kernel used a chain of shuffles.
 template <int EPI>
 __global__ __launch_bounds__(256) void k_gemm_reduce4(const float* __restrict__ part, int ksplit,
                                                       int M, int N, float* __restrict__ y,
@@ -1359,10 +1485,11 @@ __global__ __launch_bounds__(256) void k_gemm_reduce4(const float* __restrict__ 
             ss = fmaf(o[c], o[c], ss);
         }
     }
-    am = wave_max_nonneg(am);
-    ss = wave_sum(ss);
-    if ((threadIdx.x & 63) == 0 && live) {
-        const int nblk = Nout / 256, blk = col / 256;
+    am = half_max_nonneg(am);
+    ss = half_sum(ss);
+    if ((threadIdx.x & 31) == 31 && live) {
+        // the half's first output: 31 quads back
+        const int nblk = Nout / 128, blk = (col - 124) / 128;
         stats_out[((size_t)row * nblk + blk) * 2] = am;
         stats_out[((size_t)row * nblk + blk) * 2 + 1] = ss;
     }
@@ -1494,6 +1621,15 @@ extern "C" int cgx_gemv_stream_min_units(int units) {
 // Launches of at least this many blocks (four outputs a thread) take
 // k_gemm_reduce4.
 static int g_reduce4_min_blocks = 512;
+// One K split of a gate|up pair applies SwiGLU in the GEMM (1), or stores
+// partial sums for k_gemm_reduce (0).
+static int g_gemm_swiglu_here = 1;
+
+extern "C" int cgx_gemm_swiglu_here(int on) {
+    const int old = g_gemm_swiglu_here;
+    if (on >= 0) g_gemm_swiglu_here = on != 0;
+    return old;
+}
 
 extern "C" int cgx_gemm_reduce4_min_blocks(int blocks) {
     const int old = g_reduce4_min_blocks;
@@ -1539,8 +1675,12 @@ extern "C" int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int g
     const int ksteps = (nchunks + ksplit - 1) / ksplit;
     ksplit = (nchunks + ksteps - 1) / ksteps;
     // one split storing plain rows (the lm_head of a tree verify): the GEMM
-    // writes y itself, and no reduction pass copies it
-    const bool direct = ksplit == 1 && epi == kEpiStore && !stats_out && ldy == N;
+    // writes y itself, and no reduction pass copies it; one split of a
+    // gate|up pair (the tree verify's 256 rows): the GEMM applies SwiGLU and
+    // writes y and its row statistics (tree verify 12.50 -> 12.36 ms a step)
+    const bool swiglu_here = ksplit == 1 && paired && g_gemm_swiglu_here;
+    const bool direct = (ksplit == 1 && epi == kEpiStore && !stats_out && ldy == N) ||
+                        swiglu_here;
     const size_t row_bytes = (((size_t)M * 8) + 255) & ~(size_t)255;
     char* ws = (char*)cgx_scratch(CGX_SLOT_WS5,
                                   row_bytes + (direct ? 0 : (size_t)ksplit * M * N * 4));
@@ -1558,6 +1698,10 @@ extern "C" int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int g
     a.part = direct ? y : (float*)(ws + row_bytes);
     a.ksteps = ksteps;
     a.ff = N / 2;
+    a.y = swiglu_here ? y : nullptr;
+    a.ldy = ldy;
+    a.stats_out = swiglu_here ? stats_out : nullptr;
+    a.nw_next = nw_next;
     if (!stats_in) {
         hipLaunchKernelGGL(k_gemm_rows, dim3(M), dim3(256), 0, stream(), x, ldx, K, a.nw,
                            pro == kProRmsNorm, eps, smax, (float*)ws, (float*)ws + M);
@@ -1579,10 +1723,6 @@ extern "C" int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int g
     const int Nout = paired ? N / 2 : N;
     const size_t outs = (size_t)M * Nout;
     const int blocks = (int)((outs + 255) / 256);
-    if (stats_out && Nout % 256) {
-        cgx_set_error("gemm_int4: row statistics need an output width multiple of 256");
-        return -1;
-    }
     // four outputs a thread where y's rows are 16-byte aligned (the
     // decoder's buffers) and the launch keeps at least 512 blocks: 16-byte
     // loads and stores, DPP statistics (tree verify, 256 rows: 12.94 ->

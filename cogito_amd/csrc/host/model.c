@@ -426,8 +426,8 @@ static cgx_model* build(const cgx_model_config* cfg, uint64_t seed, cgx_model* s
         m->gu = (float*)cgx_malloc((size_t)Mx * c->d_ff * 4);      /* SwiGLU output */
         m->logits = (float*)cgx_malloc((size_t)Mx * V * 4);
         m->rope = (float*)cgx_malloc((size_t)Mx * c->head_dim * 4);
-        m->stats_x = (float*)cgx_malloc((size_t)Mx * (d / 256 + 1) * 2 * 4);
-        m->stats_g = (float*)cgx_malloc((size_t)Mx * (c->d_ff / 256 + 1) * 2 * 4);
+        m->stats_x = (float*)cgx_malloc((size_t)Mx * (d / 128 + 1) * 2 * 4);
+        m->stats_g = (float*)cgx_malloc((size_t)Mx * (c->d_ff / 128 + 1) * 2 * 4);
         ok = m->kv && m->tok && m->x && m->qkv && m->q && m->attn && m->gu && m->logits &&
              m->rope && m->stats_x && m->stats_g;
     }
@@ -667,8 +667,8 @@ int cgx_decoder_fused_attention(int on) {
     return old;
 }
 
-/* Row statistics handed from one GEMM's reduction to the next GEMM (rows
- * >= 32): [rows][width / 256][2] partial (max|y * nw|, sum y^2). */
+/* Row statistics handed from one GEMM's epilogue to the next GEMM (rows
+ * >= 32): [rows][width / 128][2] partial (max|y * nw|, sum y^2). */
 typedef struct {
     const float* in;      /* statistics of this linear's input, or NULL */
     int nin;
@@ -684,7 +684,7 @@ static int linear(const lin_t* L, const float* x, int ldx, int R, float* y, int 
     if (st) st->produced = 0;
     if (R >= 32 && cgk_gemm_int4_supported(R, L->K, L->N, gs, epi == EPI_SWIGLU)) {
         const int nout = epi == EPI_SWIGLU ? L->N / 2 : L->N;
-        float* so = st && st->out && nout % 256 == 0 ? st->out : NULL;
+        float* so = st && st->out && nout % 128 == 0 ? st->out : NULL;
         if (cgk_gemm_int4(x, ldx, R, L->K, L->N, gs, L->tiled, L->scales_t, L->smax, y, ldy,
                           pro, nw, eps, epi, st ? st->in : NULL, st ? st->nin : 0, so,
                           st ? st->nw_next : NULL))
@@ -764,7 +764,7 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
         uint8_t* vc = kv->v_cache + lb * slot;
         float* ks = kv->k_scales + lg * slot;
         float* vs = kv->v_scales + lg * slot;
-        stats_t sq = {xs_ok ? m->stats_x : NULL, d / 256, NULL, NULL, 0};
+        stats_t sq = {xs_ok ? m->stats_x : NULL, d / 128, NULL, NULL, 0};
         if (linear(&w[W_QKV], m->x, d, R, m->qkv, nq, PRO_RMSNORM, norm_w(m, 2 * l), eps,
                    EPI_STORE, gs, &sq))
             return -1;
@@ -795,12 +795,12 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
         if (linear(&w[W_O], m->attn, hq, R, m->x, d, PRO_NONE, NULL, 0.0f, EPI_ACCUMULATE,
                    gs, &so))
             return -1;
-        stats_t sg = {so.produced ? m->stats_x : NULL, d / 256, m->stats_g, NULL, 0};
+        stats_t sg = {so.produced ? m->stats_x : NULL, d / 128, m->stats_g, NULL, 0};
         if (linear(&w[W_GU], m->x, d, R, m->gu, ff, PRO_RMSNORM, norm_w(m, 2 * l + 1), eps,
                    EPI_SWIGLU, gs, &sg))
             return -1;
         /* the next consumer of x: layer l + 1's attention norm, or the final one */
-        stats_t sd = {sg.produced ? m->stats_g : NULL, ff / 256, m->stats_x,
+        stats_t sd = {sg.produced ? m->stats_g : NULL, ff / 128, m->stats_x,
                       norm_w(m, 2 * l + 2), 0};
         if (linear(&w[W_DOWN], m->gu, ff, R, m->x, d, PRO_NONE, NULL, 0.0f, EPI_ACCUMULATE, gs,
                    &sd))
@@ -811,7 +811,7 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
     if (!ldl) ldl = (size_t)n_logits * c->vocab;
     if (n_logits == M && ldl == (size_t)M * c->vocab) {
         /* every row, sequences in order */
-        stats_t sl = {xs_ok ? m->stats_x : NULL, d / 256, NULL, NULL, 0};
+        stats_t sl = {xs_ok ? m->stats_x : NULL, d / 128, NULL, NULL, 0};
         if (linear(&m->lm, m->x, d, R, out, c->vocab, PRO_RMSNORM, norm_w(m, 2 * c->n_layers),
                    eps, EPI_STORE, gs, &sl))
             return -1;

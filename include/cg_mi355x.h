@@ -269,6 +269,11 @@ int cgx_gemv_stream_min_units(int units);
  * 256-thread blocks (default 512; 0 always, a large value never); returns
  * the previous value (-1 only reads it). */
 int cgx_gemm_reduce4_min_blocks(int blocks);
+/* Test hook, no reference counterpart: 1 (default) applies SwiGLU inside the
+ * GEMM when a gate|up product has one K split, 0 stores its partial sums for
+ * the separate reduction pass (the same outputs, bit for bit); returns the
+ * previous setting (-1 only reads it). */
+int cgx_gemm_swiglu_here(int on);
 int cgx_attention_int4_kv_batch_dev(const float* Q, int B, int Nq, int H,
                                     cg_kv_cache_int4* cache, int slot0, const int* nk,
                                     int mask_kind, const unsigned long long* anc, int tw,

@@ -176,6 +176,31 @@ def _forward_batch_case(gpu, oracle, rng, cfg, B, replace):
     gpu.cgx_model_free(m)
 
 
+def test_gemm_swiglu_in_kernel_matches_reduction(gpu, rng):
+    # d_model 256 leaves every GEMM one K split: the gate|up product applies
+    # SwiGLU in its own epilogue (default) or stores partial sums for the
+    # reduction pass (hook off); the logits of 8 sequences x 5 rows must be
+    # the same bits either way (the consumer's row factor depends only on
+    # the row maxima, which do not depend on the order of reduction)
+    from dataclasses import replace
+    cfg = replace(TINY, max_batch=8)
+    toks = rng.integers(0, cfg.vocab, (8, 5)).astype(np.int32)
+    outs = []
+    old = gpu.cgx_gemm_swiglu_here(-1)
+    try:
+        for on in (1, 0):
+            gpu.cgx_gemm_swiglu_here(on)
+            m = new_model(gpu, cfg, 17)
+            assert gpu.cgx_model_forward_batch(m, toks.ctypes.data, 5, 5, None) == 0, \
+                last_error(gpu)
+            outs.append(logits_np(gpu, m, 40, cfg.vocab))
+            gpu.cgx_model_free(m)
+    finally:
+        gpu.cgx_gemm_swiglu_here(old)
+    assert np.isfinite(outs[0]).all()
+    np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
 def test_model_forward_head_dim_128_gqa(gpu, oracle, rng):
     cfg = Cfg(n_layers=1, d_model=512, n_heads=8, n_kv_heads=2, head_dim=128, d_ff=768,
               vocab=2048, group_size=128, kv_group_size=128, max_seq=300, max_tokens=5,
