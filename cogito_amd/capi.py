@@ -292,6 +292,7 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_rope_table_dev": (I, [I, I, I, C.c_float, VP]),
     "cgx_attention_rope_append_dev": (I, [VP, I, VP, I, I, VP, I, I, VP]),
     "cgx_decoder_fused_attention": (I, [I]),
+    "cgx_decoder_attention_stats": (I, [I]),
     "cgx_gemv_stream_min_units": (I, [I]),
     "cgx_gemm_reduce4_min_blocks": (I, [I]),
     "cgx_gemm_swiglu_here": (I, [I]),

@@ -107,6 +107,10 @@ struct DecArgs {
     float* ksw;
     float* vsw;
     int nsplit_old;
+    // row statistics of O for the GEMM that reads it (D == 128: one entry
+    // per output row and head, i.e. per 128 columns): (max|o|, sum o^2),
+    // [B][Nq][H][2]; nullptr: none
+    float* stats;
 };
 
 __device__ __forceinline__ int head_begin(int hk, int H, int Hk) { return (hk * H + Hk - 1) / Hk; }
@@ -164,6 +168,29 @@ __device__ __forceinline__ f16x2 nib_pair(uint32_t wlo, uint32_t whi, int t, con
 __device__ __forceinline__ void split16(float v, _Float16& hi, _Float16& lo) {
     hi = (_Float16)v;
     lo = (_Float16)(v - (float)hi);
+}
+
+// Sum / maximum (non-negative values) over each 32-lane half of the wave:
+// scans over the 16-lane DPP rows, then row_bcast:15 adds row 0's total into
+// row 1 and row 2's into row 3, so lanes 31 and 63 hold the halves' results.
+__device__ __forceinline__ float half_sum(float v) {
+#define CGX_DPP(CTRL, RMASK) \
+    __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, RMASK, 0xF, true))
+    v += CGX_DPP(0x111, 0xF);
+    v += CGX_DPP(0x112, 0xF);
+    v += CGX_DPP(0x114, 0xF);
+    v += CGX_DPP(0x118, 0xF);
+    v += CGX_DPP(0x142, 0xA);
+    return v;
+}
+__device__ __forceinline__ float half_max_nonneg(float v) {
+    v = fmaxf(v, CGX_DPP(0x111, 0xF));
+    v = fmaxf(v, CGX_DPP(0x112, 0xF));
+    v = fmaxf(v, CGX_DPP(0x114, 0xF));
+    v = fmaxf(v, CGX_DPP(0x118, 0xF));
+    v = fmaxf(v, CGX_DPP(0x142, 0xA));
+    return v;
+#undef CGX_DPP
 }
 
 // Workgroup barrier that orders LDS accesses only: global loads in flight
@@ -785,6 +812,15 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_dec(DecArgs a) {
             const float4 out = L > 0.0f ? make_float4(acc.x / L, acc.y / L, acc.z / L, acc.w / L)
                                         : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             *(float4*)&a.O[orow * D + d] = out;
+            if (D == 128 && a.stats) {
+                // a row's 32 quads are one half wave (rows start at multiples
+                // of 32 threads), which reduces them by DPP
+                float am = fmaxf(fmaxf(fabsf(out.x), fabsf(out.y)), fmaxf(fabsf(out.z), fabsf(out.w)));
+                float ss = fmaf(out.w, out.w, fmaf(out.z, out.z, fmaf(out.y, out.y, out.x * out.x)));
+                am = half_max_nonneg(am);
+                ss = half_sum(ss);
+                if ((threadIdx.x & 31) == 31) *(float2*)&a.stats[orow * 2] = make_float2(am, ss);
+            }
         } else {
             *(float4*)&a.part_o[((size_t)split * nrow + orow) * D + d] = acc;
             if (d == 0) {
@@ -800,9 +836,10 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_dec(DecArgs a) {
 // forms the maximum, the weights and the weighted sum in split order (the
 // same fixed order for every column), and reads the partial rows eight splits
 // at a time with independent loads.
+// With stats (D == 128: two waves), also the row's (max|o|, sum o^2).
 __global__ void k_attn_dec_combine(const float* __restrict__ part_o,
                                    const float* __restrict__ part_ml, int splits, int nrow,
-                                   int D, float* __restrict__ O) {
+                                   int D, float* __restrict__ O, float* __restrict__ stats) {
     const int row = blockIdx.x, d = threadIdx.x;
     __shared__ float s_m[128], s_l[128], s_w[128];
     for (int s = d; s < splits; s += blockDim.x) {
@@ -828,7 +865,21 @@ __global__ void k_attn_dec_combine(const float* __restrict__ part_o,
         for (int j = 0; j < 8; j++) acc += v[j] * s_w[s + j];
     }
     for (; s < splits; s++) acc += part_o[((size_t)s * nrow + row) * D + d] * s_w[s];
-    O[(size_t)row * D + d] = L > 0.0f ? acc / L : 0.0f;
+    const float o = L > 0.0f ? acc / L : 0.0f;
+    O[(size_t)row * D + d] = o;
+    if (!stats) return;
+    float am = half_max_nonneg(fabsf(o)), ss = half_sum(o * o);
+    // halves 0..3 (lanes 31, 63 of waves 0 and 1) -> s_m / s_l (free again)
+    __syncthreads();
+    if ((d & 31) == 31) {
+        s_m[d >> 5] = am;
+        s_l[d >> 5] = ss;
+    }
+    __syncthreads();
+    if (d == 0)
+        *(float2*)&stats[(size_t)row * 2] =
+            make_float2(fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3])),
+                        (s_l[0] + s_l[1]) + (s_l[2] + s_l[3]));
 }
 
 template <int D, int RT, bool FUSED = false>
@@ -915,7 +966,7 @@ static int launch_dec(DecArgs& a, int nk_split_max, bool fused, float* O) {
     if (rc) return rc;
     if (splits > 1) {
         hipLaunchKernelGGL(k_attn_dec_combine, dim3(nrow), dim3(D), 0, stream(), a.part_o,
-                           a.part_ml, splits, nrow, D, O);
+                           a.part_ml, splits, nrow, D, O, D == 128 ? a.stats : nullptr);
         if (launch_check("k_attn_dec_combine")) return -1;
     }
     return 0;
@@ -963,7 +1014,8 @@ extern "C" int cgk_attn_dec_batch(const float* Q, const uint8_t* kc, const uint8
                                   const float* ks, const float* vs, int B, const int* nk,
                                   size_t seq_kbytes, size_t seq_groups, int Nq, int H, int Hk,
                                   int D, float scale, int mask_kind,
-                                  const unsigned long long* anc, int tw, float* O) {
+                                  const unsigned long long* anc, int tw, float* O,
+                                  float* stats) {
     DecArgs a;
     int nkmax;
     if (fill_args(a, kc, vc, ks, vs, B, nk, seq_kbytes, seq_groups, Nq, H, Hk, D, scale,
@@ -974,6 +1026,7 @@ extern "C" int cgk_attn_dec_batch(const float* Q, const uint8_t* kc, const uint8
         return -1;
     }
     a.Q = Q;
+    a.stats = D == 128 ? stats : nullptr;
     return launch_dec(a, nkmax, false, O);
 }
 
@@ -986,7 +1039,8 @@ extern "C" int cgk_attn_dec_rope(const float* qkv, int ldq, const float* rope, u
                                  uint8_t* vc, float* ks, float* vs, int B, const int* nk,
                                  size_t seq_kbytes, size_t seq_groups, int Nq, int H, int Hk,
                                  int D, float scale, int mask_kind,
-                                 const unsigned long long* anc, int tw, float* O) {
+                                 const unsigned long long* anc, int tw, float* O,
+                                 float* stats) {
     DecArgs a;
     int nkmax;
     if (fill_args(a, kc, vc, ks, vs, B, nk, seq_kbytes, seq_groups, Nq, H, Hk, D, scale,
@@ -1002,6 +1056,7 @@ extern "C" int cgk_attn_dec_rope(const float* qkv, int ldq, const float* rope, u
     a.ldq = ldq;
     a.rope = (const float2*)rope;
     a.kcw = kc; a.vcw = vc; a.ksw = ks; a.vsw = vs;
+    a.stats = D == 128 ? stats : nullptr;
     int nk_old_max = 0;
     for (int b = 0; b < B; b++) nk_old_max = nk[b] - Nq > nk_old_max ? nk[b] - Nq : nk_old_max;
     return launch_dec(a, nk_old_max, true, O);
@@ -1011,5 +1066,5 @@ extern "C" int cgk_attn_dec(const float* Q, const uint8_t* kc, const uint8_t* vc
                             const float* vs, int Nq, int Nk, int H, int Hk, int D, float scale,
                             int mask_kind, const unsigned long long* anc, float* O) {
     return cgk_attn_dec_batch(Q, kc, vc, ks, vs, 1, &Nk, 0, 0, Nq, H, Hk, D, scale, mask_kind,
-                              anc, Nq, O);
+                              anc, Nq, O, nullptr);
 }

@@ -208,11 +208,14 @@ int cgk_attn_dec(const float* Q, const uint8_t* kc, const uint8_t* vc, const flo
 /* Batched decode attention: B sequences of Nq query rows, sequence b's cache
  * at kc + b * seq_kbytes (scales + b * seq_groups) with nk[b] keys.  Tree
  * mask: the last tw keys (Nq <= tw <= 64; the tree's nodes so far, the query
- * rows last) are visible to query row i only where bit j of anc[i] is set. */
+ * rows last) are visible to query row i only where bit j of anc[i] is set.
+ * stats (D == 128; NULL: none) receives the row statistics of O for the GEMM
+ * that reads it: (max|o|, sum o^2) per output row and head, [B][Nq][H][2]. */
 int cgk_attn_dec_batch(const float* Q, const uint8_t* kc, const uint8_t* vc, const float* ks,
                        const float* vs, int B, const int* nk, size_t seq_kbytes,
                        size_t seq_groups, int Nq, int H, int Hk, int D, float scale,
-                       int mask_kind, const unsigned long long* anc, int tw, float* O);
+                       int mask_kind, const unsigned long long* anc, int tw, float* O,
+                       float* stats);
 
 /* Rows of a tree forward (cgx_model_forward_tree): row i sits at cache slot
  * len + i and rotary position len + rel[i]; the last tw cached keys are the
@@ -296,7 +299,8 @@ int cgk_rope_table(int rows, int D, int pos0, float theta, float* cs);
 int cgk_attn_dec_rope(const float* qkv, int ldq, const float* rope, uint8_t* kc, uint8_t* vc,
                       float* ks, float* vs, int B, const int* nk, size_t seq_kbytes,
                       size_t seq_groups, int Nq, int H, int Hk, int D, float scale,
-                      int mask_kind, const unsigned long long* anc, int tw, float* O);
+                      int mask_kind, const unsigned long long* anc, int tw, float* O,
+                      float* stats);
 int cgk_rope_freqs(float* cs, float* sn, int S, int D, float theta);
 int cgk_alibi_slopes(float* slopes, int H);
 int cgk_alibi_bias(float* bias, int Sq, int Sk, int H, const float* slopes);

@@ -192,7 +192,7 @@ int cgx_attention_int4_kv_batch_dev(const float* Q, int B, int Nq, int H, cg_kv_
                               c->k_scales + lg * slot0, c->v_scales + lg * slot0, B, nk, lb, lg,
                               Nq, H, c->n_heads, c->head_dim, 1.0f / sqrtf((float)c->head_dim),
                               mask_kind == 1 ? CGK_MASK_TREE : CGK_MASK_CAUSAL_ALIGNED, anc, tw,
-                              O);
+                              O, NULL);
 }
 
 int cgx_rope_table_dev(int rows, int head_dim, int pos0, float theta, float* cs) {
@@ -223,7 +223,7 @@ int cgx_attention_rope_append_dev(const float* qkv, int ldq, const float* rope, 
     return cgk_attn_dec_rope(qkv, ldq, rope, c->k_cache + lb * layer, c->v_cache + lb * layer,
                              c->k_scales + lg * layer, c->v_scales + lg * layer, 1, &nk, 0, 0,
                              Nq, H, c->n_heads, c->head_dim, 1.0f / sqrtf((float)c->head_dim),
-                             CGK_MASK_CAUSAL_ALIGNED, NULL, Nq, O);
+                             CGK_MASK_CAUSAL_ALIGNED, NULL, Nq, O, NULL);
 }
 
 int cgx_attention_int4_kv_dev(const float* Q, int Nq, int H, cg_kv_cache_int4* c,

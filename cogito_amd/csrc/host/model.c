@@ -23,7 +23,8 @@ int cgk_embed_rope(const float* table, const int* tokens, int B, int M, int d, i
 int cgk_attn_dec_rope(const float* qkv, int ldq, const float* rope, uint8_t* kc, uint8_t* vc,
                       float* ks, float* vs, int B, const int* nk, size_t seq_kbytes,
                       size_t seq_groups, int Nq, int H, int Hk, int D, float scale,
-                      int mask_kind, const unsigned long long* anc, int tw, float* O);
+                      int mask_kind, const unsigned long long* anc, int tw, float* O,
+                      float* stats);
 int cgk_rope_append_batch(const float* qkv, int ld, int B, int M, int H, int Hk, int D, int gs,
                           const int* pos0, const int* rel, float theta, const float* cs,
                           float* q_out, uint8_t* kc, uint8_t* vc, float* ks, float* vs,
@@ -67,6 +68,7 @@ struct cgx_model {
     float *x, *qkv, *q, *attn, *gu, *logits;
     float* rope;             /* [rows][head_dim / 2] (cos, sin) of the step's positions */
     float *stats_x, *stats_g;  /* row statistics of x and of the SwiGLU output */
+    float* stats_a;          /* of the attention output (head_dim 128: per head) */
 };
 
 static int nqkv(const cgx_model_config* c) { return (c->n_heads + 2 * c->n_kv_heads) * c->head_dim; }
@@ -337,6 +339,7 @@ void cgx_model_free(cgx_model* m) {
     cgx_free(m->rope);
     cgx_free(m->stats_x);
     cgx_free(m->stats_g);
+    cgx_free(m->stats_a);
     free(m);
 }
 
@@ -428,8 +431,9 @@ static cgx_model* build(const cgx_model_config* cfg, uint64_t seed, cgx_model* s
         m->rope = (float*)cgx_malloc((size_t)Mx * c->head_dim * 4);
         m->stats_x = (float*)cgx_malloc((size_t)Mx * (d / 128 + 1) * 2 * 4);
         m->stats_g = (float*)cgx_malloc((size_t)Mx * (c->d_ff / 128 + 1) * 2 * 4);
+        m->stats_a = (float*)cgx_malloc((size_t)Mx * c->n_heads * 2 * 4);
         ok = m->kv && m->tok && m->x && m->qkv && m->q && m->attn && m->gu && m->logits &&
-             m->rope && m->stats_x && m->stats_g;
+             m->rope && m->stats_x && m->stats_g && m->stats_a;
     }
     if (ok) ok = !cgx_synchronize();
     cgx_free(tf);
@@ -661,6 +665,17 @@ static size_t kv_layer_groups(const cg_kv_cache_int4* c) {
  * of their own before it (0; a test hook: both must give the same cache). */
 static int g_fused_attention = 1;
 
+/* The attention writes the row statistics of its output for the O GEMM (1),
+ * or the GEMM computes them in a pass of its own (0; a test hook: the same
+ * row factors, so the same bits). */
+static int g_attention_stats = 1;
+
+int cgx_decoder_attention_stats(int on) {
+    const int old = g_attention_stats;
+    if (on >= 0) g_attention_stats = on != 0;
+    return old;
+}
+
 int cgx_decoder_fused_attention(int on) {
     const int old = g_fused_attention;
     if (on >= 0) g_fused_attention = on != 0;
@@ -768,10 +783,13 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
         if (linear(&w[W_QKV], m->x, d, R, m->qkv, nq, PRO_RMSNORM, norm_w(m, 2 * l), eps,
                    EPI_STORE, gs, &sq))
             return -1;
+        /* the attention leaves the O GEMM's row statistics (head_dim 128: one
+         * entry per head), which then needs no pass of its own over them */
+        float* as = batched && hd == 128 && R >= 32 && g_attention_stats ? m->stats_a : NULL;
         if (fused) {
             if (cgk_attn_dec_rope(m->qkv, nq, m->rope, kc, vc, ks, vs, B, nk, lb, lg, M, H, Hk,
                                   hd, scale, mask, tr ? tr->anc : NULL, tr ? tr->tw : M,
-                                  m->attn))
+                                  m->attn, as))
                 return -1;
         } else if (cgk_rope_append_batch(m->qkv, nq, B, M, H, Hk, hd, kv->group_size, pos0,
                                          tr ? tr->rel : NULL, c->rope_theta, m->rope, m->q, kc,
@@ -779,7 +797,7 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
             return -1;
         } else if (batched) {
             if (cgk_attn_dec_batch(m->q, kc, vc, ks, vs, B, nk, lb, lg, M, H, Hk, hd, scale,
-                                   mask, tr ? tr->anc : NULL, tr ? tr->tw : M, m->attn))
+                                   mask, tr ? tr->anc : NULL, tr ? tr->tw : M, m->attn, as))
                 return -1;
         } else {
             for (int b = 0; b < B; b++)
@@ -791,7 +809,7 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
         }
         /* o -> (x) -> gate|up -> (g) -> down -> (x) -> next qkv / lm_head: each
          * reduction leaves the row statistics its consumer needs */
-        stats_t so = {NULL, 0, m->stats_x, norm_w(m, 2 * l + 1), 0};
+        stats_t so = {as, H, m->stats_x, norm_w(m, 2 * l + 1), 0};
         if (linear(&w[W_O], m->attn, hq, R, m->x, d, PRO_NONE, NULL, 0.0f, EPI_ACCUMULATE,
                    gs, &so))
             return -1;

@@ -258,6 +258,12 @@ int cgx_attention_rope_append_dev(const float* qkv, int ldq, const float* rope, 
  * cache append inside the attention launch, 0 as launches of their own (the
  * same cache contents); returns the previous setting (-1 only reads it). */
 int cgx_decoder_fused_attention(int on);
+/* Test hook, no reference counterpart: 1 (default) has the decoder's
+ * attention (head_dim 128, 32+ rows) write the row statistics of its output
+ * for the O projection's GEMM, 0 leaves them to a pass of the GEMM's own (the
+ * same row factors, so the same outputs); returns the previous setting (-1
+ * only reads it). */
+int cgx_decoder_attention_stats(int on);
 /* Test hook, no reference counterpart: the INT4 GEMV takes the persistent
  * streaming kernel for K = 4096 and up to 5 rows once the busiest CU gets at
  * least this many 32-column units (default 8: a 64k- or 128k-vocabulary

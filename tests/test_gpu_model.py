@@ -201,6 +201,38 @@ def test_gemm_swiglu_in_kernel_matches_reduction(gpu, rng):
     np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
 
 
+@pytest.mark.parametrize("fused", [1, 0])
+def test_attention_row_statistics_match_gemm_pass(gpu, rng, fused):
+    # head_dim 128 and 8 sequences x 5 rows (the GEMM path): the attention
+    # (with RoPE and the cache append inside, or after a launch of their own)
+    # writes the O projection's row statistics, or the GEMM computes them
+    # from the rows; the row factors come from the row maxima either way, so
+    # the logits must be the same bits
+    cfg = Cfg(n_layers=2, d_model=512, n_heads=8, n_kv_heads=2, head_dim=128, d_ff=768,
+              vocab=2048, group_size=128, kv_group_size=128, max_seq=300, max_tokens=5,
+              init_std=0.05, max_batch=8)
+    toks = rng.integers(0, cfg.vocab, (2, 8, 5)).astype(np.int32)
+    outs = []
+    old = gpu.cgx_decoder_attention_stats(-1)
+    old_f = gpu.cgx_decoder_fused_attention(fused)
+    try:
+        for on in (1, 0):
+            gpu.cgx_decoder_attention_stats(on)
+            m = new_model(gpu, cfg, 23)
+            got = []
+            for step in range(2):        # the second step attends to the first's keys
+                assert gpu.cgx_model_forward_batch(m, toks[step].ctypes.data, 5, 5, None) == 0, \
+                    last_error(gpu)
+                got.append(logits_np(gpu, m, 40, cfg.vocab))
+            outs.append(np.stack(got))
+            gpu.cgx_model_free(m)
+    finally:
+        gpu.cgx_decoder_attention_stats(old)
+        gpu.cgx_decoder_fused_attention(old_f)
+    assert np.isfinite(outs[0]).all()
+    np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
 def test_model_forward_head_dim_128_gqa(gpu, oracle, rng):
     cfg = Cfg(n_layers=1, d_model=512, n_heads=8, n_kv_heads=2, head_dim=128, d_ff=768,
               vocab=2048, group_size=128, kv_group_size=128, max_seq=300, max_tokens=5,
