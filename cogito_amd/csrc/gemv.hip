@@ -1380,6 +1380,41 @@ __global__ __launch_bounds__(256) void k_gemm_rows(const float* __restrict__ x, 
     }
 }
 
+// 0 + p[0] + p[mn] + ... + p[(n - 1) mn] left to right, eight splits' loads
+// in flight together (one memory round trip per eight splits; past n the
+// loads repeat split n - 1, which is in bounds, and add +0, which leaves the
+// sum's bits alone: a sum that starts at +0 never becomes -0)
+__device__ __forceinline__ float split_sum(const float* __restrict__ p, size_t mn, int n) {
+    float v = 0.0f;
+    for (int z0 = 0; z0 < n; z0 += 8) {
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) t[j] = p[(size_t)min(z0 + j, n - 1) * mn];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v += z0 + j < n ? t[j] : 0.0f;
+    }
+    return v;
+}
+
+// The same for four neighbouring outputs (16-byte loads).
+__device__ __forceinline__ void split_sum4(const float* __restrict__ p, size_t mn, int n,
+                                           float (&v)[4]) {
+    v[0] = v[1] = v[2] = v[3] = 0.0f;
+    for (int z0 = 0; z0 < n; z0 += 8) {
+        float4 t[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) t[j] = *(const float4*)(p + (size_t)min(z0 + j, n - 1) * mn);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const bool in = z0 + j < n;
+            v[0] += in ? t[j].x : 0.0f;
+            v[1] += in ? t[j].y : 0.0f;
+            v[2] += in ? t[j].z : 0.0f;
+            v[3] += in ? t[j].w : 0.0f;
+        }
+    }
+}
+
 // Sum of the K splits in order, and the epilogue.  With stats_out, also the
 // (max|y * nw_next|, sum y^2) of every 128 stored outputs of a row (two
 // waves; the output width is a multiple of 128): the next GEMM's row
@@ -1391,19 +1426,21 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float* __restrict__ p
                                                      const float* __restrict__ nw_next) {
     __shared__ float s_a[4], s_s[4];
     const int Nout = EPI == kEpiSwiGlu ? N / 2 : N;
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (!stats_out && i >= (size_t)M * Nout) return;
-    const bool live = i < (size_t)M * Nout;
-    const int row = live ? (int)(i / Nout) : 0, col = live ? (int)(i % Nout) : 0;
+    // 32-bit indices (M * Nout < 2^31, checked on the host): a 64-bit
+    // division costs about a hundred instructions
+    const unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (!stats_out && i >= (unsigned)(M * Nout)) return;
+    const bool live = i < (unsigned)(M * Nout);
+    const int row = live ? (int)(i / (unsigned)Nout) : 0;
+    const int col = live ? (int)(i - (unsigned)row * (unsigned)Nout) : 0;
     const size_t mn = (size_t)M * N;
     float out = 0.0f;
     if (live) {
-        float v = 0.0f;
-        for (int z = 0; z < ksplit; z++) v += part[z * mn + (size_t)row * N + col];
+        const float* p = part + (size_t)row * N + col;
+        const float v = split_sum(p, mn, ksplit);
         float* yp = y + (size_t)row * ldy + col;
         if (EPI == kEpiSwiGlu) {
-            float u = 0.0f;
-            for (int z = 0; z < ksplit; z++) u += part[z * mn + (size_t)row * N + Nout + col];
+            const float u = split_sum(p + Nout, mn, ksplit);
             out = v / (1.0f + __expf(-v)) * u;
         } else {
             out = EPI == kEpiAccumulate ? *yp + v : v;
@@ -1445,26 +1482,20 @@ __global__ __launch_bounds__(256) void k_gemm_reduce4(const float* __restrict__ 
                                                       int ldy, float* __restrict__ stats_out,
                                                       const float* __restrict__ nw_next) {
     const int Nout = EPI == kEpiSwiGlu ? N / 2 : N;
-    const size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x;   // 4 outputs
-    const bool live = 4 * q < (size_t)M * Nout;
+    const unsigned e = 4 * (blockIdx.x * blockDim.x + threadIdx.x);   // first of 4 outputs
+    const bool live = e < (unsigned)(M * Nout);
     if (!stats_out && !live) return;
-    const int row = live ? (int)(4 * q / Nout) : 0, col = live ? (int)(4 * q % Nout) : 0;
+    const int row = live ? (int)(e / (unsigned)Nout) : 0;
+    const int col = live ? (int)(e - (unsigned)row * (unsigned)Nout) : 0;
     const size_t mn = (size_t)M * N;
     float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (live) {
         const float* p = part + (size_t)row * N + col;
-        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int z = 0; z < ksplit; z++) {
-            const float4 t = *(const float4*)(p + z * mn);
-            v[0] += t.x; v[1] += t.y; v[2] += t.z; v[3] += t.w;
-        }
+        float v[4], u[4];
+        split_sum4(p, mn, ksplit, v);
         float4* yp = (float4*)(y + (size_t)row * ldy + col);
         if (EPI == kEpiSwiGlu) {
-            float u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            for (int z = 0; z < ksplit; z++) {
-                const float4 t = *(const float4*)(p + z * mn + Nout);
-                u[0] += t.x; u[1] += t.y; u[2] += t.z; u[3] += t.w;
-            }
+            split_sum4(p + Nout, mn, ksplit, u);
 #pragma unroll
             for (int c = 0; c < 4; c++) o[c] = v[c] / (1.0f + __expf(-v[c])) * u[c];
         } else if (EPI == kEpiAccumulate) {
@@ -1650,7 +1681,7 @@ extern "C" int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int g
     const int paired = epi == kEpiSwiGlu;
     if (!cgk_gemm_int4_supported(M, K, N, gs, paired) || ldx < K || (ldx & 3) ||
         ((uintptr_t)x & 15) || (pro == kProRmsNorm && (!nw || ((uintptr_t)nw & 15))) ||
-        ldy < (paired ? N / 2 : N)) {
+        ldy < (paired ? N / 2 : N) || (size_t)M * N >= (1u << 31)) {
         cgx_set_error("gemm_int4: unsupported shape M=%d K=%d N=%d gs=%d", M, K, N, gs);
         return -1;
     }
@@ -1726,9 +1757,9 @@ extern "C" int cgk_gemm_int4(const float* x, int ldx, int M, int K, int N, int g
     // four outputs a thread where y's rows are 16-byte aligned (the
     // decoder's buffers) and the launch keeps at least 512 blocks: 16-byte
     // loads and stores, DPP statistics (tree verify, 256 rows: 12.94 ->
-    // 12.54 ms a step).  Fewer outputs keep a thread each, so that more
-    // threads cover the split loads' latency (the batch-8 verify, 40 rows and
-    // up to 16 splits, measured 1.5 % slower a step with four a thread).
+    // 12.54 ms a step).  Fewer outputs keep a thread each (the batch-8
+    // verify, 40 rows and up to 16 splits, measured the same either way once
+    // each thread's split loads were batched: 5.66 -> 5.45 ms a step).
     const int blocks4 = (int)((outs / 4 + 255) / 256);
     if (((uintptr_t)y & 15) == 0 && ldy % 4 == 0 && blocks4 >= g_reduce4_min_blocks) {
         if (epi == kEpiSwiGlu)
