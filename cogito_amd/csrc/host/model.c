@@ -683,7 +683,7 @@ int cgx_decoder_fused_attention(int on) {
 }
 
 /* Row statistics handed from one GEMM's epilogue to the next GEMM (rows
- * >= 32): [rows][width / 128][2] partial (max|y * nw|, sum y^2). */
+ * >= GEMM_MIN_ROWS): [rows][width / 128][2] partial (max|y * nw|, sum y^2). */
 typedef struct {
     const float* in;      /* statistics of this linear's input, or NULL */
     int nin;
@@ -692,12 +692,19 @@ typedef struct {
     int produced;         /* set when `out` was written */
 } stats_t;
 
-/* One linear layer over R rows: the GEMM from 32 rows on (one pass over the
- * weight), the GEMV below (it streams the weight once per 16 rows). */
+/* Rows from which a linear layer takes the GEMM: from 16 rows the GEMM's
+ * shared activation tiles beat the GEMV, whose 16-row instance needs a hi and
+ * a lo MFMA per tile (the tree draft's 16-row levels, 4096 x 128256 lm_head
+ * included: tree verify 12.38 -> 12.17 ms a step). */
+#define GEMM_MIN_ROWS 16
+
+/* One linear layer over R rows: the GEMM from GEMM_MIN_ROWS rows on (one
+ * pass over the weight), the GEMV below (it streams the weight once per 16
+ * rows). */
 static int linear(const lin_t* L, const float* x, int ldx, int R, float* y, int ldy, int pro,
                   const float* nw, float eps, int epi, int gs, stats_t* st) {
     if (st) st->produced = 0;
-    if (R >= 32 && cgk_gemm_int4_supported(R, L->K, L->N, gs, epi == EPI_SWIGLU)) {
+    if (R >= GEMM_MIN_ROWS && cgk_gemm_int4_supported(R, L->K, L->N, gs, epi == EPI_SWIGLU)) {
         const int nout = epi == EPI_SWIGLU ? L->N / 2 : L->N;
         float* so = st && st->out && nout % 128 == 0 ? st->out : NULL;
         if (cgk_gemm_int4(x, ldx, R, L->K, L->N, gs, L->tiled, L->scales_t, L->smax, y, ldy,
@@ -785,7 +792,8 @@ static int forward_rows(cgx_model* m, int B, const int* tokens, int M, int n_log
             return -1;
         /* the attention leaves the O GEMM's row statistics (head_dim 128: one
          * entry per head), which then needs no pass of its own over them */
-        float* as = batched && hd == 128 && R >= 32 && g_attention_stats ? m->stats_a : NULL;
+        float* as =
+            batched && hd == 128 && R >= GEMM_MIN_ROWS && g_attention_stats ? m->stats_a : NULL;
         if (fused) {
             if (cgk_attn_dec_rope(m->qkv, nq, m->rope, kc, vc, ks, vs, B, nk, lb, lg, M, H, Hk,
                                   hd, scale, mask, tr ? tr->anc : NULL, tr ? tr->tw : M,
