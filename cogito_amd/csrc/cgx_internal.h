@@ -74,7 +74,7 @@ int cgk_int4_dequantize_mfma(const uint8_t* w, const float* scales_t, int K, int
  * flat nibbles (K*N/2 bytes) and flat scales [K][N/gs]. */
 int cgk_int4_unpack_mfma(const uint8_t* w, const float* scales_t, int K, int N, int gs,
                          int paired, uint8_t* flat, float* scales);
-/* INT4 GEMM for M >= 32 rows over layout 3 (gemv.hip): same arguments and
+/* INT4 GEMM for M >= 16 rows over layout 3 (gemv.hip): same arguments and
  * epilogues as cgk_gemv_mfma plus smax >= every |scale| of the weight.
  * stats_in ([M][nstat_in][2] partial max|x*nw| and sum x^2, from the
  * producer's stats_out) replaces the row-statistics pass over x; stats_out

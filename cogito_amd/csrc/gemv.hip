@@ -927,7 +927,7 @@ int launch_pe(const MfmaArgs& a, int T) {
 }
 
 // ------------------------------------------------------------------ GEMM
-// y = x @ W for M >= 32 rows (batched verify, tree verify).  A block of 4
+// y = x @ W for M >= 16 rows (batched verify, tree verify).  A block of 4
 // waves covers two 128-column slots (two neighbouring scale groups, or the
 // gate and up halves of the same 128 SwiGLU columns), each wave 4 column
 // tiles of one slot, so one A fragment read from LDS feeds 4 tiles.  Per

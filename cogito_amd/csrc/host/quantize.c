@@ -266,7 +266,7 @@ int cgx_matmul_int4_dev_kernel(const float* x, int M, cg_tensor_quant* w,
             cgx_set_error("cgx_matmul_int4: MFMA kernels need a layout-3 weight");
             return -1;
         }
-        if (kernel == 4)      /* the GEMM of the batched / tree verify (M >= 32) */
+        if (kernel == 4)      /* the GEMM of the batched / tree verify (M >= 16) */
             return cgk_gemm_int4(x, info.K, M, info.K, info.N, info.group_size, w->data,
                                  w->scales, info.smax, y, info.N, 0, NULL, 0.0f, 0, NULL, 0,
                                  NULL, NULL);

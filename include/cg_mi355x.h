@@ -95,7 +95,7 @@ int cgx_matmul_int4_dev(const float* x, int M, cg_tensor_quant* w, float* y);
 /* Same with the kernel forced: 0 auto (by layout), 1 VALU GEMV (layout 2),
  * 2 generic reference-order kernel (layout 1), 3 MFMA GEMV (layout 3),
  * 4 MFMA GEMM with a shared activation tile (layout 3, N % 128 == 0,
- * group % 128 == 0; the batched and tree verify shapes, M >= 32). */
+ * group % 128 == 0; the batched and tree verify shapes, M >= 16). */
 int cgx_matmul_int4_dev_kernel(const float* x, int M, cg_tensor_quant* w,
                                float* y, int kernel);
 
@@ -259,7 +259,7 @@ int cgx_attention_rope_append_dev(const float* qkv, int ldq, const float* rope, 
  * same cache contents); returns the previous setting (-1 only reads it). */
 int cgx_decoder_fused_attention(int on);
 /* Test hook, no reference counterpart: 1 (default) has the decoder's
- * attention (head_dim 128, 32+ rows) write the row statistics of its output
+ * attention (head_dim 128, 16+ rows) write the row statistics of its output
  * for the O projection's GEMM, 0 leaves them to a pass of the GEMM's own (the
  * same row factors, so the same outputs); returns the previous setting (-1
  * only reads it). */
@@ -270,7 +270,7 @@ int cgx_decoder_attention_stats(int on);
  * lm_head; 0 never, 1 every product it supports); returns the previous value
  * (-1 only reads it). */
 int cgx_gemv_stream_min_units(int units);
-/* Test hook, no reference counterpart: the GEMM (32+ rows) sums its K splits
+/* Test hook, no reference counterpart: the GEMM (16+ rows) sums its K splits
  * with four outputs a thread once that launch has at least this many
  * 256-thread blocks (default 512; 0 always, a large value never); returns
  * the previous value (-1 only reads it). */
