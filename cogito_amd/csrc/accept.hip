@@ -74,6 +74,19 @@ __global__ void k_exp_fast_maxerr(float lo, float hi, unsigned int* out) {
     atomicMax(out, __float_as_uint(worst));
 }
 
+// The same for exp_stat.
+__global__ void k_exp_stat_maxerr(float lo, float hi, unsigned int* out) {
+    const unsigned int ulo = __float_as_uint(hi) | 0x80000000u, uhi = __float_as_uint(lo);
+    float worst = 0.0f;
+    for (unsigned long long i = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x;
+         i <= (unsigned long long)(uhi - ulo); i += (unsigned long long)gridDim.x * blockDim.x) {
+        const float x = __uint_as_float(ulo + (unsigned int)i);
+        const float g = exp_glibc(x), f = exp_stat(x);
+        if (g > 0.0f) worst = fmaxf(worst, fabsf(f - g) / g);
+    }
+    atomicMax(out, __float_as_uint(worst));
+}
+
 __global__ __launch_bounds__(kThreads) void k_ordered_sum(const float* x, int n, float* out) {
     __shared__ EosShared sh;
     float s = eos_sum(RowSrc{x}, n, sh);
@@ -237,6 +250,15 @@ extern "C" int cgk_exp_fast_maxerr(float lo, float hi, unsigned int* out_dev) {
     }
     hipLaunchKernelGGL(k_exp_fast_maxerr, dim3(4096), dim3(256), 0, stream(), lo, hi, out_dev);
     return launch_check("k_exp_fast_maxerr");
+}
+
+extern "C" int cgk_exp_stat_maxerr(float lo, float hi, unsigned int* out_dev) {
+    if (!(lo < hi) || hi > 0.0f || lo < kExpFastMin) {
+        cgx_set_error("exp_stat_maxerr: range must satisfy %g <= lo < hi <= 0", kExpFastMin);
+        return -1;
+    }
+    hipLaunchKernelGGL(k_exp_stat_maxerr, dim3(4096), dim3(256), 0, stream(), lo, hi, out_dev);
+    return launch_check("k_exp_stat_maxerr");
 }
 
 extern "C" int cgk_exact_expf(const float* x, float* y, int n) {

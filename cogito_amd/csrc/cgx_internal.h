@@ -118,6 +118,7 @@ int cgk_spec_tokens(const int* feed, const int* dtok, int B, int gamma, int* tto
 int cgx_model_forward_batch_ld(struct cgx_model* m, const int* tokens, int M, int n_logits,
                                float* logits, size_t ld);
 int cgk_exp_fast_maxerr(float lo, float hi, unsigned int* out_dev);
+int cgk_exp_stat_maxerr(float lo, float hi, unsigned int* out_dev);
 int cgk_ordered_sum(const float* x, int n, float* out);
 int cgk_sample_temperature(const float* logits, int V, float T, float u, int* out);
 int cgk_sample_corrected(const float* q, const float* p, int V, float u, int* out);

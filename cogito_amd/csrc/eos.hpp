@@ -91,6 +91,18 @@ __device__ __forceinline__ float exp_fast(float x) {
     return ldexpf(__builtin_amdgcn_exp2f(f), (int)n);
 }
 
+// A cheaper exp(x) for x in [kExpFastMin, 0], for sums that only feed
+// bounds: 2^(x log2(e)) by v_exp_f32 on the rounded product (no reduction;
+// the product's rounding, up to 2^-18 in the exponent at |x| = 87, dominates
+// the error).  Its distance to exp_glibc(x) is at most kExpStatRel *
+// exp_glibc(x) over that range (checked on every fp32 input by the GPU test
+// of cgx_exp_stat_maxerr_dev, with a factor-2 margin).
+constexpr float kExpStatRel = 0x1p-16f;
+
+__device__ __forceinline__ float exp_stat(float x) {
+    return __builtin_amdgcn_exp2f(x * 0x1.715476p+0f);
+}
+
 // exp of x as cogito computes it (exp_glibc), or its certified approximation
 __device__ __forceinline__ float exp_cert(float x) {
     return (x >= kExpFastMin && x <= 0.0f) ? exp_fast(x) : exp_glibc(x);

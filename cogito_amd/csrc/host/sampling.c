@@ -139,6 +139,15 @@ int cgx_exp_fast_maxerr_dev(float lo, float hi, unsigned int* out_dev) {
     return cgk_exp_fast_maxerr(lo, hi, out_dev);
 }
 
+int cgx_exp_stat_maxerr_dev(float lo, float hi, unsigned int* out_dev) {
+    if (!out_dev) {
+        cgx_set_error("cgx_exp_stat_maxerr_dev: invalid argument");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    return cgk_exp_stat_maxerr(lo, hi, out_dev);
+}
+
 int cgx_sort_rows_dev(const uint32_t* keys, const uint32_t* payload, int rows, int n,
                       int descending, uint32_t* keys_out, uint32_t* payload_out) {
     if (!keys || !keys_out || rows <= 0 || n <= 0) {

@@ -546,7 +546,11 @@ __device__ __forceinline__ void guide_term(double G, double H, float ms, bool mi
         const double c = ok ? (double)exp_fast(-(float)D) : 0.0;
         *cg = c * G;
         const double cu = ok ? c * (1.0 + 0x1p-19 + 0x1p-23 * D) : 0x1p-125;
-        *eb = cu * (0x1p-22 * 1.01 * H + (0x1p-23 * 1.01 * D + 0x1p-18) * G) +
+        // G's terms within kExpStatRel (2^-16) of exp_glibc, their fp32
+        // per-thread sums within 2^-20, exp_glibc within 2^-24 of exp:
+        // 2^-15 of G covers them with room to spare
+        static_assert(kExpStatRel <= 0x1p-16f, "the bound below assumes exp_stat within 2^-16");
+        *eb = cu * (0x1p-22 * 1.01 * H + (0x1p-23 * 1.01 * D + 0x1p-15) * G) +
               (cu - c) * G + 0x1p-136;
     }
 }
@@ -719,9 +723,10 @@ __global__ __launch_bounds__(kT) void k_seg_stats(Rows rows, float T, Work w) {
     const float ms = block_max256(mx, s_f);
     float g = 0.0f, h = 0.0f;
     if (ms > -__builtin_inff()) {
-        // exp_cert without a branch per element: exp_fast on the clamped
-        // argument everywhere (arguments are <= 0), exp_glibc afterwards for
-        // the rare arguments below exp_fast's range
+        // exp_stat (within kExpStatRel of exp_glibc: these sums only feed
+        // the guide's bounds) on the clamped argument everywhere (arguments
+        // are <= 0), without a branch per element; exp_glibc afterwards for
+        // the rare arguments below its range
         float a[kC], e[kC];
         bool slow = false;
         if (T == 1.0f) {
@@ -734,7 +739,7 @@ __global__ __launch_bounds__(kT) void k_seg_stats(Rows rows, float T, Work w) {
 #pragma unroll
         for (int k = 0; k < kC; k++) {
             const bool live = x[k] > -__builtin_inff();
-            const float f = exp_fast(fmaxf(a[k], kExpFastMin));
+            const float f = exp_stat(fmaxf(a[k], kExpFastMin));
             e[k] = live ? f : 0.0f;
             a[k] = live ? a[k] : 0.0f;
             slow |= live && !(a[k] >= kExpFastMin && a[k] <= 0.0f);

@@ -202,6 +202,11 @@ int cgx_sort_rows_dev(const uint32_t* keys, const uint32_t* payload, int rows, i
  * an unsigned max into *out_dev as the float's bits (caller zeroes it).  The
  * certified sampler paths assume it stays within 2^-20 on [-87, 0]. */
 int cgx_exp_fast_maxerr_dev(float lo, float hi, unsigned int* out_dev);
+/* The same for the cheaper exponential of the acceptance pipeline's
+ * segment statistics, whose sums feed only bounds (kExpFastMin = -87 <= lo <
+ * hi <= 0); the bounds assume it stays within 2^-16 on [-87, 0].  No
+ * counterpart in the reference (a test of a certified bound). */
+int cgx_exp_stat_maxerr_dev(float lo, float hi, unsigned int* out_dev);
 
 /* ------------------------------------------------ INT4 tensors on disk */
 /* COG1 files (cg_serialization.h) holding INT4 tensors: each tensor is an

@@ -56,6 +56,17 @@ def test_exp_fast_within_certified_bound(gpu):
     assert worst < 2.0 ** -21
 
 
+def test_exp_stat_within_certified_bound(gpu):
+    # every fp32 in [-87, 0]: the acceptance pipeline's segment statistics
+    # sum this exponential, and the guide's error bound charges it 2^-16
+    # (with the other terms, 2^-15 of the rescaled sum); the measured worst
+    # case must leave a factor 2 to that
+    out = DeviceArray.from_numpy(gpu, np.zeros(1, np.uint32))
+    assert gpu.cgx_exp_stat_maxerr_dev(-87.0, 0.0, out.ptr) == 0, last_error(gpu)
+    worst = out.numpy(np.uint32, (1,)).view(np.float32)[0]
+    assert 0.0 < worst <= 2.0 ** -17, worst
+
+
 def _seq_sum(x: np.ndarray) -> np.float32:
     # left-to-right binary32 accumulation (np.add.accumulate is sequential)
     return np.add.accumulate(np.ascontiguousarray(x, np.float32), dtype=np.float32)[-1]
