@@ -116,6 +116,9 @@ __device__ __forceinline__ float exp_cert(float x) {
 constexpr float kExpErr = kExpFastRel * (1.0f + 0x1p-10f);
 constexpr float kProbRel = kExpFastRel * (1.0f + 0x1p-10f) + 0x1p-21f;
 constexpr float kResRel = kProbRel + 0x1p-21f;
+// the same with exp_stat in place of exp_cert (sums that feed only bounds)
+constexpr float kStatProbRel = kExpStatRel * (1.0f + 0x1p-10f) + 0x1p-21f;
+constexpr float kStatResRel = kStatProbRel + 0x1p-21f;
 
 // ------------------------------------------------------ element generators
 

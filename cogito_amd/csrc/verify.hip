@@ -240,6 +240,17 @@ struct Eval {
             return make_float2(fmaxf(0.0f, p - q), kResRel * (p + q) + abs_err + 0x1p-140f);
         }
     }
+    // a residual's approximation and bound from exp_stat (within kExpStatRel
+    // on [-87, 0]): for sums that feed only the guide's bounds
+    __device__ __forceinline__ float2 approx_stat(float A, float B) const {
+        static_assert(KIND == kKindRes, "residual rows only");
+        const bool oa = A >= kExpFastMin, ob = B >= kExpFastMin;
+        const float ea = oa ? exp_stat(A) : 0.0f;
+        const float eb = ob ? exp_stat(B) : 0.0f;
+        const float p = ea * ia, q = eb * ib;
+        const float abs_err = (oa ? 0.0f : 0x1p-124f * ia) + (ob ? 0.0f : 0x1p-124f * ib);
+        return make_float2(fmaxf(0.0f, p - q), kStatResRel * (p + q) + abs_err + 0x1p-140f);
+    }
     // exact value of element j, from memory
     __device__ __forceinline__ float at(int j) const {
         if (j < 0 || j >= V) return 0.0f;
@@ -1115,10 +1126,12 @@ __global__ __launch_bounds__(kT) void k_res_stats(Rows rows, const int* __restri
     const int base = seg * kSeg + threadIdx.x * kC;
     float A[kC], B[kC];
     ev.args(base, A, B);
+    // the task row's segment sums feed only the pass-2 guide and its bound,
+    // where the sequential sum's k 2^-24 dwarfs the exponential's error
     float gs = 0.0f, ge = 0.0f;
 #pragma unroll
     for (int k = 0; k < kC; k++) {
-        const float2 q = ev.approx(A[k], B[k]);
+        const float2 q = ev.approx_stat(A[k], B[k]);
         gs += q.x;
         ge += q.y;
     }
