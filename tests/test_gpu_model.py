@@ -176,24 +176,26 @@ def _forward_batch_case(gpu, oracle, rng, cfg, B, replace):
     gpu.cgx_model_free(m)
 
 
-def test_gemm_swiglu_in_kernel_matches_reduction(gpu, rng):
+@pytest.mark.parametrize("M", [2, 5, 8])
+def test_gemm_swiglu_in_kernel_matches_reduction(gpu, rng, M):
     # d_model 256 leaves every GEMM one K split: the gate|up product applies
     # SwiGLU in its own epilogue (default) or stores partial sums for the
-    # reduction pass (hook off); the logits of 8 sequences x 5 rows must be
-    # the same bits either way (the consumer's row factor depends only on
-    # the row maxima, which do not depend on the order of reduction)
+    # reduction pass (hook off); the logits of 8 sequences x M rows (16, 40
+    # and 64 rows: blocks of 16, 48 and 32 rows) must be the same bits either
+    # way (the consumer's row factor depends only on the row maxima, which do
+    # not depend on the order of reduction)
     from dataclasses import replace
     cfg = replace(TINY, max_batch=8)
-    toks = rng.integers(0, cfg.vocab, (8, 5)).astype(np.int32)
+    toks = rng.integers(0, cfg.vocab, (8, M)).astype(np.int32)
     outs = []
     old = gpu.cgx_gemm_swiglu_here(-1)
     try:
         for on in (1, 0):
             gpu.cgx_gemm_swiglu_here(on)
             m = new_model(gpu, cfg, 17)
-            assert gpu.cgx_model_forward_batch(m, toks.ctypes.data, 5, 5, None) == 0, \
+            assert gpu.cgx_model_forward_batch(m, toks.ctypes.data, M, M, None) == 0, \
                 last_error(gpu)
-            outs.append(logits_np(gpu, m, 40, cfg.vocab))
+            outs.append(logits_np(gpu, m, 8 * M, cfg.vocab))
             gpu.cgx_model_free(m)
     finally:
         gpu.cgx_gemm_swiglu_here(old)
