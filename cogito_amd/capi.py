@@ -266,6 +266,8 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_typ_log_dev": (I, [VP, VP, I]),
     "cgx_exp_fast_maxerr_dev": (I, [F, F, VP]),
     "cgx_exp_stat_maxerr_dev": (I, [F, F, VP]),
+    "cgx_sample_row_certified": (I, [I]),
+    "cgx_sample_row_fallbacks": (C.c_longlong, []),
     "cgx_save_quantized": (I, [C.c_char_p, C.POINTER(PQ), C.POINTER(C.c_char_p), I]),
     "cgx_load_quantized": (I, [C.c_char_p, C.POINTER(C.POINTER(PQ)),
                                C.POINTER(C.POINTER(C.c_char_p)), C.POINTER(I)]),

@@ -93,10 +93,228 @@ __global__ __launch_bounds__(kThreads) void k_ordered_sum(const float* x, int n,
     if (threadIdx.x == 0) out[0] = s;
 }
 
+// ------------------------------------------- certified single-row draw
+// cg_sample_temperature (speculative.c:54-75) returns the first k with
+// u < C_k, C_k the binary32 running sum of p_j = fl(e_j / S), e_j =
+// expf(a_j) and S the binary32 running sum of the e_j.  For a row held in
+// registers the draw is first decided from approximations with rigorous
+// bounds:
+//   e~_j  exp_fast(a_j), within 2^-20 of e_j on [kExpFastMin, 0]; 0 below,
+//         where e_j < 2^-125;
+//   sums  fp32 within a thread (32 terms: within 31 * 2^-24 of the real
+//         sum), fp64 across threads;
+//   S     within B_S = sum_j min(e_j, h_S) of the real sum: a rounding to
+//         nearest moves a sum by at most half an ulp of its result (h_S:
+//         half an ulp of S's largest possible binade) and by at most the
+//         term added;
+//   C_k   within R_k = sum_{j<=k} min(p_j, h_C) of sum_{j<=k} p_j, each p_j
+//         within 2^-24 p_j + 2^-150 of e_j / S.
+// That gives an interval for every C_k.  With k the first index whose
+// estimate exceeds u, the token is k once the interval of C_{k-1} lies at or
+// below u and that of C_k above it (u at or above every estimate: V-1, once
+// C_{V-2} is certainly <= u).  Anything else -- u within the bounds of a
+// step, a non-finite row, an argument above 0 or NaN (T outside (0, inf]) --
+// is decided by the exact sums.
+//
+// The bounds are worst cases of the running sums' roundings (up to about
+// V 2^-24 of a sum on a diffuse row), so they settle u only where its CDF
+// step is wider than that.  A gate sends rows whose expected step (sum of
+// p^2, estimated from a quarter of the row) is below 8 V 2^-24 to the exact
+// sums at once, from a cheap exponential (2^(d log2(e) / T), v_exp_f32) and
+// one reduction: on diffuse rows (p ~ 1 / V) the bounds would settle only a
+// few draws in a hundred.
+struct CertShared {
+    double ew[kWaves], mw[kWaves], bw[kWaves];
+    float g1[kWaves], g2[kWaves];
+    int cand;
+    int tok;
+};
+
+// draws of k_sample_temperature the exact sums decided (test statistics)
+__device__ unsigned long long g_row_fallbacks;
+
+__device__ __forceinline__ float wave_incl_sum_f(float x) {
+    float o;
+#define CGX_STEP(CTRL, RMASK, S)                                                     \
+    o = __int_as_float(dpp_i<CTRL, RMASK>(__float_as_int(x)));                      \
+    if (dpp_step_valid(S)) x += o;
+    CGX_STEP(0x111, 0xF, 0)
+    CGX_STEP(0x112, 0xF, 1)
+    CGX_STEP(0x114, 0xF, 2)
+    CGX_STEP(0x118, 0xF, 3)
+    CGX_STEP(0x142, 0xA, 4)
+    CGX_STEP(0x143, 0xC, 5)
+#undef CGX_STEP
+    return x;
+}
+
+// The token from the row's register values x (element t*kCh + k) and their
+// maximum m; where the exact sums decide, -1 (the gate: x still holds the
+// row) or -2 (after the certified pass, which no longer keeps x) --
+// block-uniform.
+__device__ __forceinline__ int sample_temperature_cert(const float (&x)[kCh], float m, int V,
+                                                       float T, float u, CertShared& cs) {
+    const int t = threadIdx.x, l = lane_id(), w = wave_id(), base = t * kCh;
+    // gate, on every 4th element scaled by 4 plus the maximum's own term 1
+    // (on the rows worth certifying a few top terms dominate the sum of
+    // squares); padding: 2^-inf = 0; a non-finite m or T makes the sums NaN
+    // or the arguments positive, which the certified pass rejects
+    const float sc = 0x1.715476p+0f / T;
+    float g1 = 0.0f, g2 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kCh; k += 4) {
+        const float g = __builtin_amdgcn_exp2f(__fsub_rn(x[k], m) * sc);
+        g1 += g;
+        g2 = fmaf(g, g, g2);
+    }
+    g1 = wave_incl_sum_f(g1);
+    g2 = wave_incl_sum_f(g2);
+    if (l == 63) {
+        cs.g1[w] = g1;
+        cs.g2[w] = g2;
+    }
+    if (t == 0) cs.cand = 0x7fffffff;
+    __syncthreads();
+    float G1 = 0.0f, G2 = 0.0f;
+    for (int i = 0; i < kWaves; i++) {
+        G1 += cs.g1[i];
+        G2 += cs.g2[i];
+    }
+    G1 = fmaf(4.0f, G1, 1.0f);
+    G2 = fmaf(4.0f, G2, 1.0f);
+    if (!(G2 * 0x1p24f >= 8.0f * (float)V * G1 * G1)) return -1;
+
+    // the reference's arguments (x / 1 == x), their certified exponentials
+    // and the thread's fp32 sum; an argument that is NaN or above 0 (a
+    // non-finite row or T outside (0, inf]) sends the row to the exact path
+    float e[kCh];
+    float es = 0.0f;
+    int bad = 0;
+#pragma unroll
+    for (int k = 0; k < kCh; k++) {
+        const float d = __fsub_rn(x[k], m);
+        const float a = T == 1.0f ? d : __fdiv_rn(d, T);
+        const bool in = base + k < V;
+        bad |= in && !(a <= 0.0f);
+        e[k] = in && a >= kExpFastMin ? exp_fast(a) : 0.0f;
+        es += e[k];
+    }
+    const double ein = wave_incl_sum_d((double)es);
+    if (l == 63) cs.ew[w] = ein;
+    if (__syncthreads_or(bad)) return -2;
+    double eoff = 0.0, E = 0.0;
+    for (int i = 0; i < kWaves; i++) {
+        const double v = cs.ew[i];
+        if (i < w) eoff += v;
+        E += v;
+    }
+    const double ex0 = eoff + (ein - (double)es);   // sum of the e~ before this thread
+
+    // Bounds that need only E (>= 1: the row maximum's term is exactly 1).
+    // dl covers exp_fast (2^-20) and the fp32 sums (31 * 2^-24) with room for
+    // the fp64 roundings; S and every C_k stay within a factor (1 +- V 2^-23)
+    // of their real sums (V <= 2^15).
+    const double Vd = (double)V, dl = 0x1p-18, abs_e = Vd * 0x1p-125;
+    const double S_hi0 = (E * (1.0 + dl) + abs_e) * (1.0 + Vd * 0x1p-23);
+    const double S_lo0 = E * (1.0 - dl) * (1.0 - Vd * 0x1p-23);
+    const float hS = ldexpf(1.0f, binade_of(S_hi0) - 24);
+    // p_j <= kap e~_j + 2^-124, so min(p_j, h_C) <= kap min(e~_j, tau) + 2^-124
+    const double kap = (1.0 + dl) / S_lo0;
+    const double C_hi0 = (kap * E * (1.0 + dl) + Vd * 0x1p-124) * (1.0 + Vd * 0x1p-23);
+    const double hC = ldexp(1.0, binade_of(C_hi0) - 24);
+    const float tau = (float)(hC / kap * (1.0 + 0x1p-22));   // >= hC / kap after rounding
+    float ms = 0.0f, bs = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kCh; k++) {
+        ms += fminf(e[k], tau);
+        bs += fminf(e[k], hS);
+    }
+    const double min_ = wave_incl_sum_d((double)ms);
+    const double bin = wave_incl_sum_d((double)bs);
+    // candidate: the first index whose estimate (prefix / E) exceeds u
+    const double r = (double)u * E;
+    if (base < V && ex0 + (double)es > r && (ex0 <= r || t == 0)) {
+        float p = 0.0f;
+        int kk = -1;
+#pragma unroll
+        for (int k = 0; k < kCh; k++) {
+            p += e[k];
+            if (kk < 0 && base + k < V && ex0 + (double)p > r) kk = k;
+        }
+        if (kk >= 0) atomicMin(&cs.cand, base + kk);
+    }
+    if (l == 63) {
+        cs.mw[w] = min_;
+        cs.bw[w] = bin;
+    }
+    __syncthreads();
+    double moff = 0.0, B = 0.0;
+    for (int i = 0; i < kWaves; i++) {
+        if (i < w) moff += cs.mw[i];
+        B += cs.bw[i];
+    }
+    const double mx0 = moff + (min_ - (double)ms);
+    const int cand = cs.cand;
+    const bool none = cand == 0x7fffffff;
+    const int kc = none ? V - 1 : cand;
+    if (t == kc / kCh) {
+        const double BS = B * (1.0 + 0x1p-17) + abs_e;
+        const double S_lo = E * (1.0 - dl) - BS, S_hi = E * (1.0 + dl) + abs_e + BS;
+        // this thread's prefixes through kc - 1 and through kc (the same fp32
+        // additions as above)
+        const int kl = kc - base;
+        float pe = 0.0f, pm = 0.0f, pe0 = 0.0f, pm0 = 0.0f, pe1 = 0.0f, pm1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kCh; k++) {
+            pe += e[k];
+            pm += fminf(e[k], tau);
+            if (k == kl - 1) {
+                pe0 = pe;
+                pm0 = pm;
+            }
+            if (k == kl) {
+                pe1 = pe;
+                pm1 = pm;
+            }
+        }
+        const double Pe0 = ex0 + (double)pe0, Pm0 = mx0 + (double)pm0;
+        const double Pe1 = ex0 + (double)pe1, Pm1 = mx0 + (double)pm1;
+        const double n0 = (double)kc, n1 = n0 + 1.0;     // terms through kc - 1, kc
+        const double kAbs = 0x1p-45;                     // the fp64 sums' absolute error
+        const double R0 = kap * Pm0 * (1.0 + dl) + n0 * 0x1p-124;
+        const double R1 = kap * Pm1 * (1.0 + dl) + n1 * 0x1p-124;
+        const double up0 = (Pe0 * (1.0 + dl) + abs_e) * (1.0 + 0x1p-24) / S_lo * (1.0 + 0x1p-40) +
+                           n0 * 0x1p-150 + R0 + kAbs;
+        const double lo1 = Pe1 * (1.0 - dl) * (1.0 - 0x1p-24) / S_hi * (1.0 - 0x1p-40) -
+                           n1 * 0x1p-150 - R1 - kAbs;
+        const double ud = (double)u;
+        const bool ok = (kc == 0 || up0 <= ud) && (none || lo1 > ud);
+        cs.tok = ok ? kc : -2;
+    }
+    __syncthreads();
+    return cs.tok;
+}
+
 __global__ __launch_bounds__(kThreads) void k_sample_temperature(const float* logits, int V,
-                                                                 float T, float u, int* out) {
+                                                                 float T, float u, int cert,
+                                                                 int* out) {
     __shared__ EosShared sh;
-    int tok = sample_temperature_gen(RowSrc{logits}, V, T, u, sh);
+    __shared__ CertShared cs;
+    int tok;
+    if (V <= kRound) {
+        float x[kCh];
+        load_vals(RowSrc{logits}, V, -__builtin_inff(), x);
+        const float m = vals_max(x, sh);
+        tok = cert ? sample_temperature_cert(x, m, V, T, u, cs) : -1;
+        if (tok < 0) {
+            if (cert && threadIdx.x == 0) atomicAdd(&g_row_fallbacks, 1ull);
+            // the row again (L2-resident) where the certified pass let it go
+            if (tok == -2) load_vals(RowSrc{logits}, V, -__builtin_inff(), x);
+            tok = sample_temperature_vals_m(x, m, RowSrc{logits}, V, T, u, sh);
+        }
+    } else {
+        tok = sample_temperature_gen(RowSrc{logits}, V, T, u, sh);
+    }
     if (threadIdx.x == 0) out[0] = tok;
 }
 
@@ -281,11 +499,37 @@ extern "C" int cgk_ordered_sum(const float* x, int n, float* out) {
     return launch_check("k_ordered_sum");
 }
 
+static int g_row_cert = 1;
+
+// Certified decision of the single-row draws on (default) or off; returns the
+// previous setting (-1 only reads it).
+extern "C" int cgx_sample_row_certified(int on) {
+    const int prev = g_row_cert;
+    if (on >= 0) g_row_cert = on != 0;
+    return prev;
+}
+
+// Single-row draws since the library loaded whose certified decision left
+// the token to the exact sums (synchronises the library's stream).
+extern "C" long long cgx_sample_row_fallbacks(void) {
+    if (cgx_ensure_init()) return -1;
+    unsigned long long v = 0;
+    hipError_t e = hipStreamSynchronize(stream());
+    if (e == hipSuccess)
+        e = hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_row_fallbacks), sizeof v, 0,
+                                hipMemcpyDeviceToHost);
+    if (e != hipSuccess) {
+        cgx_set_error("cgx_sample_row_fallbacks: %s", hipGetErrorString(e));
+        return -1;
+    }
+    return (long long)v;
+}
+
 extern "C" int cgk_sample_temperature(const float* logits, int V, float T, float u,
                                       int* out) {
     if (check_v(V)) return -1;
     hipLaunchKernelGGL(k_sample_temperature, dim3(1), dim3(kThreads), 0, stream(), logits,
-                       V, T, u, out);
+                       V, T, u, g_row_cert, out);
     return launch_check("k_sample_temperature");
 }
 

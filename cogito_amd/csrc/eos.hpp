@@ -902,9 +902,9 @@ __device__ __forceinline__ float vals_at(const float (&x)[kCh], int j, EosShared
 // cg_sample_temperature on register values of a row (n <= kRound), `src`
 // regenerating elements for replays.
 template <class S>
-__device__ __forceinline__ int sample_temperature_vals(const float (&x)[kCh], const S& src, int V,
-                                                       float T, float u, EosShared& sh) {
-    const float m = vals_max(x, sh);
+__device__ __forceinline__ int sample_temperature_vals_m(const float (&x)[kCh], float m,
+                                                         const S& src, int V, float T, float u,
+                                                         EosShared& sh) {
     float e[kCh];
     vals_exp(x, m, T, V, e);
     ExpGen<S> eg{src, m, T};
@@ -914,6 +914,13 @@ __device__ __forceinline__ int sample_temperature_vals(const float (&x)[kCh], co
     for (int k = 0; k < kCh; k++) e[k] = __fdiv_rn(e[k], S_);   // (0 / S = 0 past V)
     eos_sum_vals(e, pg, V, sh);
     return gen_find(pg, V, u, V - 1, sh);
+}
+
+// the same with the row maximum computed here
+template <class S>
+__device__ __forceinline__ int sample_temperature_vals(const float (&x)[kCh], const S& src, int V,
+                                                       float T, float u, EosShared& sh) {
+    return sample_temperature_vals_m(x, vals_max(x, sh), src, V, T, u, sh);
 }
 
 // cg_sample_temperature on the values of `src` (speculative.c:54-75).

@@ -64,15 +64,12 @@ int cgx_sample_temperature_u(const float* logits, int V, float T, float u) {
     const float* d = (const float*)cgx_dev_in(logits, (size_t)V * 4, CGX_SLOT_IN0);
     int* out = (int*)cgx_scratch(CGX_SLOT_OUT1, 2 * sizeof(int));
     if (!d || !out) return -1;
-    if (cgk_verify_pipe_supported(1, 0, V, T)) {
-        /* the draw goes to the device next to the token */
-        float* du = (float*)(out + 1);
-        if (cgx_memcpy_h2d(du, &u, sizeof(float)) ||
-            cgk_sample_temperature_pipe(d, 1, V, T, du, out, (size_t)V))
-            return -1;
-    } else if (cgk_sample_temperature(d, V, T, u, out)) {
+    /* the loops' dispatch (cgx_sample_row_dev); the draw goes to the device
+     * next to the token */
+    float* du = (float*)(out + 1);
+    if (cgx_memcpy_h2d(du, &u, sizeof(float)) ||
+        cgx_sample_row_dev(d, V, T, 0, 1.0f, du, u, NULL, out, NULL))
         return -1;
-    }
     return read_token(out);
 }
 

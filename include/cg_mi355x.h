@@ -207,6 +207,16 @@ int cgx_exp_fast_maxerr_dev(float lo, float hi, unsigned int* out_dev);
  * hi <= 0); the bounds assume it stays within 2^-16 on [-87, 0].  No
  * counterpart in the reference (a test of a certified bound). */
 int cgx_exp_stat_maxerr_dev(float lo, float hi, unsigned int* out_dev);
+/* The single-row draws (cgx_sample_temperature_u and the loops' draft draws
+ * on rows of up to 32768 values) first decide the token from certified
+ * approximations and run the exact sums only where u lies within the bounds
+ * of a CDF step (the same token either way).  cgx_sample_row_certified turns
+ * that decision off (0) or on (1, the default) and returns the previous
+ * setting (-1 only reads it); cgx_sample_row_fallbacks counts the draws since
+ * the library loaded that the exact sums decided (synchronises).  No
+ * counterpart in the reference (test hooks of a certified decision). */
+int cgx_sample_row_certified(int on);
+long long cgx_sample_row_fallbacks(void);
 
 /* ------------------------------------------------ INT4 tensors on disk */
 /* COG1 files (cg_serialization.h) holding INT4 tensors: each tensor is an

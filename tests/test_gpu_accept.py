@@ -143,6 +143,55 @@ def test_sample_temperature_bitexact(gpu, oracle, rng, V):
             assert got == exp, (V, T, float(u), got, exp, last_error(gpu))
 
 
+@pytest.mark.parametrize("V", [3, 1000, 32000, 32768])
+def test_certified_row_draw_matches_exact(gpu, oracle, rng, V):
+    """The single-row draw decides from certified approximations first and
+    runs the exact sums only where u lies within the bounds of a CDF step:
+    the token equals the exact path's and the oracle's on diffuse rows, on
+    peaked rows (which the approximations settle) and for uniforms on and
+    next to the CDF steps (which they must leave to the exact sums)."""
+    assert gpu.cgx_sample_row_certified(-1) == 1
+    peaked_draws = peaked_fb = step_draws = step_fb = 0
+    try:
+        for trial, scale in enumerate([2.0, 20.0, 6.0, 40.0]):
+            T = [1.0, 0.8, 1.3, 1.0][trial]
+            x = rng.normal(0, scale, V).astype(np.float32)
+            p = _oracle_probs(oracle, x, T)
+            cdf = np.add.accumulate(p, dtype=np.float32)
+            us = list(rng.uniform(0, 1, 12).astype(np.float32)) + [np.float32(0.0)]
+            steps = []
+            for i in rng.integers(0, V, 4):
+                c = cdf[i]
+                steps += [c, np.nextafter(c, np.float32(0)), np.nextafter(c, np.float32(2))]
+            for j, u in enumerate(us + steps):
+                exp = oracle.orc_sample_temperature(ptr(x), V, T, float(u))
+                f0 = gpu.cgx_sample_row_fallbacks()
+                got = gpu.cgx_sample_temperature_u(x.ctypes.data, V, T, float(u))
+                fb = gpu.cgx_sample_row_fallbacks() - f0
+                assert f0 >= 0 and fb in (0, 1), (f0, fb, last_error(gpu))
+                assert got == exp, (V, T, scale, float(u), got, exp, last_error(gpu))
+                gpu.cgx_sample_row_certified(0)
+                try:
+                    assert gpu.cgx_sample_temperature_u(x.ctypes.data, V, T, float(u)) == exp
+                    assert gpu.cgx_sample_row_fallbacks() - f0 == fb   # off: not counted
+                finally:
+                    gpu.cgx_sample_row_certified(1)
+                if scale >= 20.0 and j < len(us):
+                    peaked_draws += 1
+                    peaked_fb += fb
+                if j >= len(us):
+                    step_draws += 1
+                    step_fb += fb
+    finally:
+        gpu.cgx_sample_row_certified(1)
+    # a peaked row's steps are wide: most random uniforms are settled by the
+    # bounds; a uniform within an ulp of a step cannot be (except at the last
+    # steps, where V-1 is the token on both sides)
+    if V > 3:
+        assert peaked_fb < peaked_draws // 2, (peaked_fb, peaked_draws)
+    assert step_fb > 0, (step_fb, step_draws)
+
+
 @pytest.mark.parametrize("V", [64, 1000, 32000])
 def test_sample_corrected_bitexact(gpu, oracle, rng, V):
     for trial in range(8):
