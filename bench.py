@@ -310,6 +310,48 @@ def bench_accept(lib, V, B, gamma, T, steps, warmup, sets=1, seed=5, top_k=0, to
             "rotating_sets": sets, "mean_accepted_last_call": float(nacc.mean())}
 
 
+def bench_draws(lib, V, draws, warmup, seed=41):
+    """The single-row draft draw (cgx_sample_temperature_dev: the
+    single-workgroup sampler the loops use for rows of up to 32768 values) on
+    device rows of three shapes, with the certified decision on and off: us
+    per draw from events around `draws` queued draws, and how many of them
+    the exact sums decided.  The same tokens either way."""
+    from cogito_amd.capi import DeviceArray, last_error
+
+    rng = np.random.default_rng(seed)
+    out = DeviceArray(lib, 4)
+    res = {}
+    for name, scale in (("diffuse_N0_2", 2.0), ("N0_6", 6.0), ("peaked_N0_20", 20.0)):
+        x = DeviceArray.from_numpy(lib, rng.normal(0, scale, V).astype(np.float32))
+        us = rng.random(draws + warmup, dtype=np.float32)
+        r = {}
+        for cert in (0, 1):
+            lib.cgx_sample_row_certified(cert)
+            for u in us[:warmup]:
+                lib.cgx_sample_temperature_dev(x.ptr, V, 1.0, float(u), out.ptr)
+            f0 = lib.cgx_sample_row_fallbacks()
+            lib.cgx_event_record(0)
+            for u in us[warmup:]:
+                if lib.cgx_sample_temperature_dev(x.ptr, V, 1.0, float(u), out.ptr):
+                    raise RuntimeError(last_error(lib))
+            lib.cgx_event_record(1)
+            lib.cgx_synchronize()
+            per = lib.cgx_event_elapsed_ms(0, 1) / draws * 1e3
+            fb = lib.cgx_sample_row_fallbacks() - f0
+            r["certified" if cert else "exact"] = {"us_per_draw": round(per, 2),
+                                                   "exact_fallbacks": fb if cert else draws}
+        lib.cgx_sample_row_certified(1)
+        x.free()
+        res[name] = r
+        log(f"[bench] row draw V={V} {name}: exact {r['exact']['us_per_draw']} us, certified "
+            f"{r['certified']['us_per_draw']} us ({r['certified']['exact_fallbacks']} of "
+            f"{draws} left to the exact sums)")
+    out.free()
+    res["V"] = V
+    res["draws"] = draws
+    return res
+
+
 def bench_accept_graph(lib, V, B, gamma, T, steps, warmup, seed=5):
     """The same verify as bench_accept (tokens only), through the
     allocation-free entry point captured once into a HIP graph and replayed:
@@ -936,12 +978,13 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=5,
                     help="activation rows M of the headline line (gamma+1 = 5)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--legs", default="floor,valu,shapes,accept,attn,e2e,tree",
+    ap.add_argument("--legs", default="floor,valu,shapes,accept,draws,attn,e2e,tree",
                     help="comma list of legs beside the headline GEMV: floor (a plain read "
                          "of the headline's bytes, rotated the same way), valu (the VALU "
                          "GEMV on the headline workload), shapes (7B-stack "
                          "GEMV shapes), accept (acceptance sampling C1 + V=128256 x 64 "
-                         "chains), attn (INT4-KV verify attention, 7B shape), e2e "
+                         "chains), draws (the single-row draft draw, V=32000, certified "
+                         "decision on and off), attn (INT4-KV verify attention, 7B shape), e2e "
                          "(verified tok/s, tiny and 7B-shape stacks), c3 (C3 alone; part of e2e), "
                          "c4 (C4 at batch 1 alone; "
                          "part of e2e), batch (C4 at batch 8 alone; part of e2e), tree (C5: the "
@@ -1009,6 +1052,8 @@ def main() -> int:
             extra["accept_c1"]["cpu_baseline"] = cpu_baseline_accept()
             log(f"[bench] CPU C1 verify: {extra['accept_c1']['cpu_baseline']['us_per_call']} "
                 f"us/call")
+    if "draws" in legs:
+        extra["row_draws"] = bench_draws(lib, 32000, 200, 20)
     if "attn" in legs:
         extra["attention_7b"] = bench_attention(lib, 4096, 5, 32, 8, 128, 128, args.steps,
                                                 args.warmup)

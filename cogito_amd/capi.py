@@ -252,6 +252,7 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_graph_launch": (I, [VP]),
     "cgx_graph_free": (I, [VP]),
     "cgx_sample_temperature_u": (I, [VP, I, F, F]),
+    "cgx_sample_temperature_dev": (I, [VP, I, F, F, VP]),
     "cgx_sample_top_k_u": (I, [VP, I, I, F]),
     "cgx_sample_top_p_u": (I, [VP, I, F, F]),
     "cgx_sample_corrected_u": (I, [VP, VP, I, F]),

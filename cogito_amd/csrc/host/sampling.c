@@ -42,10 +42,11 @@ static int read_token(const int* dev) {
 int cgx_sample_row_dev(const float* row, int V, float T, int top_k, float top_p,
                        const float* du, float uh, float* z, int* out, float* dist) {
     if (!uses_filters(V, top_k, top_p)) {
-        /* one row of up to 32768 values: the single-workgroup exact sampler
-         * (one launch, the row in registers) beats the chunk-parallel
-         * pipeline's nine launches (C4's draft draws: 3.07 -> 2.93 ms a
-         * step); longer rows take the pipeline */
+        /* one row of up to 32768 values: the single-workgroup sampler (one
+         * launch, the row in registers; a certified decision first on rows
+         * peaked enough for it, the exact sums otherwise) beats the
+         * chunk-parallel pipeline's nine launches (C4's draft draws: 3.07 ->
+         * 2.93 ms a step); longer rows take the pipeline */
         if (V > 32768 && cgk_verify_pipe_supported(1, 0, V, T))
             return cgk_sample_temperature_pipe(row, 1, V, T, du, out, (size_t)V);
         return cgk_sample_temperature(row, V, T, uh, out);
@@ -71,6 +72,20 @@ int cgx_sample_temperature_u(const float* logits, int V, float T, float u) {
         cgx_sample_row_dev(d, V, T, 0, 1.0f, du, u, NULL, out, NULL))
         return -1;
     return read_token(out);
+}
+
+int cgx_sample_temperature_dev(const float* logits, int V, float T, float u, int* out_dev) {
+    if (!logits || !out_dev || V <= 0) {
+        cgx_set_error("cgx_sample_temperature_dev: invalid argument");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    if (V > 32768 && cgk_verify_pipe_supported(1, 0, V, T)) {
+        float* du = (float*)cgx_scratch(CGX_SLOT_OUT1, sizeof(float));
+        if (!du || cgx_memcpy_h2d(du, &u, sizeof(float))) return -1;
+        return cgx_sample_row_dev(logits, V, T, 0, 1.0f, du, u, NULL, out_dev, NULL);
+    }
+    return cgx_sample_row_dev(logits, V, T, 0, 1.0f, NULL, u, NULL, out_dev, NULL);
 }
 
 int cgx_sample_corrected_u(const float* draft_probs, const float* target_probs,

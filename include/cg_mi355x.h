@@ -159,6 +159,11 @@ int cgx_verify_chain_batch_dev_noalloc(const float* target_logits,
 /* Single samplers with an explicit uniform (same arithmetic as the
  * reference samplers; logits host or device). */
 int cgx_sample_temperature_u(const float* logits, int V, float T, float u);
+/* The same draw from a device logits row into *out_dev (device int), queued
+ * on the library's stream without synchronising: the loops' draft draw
+ * (rows of up to 32768 values on one workgroup, longer rows through the
+ * chunk-parallel pipeline). */
+int cgx_sample_temperature_dev(const float* logits, int V, float T, float u, int* out_dev);
 int cgx_sample_top_k_u(const float* logits, int V, int k, float u);
 int cgx_sample_top_p_u(const float* logits, int V, float top_p, float u);
 int cgx_sample_corrected_u(const float* draft_probs, const float* target_probs,

@@ -192,6 +192,25 @@ def test_certified_row_draw_matches_exact(gpu, oracle, rng, V):
     assert step_fb > 0, (step_fb, step_draws)
 
 
+@pytest.mark.parametrize("V", [1000, 32000, 50257])
+def test_sample_temperature_dev_matches_oracle(gpu, oracle, rng, V):
+    """The device-row draw (queued, no synchronisation) returns the oracle's
+    token on a diffuse and a peaked row (rows above 32768 values: the
+    pipeline)."""
+    out = DeviceArray(gpu, 4)
+    for scale in (2.0, 20.0):
+        x = rng.normal(0, scale, V).astype(np.float32)
+        dx = DeviceArray.from_numpy(gpu, x)
+        for u in rng.uniform(0, 1, 6).astype(np.float32):
+            assert gpu.cgx_sample_temperature_dev(dx.ptr, V, 1.0, float(u), out.ptr) == 0, \
+                last_error(gpu)
+            got = out.numpy(np.int32, (1,))[0]
+            exp = oracle.orc_sample_temperature(ptr(x), V, 1.0, float(u))
+            assert got == exp, (V, scale, float(u), got, exp)
+        dx.free()
+    out.free()
+
+
 @pytest.mark.parametrize("V", [64, 1000, 32000])
 def test_sample_corrected_bitexact(gpu, oracle, rng, V):
     for trial in range(8):
