@@ -253,6 +253,7 @@ SIGNATURES: dict[str, tuple] = {
     "cgx_graph_free": (I, [VP]),
     "cgx_sample_temperature_u": (I, [VP, I, F, F]),
     "cgx_sample_temperature_dev": (I, [VP, I, F, F, VP]),
+    "cgx_sample_temperature_rows_dev": (I, [VP, I, I, F, VP, VP, C.c_size_t]),
     "cgx_sample_top_k_u": (I, [VP, I, I, F]),
     "cgx_sample_top_p_u": (I, [VP, I, F, F]),
     "cgx_sample_corrected_u": (I, [VP, VP, I, F]),

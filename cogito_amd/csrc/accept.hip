@@ -130,7 +130,7 @@ struct CertShared {
     int tok;
 };
 
-// draws of k_sample_temperature the exact sums decided (test statistics)
+// draws of k_sample_temperature(_rows) the exact sums decided (test statistics)
 __device__ unsigned long long g_row_fallbacks;
 
 __device__ __forceinline__ float wave_incl_sum_f(float x) {
@@ -295,11 +295,10 @@ __device__ __forceinline__ int sample_temperature_cert(const float (&x)[kCh], fl
     return cs.tok;
 }
 
-__global__ __launch_bounds__(kThreads) void k_sample_temperature(const float* logits, int V,
-                                                                 float T, float u, int cert,
-                                                                 int* out) {
-    __shared__ EosShared sh;
-    __shared__ CertShared cs;
+// cg_sample_temperature on one row: certified decision first (cert) on rows
+// held in registers, the exact sums where it does not settle the draw
+__device__ __forceinline__ int sample_row(const float* logits, int V, float T, float u,
+                                          int cert, EosShared& sh, CertShared& cs) {
     int tok;
     if (V <= kRound) {
         float x[kCh];
@@ -315,7 +314,28 @@ __global__ __launch_bounds__(kThreads) void k_sample_temperature(const float* lo
     } else {
         tok = sample_temperature_gen(RowSrc{logits}, V, T, u, sh);
     }
+    return tok;
+}
+
+__global__ __launch_bounds__(kThreads) void k_sample_temperature(const float* logits, int V,
+                                                                 float T, float u, int cert,
+                                                                 int* out) {
+    __shared__ EosShared sh;
+    __shared__ CertShared cs;
+    const int tok = sample_row(logits, V, T, u, cert, sh, cs);
     if (threadIdx.x == 0) out[0] = tok;
+}
+
+// One block per row: row r at logits + r * ld, its draw u[r] (device)
+__global__ __launch_bounds__(kThreads) void k_sample_temperature_rows(const float* logits,
+                                                                      size_t ld, int V,
+                                                                      float T, const float* u,
+                                                                      int cert, int* out) {
+    __shared__ EosShared sh;
+    __shared__ CertShared cs;
+    const int r = blockIdx.x;
+    const int tok = sample_row(logits + (size_t)r * ld, V, T, u[r], cert, sh, cs);
+    if (threadIdx.x == 0) out[r] = tok;
 }
 
 __global__ __launch_bounds__(kThreads) void k_sample_corrected(const float* q, const float* p,
@@ -531,6 +551,18 @@ extern "C" int cgk_sample_temperature(const float* logits, int V, float T, float
     hipLaunchKernelGGL(k_sample_temperature, dim3(1), dim3(kThreads), 0, stream(), logits,
                        V, T, u, g_row_cert, out);
     return launch_check("k_sample_temperature");
+}
+
+extern "C" int cgk_sample_temperature_rows(const float* logits, int rows, int V, float T,
+                                           const float* u, int* out, size_t ld) {
+    if (check_v(V)) return -1;
+    if (rows < 1 || (rows > 1 && ld < (size_t)V)) {
+        cgx_set_error("sample rows: %d rows of %d values at stride %zu", rows, V, ld);
+        return -1;
+    }
+    hipLaunchKernelGGL(k_sample_temperature_rows, dim3(rows), dim3(kThreads), 0, stream(),
+                       logits, ld, V, T, u, g_row_cert, out);
+    return launch_check("k_sample_temperature_rows");
 }
 
 extern "C" int cgk_sample_corrected(const float* q, const float* p, int V, float u,

@@ -121,6 +121,10 @@ int cgk_exp_fast_maxerr(float lo, float hi, unsigned int* out_dev);
 int cgk_exp_stat_maxerr(float lo, float hi, unsigned int* out_dev);
 int cgk_ordered_sum(const float* x, int n, float* out);
 int cgk_sample_temperature(const float* logits, int V, float T, float u, int* out);
+/* the same on `rows` rows (row r at logits + r * ld, draw u[r] on the
+ * device, token to out[r]), one workgroup per row */
+int cgk_sample_temperature_rows(const float* logits, int rows, int V, float T, const float* u,
+                                int* out, size_t ld);
 int cgk_sample_corrected(const float* q, const float* p, int V, float u, int* out);
 int cgk_temperature_probs(const float* logits, int V, float T, float* probs);
 int cgk_verify_chain(const float* target, const float* draft, const int* tokens,

@@ -88,6 +88,21 @@ int cgx_sample_temperature_dev(const float* logits, int V, float T, float u, int
     return cgx_sample_row_dev(logits, V, T, 0, 1.0f, NULL, u, NULL, out_dev, NULL);
 }
 
+int cgx_sample_temperature_rows_dev(const float* logits, int rows, int V, float T,
+                                    const float* u_dev, int* out_dev, size_t ld) {
+    if (!logits || !u_dev || !out_dev || rows < 1 || V <= 0) {
+        cgx_set_error("cgx_sample_temperature_rows_dev: invalid argument");
+        return -1;
+    }
+    if (cgx_ensure_init()) return -1;
+    /* rows of up to 32768 values: one workgroup per row, all in one launch
+     * (the rows in registers, the certified decision first); longer rows:
+     * the chunk-parallel pipeline over all of them */
+    if (V > 32768 && cgk_verify_pipe_supported(rows, 0, V, T))
+        return cgk_sample_temperature_pipe(logits, rows, V, T, u_dev, out_dev, ld);
+    return cgk_sample_temperature_rows(logits, rows, V, T, u_dev, out_dev, ld);
+}
+
 int cgx_sample_corrected_u(const float* draft_probs, const float* target_probs,
                            int V, float u) {
     if (!draft_probs || !target_probs || V <= 0) {

@@ -383,13 +383,13 @@ int cgx_spec_batch_step(cgx_spec_batch* s, const float* u_draft, const float* u_
     const float* uv = s->d_u + (size_t)g * B;
     /* draft: d_1 from (prev, last), then d_2 .. d_gamma */
     if (cgx_model_forward_batch_ld(s->draft, s->d_feed, 2, 1, s->d_draft_logits, ldd) ||
-        cgk_sample_temperature_pipe(s->d_draft_logits, B, s->V, s->T, ud, s->d_dtok, ldd))
+        cgx_sample_temperature_rows_dev(s->d_draft_logits, B, s->V, s->T, ud, s->d_dtok, ldd))
         return -1;
     for (int i = 1; i < g; i++) {
         if (cgx_model_forward_batch_ld(s->draft, s->d_dtok + (size_t)(i - 1) * B, 1, 1,
                                        s->d_draft_logits + (size_t)i * V, ldd) ||
-            cgk_sample_temperature_pipe(s->d_draft_logits + (size_t)i * V, B, s->V, s->T,
-                                        ud + (size_t)i * B, s->d_dtok + (size_t)i * B, ldd))
+            cgx_sample_temperature_rows_dev(s->d_draft_logits + (size_t)i * V, B, s->V, s->T,
+                                            ud + (size_t)i * B, s->d_dtok + (size_t)i * B, ldd))
             return -1;
     }
     /* target over last, d_1 .. d_gamma of every sequence, then the verify */

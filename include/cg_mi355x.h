@@ -164,6 +164,12 @@ int cgx_sample_temperature_u(const float* logits, int V, float T, float u);
  * (rows of up to 32768 values on one workgroup, longer rows through the
  * chunk-parallel pipeline). */
 int cgx_sample_temperature_dev(const float* logits, int V, float T, float u, int* out_dev);
+/* The same on `rows` device rows at once (row r at logits + r * ld, its
+ * draw u_dev[r] on the device, token to out_dev[r]), queued without
+ * synchronising: the batched loop's draft draws (rows of up to 32768 values
+ * one workgroup each in one launch, longer rows through the pipeline). */
+int cgx_sample_temperature_rows_dev(const float* logits, int rows, int V, float T,
+                                    const float* u_dev, int* out_dev, size_t ld);
 int cgx_sample_top_k_u(const float* logits, int V, int k, float u);
 int cgx_sample_top_p_u(const float* logits, int V, float top_p, float u);
 int cgx_sample_corrected_u(const float* draft_probs, const float* target_probs,

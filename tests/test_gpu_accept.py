@@ -211,6 +211,35 @@ def test_sample_temperature_dev_matches_oracle(gpu, oracle, rng, V):
     out.free()
 
 
+@pytest.mark.parametrize("V,ld_pad", [(1000, 0), (32000, 4000), (32768, 0), (50257, 7)])
+def test_sample_temperature_rows_dev_matches_oracle(gpu, oracle, rng, V, ld_pad):
+    """Draws from several device rows in one call (one workgroup per row up
+    to 32768 values, the pipeline above) equal the oracle's row by row:
+    diffuse and peaked rows, T = 1 and 0.8, uniforms on and next to a CDF
+    step."""
+    rows, ld = 6, V + ld_pad
+    for T in (1.0, 0.8):
+        x = np.zeros((rows, ld), np.float32)
+        x[:, :V] = rng.normal(0, 2, (rows, V)) * np.array([2, 2, 10, 10, 1, 30])[:, None]
+        u = rng.uniform(0, 1, rows).astype(np.float32)
+        for r in (1, 3):
+            p = _oracle_probs(oracle, np.ascontiguousarray(x[r, :V]), T)
+            cdf = np.add.accumulate(p, dtype=np.float32)
+            c = cdf[rng.integers(0, V)]
+            u[r] = c if r == 1 else np.nextafter(c, np.float32(0))
+        dx, du = DeviceArray.from_numpy(gpu, x), DeviceArray.from_numpy(gpu, u)
+        out = DeviceArray(gpu, rows * 4)
+        assert gpu.cgx_sample_temperature_rows_dev(dx.ptr, rows, V, T, du.ptr, out.ptr,
+                                                   ld) == 0, last_error(gpu)
+        got = out.numpy(np.int32, (rows,))
+        for r in range(rows):
+            row = np.ascontiguousarray(x[r, :V])
+            exp = oracle.orc_sample_temperature(ptr(row), V, T, float(u[r]))
+            assert got[r] == exp, (V, T, r, float(u[r]), got[r], exp)
+        for a in (dx, du, out):
+            a.free()
+
+
 @pytest.mark.parametrize("V", [64, 1000, 32000])
 def test_sample_corrected_bitexact(gpu, oracle, rng, V):
     for trial in range(8):
