@@ -2,6 +2,7 @@
 declares (no compute calls: there is no GPU here)."""
 from __future__ import annotations
 
+import ctypes
 import re
 from pathlib import Path
 
@@ -67,3 +68,20 @@ def test_declared_only_functions_report_errors(lib):
     lib.cgx_clear_error()
     assert not lib.cg_quantize_gptq(None, None, 128, 4)
     assert "not implemented" in capi.last_error(lib)
+
+
+def test_device_draws_reject_bad_arguments_without_gpu(lib):
+    """The device-row draw entry points check their arguments before any
+    device call: null pointers and empty rows are errors, on any host."""
+    lib.cgx_clear_error()
+    assert lib.cgx_sample_temperature_dev(None, 32000, 1.0, 0.5, None) == -1
+    assert "invalid argument" in capi.last_error(lib)
+    lib.cgx_clear_error()
+    assert lib.cgx_sample_temperature_rows_dev(None, 4, 32000, 1.0, None, None, 32000) == -1
+    assert "invalid argument" in capi.last_error(lib)
+    lib.cgx_clear_error()
+    buf = ctypes.create_string_buffer(16)
+    p = ctypes.addressof(buf)
+    assert lib.cgx_sample_temperature_rows_dev(p, 0, 32000, 1.0, p, p, 32000) == -1
+    assert "invalid argument" in capi.last_error(lib)
+    assert lib.cgx_sample_row_certified(-1) in (0, 1)
